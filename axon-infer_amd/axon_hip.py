@@ -1,0 +1,171 @@
+"""ctypes binding of the hip kernel table's C ABI (include/axon_hip.h) and of the device-resident
+forward pass (include/axon_model.h).
+
+This is the Python face of the library for tests, the benchmark and smoke checks. Device memory
+is owned by DeviceBuffer; every call raises HipError with the library's message on a non-zero
+status. Nothing here computes on the CPU: if libaxon_hip.so is missing or no gfx950 device is
+present, the calls fail loudly.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+from pathlib import Path
+
+import numpy as np
+
+PKG = Path(__file__).resolve().parent
+HIP_SO = PKG / "libaxon_hip.so"
+HOST_SO = PKG / "libaxon_host.so"
+
+F32, F16, Q4_0, Q4_1, Q8_0, Q6_K, BF16 = 0, 1, 2, 3, 8, 14, 30
+
+
+class HipError(RuntimeError):
+    pass
+
+
+_lib = None
+
+
+def lib() -> C.CDLL:
+    """libaxon_hip.so, loaded once. Raises when it has not been built."""
+    global _lib
+    if _lib is None:
+        if not HIP_SO.exists():
+            raise HipError(f"{HIP_SO} is missing: build it with __graft_entry__.build()")
+        L = C.CDLL(str(HIP_SO))
+        L.axon_hip_last_error.restype = C.c_char_p
+        L.axon_hip_attention_scratch_floats.restype = C.c_size_t
+        _lib = L
+    return _lib
+
+
+def check(rc: int, what: str = "") -> None:
+    if rc != 0:
+        raise HipError(f"{what}: status {rc}: {lib().axon_hip_last_error().decode()}")
+
+
+def device_count() -> int:
+    n = C.c_int(0)
+    lib().axon_hip_device_count(C.byref(n))
+    return n.value
+
+
+def init(device: int = 0) -> None:
+    check(lib().axon_hip_init(device), "axon_hip_init")
+
+
+def synchronize() -> None:
+    check(lib().axon_hip_synchronize(), "synchronize")
+
+
+def _arg(a):
+    if isinstance(a, DeviceBuffer):
+        return C.c_void_p(a.ptr)
+    if a is None:
+        return C.c_void_p(0)
+    if isinstance(a, float):
+        return C.c_float(a)
+    if isinstance(a, (C._SimpleCData, C.c_void_p, C.Array)) or hasattr(a, "_fields_"):
+        return a
+    if isinstance(a, np.ndarray):
+        return C.c_void_p(a.ctypes.data)
+    return C.c_size_t(a)
+
+
+def call(name: str, *args) -> None:
+    """Calls axon_hip_<name> with DeviceBuffers as device pointers, ints as size_t, floats
+    as float, raising on a non-zero status."""
+    check(getattr(lib(), "axon_hip_" + name)(*[_arg(a) for a in args]), name)
+
+
+class DeviceBuffer:
+    """An owned device allocation."""
+
+    def __init__(self, nbytes: int):
+        self.nbytes = int(nbytes)
+        p = C.c_void_p(0)
+        check(lib().axon_hip_malloc(C.byref(p), C.c_size_t(max(self.nbytes, 1))), "malloc")
+        self.ptr = p.value or 0
+
+    @classmethod
+    def of(cls, a: np.ndarray) -> "DeviceBuffer":
+        a = np.ascontiguousarray(a)
+        b = cls(a.nbytes)
+        b.upload(a)
+        return b
+
+    def upload(self, a: np.ndarray, offset: int = 0) -> None:
+        a = np.ascontiguousarray(a)
+        assert offset + a.nbytes <= self.nbytes
+        check(lib().axon_hip_memcpy_h2d(C.c_void_p(self.ptr + offset), C.c_void_p(a.ctypes.data),
+                                         C.c_size_t(a.nbytes)), "memcpy_h2d")
+
+    def download(self, dtype, count: int | None = None, offset: int = 0) -> np.ndarray:
+        dt = np.dtype(dtype)
+        if count is None:
+            count = (self.nbytes - offset) // dt.itemsize
+        out = np.empty(count, dtype=dt)
+        check(lib().axon_hip_memcpy_d2h(C.c_void_p(out.ctypes.data), C.c_void_p(self.ptr + offset),
+                                         C.c_size_t(out.nbytes)), "memcpy_d2h")
+        return out
+
+    def fill(self, value: int = 0) -> None:
+        check(lib().axon_hip_memset(C.c_void_p(self.ptr), C.c_int(value), C.c_size_t(self.nbytes)), "memset")
+
+    def at(self, offset_bytes: int) -> C.c_void_p:
+        return C.c_void_p(self.ptr + offset_bytes)
+
+    def free(self) -> None:
+        if self.ptr:
+            lib().axon_hip_free(C.c_void_p(self.ptr))
+            self.ptr = 0
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass
+
+
+class Event:
+    def __init__(self):
+        p = C.c_void_p(0)
+        check(lib().axon_hip_event_create(C.byref(p)), "event_create")
+        self.h = p
+
+    def record(self) -> None:
+        check(lib().axon_hip_event_record(self.h), "event_record")
+
+    def elapsed_ms(self, later: "Event") -> float:
+        ms = C.c_float(0)
+        check(lib().axon_hip_event_elapsed_ms(self.h, later.h, C.byref(ms)), "event_elapsed")
+        return ms.value
+
+    def __del__(self):
+        try:
+            lib().axon_hip_event_destroy(self.h)
+        except Exception:
+            pass
+
+
+class RopeRowsArgs(C.Structure):
+    _fields_ = [("q", C.c_void_p), ("k", C.c_void_p), ("v", C.c_void_p), ("bq", C.c_void_p), ("bk", C.c_void_p),
+                ("bv", C.c_void_p), ("pos", C.c_void_p), ("pos0", C.c_int32), ("q_stride", C.c_uint32),
+                ("k_stride", C.c_uint32), ("n_head", C.c_uint32), ("n_kv", C.c_uint32), ("head_dim", C.c_uint32),
+                ("rotary_dim", C.c_uint32), ("neox", C.c_int), ("theta", C.c_float), ("freq_factors", C.c_void_p),
+                ("table", C.c_void_p), ("cache", C.c_void_p), ("cache_off", C.c_void_p),
+                ("k_layer_off", C.c_int64), ("v_layer_off", C.c_int64)]
+
+
+class AttentionRowsArgs(C.Structure):
+    _fields_ = [("q", C.c_void_p), ("out", C.c_void_p), ("q_stride", C.c_uint32), ("out_stride", C.c_uint32),
+                ("kv", C.c_void_p), ("k_off", C.c_void_p), ("v_off", C.c_void_p), ("n_vis", C.c_void_p),
+                ("k_layer_off", C.c_int64), ("v_layer_off", C.c_int64), ("n_past", C.c_int32),
+                ("n_head", C.c_uint32), ("n_kv", C.c_uint32), ("head_dim", C.c_uint32), ("scale", C.c_float),
+                ("f16", C.c_int), ("scratch", C.c_void_p), ("max_vis", C.c_uint32)]
+
+
+def ptr_of(b) -> int:
+    return 0 if b is None else (b.ptr if isinstance(b, DeviceBuffer) else int(b))

@@ -1,0 +1,604 @@
+// The C ABI of the hip table (include/axon_hip.h): device detection and lifecycle, and one
+// thin adapter per entry that validates sizes on the host, then launches the kernels of this
+// library on the library stream. No entry falls back to the CPU.
+#include "common.h"
+#include "elementwise.h"
+#include "matmul_float.h"
+#include "matvec.h"
+
+#include "../../../include/axon_hip.h"
+
+#include <algorithm>
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <mutex>
+
+namespace axon_hip {
+
+namespace {
+
+thread_local char g_error[512] = "";
+hipStream_t g_stream = nullptr;
+int g_device = -1;
+std::mutex g_init_mutex;
+
+int hip_fail(hipError_t e, const char* what) {
+  return fail(kHipError, "%s: %s", what, hipGetErrorString(e));
+}
+
+int init_device(int device) {
+  std::lock_guard<std::mutex> lock(g_init_mutex);
+  if (g_device == device && g_stream != nullptr) return kOk;
+  if (g_stream != nullptr) return fail(kInvalidArgument, "axon_hip_init: already bound to device %d", g_device);
+  int count = 0;
+  if (hipGetDeviceCount(&count) != hipSuccess || count == 0) {
+    (void)hipGetLastError();
+    return fail(kNoDevice, "hip: no GPU visible to this process");
+  }
+  if (device < 0 || device >= count) return fail(kInvalidArgument, "hip: device %d of %d", device, count);
+  hipDeviceProp_t prop;
+  hipError_t e = hipGetDeviceProperties(&prop, device);
+  if (e != hipSuccess) return hip_fail(e, "hipGetDeviceProperties");
+  if (std::strncmp(prop.gcnArchName, "gfx950", 6) != 0)
+    return fail(kNoDevice, "hip: device %d is %s; this table is built for gfx950 (MI355X) only", device,
+                prop.gcnArchName);
+  e = hipSetDevice(device);
+  if (e != hipSuccess) return hip_fail(e, "hipSetDevice");
+  e = hipStreamCreateWithFlags(&g_stream, hipStreamNonBlocking);
+  if (e != hipSuccess) return hip_fail(e, "hipStreamCreateWithFlags");
+  g_device = device;
+  return kOk;
+}
+
+int ready() {
+  if (g_stream != nullptr) return kOk;
+  return init_device(0);
+}
+
+#define AXON_READY()                 \
+  do {                               \
+    const int rc_ = ready();         \
+    if (rc_ != kOk) return rc_;      \
+  } while (0)
+
+bool fits_u32(size_t v) { return v <= 0xffffffffull; }
+
+// The Q8_0-activation path: groups of up to four rows on the dot4 matvec below 16 rows,
+// int8 MFMA tiles from 16 rows.
+int q8_matmul(int type, const void* xq, size_t n_rows, size_t n_in, size_t n_seg, const void* const* w,
+              float* const* y, const size_t* n_out, const size_t* y_stride, int accumulate) {
+  if (n_in % kQK != 0) return fail(kInvalidArgument, "quantized matmul: n_in %zu is not a multiple of 32", n_in);
+  if (type != Q8_0 && type != Q4_0 && type != Q4_1) return fail(kUnsupported, "matmul_q8: weight type %d", type);
+  if (n_seg < 1 || n_seg > 3) return fail(kInvalidArgument, "matmul_q8: %zu segments", n_seg);
+  if (!fits_u32(n_rows) || !fits_u32(n_in)) return fail(kInvalidArgument, "matmul_q8: sizes too large");
+  for (size_t s = 0; s < n_seg; ++s) {
+    if (!fits_u32(n_out[s]) || !fits_u32(y_stride[s])) return fail(kInvalidArgument, "matmul_q8: sizes too large");
+    if (n_rows > 1 && y_stride[s] < n_out[s]) return fail(kInvalidArgument, "matmul_q8: y_stride %zu < n_out %zu", y_stride[s], n_out[s]);
+  }
+  if (n_rows == 0) return kOk;
+  const uint32_t nb = static_cast<uint32_t>(n_in / kQK);
+  const size_t xrow = static_cast<size_t>(nb) * kBytesQ8_0;
+  if (n_rows >= 16) {
+    for (size_t s = 0; s < n_seg; ++s) {
+      MatvecArgs a{};
+      a.seg[0] = MatvecSeg{static_cast<const uint8_t*>(w[s]), y[s], static_cast<uint32_t>(n_out[s]),
+                           static_cast<uint32_t>(y_stride[s]), 0};
+      a.n_seg = 1;
+      a.xq = static_cast<const uint8_t*>(xq);
+      a.nb = nb;
+      a.m = static_cast<uint32_t>(n_rows);
+      a.accumulate = accumulate;
+      const int rc = matmul_q8_mfma_launch(type, a);
+      if (rc != kOk) return rc;
+    }
+    return kOk;
+  }
+  const uint32_t group = matvec_q8_max_rows(type, nb);
+  for (size_t m0 = 0; m0 < n_rows; m0 += group) {
+    const uint32_t mm = static_cast<uint32_t>(std::min<size_t>(group, n_rows - m0));
+    MatvecArgs a{};
+    for (size_t s = 0; s < n_seg; ++s) {
+      a.seg[s] = MatvecSeg{static_cast<const uint8_t*>(w[s]), y[s] + m0 * y_stride[s], static_cast<uint32_t>(n_out[s]),
+                           static_cast<uint32_t>(y_stride[s]), 0};
+    }
+    a.n_seg = static_cast<int>(n_seg);
+    a.xq = static_cast<const uint8_t*>(xq) + m0 * xrow;
+    a.nb = nb;
+    a.m = mm;
+    a.accumulate = accumulate;
+    const int rc = matvec_q8_launch(type, a);
+    if (rc != kOk) return rc;
+  }
+  return kOk;
+}
+
+int q8_rows(int type, const void* w, const void* xq, float* y, size_t n_rows, size_t n_out, size_t n_in,
+            size_t y_stride) {
+  AXON_READY();
+  const void* ws[1] = {w};
+  float* ys[1] = {y};
+  const size_t no[1] = {n_out};
+  const size_t st[1] = {y_stride};
+  return q8_matmul(type, xq, n_rows, n_in, 1, ws, ys, no, st, 0);
+}
+
+int float_rows(int type, const void* w, const float* x, float* y, size_t n_rows, size_t n_out, size_t n_in,
+               size_t y_stride) {
+  AXON_READY();
+  if (!fits_u32(n_rows) || !fits_u32(n_out) || !fits_u32(n_in) || !fits_u32(y_stride))
+    return fail(kInvalidArgument, "matmul: sizes too large");
+  if (n_rows > 1 && y_stride < n_out) return fail(kInvalidArgument, "matmul: y_stride %zu < n_out %zu", y_stride, n_out);
+  return matmul_float_launch(type, w, x, y, static_cast<uint32_t>(n_rows), static_cast<uint32_t>(n_out),
+                             static_cast<uint32_t>(n_in), static_cast<uint32_t>(y_stride));
+}
+
+int q6k_rows(const void* w, const float* x, float* y, size_t n_rows, size_t n_out, size_t n_in, size_t y_stride) {
+  AXON_READY();
+  if (n_in % kQKK != 0) return fail(kInvalidArgument, "matmul_q6_k: n_in %zu is not a multiple of 256", n_in);
+  if (!fits_u32(n_rows) || !fits_u32(n_out) || !fits_u32(n_in) || !fits_u32(y_stride))
+    return fail(kInvalidArgument, "matmul_q6_k: sizes too large");
+  if (n_rows > 1 && y_stride < n_out) return fail(kInvalidArgument, "matmul_q6_k: y_stride %zu < n_out %zu", y_stride, n_out);
+  MatvecArgs a{};
+  a.seg[0] = MatvecSeg{static_cast<const uint8_t*>(w), y, static_cast<uint32_t>(n_out), static_cast<uint32_t>(y_stride), 0};
+  a.n_seg = 1;
+  a.xq = reinterpret_cast<const uint8_t*>(x);
+  a.nb = static_cast<uint32_t>(n_in / kQKK);
+  a.m = static_cast<uint32_t>(n_rows);
+  return matvec_q6k_launch(a, static_cast<uint32_t>(n_in));
+}
+
+int attention_heads(const float* q, const void* k, const void* v, float* out, float* scores, size_t n_q,
+                    size_t n_past, size_t n_head, size_t n_kv, size_t head_dim, float scale, size_t hb, size_t he,
+                    int f16) {
+  AXON_READY();
+  if (!fits_u32(n_q) || !fits_u32(n_past + n_q) || !fits_u32(n_head) || !fits_u32(head_dim))
+    return fail(kInvalidArgument, "attention: sizes too large");
+  // One cache for all rows; K and V are separate arrays, so address both from the K base.
+  AttnArgs a{};
+  a.q = q;
+  a.out = out;
+  a.q_stride = static_cast<uint32_t>(n_head * head_dim);
+  a.out_stride = a.q_stride;
+  a.kv = k;
+  const ptrdiff_t elem = f16 ? 2 : 4;
+  a.k_off_c = 0;
+  a.v_off_c = (static_cast<const char*>(v) - static_cast<const char*>(k)) / elem;
+  if ((static_cast<const char*>(v) - static_cast<const char*>(k)) % elem != 0)
+    return fail(kInvalidArgument, "attention: v_cache is not element-aligned with k_cache");
+  a.n_past = static_cast<int32_t>(n_past);
+  a.n_head = static_cast<uint32_t>(n_head);
+  a.n_kv = static_cast<uint32_t>(n_kv);
+  a.head_dim = static_cast<uint32_t>(head_dim);
+  a.head_begin = static_cast<uint32_t>(hb);
+  a.head_end = static_cast<uint32_t>(he);
+  a.scale = scale;
+  a.f16 = f16;
+  a.scratch = scores;
+  a.max_vis = static_cast<uint32_t>(n_past + n_q);
+  return attention_launch(a, static_cast<uint32_t>(n_q));
+}
+
+}  // namespace
+
+hipStream_t stream() { return g_stream; }
+
+int fail(int code, const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  std::vsnprintf(g_error, sizeof(g_error), fmt, ap);
+  va_end(ap);
+  return code;
+}
+
+int check_launch(const char* what) {
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return hip_fail(e, what);
+  return kOk;
+}
+
+}  // namespace axon_hip
+
+using namespace axon_hip;
+
+extern "C" {
+
+// ---- lifecycle ------------------------------------------------------------------------------
+
+int axon_hip_device_count(int* count) {
+  int n = 0;
+  if (hipGetDeviceCount(&n) != hipSuccess) {
+    (void)hipGetLastError();
+    n = 0;
+  }
+  *count = n;
+  return kOk;
+}
+
+int axon_hip_init(int device) { return init_device(device); }
+
+int axon_hip_device_arch(char* buf, size_t len) {
+  AXON_READY();
+  hipDeviceProp_t prop;
+  const hipError_t e = hipGetDeviceProperties(&prop, g_device);
+  if (e != hipSuccess) return hip_fail(e, "hipGetDeviceProperties");
+  std::snprintf(buf, len, "%s", prop.gcnArchName);
+  return kOk;
+}
+
+const char* axon_hip_last_error(void) { return g_error; }
+
+int axon_hip_malloc(void** ptr, size_t bytes) {
+  AXON_READY();
+  *ptr = nullptr;
+  if (bytes == 0) return kOk;
+  const hipError_t e = hipMalloc(ptr, bytes);
+  if (e == hipErrorOutOfMemory) {
+    (void)hipGetLastError();
+    return fail(kOutOfMemory, "hipMalloc: %zu bytes: out of device memory", bytes);
+  }
+  if (e != hipSuccess) return hip_fail(e, "hipMalloc");
+  return kOk;
+}
+
+int axon_hip_free(void* ptr) {
+  if (ptr == nullptr) return kOk;
+  const hipError_t e = hipFree(ptr);
+  return e == hipSuccess ? kOk : hip_fail(e, "hipFree");
+}
+
+int axon_hip_host_malloc(void** ptr, size_t bytes) {
+  AXON_READY();
+  const hipError_t e = hipHostMalloc(ptr, bytes, hipHostMallocDefault);
+  return e == hipSuccess ? kOk : hip_fail(e, "hipHostMalloc");
+}
+
+int axon_hip_host_free(void* ptr) {
+  const hipError_t e = hipHostFree(ptr);
+  return e == hipSuccess ? kOk : hip_fail(e, "hipHostFree");
+}
+
+static int copy_sync(void* dst, const void* src, size_t bytes, hipMemcpyKind kind, const char* what) {
+  AXON_READY();
+  if (bytes == 0) return kOk;
+  hipError_t e = hipMemcpyAsync(dst, src, bytes, kind, g_stream);
+  if (e == hipSuccess) e = hipStreamSynchronize(g_stream);
+  return e == hipSuccess ? kOk : hip_fail(e, what);
+}
+
+int axon_hip_memcpy_h2d(void* dst, const void* src, size_t bytes) {
+  return copy_sync(dst, src, bytes, hipMemcpyHostToDevice, "memcpy_h2d");
+}
+int axon_hip_memcpy_d2h(void* dst, const void* src, size_t bytes) {
+  return copy_sync(dst, src, bytes, hipMemcpyDeviceToHost, "memcpy_d2h");
+}
+int axon_hip_memcpy_d2d(void* dst, const void* src, size_t bytes) {
+  return copy_sync(dst, src, bytes, hipMemcpyDeviceToDevice, "memcpy_d2d");
+}
+
+int axon_hip_memcpy_h2d_async(void* dst, const void* src, size_t bytes) {
+  AXON_READY();
+  if (bytes == 0) return kOk;
+  const hipError_t e = hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, g_stream);
+  return e == hipSuccess ? kOk : hip_fail(e, "memcpy_h2d_async");
+}
+
+int axon_hip_memset(void* dst, int value, size_t bytes) {
+  AXON_READY();
+  if (bytes == 0) return kOk;
+  hipError_t e = hipMemsetAsync(dst, value, bytes, g_stream);
+  if (e == hipSuccess) e = hipStreamSynchronize(g_stream);
+  return e == hipSuccess ? kOk : hip_fail(e, "memset");
+}
+
+int axon_hip_synchronize(void) {
+  AXON_READY();
+  const hipError_t e = hipStreamSynchronize(g_stream);
+  return e == hipSuccess ? kOk : hip_fail(e, "hipStreamSynchronize");
+}
+
+int axon_hip_event_create(void** event) {
+  AXON_READY();
+  hipEvent_t ev;
+  const hipError_t e = hipEventCreate(&ev);
+  if (e != hipSuccess) return hip_fail(e, "hipEventCreate");
+  *event = ev;
+  return kOk;
+}
+
+int axon_hip_event_record(void* event) {
+  AXON_READY();
+  const hipError_t e = hipEventRecord(static_cast<hipEvent_t>(event), g_stream);
+  return e == hipSuccess ? kOk : hip_fail(e, "hipEventRecord");
+}
+
+int axon_hip_event_elapsed_ms(void* start, void* stop, float* ms) {
+  hipError_t e = hipEventSynchronize(static_cast<hipEvent_t>(stop));
+  if (e == hipSuccess) e = hipEventElapsedTime(ms, static_cast<hipEvent_t>(start), static_cast<hipEvent_t>(stop));
+  return e == hipSuccess ? kOk : hip_fail(e, "hipEventElapsedTime");
+}
+
+int axon_hip_event_destroy(void* event) {
+  const hipError_t e = hipEventDestroy(static_cast<hipEvent_t>(event));
+  return e == hipSuccess ? kOk : hip_fail(e, "hipEventDestroy");
+}
+
+int axon_hip_graph_begin(void) {
+  AXON_READY();
+  const hipError_t e = hipStreamBeginCapture(g_stream, hipStreamCaptureModeThreadLocal);
+  return e == hipSuccess ? kOk : hip_fail(e, "hipStreamBeginCapture");
+}
+
+int axon_hip_graph_end(void** graph) {
+  AXON_READY();
+  hipGraph_t g = nullptr;
+  hipError_t e = hipStreamEndCapture(g_stream, &g);
+  if (e != hipSuccess) return hip_fail(e, "hipStreamEndCapture");
+  hipGraphExec_t exec = nullptr;
+  e = hipGraphInstantiate(&exec, g, nullptr, nullptr, 0);
+  (void)hipGraphDestroy(g);
+  if (e != hipSuccess) return hip_fail(e, "hipGraphInstantiate");
+  *graph = exec;
+  return kOk;
+}
+
+int axon_hip_graph_launch(void* graph) {
+  AXON_READY();
+  const hipError_t e = hipGraphLaunch(static_cast<hipGraphExec_t>(graph), g_stream);
+  return e == hipSuccess ? kOk : hip_fail(e, "hipGraphLaunch");
+}
+
+int axon_hip_graph_destroy(void* graph) {
+  const hipError_t e = hipGraphExecDestroy(static_cast<hipGraphExec_t>(graph));
+  return e == hipSuccess ? kOk : hip_fail(e, "hipGraphExecDestroy");
+}
+
+// ---- KernelTable entries -----------------------------------------------------------------
+
+int axon_hip_matmul_f32(const float* w, const float* x, float* y, size_t n_out, size_t n_in) {
+  return float_rows(F32, w, x, y, 1, n_out, n_in, n_out);
+}
+int axon_hip_matmul_f16(const uint16_t* w, const float* x, float* y, size_t n_out, size_t n_in) {
+  return float_rows(F16, w, x, y, 1, n_out, n_in, n_out);
+}
+int axon_hip_matmul_bf16(const uint16_t* w, const float* x, float* y, size_t n_out, size_t n_in) {
+  return float_rows(BF16, w, x, y, 1, n_out, n_in, n_out);
+}
+int axon_hip_matmul_f32_rows(const float* w, const float* x, float* y, size_t n_rows, size_t n_out, size_t n_in,
+                             size_t y_stride) {
+  return float_rows(F32, w, x, y, n_rows, n_out, n_in, y_stride);
+}
+int axon_hip_matmul_f16_rows(const uint16_t* w, const float* x, float* y, size_t n_rows, size_t n_out, size_t n_in,
+                             size_t y_stride) {
+  return float_rows(F16, w, x, y, n_rows, n_out, n_in, y_stride);
+}
+int axon_hip_matmul_bf16_rows(const uint16_t* w, const float* x, float* y, size_t n_rows, size_t n_out,
+                              size_t n_in, size_t y_stride) {
+  return float_rows(BF16, w, x, y, n_rows, n_out, n_in, y_stride);
+}
+
+int axon_hip_rmsnorm(const float* x, const float* weight, float* y, size_t n, float eps) {
+  AXON_READY();
+  if (n == 0) return fail(kInvalidArgument, "rmsnorm: n is 0");
+  if (!fits_u32(n)) return fail(kInvalidArgument, "rmsnorm: n too large");
+  return rmsnorm_launch(x, weight, y, nullptr, static_cast<uint32_t>(n), 1, eps);
+}
+
+int axon_hip_rope(float* x, size_t n_heads, size_t pos, size_t head_dim, size_t rotary_dim, float theta, int style,
+                  const float* freq_factors) {
+  AXON_READY();
+  if (!fits_u32(n_heads) || !fits_u32(head_dim) || pos > 0x7fffffffull) return fail(kInvalidArgument, "rope: sizes too large");
+  RopeRowsArgs a{};
+  a.q = x;
+  a.pos0 = static_cast<int32_t>(pos);
+  a.q_stride = static_cast<uint32_t>(n_heads * head_dim);
+  a.n_head = static_cast<uint32_t>(n_heads);
+  a.head_dim = static_cast<uint32_t>(head_dim);
+  a.rotary_dim = static_cast<uint32_t>(rotary_dim);
+  a.neox = style;
+  a.theta = theta;
+  a.freq_factors = freq_factors;
+  return rope_rows_launch(a, 1);
+}
+
+int axon_hip_softmax(float* x, size_t n) {
+  AXON_READY();
+  if (n == 0) return fail(kInvalidArgument, "softmax: n is 0");
+  if (!fits_u32(n)) return fail(kInvalidArgument, "softmax: n too large");
+  return softmax_launch(x, static_cast<uint32_t>(n));
+}
+
+int axon_hip_silu_mul(const float* gate, const float* up, float* out, size_t n) {
+  AXON_READY();
+  if (!fits_u32(n)) return fail(kInvalidArgument, "silu_mul: n too large");
+  return silu_mul_launch(gate, up, out, nullptr, static_cast<uint32_t>(n), 1);
+}
+
+int axon_hip_embedding_row(int type, const void* table, size_t n, int64_t index, float* out) {
+  AXON_READY();
+  if (index < 0) return fail(kInvalidArgument, "embedding_row: index %lld", static_cast<long long>(index));
+  if (!fits_u32(n)) return fail(kInvalidArgument, "embedding_row: n too large");
+  return embedding_launch(type, static_cast<const uint8_t*>(table), static_cast<uint32_t>(n), nullptr, index, 1, out);
+}
+
+int axon_hip_attention(const float* q, const float* k, const float* v, float* out, float* scores, size_t seq,
+                       size_t n_head, size_t n_head_kv, size_t head_dim, float scale) {
+  return attention_heads(q, k, v, out, scores, seq, 0, n_head, n_head_kv, head_dim, scale, 0, n_head, 0);
+}
+
+int axon_hip_attention_kv(const float* q, const float* k_cache, const float* v_cache, float* out, float* scores,
+                          size_t n_q, size_t n_past, size_t n_head, size_t n_head_kv, size_t head_dim, float scale) {
+  return attention_heads(q, k_cache, v_cache, out, scores, n_q, n_past, n_head, n_head_kv, head_dim, scale, 0,
+                         n_head, 0);
+}
+
+int axon_hip_attention_kv_heads(const float* q, const float* k_cache, const float* v_cache, float* out,
+                                float* scores, size_t n_q, size_t n_past, size_t n_head, size_t n_head_kv,
+                                size_t head_dim, float scale, size_t head_begin, size_t head_end) {
+  return attention_heads(q, k_cache, v_cache, out, scores, n_q, n_past, n_head, n_head_kv, head_dim, scale,
+                         head_begin, head_end, 0);
+}
+
+int axon_hip_attention_kv_heads_f16(const float* q, const uint16_t* k_cache, const uint16_t* v_cache, float* out,
+                                    float* scores, size_t n_q, size_t n_past, size_t n_head, size_t n_head_kv,
+                                    size_t head_dim, float scale, size_t head_begin, size_t head_end) {
+  return attention_heads(q, k_cache, v_cache, out, scores, n_q, n_past, n_head, n_head_kv, head_dim, scale,
+                         head_begin, head_end, 1);
+}
+
+int axon_hip_matmul_q8_0(const void* w, const float* x, float* y, size_t n_out, size_t n_in) {
+  return float_rows(Q8_0, w, x, y, 1, n_out, n_in, n_out);
+}
+int axon_hip_matmul_q4_0(const void* w, const float* x, float* y, size_t n_out, size_t n_in) {
+  return float_rows(Q4_0, w, x, y, 1, n_out, n_in, n_out);
+}
+int axon_hip_matmul_q8_0_q8(const void* w, const void* xq, float* y, size_t n_out, size_t n_in) {
+  return q8_rows(Q8_0, w, xq, y, 1, n_out, n_in, n_out);
+}
+int axon_hip_matmul_q4_0_q8(const void* w, const void* xq, float* y, size_t n_out, size_t n_in) {
+  return q8_rows(Q4_0, w, xq, y, 1, n_out, n_in, n_out);
+}
+int axon_hip_matmul_q8_0_rows(const void* w, const float* x, float* y, size_t n_rows, size_t n_out, size_t n_in,
+                              size_t y_stride) {
+  return float_rows(Q8_0, w, x, y, n_rows, n_out, n_in, y_stride);
+}
+int axon_hip_matmul_q4_0_rows(const void* w, const float* x, float* y, size_t n_rows, size_t n_out, size_t n_in,
+                              size_t y_stride) {
+  return float_rows(Q4_0, w, x, y, n_rows, n_out, n_in, y_stride);
+}
+int axon_hip_matmul_q8_0_q8_rows(const void* w, const void* xq, float* y, size_t n_rows, size_t n_out, size_t n_in,
+                                 size_t y_stride) {
+  return q8_rows(Q8_0, w, xq, y, n_rows, n_out, n_in, y_stride);
+}
+int axon_hip_matmul_q4_0_q8_rows(const void* w, const void* xq, float* y, size_t n_rows, size_t n_out, size_t n_in,
+                                 size_t y_stride) {
+  return q8_rows(Q4_0, w, xq, y, n_rows, n_out, n_in, y_stride);
+}
+
+int axon_hip_quantize_row_q8_0(const float* x, void* out, size_t n) {
+  AXON_READY();
+  if (!fits_u32(n)) return fail(kInvalidArgument, "quantize_row_q8_0: n too large");
+  return quantize_rows_launch(x, static_cast<uint8_t*>(out), static_cast<uint32_t>(n), 1, static_cast<uint32_t>(n));
+}
+
+int axon_hip_matmul_q4_1(const void* w, const float* x, float* y, size_t n_out, size_t n_in) {
+  return float_rows(Q4_1, w, x, y, 1, n_out, n_in, n_out);
+}
+int axon_hip_matmul_q4_1_q8(const void* w, const void* xq, float* y, size_t n_out, size_t n_in) {
+  return q8_rows(Q4_1, w, xq, y, 1, n_out, n_in, n_out);
+}
+int axon_hip_matmul_q4_1_rows(const void* w, const float* x, float* y, size_t n_rows, size_t n_out, size_t n_in,
+                              size_t y_stride) {
+  return float_rows(Q4_1, w, x, y, n_rows, n_out, n_in, y_stride);
+}
+int axon_hip_matmul_q4_1_q8_rows(const void* w, const void* xq, float* y, size_t n_rows, size_t n_out, size_t n_in,
+                                 size_t y_stride) {
+  return q8_rows(Q4_1, w, xq, y, n_rows, n_out, n_in, y_stride);
+}
+int axon_hip_matmul_q6_k(const void* w, const float* x, float* y, size_t n_out, size_t n_in) {
+  return q6k_rows(w, x, y, 1, n_out, n_in, n_out);
+}
+int axon_hip_matmul_q6_k_rows(const void* w, const float* x, float* y, size_t n_rows, size_t n_out, size_t n_in,
+                              size_t y_stride) {
+  return q6k_rows(w, x, y, n_rows, n_out, n_in, y_stride);
+}
+
+// ---- coarse entries ---------------------------------------------------------------------
+
+int axon_hip_rmsnorm_rows(const float* x, const float* weight, float* y, void* yq, size_t n, size_t n_rows,
+                          float eps) {
+  AXON_READY();
+  if (n == 0) return fail(kInvalidArgument, "rmsnorm: n is 0");
+  if (!fits_u32(n) || !fits_u32(n_rows)) return fail(kInvalidArgument, "rmsnorm: sizes too large");
+  if (y == nullptr && yq == nullptr) return fail(kInvalidArgument, "rmsnorm_rows: no output");
+  return rmsnorm_launch(x, weight, y, static_cast<uint8_t*>(yq), static_cast<uint32_t>(n),
+                        static_cast<uint32_t>(n_rows), eps);
+}
+
+int axon_hip_quantize_rows_q8_0(const float* x, void* out, size_t n, size_t n_rows, size_t x_stride) {
+  AXON_READY();
+  if (!fits_u32(n) || !fits_u32(n_rows) || !fits_u32(x_stride)) return fail(kInvalidArgument, "quantize_rows: sizes too large");
+  return quantize_rows_launch(x, static_cast<uint8_t*>(out), static_cast<uint32_t>(n), static_cast<uint32_t>(n_rows),
+                              static_cast<uint32_t>(x_stride));
+}
+
+int axon_hip_silu_mul_rows(const float* gate, const float* up, float* out, void* outq, size_t n, size_t n_rows) {
+  AXON_READY();
+  if (!fits_u32(n) || !fits_u32(n_rows)) return fail(kInvalidArgument, "silu_mul_rows: sizes too large");
+  return silu_mul_launch(gate, up, out, static_cast<uint8_t*>(outq), static_cast<uint32_t>(n),
+                         static_cast<uint32_t>(n_rows));
+}
+
+int axon_hip_add(float* x, const float* y, size_t n) {
+  AXON_READY();
+  return add_launch(x, y, n);
+}
+
+int axon_hip_matmul_q8_fused(int type, const void* xq, size_t n_rows, size_t n_in, size_t n_seg,
+                             const void* const* w, float* const* y, const size_t* n_out, const size_t* y_stride,
+                             int accumulate) {
+  AXON_READY();
+  return q8_matmul(type, xq, n_rows, n_in, n_seg, w, y, n_out, y_stride, accumulate);
+}
+
+int axon_hip_rope_rows(const axon_hip_rope_rows_args* args, size_t n_rows) {
+  AXON_READY();
+  if (!fits_u32(n_rows)) return fail(kInvalidArgument, "rope_rows: too many rows");
+  static_assert(sizeof(axon_hip_rope_rows_args) == sizeof(RopeRowsArgs), "rope args layout");
+  RopeRowsArgs a;
+  std::memcpy(&a, args, sizeof(a));
+  if ((a.bq == nullptr) != (a.bk == nullptr)) return fail(kInvalidArgument, "rope_rows: bq and bk go together");
+  return rope_rows_launch(a, static_cast<uint32_t>(n_rows));
+}
+
+static AttnArgs attn_from(const axon_hip_attention_rows_args* args) {
+  AttnArgs a{};
+  a.q = args->q;
+  a.out = args->out;
+  a.q_stride = args->q_stride;
+  a.out_stride = args->out_stride;
+  a.kv = args->kv;
+  a.k_off = args->k_off;
+  a.v_off = args->v_off;
+  a.n_vis = args->n_vis;
+  a.k_off_c = args->k_layer_off;
+  a.v_off_c = args->v_layer_off;
+  a.n_past = args->n_past;
+  a.n_head = args->n_head;
+  a.n_kv = args->n_kv;
+  a.head_dim = args->head_dim;
+  a.head_begin = 0;
+  a.head_end = args->n_head;
+  a.scale = args->scale;
+  a.f16 = args->f16;
+  a.scratch = args->scratch;
+  a.max_vis = args->max_vis;
+  return a;
+}
+
+int axon_hip_attention_rows(const axon_hip_attention_rows_args* args, size_t n_rows) {
+  AXON_READY();
+  if (!fits_u32(n_rows)) return fail(kInvalidArgument, "attention_rows: too many rows");
+  return attention_launch(attn_from(args), static_cast<uint32_t>(n_rows));
+}
+
+size_t axon_hip_attention_scratch_floats(const axon_hip_attention_rows_args* args, size_t n_rows) {
+  return attention_scratch_floats(attn_from(args), static_cast<uint32_t>(n_rows));
+}
+
+int axon_hip_embedding_rows(int type, const void* table, size_t n, const int32_t* ids, size_t n_rows, float* out) {
+  AXON_READY();
+  if (!fits_u32(n) || !fits_u32(n_rows)) return fail(kInvalidArgument, "embedding_rows: sizes too large");
+  if (ids == nullptr) return fail(kInvalidArgument, "embedding_rows: ids is NULL");
+  return embedding_launch(type, static_cast<const uint8_t*>(table), static_cast<uint32_t>(n), ids, 0,
+                          static_cast<uint32_t>(n_rows), out);
+}
+
+int axon_hip_block_sums(int type, const void* w_row, const void* xq, size_t n_blocks, int32_t* sumi,
+                        int32_t* sumx) {
+  AXON_READY();
+  if (!fits_u32(n_blocks)) return fail(kInvalidArgument, "block_sums: too many blocks");
+  return block_sums_launch(type, w_row, xq, static_cast<uint32_t>(n_blocks), sumi, sumx);
+}
+
+}  // extern "C"

@@ -1,0 +1,232 @@
+// Device-side building blocks shared by every kernel of the hip table: the GGUF block formats,
+// exact half/bfloat conversions, LDS staging of unaligned block streams, and the launch
+// plumbing (the library stream, status codes, the thread-local error message).
+//
+// All code here is gfx950 (CDNA4) only: 64-lane wavefronts, 160 KB of LDS per CU.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstddef>
+#include <cstdint>
+
+namespace axon_hip {
+
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+constexpr int kQK = 32;     // elements per Q8_0 / Q4_0 / Q4_1 block
+constexpr int kQKK = 256;   // elements per Q6_K super-block
+constexpr int kBytesQ8_0 = 34;
+constexpr int kBytesQ4_0 = 18;
+constexpr int kBytesQ4_1 = 20;
+constexpr int kBytesQ6_K = 210;
+
+// ggml type ids (GGUF tensor types), the subset the table handles.
+enum DType : int { F32 = 0, F16 = 1, Q4_0 = 2, Q4_1 = 3, Q8_0 = 8, Q6_K = 14, BF16 = 30 };
+
+// Status codes returned across the C ABI.
+enum Status : int {
+  kOk = 0,
+  kInvalidArgument = -1,
+  kUnsupported = -2,
+  kNoDevice = -3,
+  kHipError = -4,
+  kOutOfMemory = -5,
+};
+
+// ------------------------------------------------------------------------------------------
+// Exact conversions (IEEE binary16 / bfloat16 <-> binary32), written with integer operations
+// so that NaN payloads, signed zeros and subnormals come out bit for bit as the scalar table
+// produces them (trickymind1324/axon-infer src/core/dtype.cpp:198-272).
+
+__device__ __forceinline__ float half_bits_to_float(uint32_t h) {
+  const uint32_t sign = (h & 0x8000u) << 16;
+  const uint32_t e = (h >> 10) & 0x1fu;
+  const uint32_t m = h & 0x3ffu;
+  if (e == 0x1fu) return __uint_as_float(sign | 0x7f800000u | (m << 13));
+  if (e != 0) return __uint_as_float(sign | ((e + 112u) << 23) | (m << 13));
+  // Zero or subnormal: m * 2^-24 is exact in binary32 (a normal number there).
+  return __uint_as_float(sign | __float_as_uint(static_cast<float>(m) * 0x1p-24f));
+}
+
+// Round to nearest even, overflow to infinity, gradual underflow, NaN kept non-zero.
+__device__ __forceinline__ uint32_t float_to_half_bits(float f) {
+  const uint32_t x = __float_as_uint(f);
+  const uint32_t sign = (x >> 16) & 0x8000u;
+  const uint32_t e = (x >> 23) & 0xffu;
+  const uint32_t m = x & 0x7fffffu;
+  if (e == 0xffu) {
+    const uint32_t payload = m >> 13;
+    return sign | 0x7c00u | (m != 0 && payload == 0 ? 1u : payload);
+  }
+  const int ue = static_cast<int>(e) - 127;
+  if (ue > 15) return sign | 0x7c00u;
+  if (ue >= -14) {
+    // The carry of a mantissa round-up walks into the exponent, up to infinity (0x7c00).
+    uint32_t r = (static_cast<uint32_t>(ue + 15) << 10) | (m >> 13);
+    const uint32_t rest = m & 0x1fffu;
+    if (rest > 0x1000u || (rest == 0x1000u && (r & 1u))) ++r;
+    return sign | r;
+  }
+  if (ue >= -25) {
+    const uint32_t full = m | 0x800000u;
+    const uint32_t shift = static_cast<uint32_t>(-1 - ue);  // 14 .. 24
+    uint32_t hm = full >> shift;
+    const uint32_t rest = full & ((1u << shift) - 1u);
+    const uint32_t halfway = 1u << (shift - 1);
+    if (rest > halfway || (rest == halfway && (hm & 1u))) ++hm;
+    return sign | hm;
+  }
+  return sign;
+}
+
+__device__ __forceinline__ float bf16_bits_to_float(uint32_t h) { return __uint_as_float(h << 16); }
+
+// exp of a binary32 argument, evaluated in binary64 and rounded once: the correctly rounded
+// binary32 exponential except for arguments within ~2^-29 ulp of a rounding midpoint.
+__device__ __forceinline__ float exp_rounded(float x) {
+  return static_cast<float>(exp(static_cast<double>(x)));
+}
+
+// ------------------------------------------------------------------------------------------
+// Byte streams in LDS. GGUF blocks are 18, 20, 34 or 210 bytes, so a block starts on a 2-byte
+// boundary at best. Tiles are copied HBM -> LDS with the widest aligned loads the tile allows
+// (coalesced across the workgroup), and blocks are then read out of LDS as aligned dwords and
+// funnel-shifted into place.
+
+// Copies nbytes (a multiple of 2) from global src to LDS dst (16-byte aligned), using 16-, 4-
+// or 2-byte accesses, whichever the alignment of src and nbytes permits. Every thread of the
+// block must call it; it does not synchronise.
+__device__ __forceinline__ void stage_bytes(const uint8_t* __restrict__ src, uint8_t* dst,
+                                            uint32_t nbytes, uint32_t tid, uint32_t nthreads) {
+  const uintptr_t a = reinterpret_cast<uintptr_t>(src);
+  if (((a | nbytes) & 15u) == 0) {
+    const u32x4* s = reinterpret_cast<const u32x4*>(src);
+    u32x4* d = reinterpret_cast<u32x4*>(dst);
+    const uint32_t n = nbytes >> 4;
+    uint32_t i = tid;
+    // Eight loads in flight per thread before the first LDS store.
+    for (; i + 7 * nthreads < n; i += 8 * nthreads) {
+      u32x4 v[8];
+#pragma unroll
+      for (int k = 0; k < 8; ++k) v[k] = __builtin_nontemporal_load(s + i + k * nthreads);
+#pragma unroll
+      for (int k = 0; k < 8; ++k) d[i + k * nthreads] = v[k];
+    }
+    for (; i < n; i += nthreads) d[i] = __builtin_nontemporal_load(s + i);
+  } else if (((a | nbytes) & 3u) == 0) {
+    const uint32_t* s = reinterpret_cast<const uint32_t*>(src);
+    uint32_t* d = reinterpret_cast<uint32_t*>(dst);
+    const uint32_t n = nbytes >> 2;
+    uint32_t i = tid;
+    for (; i + 7 * nthreads < n; i += 8 * nthreads) {
+      uint32_t v[8];
+#pragma unroll
+      for (int k = 0; k < 8; ++k) v[k] = __builtin_nontemporal_load(s + i + k * nthreads);
+#pragma unroll
+      for (int k = 0; k < 8; ++k) d[i + k * nthreads] = v[k];
+    }
+    for (; i < n; i += nthreads) d[i] = __builtin_nontemporal_load(s + i);
+  } else {
+    const uint16_t* s = reinterpret_cast<const uint16_t*>(src);
+    uint16_t* d = reinterpret_cast<uint16_t*>(dst);
+    const uint32_t n = nbytes >> 1;
+    for (uint32_t i = tid; i < n; i += nthreads) d[i] = s[i];
+  }
+}
+
+// Copies n_rows rows of row_bytes each from global src (rows src_pitch bytes apart) to LDS
+// dst (rows dst_pitch bytes apart), with 4-byte accesses when src, src_pitch, dst_pitch and
+// row_bytes allow it and 2-byte accesses otherwise. Does not synchronise.
+__device__ __forceinline__ void stage_rows(const uint8_t* __restrict__ src, size_t src_pitch, uint8_t* dst,
+                                           uint32_t dst_pitch, uint32_t n_rows, uint32_t row_bytes,
+                                           uint32_t tid, uint32_t nthreads) {
+  const uintptr_t a = reinterpret_cast<uintptr_t>(src);
+  if (((a | src_pitch | dst_pitch | row_bytes) & 3u) == 0) {
+    const uint32_t per_row = row_bytes >> 2;
+    const uint32_t n = per_row * n_rows;
+    uint32_t i = tid;
+    for (; i + 7 * nthreads < n; i += 8 * nthreads) {
+      uint32_t v[8];
+#pragma unroll
+      for (int k = 0; k < 8; ++k) {
+        const uint32_t j = i + k * nthreads;
+        const uint32_t r = j / per_row;
+        v[k] = __builtin_nontemporal_load(reinterpret_cast<const uint32_t*>(src + r * src_pitch) + (j - r * per_row));
+      }
+#pragma unroll
+      for (int k = 0; k < 8; ++k) {
+        const uint32_t j = i + k * nthreads;
+        const uint32_t r = j / per_row;
+        reinterpret_cast<uint32_t*>(dst + r * dst_pitch)[j - r * per_row] = v[k];
+      }
+    }
+    for (; i < n; i += nthreads) {
+      const uint32_t r = i / per_row;
+      reinterpret_cast<uint32_t*>(dst + r * dst_pitch)[i - r * per_row] =
+          __builtin_nontemporal_load(reinterpret_cast<const uint32_t*>(src + r * src_pitch) + (i - r * per_row));
+    }
+  } else {
+    const uint32_t per_row = row_bytes >> 1;
+    const uint32_t n = per_row * n_rows;
+    for (uint32_t i = tid; i < n; i += nthreads) {
+      const uint32_t r = i / per_row;
+      reinterpret_cast<uint16_t*>(dst + r * dst_pitch)[i - r * per_row] =
+          reinterpret_cast<const uint16_t*>(src + r * src_pitch)[i - r * per_row];
+    }
+  }
+}
+
+// Reads N consecutive dwords starting at LDS byte offset `off` (2-byte aligned).
+template <int N>
+__device__ __forceinline__ void lds_read_unaligned(const uint8_t* lds, uint32_t off, uint32_t (&out)[N]) {
+  const uint32_t* base = reinterpret_cast<const uint32_t*>(lds + (off & ~3u));
+  const uint32_t shift = (off & 3u) * 8u;
+  uint32_t w[N + 1];
+#pragma unroll
+  for (int i = 0; i <= N; ++i) w[i] = base[i];
+#pragma unroll
+  for (int i = 0; i < N; ++i) out[i] = __builtin_amdgcn_alignbit(w[i + 1], w[i], shift);
+}
+
+// Q8_0 activation block as staged in LDS: 32 int8 quants in 8 dwords, the scale widened to
+// float, and the sum of the quants (the Q4_0 offset and Q4_1 minimum terms need it).
+struct __attribute__((aligned(8))) ActBlock {
+  int32_t qs[8];
+  float d;
+  int32_t sum;
+};
+
+// Converts the raw Q8_0 block at LDS byte offset `off` into an ActBlock.
+__device__ __forceinline__ ActBlock unpack_q8_0_lds(const uint8_t* lds, uint32_t off) {
+  uint32_t w[9];
+  lds_read_unaligned<9>(lds, off, w);
+  ActBlock a;
+  a.d = half_bits_to_float(w[0] & 0xffffu);
+  int32_t s = 0;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    a.qs[i] = static_cast<int32_t>(__builtin_amdgcn_alignbit(w[i + 1], w[i], 16));
+    s = __builtin_amdgcn_sdot4(a.qs[i], 0x01010101, s, false);
+  }
+  a.sum = s;
+  return a;
+}
+
+// Signed dot of 8 dwords of int8 against 8 dwords of int8.
+__device__ __forceinline__ int32_t dot32(const int32_t (&a)[8], const int32_t (&b)[8]) {
+  int32_t s = 0;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) s = __builtin_amdgcn_sdot4(a[i], b[i], s, false);
+  return s;
+}
+
+// ------------------------------------------------------------------------------------------
+// Host-side plumbing shared by the translation units.
+
+hipStream_t stream();
+int fail(int code, const char* fmt, ...);
+int check_launch(const char* what);
+inline size_t ceil_div(size_t a, size_t b) { return (a + b - 1) / b; }
+
+}  // namespace axon_hip

@@ -1,0 +1,38 @@
+// Launch descriptors shared between the kernel translation units and the C ABI layer.
+#pragma once
+
+#include <cstdint>
+
+namespace axon_hip {
+
+// One weight of a fused matvec launch: rows [0, n_out) of w, written to y[m * y_stride + o].
+struct MatvecSeg {
+  const uint8_t* w;
+  float* y;
+  uint32_t n_out;
+  uint32_t y_stride;
+  uint32_t wg_begin;  // first workgroup of this segment (filled by the launcher)
+};
+
+struct MatvecArgs {
+  MatvecSeg seg[3];
+  const uint8_t* xq;  // [m][nb] Q8_0 blocks (Q8_0-activation paths) or [m][n_in] floats
+  uint32_t nb;        // blocks (or super-blocks) per weight row
+  uint32_t m;         // activation rows in this launch
+  uint32_t rows;      // weight rows per workgroup (filled by the launcher)
+  uint32_t lds_tile;  // LDS byte offsets (filled by the launcher)
+  uint32_t lds_scratch;
+  int n_seg;
+  int accumulate;     // y += W x instead of y = W x
+};
+
+// Quantized weights (Q8_0 / Q4_0 / Q4_1) against Q8_0 activations, m <= 4 rows.
+int matvec_q8_launch(int type, MatvecArgs& a);
+// The most activation rows (1..4) one matvec launch takes at nb blocks per row.
+uint32_t matvec_q8_max_rows(int type, uint32_t nb);
+// Q6_K weights against float activations, any m (launched in groups that fit LDS).
+int matvec_q6k_launch(MatvecArgs& a, uint32_t n_in);
+// int8 MFMA tiles for 16 or more Q8_0 activation rows.
+int matmul_q8_mfma_launch(int type, MatvecArgs& a);
+
+}  // namespace axon_hip

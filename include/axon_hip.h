@@ -1,0 +1,226 @@
+/*
+ * axon_hip — the C ABI of the MI355X (gfx950) kernel table for trickymind1324/axon-infer.
+ *
+ * Every pointer argument named after a tensor is a DEVICE pointer (memory from
+ * axon_hip_malloc, or any HIP device allocation). Sizes are element counts unless the name
+ * says bytes. Every function returns 0 on success or a negative status (AXON_HIP_E_*); the
+ * message of the last failure on the calling thread is axon_hip_last_error(). Nothing here
+ * throws, allocates host memory the caller must free, or falls back to the CPU: a host without
+ * a usable gfx950 device gets AXON_HIP_E_NO_DEVICE from axon_hip_init.
+ *
+ * Kernel entries are asynchronous on the library's stream (one non-blocking stream per
+ * process, default priority) and execute in call order; axon_hip_synchronize waits for them.
+ *
+ * The first block mirrors the reference's KernelTable one for one
+ * (src/kernels/kernels.h:33-128): same names, same argument order and meaning, same layouts
+ * (weights [n_out][n_in] in GGUF block layout, no transposition). The second block holds the
+ * coarse entries its device-resident forward pass uses (fused norm + quantize, rope + bias +
+ * KV write, SiLU + quantize, fused multi-weight matvec, ragged attention); each names the
+ * reference code it replaces.
+ */
+#ifndef AXON_HIP_H
+#define AXON_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define AXON_HIP_OK 0
+#define AXON_HIP_E_INVALID (-1)
+#define AXON_HIP_E_UNSUPPORTED (-2)
+#define AXON_HIP_E_NO_DEVICE (-3)
+#define AXON_HIP_E_HIP (-4)
+#define AXON_HIP_E_OOM (-5)
+
+/* ggml tensor type ids accepted by the typed entries (src/core/dtype.h:17-49). */
+#define AXON_HIP_F32 0
+#define AXON_HIP_F16 1
+#define AXON_HIP_Q4_0 2
+#define AXON_HIP_Q4_1 3
+#define AXON_HIP_Q8_0 8
+#define AXON_HIP_Q6_K 14
+#define AXON_HIP_BF16 30
+
+/* ---- Lifecycle: device detection, memory, stream, timing, graphs --------------------------
+ * Stands where src/kernels/kernels.cpp:79-103 (select) checks the CPU: a gfx950 device must be
+ * present, or AXON_HIP_E_NO_DEVICE. */
+int axon_hip_device_count(int* count);
+int axon_hip_init(int device);
+/* Name of the device's ISA ("gfx950") into buf. */
+int axon_hip_device_arch(char* buf, size_t len);
+const char* axon_hip_last_error(void);
+int axon_hip_malloc(void** ptr, size_t bytes);
+int axon_hip_free(void* ptr);
+/* Page-locked host memory for fast transfers. */
+int axon_hip_host_malloc(void** ptr, size_t bytes);
+int axon_hip_host_free(void* ptr);
+int axon_hip_memcpy_h2d(void* dst, const void* src, size_t bytes);
+int axon_hip_memcpy_d2h(void* dst, const void* src, size_t bytes);
+int axon_hip_memcpy_d2d(void* dst, const void* src, size_t bytes);
+/* Asynchronous host-to-device copy on the library stream (src must stay valid until it ran). */
+int axon_hip_memcpy_h2d_async(void* dst, const void* src, size_t bytes);
+int axon_hip_memset(void* dst, int value, size_t bytes);
+int axon_hip_synchronize(void);
+int axon_hip_event_create(void** event);
+int axon_hip_event_record(void* event);
+int axon_hip_event_elapsed_ms(void* start, void* stop, float* ms);
+int axon_hip_event_destroy(void* event);
+/* Captures the entries called between begin and end into a replayable graph. */
+int axon_hip_graph_begin(void);
+int axon_hip_graph_end(void** graph);
+int axon_hip_graph_launch(void* graph);
+int axon_hip_graph_destroy(void* graph);
+
+/* ---- The KernelTable entries (src/kernels/kernels.h:33-128) ------------------------------ */
+
+/* kernels.h:35-39 */
+int axon_hip_matmul_f32(const float* w, const float* x, float* y, size_t n_out, size_t n_in);
+int axon_hip_matmul_f16(const uint16_t* w, const float* x, float* y, size_t n_out, size_t n_in);
+int axon_hip_matmul_bf16(const uint16_t* w, const float* x, float* y, size_t n_out, size_t n_in);
+/* kernels.h:40-47 */
+int axon_hip_matmul_f32_rows(const float* w, const float* x, float* y, size_t n_rows, size_t n_out,
+                             size_t n_in, size_t y_stride);
+int axon_hip_matmul_f16_rows(const uint16_t* w, const float* x, float* y, size_t n_rows, size_t n_out,
+                             size_t n_in, size_t y_stride);
+int axon_hip_matmul_bf16_rows(const uint16_t* w, const float* x, float* y, size_t n_rows, size_t n_out,
+                              size_t n_in, size_t y_stride);
+/* kernels.h:49-50 */
+int axon_hip_rmsnorm(const float* x, const float* weight, float* y, size_t n, float eps);
+/* kernels.h:51-52 with RopeParams (kernels.h:25-31) spelled out; style 0 Normal, 1 NeoX;
+ * freq_factors is a device pointer or NULL. */
+int axon_hip_rope(float* x, size_t n_heads, size_t pos, size_t head_dim, size_t rotary_dim, float theta,
+                  int style, const float* freq_factors);
+/* kernels.h:53-54 */
+int axon_hip_softmax(float* x, size_t n);
+/* kernels.h:55-56 */
+int axon_hip_silu_mul(const float* gate, const float* up, float* out, size_t n);
+/* kernels.h:57-59 */
+int axon_hip_embedding_row(int type, const void* table, size_t n, int64_t index, float* out);
+/* kernels.h:60-66. scores: the reference's per-call scratch; this table keeps scores in LDS
+ * and only reads the pointer for contexts too long for LDS, where it must hold
+ * n_q * n_head * (n_past + n_q) floats. */
+int axon_hip_attention(const float* q, const float* k, const float* v, float* out, float* scores, size_t seq,
+                       size_t n_head, size_t n_head_kv, size_t head_dim, float scale);
+/* kernels.h:67-75 */
+int axon_hip_attention_kv(const float* q, const float* k_cache, const float* v_cache, float* out, float* scores,
+                          size_t n_q, size_t n_past, size_t n_head, size_t n_head_kv, size_t head_dim, float scale);
+/* kernels.h:76-81 */
+int axon_hip_attention_kv_heads(const float* q, const float* k_cache, const float* v_cache, float* out,
+                                float* scores, size_t n_q, size_t n_past, size_t n_head, size_t n_head_kv,
+                                size_t head_dim, float scale, size_t head_begin, size_t head_end);
+/* kernels.h:82-87 */
+int axon_hip_attention_kv_heads_f16(const float* q, const uint16_t* k_cache, const uint16_t* v_cache, float* out,
+                                    float* scores, size_t n_q, size_t n_past, size_t n_head, size_t n_head_kv,
+                                    size_t head_dim, float scale, size_t head_begin, size_t head_end);
+/* kernels.h:89-94. Blocks are the GGUF structs: Q8_0 34 bytes, Q4_0 18, Q4_1 20, Q6_K 210. */
+int axon_hip_matmul_q8_0(const void* w, const float* x, float* y, size_t n_out, size_t n_in);
+int axon_hip_matmul_q4_0(const void* w, const float* x, float* y, size_t n_out, size_t n_in);
+/* kernels.h:95-101 */
+int axon_hip_matmul_q8_0_q8(const void* w, const void* xq, float* y, size_t n_out, size_t n_in);
+int axon_hip_matmul_q4_0_q8(const void* w, const void* xq, float* y, size_t n_out, size_t n_in);
+/* kernels.h:102-110 */
+int axon_hip_matmul_q8_0_rows(const void* w, const float* x, float* y, size_t n_rows, size_t n_out, size_t n_in,
+                              size_t y_stride);
+int axon_hip_matmul_q4_0_rows(const void* w, const float* x, float* y, size_t n_rows, size_t n_out, size_t n_in,
+                              size_t y_stride);
+int axon_hip_matmul_q8_0_q8_rows(const void* w, const void* xq, float* y, size_t n_rows, size_t n_out,
+                                 size_t n_in, size_t y_stride);
+int axon_hip_matmul_q4_0_q8_rows(const void* w, const void* xq, float* y, size_t n_rows, size_t n_out,
+                                 size_t n_in, size_t y_stride);
+/* kernels.h:111-112 */
+int axon_hip_quantize_row_q8_0(const float* x, void* out, size_t n);
+/* kernels.h:114-124 */
+int axon_hip_matmul_q4_1(const void* w, const float* x, float* y, size_t n_out, size_t n_in);
+int axon_hip_matmul_q4_1_q8(const void* w, const void* xq, float* y, size_t n_out, size_t n_in);
+int axon_hip_matmul_q4_1_rows(const void* w, const float* x, float* y, size_t n_rows, size_t n_out, size_t n_in,
+                              size_t y_stride);
+int axon_hip_matmul_q4_1_q8_rows(const void* w, const void* xq, float* y, size_t n_rows, size_t n_out,
+                                 size_t n_in, size_t y_stride);
+/* kernels.h:125-128 */
+int axon_hip_matmul_q6_k(const void* w, const float* x, float* y, size_t n_out, size_t n_in);
+int axon_hip_matmul_q6_k_rows(const void* w, const float* x, float* y, size_t n_rows, size_t n_out, size_t n_in,
+                              size_t y_stride);
+
+/* ---- Coarse entries of the device-resident forward pass --------------------------------- */
+
+/* rmsnorm over rows (src/model/llama.cpp:128-134), writing y, its Q8_0 blocks (the next
+ * matmul's input, llama.cpp:399-417), or both (either may be NULL). */
+int axon_hip_rmsnorm_rows(const float* x, const float* weight, float* y, void* yq, size_t n, size_t n_rows,
+                          float eps);
+/* quantize_row_q8_0 over rows of n floats, x rows x_stride floats apart (llama.cpp:407-415). */
+int axon_hip_quantize_rows_q8_0(const float* x, void* out, size_t n, size_t n_rows, size_t x_stride);
+/* silu_mul over rows, optionally quantizing the product to Q8_0 blocks (llama.cpp:600-620). */
+int axon_hip_silu_mul_rows(const float* gate, const float* up, float* out, void* outq, size_t n, size_t n_rows);
+/* x += y (add_rows, llama.cpp:122-126). */
+int axon_hip_add(float* x, const float* y, size_t n);
+/* Y_s[n_rows][n_out_s] (+)= X W_s^T for up to three weights of one type sharing one Q8_0
+ * input (mm_fused, llama.cpp:425-472). w[s], y[s] device pointers in host arrays. Rows below
+ * 16 run the v_dot4 matvec, 16 and more the int8 MFMA tiles. accumulate adds into y (the
+ * residual add fused, llama.cpp:594-595, 621-623). */
+int axon_hip_matmul_q8_fused(int type, const void* xq, size_t n_rows, size_t n_in, size_t n_seg,
+                             const void* const* w, float* const* y, const size_t* n_out, const size_t* y_stride,
+                             int accumulate);
+
+/* rope + Qwen2 bias + KV-cache write over rows (llama.cpp:493-537). */
+typedef struct {
+  float* q;               /* [rows][q_stride]: n_head heads rotated in place, or NULL */
+  float* k;               /* [rows][k_stride]: n_kv heads rotated in place, or NULL */
+  float* v;               /* [rows][k_stride]: biased, then copied to the cache, or NULL */
+  const float* bq;        /* biases [n_head*head_dim], [n_kv*head_dim] x2, all or none */
+  const float* bk;
+  const float* bv;
+  const int32_t* pos;     /* per-row positions (device), or NULL for pos0 + row */
+  int32_t pos0;
+  uint32_t q_stride, k_stride;
+  uint32_t n_head, n_kv, head_dim, rotary_dim;
+  int neox;               /* RopeStyle::NeoX */
+  float theta;
+  const float* freq_factors; /* device, or NULL */
+  const float* table;     /* device cos/sin pairs [pos][rotary_dim/2] built on the host, or NULL */
+  float* cache;           /* KV pool base, or NULL for no cache write */
+  const int64_t* cache_off; /* per-row element offset of the row's sequence (device), or NULL */
+  int64_t k_layer_off, v_layer_off;
+} axon_hip_rope_rows_args;
+int axon_hip_rope_rows(const axon_hip_rope_rows_args* args, size_t n_rows);
+
+/* Ragged grouped-query attention: row r attends over positions [0, n_vis[r]) of its own
+ * sequence's K/V rows, found at kv + k_off[r] + k_layer_off and kv + v_off[r] + v_layer_off
+ * (elements). One launch serves every sequence of a batch (llama.cpp:539-556) or every query
+ * row of a prefill chunk (llama.cpp:566-590). Per-row arrays are device pointers; with them
+ * NULL, row r sees n_past + r + 1 positions at the constant offsets. */
+typedef struct {
+  const float* q;
+  float* out;
+  uint32_t q_stride, out_stride;
+  const void* kv;
+  const int64_t* k_off;
+  const int64_t* v_off;
+  const int32_t* n_vis;
+  int64_t k_layer_off, v_layer_off;
+  int32_t n_past;
+  uint32_t n_head, n_kv, head_dim;
+  float scale;
+  int f16;                /* the cache holds fp16 bit patterns */
+  float* scratch;         /* device score scratch for contexts beyond LDS, or NULL */
+  uint32_t max_vis;       /* >= every n_vis */
+} axon_hip_attention_rows_args;
+int axon_hip_attention_rows(const axon_hip_attention_rows_args* args, size_t n_rows);
+/* Floats of scratch axon_hip_attention_rows needs for n_rows rows (0: LDS suffices). */
+size_t axon_hip_attention_scratch_floats(const axon_hip_attention_rows_args* args, size_t n_rows);
+
+/* embedding_row for a device array of token ids (llama.cpp:482-485). */
+int axon_hip_embedding_rows(int type, const void* table, size_t n, const int32_t* ids, size_t n_rows, float* out);
+
+/* Test hook: per-block int32 sums of one weight row against one Q8_0 activation row, the
+ * integer phase of matmul_*_q8 (src/kernels/ref/quant.cpp:47-50, 59-65, 166-175); sumx (Q4_1
+ * only, else may be NULL) receives the activation's quant sum per block. */
+int axon_hip_block_sums(int type, const void* w_row, const void* xq, size_t n_blocks, int32_t* sumi,
+                        int32_t* sumx);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -126,3 +126,81 @@ def relative_error(a, b, w, x):
     """|a - b| relative to sum |w_i x_i| per output (test_kernels_neon.cpp:45-59)."""
     mag = np.abs(w.astype(np.float64)) @ np.abs(x.astype(np.float64))
     return float(np.max(np.abs(a.astype(np.float64) - b.astype(np.float64)) / (mag + 1e-30)))
+
+
+# ------------------------------------------------------------------------------------------
+# The hip table through its C ABI (libaxon_hip.so). Same methods as CTable: host arrays in,
+# host arrays out; the data crosses to HBM, the entry runs there, the result comes back.
+
+class HipTable:
+    name = "hip"
+
+    def __init__(self):
+        import axon_hip as H
+        self.H = H
+        H.init(0)
+
+    def _dev(self, a):
+        return self.H.DeviceBuffer.of(np.ascontiguousarray(a))
+
+    def quantize_row_q8_0(self, x: np.ndarray) -> np.ndarray:
+        x = np.ascontiguousarray(x, dtype=np.float32)
+        dx = self._dev(x)
+        out = self.H.DeviceBuffer(x.size // 32 * 34)
+        self.H.call("quantize_row_q8_0", dx, out, x.size)
+        return out.download(Q8_0)
+
+    def matmul(self, kind: str, w, x, n_out, n_in, n_rows=None, y_stride=None):
+        dw, dx = self._dev(w), self._dev(x)
+        if n_rows is None:
+            y = self.H.DeviceBuffer(n_out * 4)
+            self.H.call(f"matmul_{kind}", dw, dx, y, n_out, n_in)
+            return y.download(np.float32)
+        stride = y_stride if y_stride is not None else n_out
+        y = self._dev(np.full(n_rows * stride, np.float32(-7.25), dtype=np.float32))
+        self.H.call(f"matmul_{kind}_rows", dw, dx, y, n_rows, n_out, n_in, stride)
+        return y.download(np.float32)
+
+    def rmsnorm(self, x, w, eps):
+        dx, dw = self._dev(np.asarray(x, np.float32)), self._dev(np.asarray(w, np.float32))
+        y = self.H.DeviceBuffer(x.size * 4)
+        self.H.call("rmsnorm", dx, dw, y, x.size, float(eps))
+        return y.download(np.float32)
+
+    def rope(self, x, n_heads, pos, head_dim, rotary_dim, theta, style, factors=None):
+        dx = self._dev(np.asarray(x, np.float32))
+        df = None if factors is None else self._dev(np.asarray(factors, np.float32))
+        self.H.call("rope", dx, n_heads, pos, head_dim, rotary_dim, float(theta), C.c_int(style), df)
+        return dx.download(np.float32)
+
+    def softmax(self, x):
+        dx = self._dev(np.asarray(x, np.float32))
+        self.H.call("softmax", dx, x.size)
+        return dx.download(np.float32)
+
+    def silu_mul(self, g, u):
+        dg, du = self._dev(np.asarray(g, np.float32)), self._dev(np.asarray(u, np.float32))
+        out = self.H.DeviceBuffer(g.size * 4)
+        self.H.call("silu_mul", dg, du, out, g.size)
+        return out.download(np.float32)
+
+    def embedding_row(self, type_id, table, n, index):
+        dt = self._dev(np.ascontiguousarray(table))
+        out = self.H.DeviceBuffer(n * 4)
+        self.H.call("embedding_row", C.c_int(type_id), dt, n, C.c_int64(index), out)
+        return out.download(np.float32)
+
+    def attention_kv_heads(self, q, k, v, n_q, n_past, n_head, n_head_kv, head_dim, scale, hb, he, f16=False):
+        dq, dk, dv = self._dev(q), self._dev(k), self._dev(v)
+        out = self._dev(np.zeros((n_q, n_head, head_dim), dtype=np.float32))
+        scores = self.H.DeviceBuffer(max(1, n_q * n_head * (n_past + n_q)) * 4)
+        self.H.call("attention_kv_heads_f16" if f16 else "attention_kv_heads", dq, dk, dv, out, scores, n_q, n_past,
+                    n_head, n_head_kv, head_dim, float(scale), hb, he)
+        return out.download(np.float32).reshape(n_q, n_head, head_dim)
+
+    def block_sums(self, type_id, w_row, xq, n_blocks):
+        dw, dx = self._dev(w_row), self._dev(xq)
+        si = self.H.DeviceBuffer(n_blocks * 4)
+        sx = self.H.DeviceBuffer(n_blocks * 4)
+        self.H.call("block_sums", C.c_int(type_id), dw, dx, n_blocks, si, sx)
+        return si.download(np.int32), sx.download(np.int32)

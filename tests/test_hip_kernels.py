@@ -1,0 +1,311 @@
+"""The hip table against the CPU oracle, entry by entry, through the C ABI of libaxon_hip.so.
+
+Integer paths (Q8_0 activation quantization, per-block int32 sums, every matmul with Q8_0
+activations) and the float chains the kernels keep in the scalar table's order (float matmuls,
+RMSNorm, embedding rows) must be bit-identical. Entries whose only difference is the rounding of
+a transcendental (exp in softmax / SiLU / attention, cos and sin in the table-less RoPE) are held
+to a few ulp; Q6_K, which regroups its float sum, to 1e-5 of sum |w x| (the north star's float
+matmul bound). Patterned on the reference's cross-table tests (tests/unit/test_kernels_neon.cpp,
+test_kernels_attention_neon.cpp) and its fixture tests (test_dtype_quant.cpp,
+test_kernels_quant.cpp, test_kernels_norm_act.cpp, test_kernels_rope.cpp,
+test_kernels_attention.cpp, test_kernels_embedding.cpp)."""
+import ctypes as C
+
+import numpy as np
+import pytest
+
+from helpers import (BLOCK, GOLDEN, Q4_0, Q4_1, Q6_K, Q8_0, golden, golden_blocks)
+from tables import CTable, HipTable, QUANT_TYPES, dequantize, random_floats, random_weights, relative_error
+
+pytestmark = pytest.mark.gpu
+
+TYPE_ID = {"q8_0": 8, "q4_0": 2, "q4_1": 3, "q6_k": 14}
+
+
+@pytest.fixture(scope="module")
+def o():
+    return CTable("oracle")
+
+
+@pytest.fixture(scope="module")
+def h():
+    return HipTable()
+
+
+def ulp_diff(a, b):
+    a = np.ascontiguousarray(a, np.float32).view(np.int32).astype(np.int64)
+    b = np.ascontiguousarray(b, np.float32).view(np.int32).astype(np.int64)
+    a = np.where(a < 0, -(a & 0x7fffffff), a)
+    b = np.where(b < 0, -(b & 0x7fffffff), b)
+    return int(np.max(np.abs(a - b))) if a.size else 0
+
+
+# ---- Q8_0 activation quantization ------------------------------------------------------------
+
+@pytest.mark.parametrize("base", ["row", "act"])
+def test_quantize_matches_fixture_bytes(h, base):
+    x = golden(f"quant/{base}.f32.axt").ravel()
+    want = (GOLDEN / f"quant/{base}.q8_0.bin").read_bytes()
+    assert h.quantize_row_q8_0(x).tobytes() == want
+
+
+def test_quantize_random_and_edge_rows_bit_exact(h, o):
+    rng = np.random.default_rng(1)
+    rows = [rng.normal(0, 1, 4096).astype(np.float32),
+            rng.normal(0, 40, 4096).astype(np.float32),
+            np.zeros(64, np.float32),
+            np.full(64, 1e-30, np.float32),                       # fp16 underflow of d
+            (np.arange(128, dtype=np.float32) - 64) * 0.5,        # exact .5 ties
+            np.full(32, 65504.0 * 127, np.float32),               # d overflows fp16
+            rng.normal(0, 1e-6, 2048).astype(np.float32)]
+    for x in rows:
+        assert h.quantize_row_q8_0(x).tobytes() == o.quantize_row_q8_0(x).tobytes()
+
+
+# ---- per-block integer sums (test hook) ------------------------------------------------------
+
+@pytest.mark.parametrize("kind", QUANT_TYPES)
+def test_block_sums_bit_exact(h, o, kind):
+    nb = 64
+    w = random_weights(kind, 1, nb * 32, 5)
+    xq = o.quantize_row_q8_0(random_floats(nb * 32, 6, 3.0))
+    si, sx = h.block_sums(TYPE_ID[kind], w, xq, nb)
+    want_i = np.zeros(nb, np.int32)
+    want_x = np.zeros(nb, np.int32)
+    o._c("block_sums", C.c_int(TYPE_ID[kind]), w, xq, nb, want_i, want_x)
+    assert np.array_equal(si, want_i)
+    if kind == "q4_1":
+        assert np.array_equal(sx, want_x)
+
+
+# ---- matmuls with Q8_0 activations: bit-exact at every row count ---------------------------
+
+@pytest.mark.parametrize("n_in", [32, 96, 576, 2048])
+@pytest.mark.parametrize("n_out", [1, 7, 48, 300])
+def test_q8_matvec_bit_exact(h, o, n_in, n_out):
+    x = random_floats(n_in, n_in + n_out, 4.0)
+    xq = o.quantize_row_q8_0(x)
+    for kind in QUANT_TYPES:
+        w = random_weights(kind, n_out, n_in, n_in * 7 + n_out)
+        assert np.array_equal(h.matmul(f"{kind}_q8", w, xq, n_out, n_in),
+                              o.matmul(f"{kind}_q8", w, xq, n_out, n_in)), kind
+
+
+@pytest.mark.parametrize("n_rows", [1, 2, 3, 4, 5, 9, 15, 16, 17, 33, 64, 65])
+def test_q8_rows_bit_exact_dot4_and_mfma(h, o, n_rows):
+    n_in, n_out = 256, 80
+    xs = random_floats(n_rows * n_in, n_rows, 3.0)
+    xq = np.concatenate([o.quantize_row_q8_0(xs[i * n_in:(i + 1) * n_in]) for i in range(n_rows)])
+    for kind in QUANT_TYPES:
+        w = random_weights(kind, n_out, n_in, 40 + n_rows)
+        got = h.matmul(f"{kind}_q8", w, xq, n_out, n_in, n_rows=n_rows, y_stride=n_out + 3)
+        want = o.matmul(f"{kind}_q8", w, xq, n_out, n_in, n_rows=n_rows, y_stride=n_out + 3)
+        assert np.array_equal(got, want), (kind, n_rows)   # sentinels between rows untouched too
+
+
+@pytest.mark.parametrize("kind", QUANT_TYPES)
+def test_q8_rows_long_k_and_unaligned_weights(h, o, kind):
+    # K = 8192 spans several LDS chunks of the MFMA path. The weight pointer is then moved 2
+    # bytes off any 4-byte boundary, as a column chunk of an odd block count leaves it
+    # (matmul_columns passes base + begin * row_bytes, llama.cpp:36-37).
+    import axon_hip as H
+    n_in, n_out, n_rows = 8192, 40, 20
+    xs = random_floats(n_rows * n_in, 77, 2.0)
+    xq = np.concatenate([o.quantize_row_q8_0(xs[i * n_in:(i + 1) * n_in]) for i in range(n_rows)])
+    w = random_weights(kind, n_out, n_in, 78)
+    for rows in (1, 3, n_rows):
+        want = o.matmul(f"{kind}_q8", w, xq[: rows * n_in // 32], n_out, n_in, n_rows=rows)
+        assert np.array_equal(h.matmul(f"{kind}_q8", w, xq[: rows * n_in // 32], n_out, n_in, n_rows=rows), want)
+        raw = w.tobytes()
+        buf = H.DeviceBuffer(len(raw) + 16)
+        buf.upload(np.frombuffer(raw, np.uint8), offset=2)
+        dx = H.DeviceBuffer.of(xq[: rows * n_in // 32])
+        y = H.DeviceBuffer.of(np.zeros(rows * n_out, np.float32))
+        H.call(f"matmul_{kind}_q8_rows", buf.at(2), dx, y, rows, n_out, n_in, n_out)
+        assert np.array_equal(y.download(np.float32), want), (kind, rows)
+
+
+@pytest.mark.parametrize("name,dt", [("q8_0", Q8_0), ("q4_0", Q4_0), ("q4_1", Q4_1)])
+def test_q8_matmul_fixtures(h, name, dt):
+    # The reference's float64 integer-dot fixtures (test_kernels_quant.cpp:50-84, 101-134).
+    w = golden_blocks(f"quant/matmul_{name}.w.bin", dt)
+    xq = golden_blocks(f"quant/matmul_{name}.xq.bin", Q8_0)
+    want = golden(f"quant/matmul_{name}.yq.axt").ravel()
+    n_out, n_in = want.size, xq.size * 32
+    got = h.matmul(f"{name}_q8", w, xq, n_out, n_in)
+    assert np.max(np.abs(got - want) / (np.abs(want) + 1e-6)) < 1e-5
+
+
+# ---- float matmuls: bit-exact -----------------------------------------------------------------
+
+@pytest.mark.parametrize("n_in,n_out", [(64, 5), (320, 33)])
+def test_float_matmuls_bit_exact(h, o, n_in, n_out):
+    wf = random_floats(n_out * n_in, 3)
+    w16 = wf.astype(np.float16).view(np.uint16)
+    wb = (wf.view(np.uint32) >> 16).astype(np.uint16)
+    x = random_floats(n_in, 4)
+    xs = random_floats(3 * n_in, 5)
+    for kind, w in (("f32", wf), ("f16", w16), ("bf16", wb)):
+        assert np.array_equal(h.matmul(kind, w, x, n_out, n_in), o.matmul(kind, w, x, n_out, n_in)), kind
+        assert np.array_equal(h.matmul(kind, w, xs, n_out, n_in, n_rows=3, y_stride=n_out + 2),
+                              o.matmul(kind, w, xs, n_out, n_in, n_rows=3, y_stride=n_out + 2)), kind
+    for kind in QUANT_TYPES:
+        w = random_weights(kind, n_out, n_in, 6)
+        assert np.array_equal(h.matmul(kind, w, x, n_out, n_in), o.matmul(kind, w, x, n_out, n_in)), kind
+        assert np.array_equal(h.matmul(kind, w, xs, n_out, n_in, n_rows=3),
+                              o.matmul(kind, w, xs, n_out, n_in, n_rows=3)), kind
+
+
+@pytest.mark.parametrize("name", ["matmul_f32", "matmul_f16", "matmul_bf16", "matmul_f32_odd"])
+def test_float_matmul_fixtures(h, name):
+    kind = name.split("_")[1]
+    w = golden(f"kernels/{name}.w.axt")
+    x = golden(f"kernels/{name}.x.axt").ravel()
+    want = golden(f"kernels/{name}.y.axt").ravel()
+    got = h.matmul(kind, w, x, want.size, x.size)
+    assert np.max(np.abs(got - want)) <= 1e-5 * max(1.0, np.max(np.abs(want)))
+
+
+# ---- Q6_K: float path, 1e-5 of sum |w x| ------------------------------------------------------
+
+@pytest.mark.parametrize("n_in,n_out,n_rows", [(256, 9, 1), (2048, 300, 1), (2048, 64, 3), (2048, 40, 9)])
+def test_q6_k_within_float_budget(h, o, n_in, n_out, n_rows):
+    w = random_weights("q6_k", n_out, n_in, n_in + n_out)
+    x = random_floats(n_rows * n_in, 9)
+    deq = dequantize("q6_k", w, n_out, n_in)
+    if n_rows == 1:
+        got, want = h.matmul("q6_k", w, x, n_out, n_in), o.matmul("q6_k", w, x, n_out, n_in)
+        assert relative_error(got, want, deq, x) < 1e-5
+    else:
+        got = h.matmul("q6_k", w, x, n_out, n_in, n_rows=n_rows).reshape(n_rows, n_out)
+        want = o.matmul("q6_k", w, x, n_out, n_in, n_rows=n_rows).reshape(n_rows, n_out)
+        for r in range(n_rows):
+            assert relative_error(got[r], want[r], deq, x[r * n_in:(r + 1) * n_in]) < 1e-5
+
+
+def test_q6_k_fixture(h):
+    w = golden_blocks("quant/matmul_q6_k.w.bin", Q6_K)
+    x = golden("quant/matmul_q6_k.x.axt").ravel()
+    want = golden("quant/matmul_q6_k.y.axt").ravel()
+    got = h.matmul("q6_k", w, x, want.size, x.size)
+    assert np.max(np.abs(got - want)) <= 1e-3 * max(1.0, np.max(np.abs(want)))
+
+
+# ---- norms, activations, rope, softmax -------------------------------------------------------
+
+@pytest.mark.parametrize("n", [1, 64, 576, 2048, 5000])
+def test_rmsnorm_bit_exact(h, o, n):
+    x = random_floats(n, n, 3.0)
+    w = 1.0 + random_floats(n, n + 1, 0.1)
+    assert np.array_equal(h.rmsnorm(x, w, 1e-5), o.rmsnorm(x, w, 1e-5))
+
+
+@pytest.mark.parametrize("n", [1, 64])
+def test_rmsnorm_fixtures(h, n):
+    x, w, y = (golden(f"kernels/rmsnorm_{n}.{s}.axt").ravel() for s in "xwy")
+    assert np.max(np.abs(h.rmsnorm(x, w, 1e-5) - y)) < 1e-5
+
+
+def test_silu_mul_within_one_ulp(h, o):
+    g = random_floats(5000, 1, 12.0)
+    u = random_floats(5000, 2, 3.0)
+    assert ulp_diff(h.silu_mul(g, u), o.silu_mul(g, u)) <= 1
+    gg, uu, want = (golden(f"kernels/silu_mul.{s}.axt").ravel() for s in ("gate", "up", "out"))
+    assert np.max(np.abs(h.silu_mul(gg, uu) - want)) < 1e-5
+
+
+@pytest.mark.parametrize("n", [1, 5, 64, 3000])
+def test_softmax_within_two_ulp(h, o, n):
+    x = random_floats(n, n, 20.0)
+    assert ulp_diff(h.softmax(x), o.softmax(x)) <= 2
+    if n in (1, 5, 64):
+        xx, yy = golden(f"kernels/softmax_{n}.x.axt").ravel(), golden(f"kernels/softmax_{n}.y.axt").ravel()
+        assert np.max(np.abs(h.softmax(xx) - yy)) < 1e-5
+
+
+@pytest.mark.parametrize("name,style,theta,factors", [("rope_normal", 0, 10000.0, False),
+                                                      ("rope_neox", 1, 1000000.0, False),
+                                                      ("rope_llama3", 0, 500000.0, True)])
+def test_rope_fixtures_and_oracle(h, o, name, style, theta, factors):
+    x = golden(f"kernels/{name}.x.axt")
+    pos = golden(f"kernels/{name}.pos.axt").ravel()
+    y = golden(f"kernels/{name}.y.axt")
+    f = golden(f"kernels/{name}.factors.axt").ravel() if factors else None
+    n_rows, n_heads, hd = x.shape
+    for r in range(n_rows):
+        got = h.rope(x[r], n_heads, int(pos[r]), hd, hd, theta, style, f).reshape(n_heads, hd)
+        assert np.max(np.abs(got - y[r])) < 1e-4 * max(1.0, float(pos[r]) / 100)
+        want = o.rope(x[r], n_heads, int(pos[r]), hd, hd, theta, style, f)
+        # cos/sin evaluated on the device in double: the float results agree to an ulp or two
+        assert np.max(np.abs(got - want)) <= 4 * np.finfo(np.float32).eps * max(1.0, np.max(np.abs(want)))
+
+
+# ---- embedding rows: exact for every type -----------------------------------------------------
+
+@pytest.mark.parametrize("name,type_id,dt", [("q8_0", 8, Q8_0), ("q4_0", 2, Q4_0), ("q4_1", 3, Q4_1),
+                                             ("q6_k", 14, Q6_K)])
+def test_quantized_embedding_exact(h, o, name, type_id, dt):
+    table = golden_blocks(f"quant/embedding_{name}.table.bin", dt)
+    idx = golden(f"quant/embedding_{name}.index.axt").ravel()
+    rows = golden(f"quant/embedding_{name}.rows.axt")
+    n = rows.shape[-1]
+    for i, r in enumerate(idx):
+        got = h.embedding_row(type_id, table, n, int(r))
+        assert np.array_equal(got, rows[i])
+        assert np.array_equal(got, o.embedding_row(type_id, table, n, int(r)))
+
+
+@pytest.mark.parametrize("name,type_id", [("f32", 0), ("f16", 1), ("bf16", 30)])
+def test_float_embedding_exact(h, name, type_id):
+    table = golden(f"kernels/embedding_{name}.table.axt")
+    idx = golden(f"kernels/embedding_{name}.index.axt").ravel()
+    rows = golden(f"kernels/embedding_{name}.rows.axt")
+    n = rows.shape[-1]
+    for i, r in enumerate(idx):
+        assert np.array_equal(h.embedding_row(type_id, table, n, int(r)), rows[i])
+
+
+# ---- attention -----------------------------------------------------------------------------------
+
+@pytest.mark.parametrize("n_q,n_past,n_head,n_kv,hd", [(1, 0, 4, 2, 64), (1, 37, 9, 3, 64), (5, 11, 8, 2, 64),
+                                                       (16, 100, 32, 8, 64), (3, 600, 14, 2, 64),
+                                                       (2, 5, 4, 4, 16), (1, 3000, 4, 1, 64)])
+def test_attention_matches_oracle(h, o, n_q, n_past, n_head, n_kv, hd):
+    rng = np.random.default_rng(n_q * 1000 + n_past)
+    total = n_past + n_q
+    q = rng.normal(0, 1, (n_q, n_head, hd)).astype(np.float32)
+    k = rng.normal(0, 1, (total, n_kv, hd)).astype(np.float32)
+    v = rng.normal(0, 1, (total, n_kv, hd)).astype(np.float32)
+    scale = 1.0 / np.sqrt(hd)
+    got = h.attention_kv_heads(q, k, v, n_q, n_past, n_head, n_kv, hd, scale, 0, n_head)
+    want = o.attention_kv_heads(q, k, v, n_q, n_past, n_head, n_kv, hd, scale, 0, n_head)
+    # exp rounded once from double vs libm's expf: equal but for rare last-bit cases
+    assert np.max(np.abs(got - want)) <= 1e-6 * max(1.0, np.max(np.abs(want)))
+    assert np.mean(got == want) > 0.9
+    # head ranges compose (test_kernels_attention.cpp:187-210)
+    part = h.attention_kv_heads(q, k, v, n_q, n_past, n_head, n_kv, hd, scale, 1, n_head)
+    assert np.array_equal(part[:, 1:], got[:, 1:])
+    # the fp16 cache variant widens exactly
+    k16, v16 = k.astype(np.float16).view(np.uint16), v.astype(np.float16).view(np.uint16)
+    got16 = h.attention_kv_heads(q, k16, v16, n_q, n_past, n_head, n_kv, hd, scale, 0, n_head, f16=True)
+    want16 = o.attention_kv_heads(q, k16, v16, n_q, n_past, n_head, n_kv, hd, scale, 0, n_head, f16=True)
+    assert np.max(np.abs(got16 - want16)) <= 1e-6 * max(1.0, np.max(np.abs(want16)))
+
+
+@pytest.mark.parametrize("name,seq,nh,nkv,hd", [("attention_s8_h4_kv2_d16", 8, 4, 2, 16),
+                                                ("attention_s1_h2_kv1_d8", 1, 2, 1, 8),
+                                                ("attention_s5_h2_kv1_d8", 5, 2, 1, 8)])
+def test_attention_fixtures(h, name, seq, nh, nkv, hd):
+    q, k, v, want = (golden(f"kernels/{name}.{s}.axt") for s in ("q", "k", "v", "out"))
+    got = h.attention_kv_heads(q, k, v, seq, 0, nh, nkv, hd, 1.0 / np.sqrt(hd), 0, nh)
+    assert np.max(np.abs(got - want.reshape(got.shape))) < 1e-5
+
+
+def test_attention_over_one_position_returns_its_value(h):
+    # attention.cpp closed form (test_kernels_attention.cpp:55-76)
+    rng = np.random.default_rng(3)
+    q = rng.normal(0, 1, (1, 4, 64)).astype(np.float32)
+    k = rng.normal(0, 1, (1, 2, 64)).astype(np.float32)
+    v = rng.normal(0, 1, (1, 2, 64)).astype(np.float32)
+    got = h.attention_kv_heads(q, k, v, 1, 0, 4, 2, 64, 0.125, 0, 4)
+    assert np.array_equal(got[0, 0], v[0, 0]) and np.array_equal(got[0, 3], v[0, 1])
