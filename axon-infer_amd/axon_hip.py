@@ -169,3 +169,125 @@ class AttentionRowsArgs(C.Structure):
 
 def ptr_of(b) -> int:
     return 0 if b is None else (b.ptr if isinstance(b, DeviceBuffer) else int(b))
+
+
+# ---------------------------------------------------------------------------------------------
+# The device-resident forward pass (libaxon_host.so, include/axon_model.h)
+
+class ModelOptions(C.Structure):
+    _fields_ = [("max_seq", C.c_size_t), ("max_ctx", C.c_size_t), ("max_batch", C.c_size_t),
+                ("max_caches", C.c_size_t), ("exact_activations", C.c_int), ("kernels", C.c_char_p)]
+
+
+class ModelInfo(C.Structure):
+    _fields_ = [("n_layer", C.c_uint32), ("n_embd", C.c_uint32), ("n_head", C.c_uint32), ("n_head_kv", C.c_uint32),
+                ("n_ff", C.c_uint32), ("n_vocab", C.c_uint32), ("head_dim", C.c_uint32), ("rotary_dim", C.c_uint32),
+                ("max_seq", C.c_size_t), ("max_ctx", C.c_size_t), ("max_batch", C.c_size_t),
+                ("weight_bytes_per_token", C.c_size_t), ("device_bytes", C.c_size_t),
+                ("kv_bytes_per_position", C.c_size_t)]
+
+
+_host = None
+
+
+def host() -> C.CDLL:
+    """libaxon_host.so, loaded once (it links libaxon_hip.so)."""
+    global _host
+    if _host is None:
+        if not HOST_SO.exists():
+            raise HipError(f"{HOST_SO} is missing: build it with __graft_entry__.build()")
+        lib()
+        L = C.CDLL(str(HOST_SO))
+        L.axon_model_last_error.restype = C.c_char_p
+        L.axon_model_table_name.restype = C.c_char_p
+        L.axon_model_table_name.argtypes = [C.c_void_p]
+        L.axon_model_load.argtypes = [C.c_char_p, C.POINTER(ModelOptions), C.POINTER(C.c_void_p)]
+        L.axon_model_free.argtypes = [C.c_void_p]
+        L.axon_model_get_info.argtypes = [C.c_void_p, C.POINTER(ModelInfo)]
+        L.axon_model_cache_new.argtypes = [C.c_void_p, C.POINTER(C.c_int)]
+        L.axon_model_cache_free.argtypes = [C.c_void_p, C.c_int]
+        L.axon_model_cache_pos.argtypes = [C.c_void_p, C.c_int, C.POINTER(C.c_size_t)]
+        L.axon_model_cache_truncate.argtypes = [C.c_void_p, C.c_int, C.c_size_t]
+        L.axon_model_cache_read.argtypes = [C.c_void_p, C.c_int, C.c_size_t, C.c_int, C.c_size_t, C.c_void_p]
+        L.axon_model_forward.argtypes = [C.c_void_p, C.c_void_p, C.c_size_t, C.c_void_p]
+        L.axon_model_forward_prefill.argtypes = [C.c_void_p, C.c_int, C.c_void_p, C.c_size_t, C.c_void_p]
+        L.axon_model_forward_batch.argtypes = [C.c_void_p, C.c_void_p, C.c_void_p, C.c_size_t, C.c_void_p]
+        _host = L
+    return _host
+
+
+def _mcheck(rc: int, what: str) -> None:
+    if rc != 0:
+        raise HipError(f"{what}: status {rc}: {host().axon_model_last_error().decode()}")
+
+
+class Model:
+    """LlamaModel on the hip table (src/model/llama.h:87-110): logits come back as numpy
+    arrays [rows, n_vocab]; caches are int slot ids of the device KV pool."""
+
+    def __init__(self, path, max_seq=512, max_ctx=4096, max_batch=1, max_caches=0, exact=False, kernels="hip"):
+        o = ModelOptions(max_seq, max_ctx, max_batch, max_caches, int(exact), kernels.encode())
+        h = C.c_void_p(0)
+        _mcheck(host().axon_model_load(str(path).encode(), C.byref(o), C.byref(h)), f"load {path}")
+        self.h = h
+        info = ModelInfo()
+        host().axon_model_get_info(self.h, C.byref(info))
+        self.info = info
+        self.n_vocab = info.n_vocab
+        self.table_name = host().axon_model_table_name(self.h).decode()
+
+    def close(self) -> None:
+        if getattr(self, "h", None):
+            host().axon_model_free(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def new_cache(self) -> int:
+        c = C.c_int(-1)
+        _mcheck(host().axon_model_cache_new(self.h, C.byref(c)), "cache_new")
+        return c.value
+
+    def free_cache(self, cache: int) -> None:
+        _mcheck(host().axon_model_cache_free(self.h, cache), "cache_free")
+
+    def cache_pos(self, cache: int) -> int:
+        p = C.c_size_t(0)
+        _mcheck(host().axon_model_cache_pos(self.h, cache, C.byref(p)), "cache_pos")
+        return p.value
+
+    def truncate(self, cache: int, pos: int) -> None:
+        _mcheck(host().axon_model_cache_truncate(self.h, cache, pos), "cache_truncate")
+
+    def cache_rows(self, cache: int, layer: int, values: bool, n: int) -> np.ndarray:
+        out = np.zeros((n, self.info.n_head_kv * self.info.head_dim), np.float32)
+        _mcheck(host().axon_model_cache_read(self.h, cache, layer, int(values), n, out.ctypes.data), "cache_read")
+        return out
+
+    def _logits(self, n: int, want: bool):
+        return np.zeros((n, self.n_vocab), np.float32) if want else None
+
+    def forward(self, tokens) -> np.ndarray:
+        t = np.ascontiguousarray(tokens, np.int32)
+        out = self._logits(len(t), True)
+        _mcheck(host().axon_model_forward(self.h, t.ctypes.data, len(t), out.ctypes.data), "forward")
+        return out
+
+    def forward_prefill(self, cache: int, tokens, logits: bool = True):
+        t = np.ascontiguousarray(tokens, np.int32)
+        out = self._logits(len(t), logits)
+        _mcheck(host().axon_model_forward_prefill(self.h, cache, t.ctypes.data, len(t),
+                                                 out.ctypes.data if out is not None else None), "forward_prefill")
+        return out
+
+    def forward_batch(self, caches, tokens, logits: bool = True):
+        t = np.ascontiguousarray(tokens, np.int32)
+        cs = np.ascontiguousarray(caches, np.int32)
+        out = self._logits(len(t), logits)
+        _mcheck(host().axon_model_forward_batch(self.h, cs.ctypes.data, t.ctypes.data, len(t),
+                                               out.ctypes.data if out is not None else None), "forward_batch")
+        return out

@@ -1,0 +1,160 @@
+// C ABI of the device-resident forward pass (include/axon_model.h).
+
+#include "axon_model.h"
+
+#include "axon_hip.h"
+#include "model.h"
+
+#include <cstdio>
+#include <cstring>
+#include <map>
+#include <memory>
+#include <string>
+#include <vector>
+
+struct axon_model {
+  std::unique_ptr<axon::model::LlamaModel> m;
+  std::map<int, std::unique_ptr<axon::model::KVCache>> caches;
+};
+
+namespace {
+
+thread_local std::string g_error;
+
+int fail(const axon::Error& e) {
+  g_error = e.message;
+  return e.code == axon::ErrorCode::Device ? AXON_HIP_E_HIP
+         : e.code == axon::ErrorCode::Unsupported ? AXON_HIP_E_UNSUPPORTED
+                                                  : AXON_HIP_E_INVALID;
+}
+
+int fail(const std::string& msg) {
+  g_error = msg;
+  return AXON_HIP_E_INVALID;
+}
+
+axon::model::KVCache* find(axon_model* model, int cache) {
+  const auto it = model->caches.find(cache);
+  return it == model->caches.end() ? nullptr : it->second.get();
+}
+
+int copy_out(const axon::Expected<std::span<const float>>& r, float* logits) {
+  if (!r) return fail(r.error());
+  if (logits != nullptr) std::memcpy(logits, r->data(), r->size() * sizeof(float));
+  return 0;
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* axon_model_last_error(void) { return g_error.c_str(); }
+
+int axon_model_load(const char* path, const axon_model_options* options, axon_model** out) {
+  *out = nullptr;
+  axon::model::LoadOptions o;
+  if (options != nullptr) {
+    if (options->max_seq) o.max_seq = options->max_seq;
+    if (options->max_ctx) o.max_ctx = options->max_ctx;
+    if (options->max_batch) o.max_batch = options->max_batch;
+    o.max_caches = options->max_caches;
+    o.exact_activations = options->exact_activations != 0;
+    if (options->kernels != nullptr && !axon::kernels::parse_kernel_set(options->kernels, o.kernels))
+      return fail(std::string("kernels: expected auto, scalar, neon or hip, found '") + options->kernels + "'");
+  }
+  auto m = axon::model::LlamaModel::load(path, o);
+  if (!m) return fail(m.error());
+  *out = new axon_model{std::move(*m), {}};
+  return 0;
+}
+
+void axon_model_free(axon_model* model) { delete model; }
+
+int axon_model_get_info(const axon_model* model, axon_model_info* out) {
+  const auto& c = model->m->config();
+  out->n_layer = c.n_layer;
+  out->n_embd = c.n_embd;
+  out->n_head = c.n_head;
+  out->n_head_kv = c.n_head_kv;
+  out->n_ff = c.n_ff;
+  out->n_vocab = c.n_vocab;
+  out->head_dim = c.head_dim;
+  out->rotary_dim = c.rotary_dim;
+  out->max_seq = model->m->max_seq();
+  out->max_ctx = model->m->max_ctx();
+  out->max_batch = model->m->max_batch();
+  out->weight_bytes_per_token = model->m->weight_bytes_per_token();
+  out->device_bytes = model->m->device_bytes();
+  out->kv_bytes_per_position = static_cast<size_t>(c.n_layer) * 2 * c.n_embd_kv() * sizeof(float);
+  return 0;
+}
+
+const char* axon_model_table_name(const axon_model* model) {
+  static thread_local std::string name;
+  name = std::string(axon::kernels::name(model->m->table()));
+  return name.c_str();
+}
+
+int axon_model_cache_new(axon_model* model, int* cache) {
+  auto c = model->m->new_cache();
+  if (!c) return fail(c.error());
+  *cache = (*c)->slot();
+  model->caches[*cache] = std::move(*c);
+  return 0;
+}
+
+int axon_model_cache_free(axon_model* model, int cache) {
+  axon::model::KVCache* c = find(model, cache);
+  if (c == nullptr) return fail("cache_free: unknown cache " + std::to_string(cache));
+  model->m->release_cache(*c);
+  model->caches.erase(cache);
+  return 0;
+}
+
+int axon_model_cache_pos(axon_model* model, int cache, size_t* pos) {
+  axon::model::KVCache* c = find(model, cache);
+  if (c == nullptr) return fail("cache_pos: unknown cache " + std::to_string(cache));
+  *pos = c->pos();
+  return 0;
+}
+
+int axon_model_cache_truncate(axon_model* model, int cache, size_t pos) {
+  axon::model::KVCache* c = find(model, cache);
+  if (c == nullptr) return fail("cache_truncate: unknown cache " + std::to_string(cache));
+  if (!c->truncate(pos)) return fail("truncate: " + std::to_string(pos) + " exceeds the cached " + std::to_string(c->pos()));
+  return 0;
+}
+
+int axon_model_cache_read(axon_model* model, int cache, size_t layer, int values, size_t n, float* out) {
+  axon::model::KVCache* c = find(model, cache);
+  if (c == nullptr) return fail("cache_read: unknown cache " + std::to_string(cache));
+  auto r = model->m->read_cache(*c, layer, values != 0, n);
+  if (!r) return fail(r.error());
+  std::memcpy(out, r->data(), r->size() * sizeof(float));
+  return 0;
+}
+
+int axon_model_forward(axon_model* model, const int32_t* tokens, size_t n, float* logits) {
+  return copy_out(model->m->forward(std::span<const int32_t>(tokens, n)), logits);
+}
+
+int axon_model_forward_prefill(axon_model* model, int cache, const int32_t* tokens, size_t n, float* logits) {
+  axon::model::KVCache* c = find(model, cache);
+  if (c == nullptr) return fail("forward_prefill: unknown cache " + std::to_string(cache));
+  return copy_out(model->m->forward_prefill(*c, std::span<const int32_t>(tokens, n)), logits);
+}
+
+int axon_model_forward_batch(axon_model* model, const int* caches, const int32_t* tokens, size_t n, float* logits) {
+  std::vector<axon::model::KVCache*> cs(n);
+  for (size_t i = 0; i < n; ++i) {
+    cs[i] = find(model, caches[i]);
+    if (cs[i] == nullptr) return fail("forward_batch: unknown cache " + std::to_string(caches[i]));
+  }
+  if (logits == nullptr) {
+    auto r = model->m->forward_batch_device(cs, std::span<const int32_t>(tokens, n));
+    return r ? 0 : fail(r.error());
+  }
+  return copy_out(model->m->forward_batch(cs, std::span<const int32_t>(tokens, n)), logits);
+}
+
+}  // extern "C"

@@ -1,0 +1,597 @@
+#include "model.h"
+
+#include "axon_hip.h"
+
+#include <algorithm>
+#include <cmath>
+#include <cstring>
+#include <string>
+
+namespace axon::model {
+
+namespace {
+
+std::string fmt_shape(std::uint64_t a, std::uint64_t b) { return std::to_string(a) + "x" + std::to_string(b); }
+
+bool matmul_type(DType t) {
+  switch (t) {
+  case DType::F32: case DType::F16: case DType::BF16: case DType::Q8_0: case DType::Q4_0: case DType::Q4_1:
+  case DType::Q6_K:
+    return true;
+  }
+  return false;
+}
+
+enum class Kind { Matmul, Norm };
+
+// Binds one tensor with the exact shape and dtype checks of src/model/weights.cpp:15-67.
+Expected<Tensor> bind_tensor(const GgufFile& f, const std::string& name, Kind kind, std::uint64_t ne0, std::uint64_t ne1) {
+  const GgufTensor* t = f.tensor(name);
+  if (t == nullptr) return make_error(ErrorCode::InvalidArgument, name + ": missing");
+  const std::uint64_t got1 = t->n_dims > 1 ? t->ne[1] : 1;
+  if (t->ne[0] != ne0 || got1 != ne1 || t->ne[2] != 1 || t->ne[3] != 1)
+    return make_error(ErrorCode::InvalidArgument,
+                      name + ": expected shape " + fmt_shape(ne0, ne1) + ", found " + fmt_shape(t->ne[0], got1));
+  if (kind == Kind::Norm && t->type != DType::F32)
+    return make_error(ErrorCode::Unsupported, name + ": expected F32, found type " + std::to_string(int(t->type)));
+  if (kind == Kind::Matmul && !matmul_type(t->type))
+    return make_error(ErrorCode::Unsupported, name + ": unsupported matmul type " + std::to_string(int(t->type)));
+  const std::size_t row = row_bytes_of(t->type, ne0);
+  if (row == 0)
+    return make_error(ErrorCode::InvalidArgument, name + ": row length " + std::to_string(ne0) + " is not a whole number of blocks");
+  Tensor out;
+  out.type = t->type;
+  out.ne0 = ne0;
+  out.ne1 = ne1;
+  out.row_bytes = row;
+  out.total_bytes = row * ne1;
+  out.host = t->data;
+  return out;
+}
+
+Expected<Config> config_of(const GgufFile& f) {
+  Config c;
+  c.arch = f.string_or("general.architecture", "");
+  if (c.arch == "llama") {
+    c.rope_style = kernels::RopeStyle::Normal;
+  } else if (c.arch == "qwen2") {
+    c.rope_style = kernels::RopeStyle::NeoX;
+  } else {
+    return make_error(ErrorCode::Unsupported, "general.architecture: expected llama or qwen2, found '" + c.arch + "'");
+  }
+  const auto key = [&](const char* s) { return c.arch + "." + s; };
+  const char* required[] = {"block_count", "embedding_length", "attention.head_count", "feed_forward_length",
+                            "context_length"};
+  std::uint32_t* fields[] = {&c.n_layer, &c.n_embd, &c.n_head, &c.n_ff, &c.n_ctx_train};
+  for (int i = 0; i < 5; ++i) {
+    const GgufValue* v = f.meta(key(required[i]));
+    if (v == nullptr || v->kind != GgufValue::Kind::UInt || v->u > 0xffffffffull)
+      return make_error(ErrorCode::InvalidArgument, key(required[i]) + ": missing or not a 32-bit unsigned value");
+    *fields[i] = static_cast<std::uint32_t>(v->u);
+  }
+  c.n_head_kv = static_cast<std::uint32_t>(f.uint_or(key("attention.head_count_kv"), c.n_head));
+  if (c.n_layer == 0 || c.n_embd == 0 || c.n_head == 0 || c.n_ff == 0)
+    return make_error(ErrorCode::InvalidArgument, c.arch + ": layer, embedding, head and feed-forward counts must be non-zero");
+  if (c.n_head_kv == 0 || c.n_head % c.n_head_kv != 0)
+    return make_error(ErrorCode::InvalidArgument, key("attention.head_count_kv") + ": does not divide head_count");
+  c.head_dim = static_cast<std::uint32_t>(f.uint_or(key("attention.key_length"), c.n_embd / c.n_head));
+  if (c.head_dim == 0 || c.head_dim % 2 != 0) return make_error(ErrorCode::InvalidArgument, c.arch + ": expected an even head size");
+  c.rotary_dim = static_cast<std::uint32_t>(f.uint_or(key("rope.dimension_count"), c.head_dim));
+  if (c.rotary_dim == 0 || c.rotary_dim % 2 != 0 || c.rotary_dim > c.head_dim)
+    return make_error(ErrorCode::InvalidArgument, key("rope.dimension_count") + ": expected an even value up to the head size");
+  c.rope_theta = static_cast<float>(f.float_or(key("rope.freq_base"), 10000.0));
+  c.rms_eps = static_cast<float>(f.float_or(key("attention.layer_norm_rms_epsilon"), 1e-5));
+  const GgufTensor* embd = f.tensor("token_embd.weight");
+  if (embd == nullptr) return make_error(ErrorCode::InvalidArgument, "token_embd.weight: missing");
+  if (embd->n_dims != 2 || embd->ne[0] != c.n_embd)
+    return make_error(ErrorCode::InvalidArgument, "token_embd.weight: expected shape " + std::to_string(c.n_embd) + "xN");
+  c.n_vocab = static_cast<std::uint32_t>(embd->ne[1]);
+  if (const GgufValue* vs = f.meta(key("vocab_size")); vs != nullptr && vs->u != c.n_vocab)
+    return make_error(ErrorCode::InvalidArgument, key("vocab_size") + ": differs from the embedding rows");
+  if (const GgufValue* toks = f.meta("tokenizer.ggml.tokens"); toks != nullptr && toks->array_size != c.n_vocab)
+    return make_error(ErrorCode::InvalidArgument, "tokenizer.ggml.tokens: expected one entry per embedding row");
+  c.tie_embeddings = f.tensor("output.weight") == nullptr;
+  c.attn_bias = f.tensor("blk.0.attn_q.bias") != nullptr;
+  c.llama3 = f.tensor("rope_freqs.weight") != nullptr;
+  return c;
+}
+
+std::size_t align_up(std::size_t v, std::size_t a) { return (v + a - 1) / a * a; }
+
+}  // namespace
+
+bool KVCache::truncate(std::size_t pos) {
+  if (pos > pos_) return false;
+  pos_ = pos;
+  return true;
+}
+
+Error LlamaModel::device_error(const char* what) const {
+  return make_error(ErrorCode::Device, std::string(what) + ": " + axon_hip_last_error());
+}
+
+Expected<std::unique_ptr<LlamaModel>> LlamaModel::load(const std::string& path, LoadOptions options) {
+  if (options.max_seq == 0) return make_error(ErrorCode::InvalidArgument, "max_seq: expected at least 1, found 0");
+  if (options.max_ctx < options.max_seq)
+    return make_error(ErrorCode::InvalidArgument, "max_ctx is smaller than max_seq");
+  auto file = GgufFile::open(path);
+  if (!file) return file.error();
+  auto cfg = config_of(*file);
+  if (!cfg) return make_error(cfg.error().code, path + ": " + cfg.error().message);
+  auto table = kernels::select(options.kernels);
+  if (!table) return table.error();
+
+  std::unique_ptr<LlamaModel> m(new LlamaModel());
+  m->cfg_ = *cfg;
+  m->kernels_ = *table;
+  const Config& c = m->cfg_;
+  // As llama.cpp:203-208: a cache longer than the training context is clamped, not refused.
+  m->max_ctx_ = std::min<std::size_t>(options.max_ctx, c.n_ctx_train);
+  m->max_seq_ = std::min(options.max_seq, m->max_ctx_);
+  m->max_batch_ = std::max<std::size_t>(1, options.max_batch);
+  m->max_rows_ = std::max(m->max_seq_, m->max_batch_);
+  m->n_slots_ = options.max_caches != 0 ? options.max_caches : m->max_batch_ + 1;
+  m->exact_ = options.exact_activations;
+
+  // Bind (weights.cpp:71-127).
+  const std::uint64_t d = c.n_embd, dq = c.n_embd_q(), dkv = c.n_embd_kv(), ff = c.n_ff;
+#define BIND(target, name, kind, a, b)                                                            \
+  do {                                                                                             \
+    auto bound = bind_tensor(*file, name, kind, a, b);                                                    \
+    if (!bound) return make_error(bound.error().code, path + ": " + bound.error().message);        \
+    (target) = *bound;                                                                             \
+  } while (0)
+  BIND(m->token_embd_, "token_embd.weight", Kind::Matmul, d, c.n_vocab);
+  BIND(m->output_norm_, "output_norm.weight", Kind::Norm, d, 1);
+  if (c.tie_embeddings) {
+    m->output_ = m->token_embd_;
+  } else {
+    BIND(m->output_, "output.weight", Kind::Matmul, d, c.n_vocab);
+  }
+  if (c.llama3) {
+    BIND(m->rope_freqs_, "rope_freqs.weight", Kind::Norm, c.rotary_dim / 2, 1);
+    m->have_rope_freqs_ = true;
+  }
+  m->layers_.resize(c.n_layer);
+  for (std::uint32_t i = 0; i < c.n_layer; ++i) {
+    Layer& L = m->layers_[i];
+    const std::string p = "blk." + std::to_string(i) + ".";
+    BIND(L.attn_norm, p + "attn_norm.weight", Kind::Norm, d, 1);
+    BIND(L.wq, p + "attn_q.weight", Kind::Matmul, d, dq);
+    BIND(L.wk, p + "attn_k.weight", Kind::Matmul, d, dkv);
+    BIND(L.wv, p + "attn_v.weight", Kind::Matmul, d, dkv);
+    BIND(L.wo, p + "attn_output.weight", Kind::Matmul, dq, d);
+    BIND(L.ffn_norm, p + "ffn_norm.weight", Kind::Norm, d, 1);
+    BIND(L.w_gate, p + "ffn_gate.weight", Kind::Matmul, d, ff);
+    BIND(L.w_up, p + "ffn_up.weight", Kind::Matmul, d, ff);
+    BIND(L.w_down, p + "ffn_down.weight", Kind::Matmul, ff, d);
+    if (c.attn_bias) {
+      BIND(L.bq, p + "attn_q.bias", Kind::Norm, dq, 1);
+      BIND(L.bk, p + "attn_k.bias", Kind::Norm, dkv, 1);
+      BIND(L.bv, p + "attn_v.bias", Kind::Norm, dkv, 1);
+      L.bias = true;
+    }
+  }
+#undef BIND
+
+  // Bytes one token reads (llama.cpp:151-167): one embedding row, the output norm and matrix,
+  // the rope factors, and every layer tensor.
+  std::size_t wb = m->token_embd_.row_bytes + m->output_norm_.total_bytes + m->output_.total_bytes;
+  if (m->have_rope_freqs_) wb += m->rope_freqs_.total_bytes;
+  for (const Layer& L : m->layers_) {
+    wb += L.attn_norm.total_bytes + L.wq.total_bytes + L.wk.total_bytes + L.wv.total_bytes + L.wo.total_bytes +
+          L.ffn_norm.total_bytes + L.w_gate.total_bytes + L.w_up.total_bytes + L.w_down.total_bytes;
+    if (L.bias) wb += L.bq.total_bytes + L.bk.total_bytes + L.bv.total_bytes;
+  }
+  m->weight_bytes_ = wb;
+
+  // Upload every bound tensor into one HBM allocation, each at a 256-byte boundary.
+  std::vector<Tensor*> all = {&m->token_embd_, &m->output_norm_};
+  if (!c.tie_embeddings) all.push_back(&m->output_);
+  if (m->have_rope_freqs_) all.push_back(&m->rope_freqs_);
+  for (Layer& L : m->layers_) {
+    for (Tensor* t : {&L.attn_norm, &L.wq, &L.wk, &L.wv, &L.wo, &L.ffn_norm, &L.w_gate, &L.w_up, &L.w_down})
+      all.push_back(t);
+    if (L.bias) {
+      all.push_back(&L.bq);
+      all.push_back(&L.bk);
+      all.push_back(&L.bv);
+    }
+  }
+  std::size_t total = 0;
+  std::vector<std::size_t> offs;
+  for (Tensor* t : all) {
+    offs.push_back(total);
+    total = align_up(total + t->total_bytes, 256);
+  }
+  if (axon_hip_malloc(&m->weights_, total) != AXON_HIP_OK) return m->device_error("weights");
+  for (std::size_t i = 0; i < all.size(); ++i) {
+    all[i]->dev = static_cast<std::byte*>(m->weights_) + offs[i];
+    if (axon_hip_memcpy_h2d(all[i]->dev, all[i]->host, all[i]->total_bytes) != AXON_HIP_OK)
+      return m->device_error("weight upload");
+  }
+  if (c.tie_embeddings) m->output_ = m->token_embd_;
+  m->device_bytes_ = total;
+
+  // cos/sin table [pos][rotary_dim/2], evaluated in double with the host libm exactly as
+  // src/kernels/ref/rope.cpp:19-26 does, then rounded to float.
+  {
+    const std::size_t half = c.rotary_dim / 2;
+    std::vector<float> tab(m->max_ctx_ * half * 2);
+    const auto theta = static_cast<double>(c.rope_theta);
+    const auto rot = static_cast<double>(c.rotary_dim);
+    const float* factors = m->have_rope_freqs_ ? reinterpret_cast<const float*>(m->rope_freqs_.host) : nullptr;
+    for (std::size_t i = 0; i < half; ++i) {
+      double inv_freq = std::pow(theta, -static_cast<double>(2 * i) / rot);
+      if (factors != nullptr) inv_freq /= static_cast<double>(factors[i]);
+      for (std::size_t pos = 0; pos < m->max_ctx_; ++pos) {
+        const double angle = static_cast<double>(pos) * inv_freq;
+        tab[(pos * half + i) * 2] = static_cast<float>(std::cos(angle));
+        tab[(pos * half + i) * 2 + 1] = static_cast<float>(std::sin(angle));
+      }
+    }
+    if (axon_hip_malloc(reinterpret_cast<void**>(&m->rope_table_), tab.size() * 4) != AXON_HIP_OK ||
+        axon_hip_memcpy_h2d(m->rope_table_, tab.data(), tab.size() * 4) != AXON_HIP_OK)
+      return m->device_error("rope table");
+    m->device_bytes_ += tab.size() * 4;
+  }
+
+  // Activations for max_rows rows (activations.h:18-55), the KV pool, row metadata.
+  const std::size_t R = m->max_rows_;
+  const std::size_t widest = std::max({d, dq, ff});
+  struct Buf {
+    float** p;
+    std::size_t floats;
+  };
+  const Buf bufs[] = {{&m->x_, R * d},       {&m->h_, R * d},   {&m->q_, R * dq},     {&m->k_, R * dkv},
+                      {&m->v_, R * dkv},     {&m->attn_, R * dq}, {&m->gate_, R * ff}, {&m->up_, R * ff},
+                      {&m->tmp_, R * widest}, {&m->logits_, R * c.n_vocab}};
+  for (const Buf& b : bufs) {
+    if (axon_hip_malloc(reinterpret_cast<void**>(b.p), b.floats * 4) != AXON_HIP_OK) return m->device_error("activations");
+    m->device_bytes_ += b.floats * 4;
+  }
+  if (axon_hip_malloc(&m->xq_, R * (widest / 32) * sizeof(BlockQ8_0) + 64) != AXON_HIP_OK)
+    return m->device_error("activation blocks");
+  const std::size_t info_bytes = align_up(12 * R, 8) + 8 * R;
+  if (axon_hip_malloc(&m->rowinfo_, info_bytes) != AXON_HIP_OK ||
+      axon_hip_host_malloc(&m->rowinfo_host_, info_bytes) != AXON_HIP_OK)
+    return m->device_error("row table");
+  m->slot_elems_ = static_cast<std::size_t>(c.n_layer) * 2 * m->max_ctx_ * dkv;
+  const std::size_t pool = (m->n_slots_ + 1) * m->slot_elems_;  // +1: the cache-free forward's slot
+  if (axon_hip_malloc(reinterpret_cast<void**>(&m->kv_), pool * 4) != AXON_HIP_OK) return m->device_error("kv pool");
+  m->device_bytes_ += pool * 4;
+  axon_hip_attention_rows_args probe{};
+  probe.n_head = c.n_head;
+  probe.n_kv = c.n_head_kv;
+  probe.head_dim = c.head_dim;
+  probe.max_vis = static_cast<std::uint32_t>(m->max_ctx_);
+  m->scores_floats_ = axon_hip_attention_scratch_floats(&probe, R);
+  if (m->scores_floats_ != 0 &&
+      axon_hip_malloc(reinterpret_cast<void**>(&m->scores_), m->scores_floats_ * 4) != AXON_HIP_OK)
+    return m->device_error("attention scratch");
+  m->slot_used_.assign(m->n_slots_, false);
+  m->file_ = std::make_unique<GgufFile>(std::move(*file));
+  return m;
+}
+
+LlamaModel::~LlamaModel() {
+  axon_hip_synchronize();
+  for (void* p : {static_cast<void*>(x_), static_cast<void*>(h_), static_cast<void*>(q_), static_cast<void*>(k_),
+                  static_cast<void*>(v_), static_cast<void*>(attn_), static_cast<void*>(gate_),
+                  static_cast<void*>(up_), static_cast<void*>(tmp_), static_cast<void*>(logits_),
+                  static_cast<void*>(scores_), xq_, rowinfo_, static_cast<void*>(kv_),
+                  static_cast<void*>(rope_table_), weights_}) {
+    if (p != nullptr) axon_hip_free(p);
+  }
+  if (rowinfo_host_ != nullptr) axon_hip_host_free(rowinfo_host_);
+}
+
+Expected<std::unique_ptr<KVCache>> LlamaModel::new_cache() {
+  for (std::size_t s = 0; s < n_slots_; ++s) {
+    if (!slot_used_[s]) {
+      slot_used_[s] = true;
+      return std::make_unique<KVCache>(static_cast<int>(s), max_ctx_);
+    }
+  }
+  return make_error(ErrorCode::OutOfRange, "new_cache: all " + std::to_string(n_slots_) + " device KV slots are in use");
+}
+
+void LlamaModel::release_cache(const KVCache& cache) {
+  if (cache.slot() >= 0 && static_cast<std::size_t>(cache.slot()) < n_slots_) slot_used_[cache.slot()] = false;
+}
+
+Expected<std::vector<float>> LlamaModel::read_cache(const KVCache& cache, std::size_t layer, bool values, std::size_t n) {
+  if (layer >= cfg_.n_layer || n > max_ctx_) return make_error(ErrorCode::InvalidArgument, "read_cache: out of range");
+  const std::size_t dkv = cfg_.n_embd_kv();
+  std::vector<float> out(n * dkv);
+  const float* src = kv_ + cache.slot() * slot_elems_ + (2 * layer + (values ? 1 : 0)) * max_ctx_ * dkv;
+  if (axon_hip_memcpy_d2h(out.data(), src, out.size() * 4) != AXON_HIP_OK) return device_error("read_cache");
+  return out;
+}
+
+bool LlamaModel::q8_path(const Tensor& w) const {
+  return !exact_ && (w.type == DType::Q8_0 || w.type == DType::Q4_0 || w.type == DType::Q4_1);
+}
+
+// Y = X W^T for one weight (matmul_columns, llama.cpp:30-101), whole matrix per launch;
+// with accumulate, Y += X W^T (the residual add of llama.cpp:594-595, 621-623).
+int LlamaModel::mm(const Tensor& w, const float* x, const void* xq, float* y, std::size_t n, bool accumulate) {
+  const std::size_t n_out = w.ne1, n_in = w.ne0;
+  if (q8_path(w)) {
+    const void* ws[1] = {w.dev};
+    float* ys[1] = {y};
+    const std::size_t no[1] = {n_out};
+    return axon_hip_matmul_q8_fused(static_cast<int>(w.type), xq, n, n_in, 1, ws, ys, no, no, accumulate ? 1 : 0);
+  }
+  float* out = accumulate ? tmp_ : y;
+  const kernels::KernelTable& k = *kernels_;
+  const bool one = n == 1;
+  switch (w.type) {
+  case DType::F32: {
+    const auto* p = static_cast<const float*>(w.dev);
+    one ? k.matmul_f32(p, x, out, n_out, n_in) : k.matmul_f32_rows(p, x, out, n, n_out, n_in, n_out);
+    break;
+  }
+  case DType::F16: {
+    const auto* p = static_cast<const std::uint16_t*>(w.dev);
+    one ? k.matmul_f16(p, x, out, n_out, n_in) : k.matmul_f16_rows(p, x, out, n, n_out, n_in, n_out);
+    break;
+  }
+  case DType::BF16: {
+    const auto* p = static_cast<const std::uint16_t*>(w.dev);
+    one ? k.matmul_bf16(p, x, out, n_out, n_in) : k.matmul_bf16_rows(p, x, out, n, n_out, n_in, n_out);
+    break;
+  }
+  case DType::Q8_0: {
+    const auto* p = static_cast<const BlockQ8_0*>(w.dev);
+    one ? k.matmul_q8_0(p, x, out, n_out, n_in) : k.matmul_q8_0_rows(p, x, out, n, n_out, n_in, n_out);
+    break;
+  }
+  case DType::Q4_0: {
+    const auto* p = static_cast<const BlockQ4_0*>(w.dev);
+    one ? k.matmul_q4_0(p, x, out, n_out, n_in) : k.matmul_q4_0_rows(p, x, out, n, n_out, n_in, n_out);
+    break;
+  }
+  case DType::Q4_1: {
+    const auto* p = static_cast<const BlockQ4_1*>(w.dev);
+    one ? k.matmul_q4_1(p, x, out, n_out, n_in) : k.matmul_q4_1_rows(p, x, out, n, n_out, n_in, n_out);
+    break;
+  }
+  case DType::Q6_K: {
+    const auto* p = static_cast<const BlockQ6_K*>(w.dev);
+    one ? k.matmul_q6_k(p, x, out, n_out, n_in) : k.matmul_q6_k_rows(p, x, out, n, n_out, n_in, n_out);
+    break;
+  }
+  }
+  return accumulate ? axon_hip_add(y, tmp_, n * n_out) : AXON_HIP_OK;
+}
+
+Expected<std::size_t> LlamaModel::run(std::span<const Row> rows, bool copy_logits) {
+  const std::size_t n = rows.size();
+  const Config& c = cfg_;
+  const std::size_t d = c.n_embd, dq = c.n_embd_q(), dkv = c.n_embd_kv(), ff = c.n_ff;
+  const std::size_t R = max_rows_;
+  // Row table: ids | pos | n_vis | cache_off (llama.cpp:360: each row's own position).
+  auto* ids = static_cast<std::int32_t*>(rowinfo_host_);
+  std::int32_t* pos = ids + R;
+  std::int32_t* nvis = pos + R;
+  auto* coff = reinterpret_cast<std::int64_t*>(static_cast<std::byte*>(rowinfo_host_) + align_up(12 * R, 8));
+  // The previous call's row table may still be in flight when its logits stayed on the device.
+  if (axon_hip_synchronize() != AXON_HIP_OK) return device_error("synchronize");
+  std::uint32_t max_vis = 0;
+  for (std::size_t i = 0; i < n; ++i) {
+    ids[i] = rows[i].token;
+    pos[i] = rows[i].pos;
+    nvis[i] = rows[i].pos + 1;
+    coff[i] = static_cast<std::int64_t>(rows[i].slot) * static_cast<std::int64_t>(slot_elems_);
+    max_vis = std::max<std::uint32_t>(max_vis, static_cast<std::uint32_t>(nvis[i]));
+  }
+  const std::size_t info_bytes = align_up(12 * R, 8) + 8 * R;
+  if (axon_hip_memcpy_h2d_async(rowinfo_, rowinfo_host_, info_bytes) != AXON_HIP_OK) return device_error("row table");
+  const auto* d_ids = static_cast<const std::int32_t*>(rowinfo_);
+  const std::int32_t* d_pos = d_ids + R;
+  const std::int32_t* d_nvis = d_pos + R;
+  const auto* d_coff = reinterpret_cast<const std::int64_t*>(static_cast<const std::byte*>(rowinfo_) + align_up(12 * R, 8));
+
+  const float scale = 1.0f / std::sqrt(static_cast<float>(c.head_dim));
+  const float eps = c.rms_eps;
+#define DEV(call)                                                  \
+  do {                                                             \
+    if ((call) != AXON_HIP_OK) return device_error(#call);         \
+  } while (0)
+
+  DEV(axon_hip_embedding_rows(static_cast<int>(token_embd_.type), token_embd_.dev, d, d_ids, n, x_));
+  for (std::size_t l = 0; l < c.n_layer; ++l) {
+    const Layer& L = layers_[l];
+    const std::int64_t k_layer = static_cast<std::int64_t>(2 * l) * max_ctx_ * dkv;
+    const std::int64_t v_layer = k_layer + static_cast<std::int64_t>(max_ctx_ * dkv);
+
+    // attention block (llama.cpp:500-595)
+    const bool qkv_q8 = q8_path(L.wq) && q8_path(L.wk) && q8_path(L.wv) && L.wq.type == L.wk.type &&
+                        L.wk.type == L.wv.type;
+    const bool need_q8 = q8_path(L.wq) || q8_path(L.wk) || q8_path(L.wv);
+    const bool need_f = !q8_path(L.wq) || !q8_path(L.wk) || !q8_path(L.wv);
+    DEV(axon_hip_rmsnorm_rows(x_, static_cast<const float*>(L.attn_norm.dev), need_f ? h_ : nullptr,
+                              need_q8 ? xq_ : nullptr, d, n, eps));
+    if (qkv_q8) {
+      const void* ws[3] = {L.wq.dev, L.wk.dev, L.wv.dev};
+      float* ys[3] = {q_, k_, v_};
+      const std::size_t no[3] = {dq, dkv, dkv};
+      DEV(axon_hip_matmul_q8_fused(static_cast<int>(L.wq.type), xq_, n, d, 3, ws, ys, no, no, 0));
+    } else {
+      DEV(mm(L.wq, h_, xq_, q_, n, false));
+      DEV(mm(L.wk, h_, xq_, k_, n, false));
+      DEV(mm(L.wv, h_, xq_, v_, n, false));
+    }
+    axon_hip_rope_rows_args ra{};
+    ra.q = q_;
+    ra.k = k_;
+    ra.v = v_;
+    if (L.bias) {
+      ra.bq = static_cast<const float*>(L.bq.dev);
+      ra.bk = static_cast<const float*>(L.bk.dev);
+      ra.bv = static_cast<const float*>(L.bv.dev);
+    }
+    ra.pos = d_pos;
+    ra.q_stride = static_cast<std::uint32_t>(dq);
+    ra.k_stride = static_cast<std::uint32_t>(dkv);
+    ra.n_head = c.n_head;
+    ra.n_kv = c.n_head_kv;
+    ra.head_dim = c.head_dim;
+    ra.rotary_dim = c.rotary_dim;
+    ra.neox = c.rope_style == kernels::RopeStyle::NeoX ? 1 : 0;
+    ra.theta = c.rope_theta;
+    ra.table = rope_table_;
+    ra.cache = kv_;
+    ra.cache_off = d_coff;
+    ra.k_layer_off = k_layer;
+    ra.v_layer_off = v_layer;
+    DEV(axon_hip_rope_rows(&ra, n));
+
+    axon_hip_attention_rows_args aa{};
+    aa.q = q_;
+    aa.out = attn_;
+    aa.q_stride = static_cast<std::uint32_t>(dq);
+    aa.out_stride = static_cast<std::uint32_t>(dq);
+    aa.kv = kv_;
+    aa.k_off = d_coff;
+    aa.v_off = d_coff;
+    aa.n_vis = d_nvis;
+    aa.k_layer_off = k_layer;
+    aa.v_layer_off = v_layer;
+    aa.n_head = c.n_head;
+    aa.n_kv = c.n_head_kv;
+    aa.head_dim = c.head_dim;
+    aa.scale = scale;
+    aa.scratch = scores_;
+    aa.max_vis = max_vis;
+    DEV(axon_hip_attention_rows(&aa, n));
+
+    if (q8_path(L.wo)) DEV(axon_hip_quantize_rows_q8_0(attn_, xq_, dq, n, dq));
+    DEV(mm(L.wo, attn_, xq_, x_, n, true));
+
+    // feed-forward block (llama.cpp:598-623)
+    const bool gu_q8 = q8_path(L.w_gate) && q8_path(L.w_up) && L.w_gate.type == L.w_up.type;
+    const bool ff_q8 = q8_path(L.w_gate) || q8_path(L.w_up);
+    const bool ff_f = !q8_path(L.w_gate) || !q8_path(L.w_up);
+    DEV(axon_hip_rmsnorm_rows(x_, static_cast<const float*>(L.ffn_norm.dev), ff_f ? h_ : nullptr,
+                              ff_q8 ? xq_ : nullptr, d, n, eps));
+    if (gu_q8) {
+      const void* ws[2] = {L.w_gate.dev, L.w_up.dev};
+      float* ys[2] = {gate_, up_};
+      const std::size_t no[2] = {ff, ff};
+      DEV(axon_hip_matmul_q8_fused(static_cast<int>(L.w_gate.type), xq_, n, d, 2, ws, ys, no, no, 0));
+    } else {
+      DEV(mm(L.w_gate, h_, xq_, gate_, n, false));
+      DEV(mm(L.w_up, h_, xq_, up_, n, false));
+    }
+    if (q8_path(L.w_down)) {
+      DEV(axon_hip_silu_mul_rows(gate_, up_, nullptr, xq_, ff, n));
+    } else {
+      DEV(axon_hip_silu_mul_rows(gate_, up_, gate_, nullptr, ff, n));
+    }
+    DEV(mm(L.w_down, gate_, xq_, x_, n, true));
+  }
+  const bool out_q8 = q8_path(output_);
+  DEV(axon_hip_rmsnorm_rows(x_, static_cast<const float*>(output_norm_.dev), out_q8 ? nullptr : h_,
+                            out_q8 ? xq_ : nullptr, d, n, eps));
+  DEV(mm(output_, h_, xq_, logits_, n, false));
+  if (copy_logits) {
+    logits_host_.resize(n * c.n_vocab);
+    DEV(axon_hip_memcpy_d2h(logits_host_.data(), logits_, logits_host_.size() * 4));
+  }
+#undef DEV
+  (void)R;
+  return n;
+}
+
+Expected<std::span<const float>> LlamaModel::forward(std::span<const std::int32_t> tokens) {
+  if (tokens.empty()) return make_error(ErrorCode::InvalidArgument, "forward: empty token sequence");
+  if (tokens.size() > max_seq_)
+    return make_error(ErrorCode::InvalidArgument, "forward: " + std::to_string(tokens.size()) + " tokens exceed max_seq");
+  std::vector<Row> rows(tokens.size());
+  for (std::size_t i = 0; i < tokens.size(); ++i) {
+    if (tokens[i] < 0 || static_cast<std::uint32_t>(tokens[i]) >= cfg_.n_vocab)
+      return make_error(ErrorCode::InvalidArgument, "forward: token id " + std::to_string(tokens[i]) + " outside the vocabulary");
+    rows[i] = Row{tokens[i], static_cast<std::int32_t>(i), static_cast<int>(n_slots_)};
+  }
+  auto r = run(rows, true);
+  if (!r) return r.error();
+  return std::span<const float>(logits_host_);
+}
+
+Expected<std::span<const float>> LlamaModel::forward_prefill(KVCache& cache, std::span<const std::int32_t> tokens) {
+  if (tokens.empty()) return make_error(ErrorCode::InvalidArgument, "forward: empty token sequence");
+  if (tokens.size() > max_seq_)
+    return make_error(ErrorCode::InvalidArgument, "forward: " + std::to_string(tokens.size()) + " tokens exceed max_seq");
+  if (cache.pos() + tokens.size() > cache.max_ctx())
+    return make_error(ErrorCode::InvalidArgument, "context overflow: " + std::to_string(cache.pos()) + " cached + " +
+                                                      std::to_string(tokens.size()) + " new tokens exceed " +
+                                                      std::to_string(cache.max_ctx()));
+  std::vector<Row> rows(tokens.size());
+  for (std::size_t i = 0; i < tokens.size(); ++i) {
+    if (tokens[i] < 0 || static_cast<std::uint32_t>(tokens[i]) >= cfg_.n_vocab)
+      return make_error(ErrorCode::InvalidArgument, "forward: token id " + std::to_string(tokens[i]) + " outside the vocabulary");
+    rows[i] = Row{tokens[i], static_cast<std::int32_t>(cache.pos() + i), cache.slot()};
+  }
+  auto r = run(rows, true);
+  if (!r) return r.error();
+  cache.advance(tokens.size());
+  return std::span<const float>(logits_host_);
+}
+
+Expected<std::span<const float>> LlamaModel::forward_one(KVCache& cache, std::int32_t token) {
+  return forward_prefill(cache, std::span<const std::int32_t>(&token, 1));
+}
+
+Expected<std::vector<LlamaModel::Row>> LlamaModel::batch_rows(std::span<KVCache* const> caches,
+                                                               std::span<const std::int32_t> tokens) const {
+  // The checks of llama.cpp:269-302.
+  if (caches.empty() || caches.size() != tokens.size())
+    return make_error(ErrorCode::InvalidArgument, "forward_batch: " + std::to_string(caches.size()) + " caches for " +
+                                                      std::to_string(tokens.size()) + " tokens");
+  if (caches.size() > max_batch_)
+    return make_error(ErrorCode::InvalidArgument, "forward_batch: " + std::to_string(caches.size()) +
+                                                      " sequences exceed max_batch " + std::to_string(max_batch_));
+  std::vector<Row> rows(tokens.size());
+  for (std::size_t i = 0; i < caches.size(); ++i) {
+    const KVCache* cache = caches[i];
+    if (cache == nullptr || cache->slot() < 0 || static_cast<std::size_t>(cache->slot()) >= n_slots_ ||
+        cache->max_ctx() != max_ctx_)
+      return make_error(ErrorCode::InvalidArgument, "forward_batch: cache " + std::to_string(i) + " was built for a different model");
+    if (cache->pos() >= cache->max_ctx())
+      return make_error(ErrorCode::InvalidArgument, "context overflow: cache " + std::to_string(i) + " holds " +
+                                                        std::to_string(cache->pos()) + " of " +
+                                                        std::to_string(cache->max_ctx()) + " positions");
+    for (std::size_t j = 0; j < i; ++j) {
+      if (caches[j] == cache || caches[j]->slot() == cache->slot())
+        return make_error(ErrorCode::InvalidArgument, "forward_batch: cache " + std::to_string(i) + " appears twice");
+    }
+    if (tokens[i] < 0 || static_cast<std::uint32_t>(tokens[i]) >= cfg_.n_vocab)
+      return make_error(ErrorCode::InvalidArgument, "forward: token id " + std::to_string(tokens[i]) + " outside the vocabulary");
+    rows[i] = Row{tokens[i], static_cast<std::int32_t>(cache->pos()), cache->slot()};
+  }
+  return rows;
+}
+
+Expected<std::span<const float>> LlamaModel::forward_batch(std::span<KVCache* const> caches,
+                                                           std::span<const std::int32_t> tokens) {
+  auto rows = batch_rows(caches, tokens);
+  if (!rows) return rows.error();
+  auto r = run(*rows, true);
+  if (!r) return r.error();
+  for (KVCache* cache : caches) cache->advance(1);
+  return std::span<const float>(logits_host_);
+}
+
+Expected<std::size_t> LlamaModel::forward_batch_device(std::span<KVCache* const> caches,
+                                                       std::span<const std::int32_t> tokens) {
+  auto rows = batch_rows(caches, tokens);
+  if (!rows) return rows.error();
+  auto r = run(*rows, false);
+  if (!r) return r.error();
+  for (KVCache* cache : caches) cache->advance(1);
+  return *r;
+}
+
+}  // namespace axon::model

@@ -1,0 +1,150 @@
+#pragma once
+
+// The device-resident LlamaModel: the caller of the hip table. It mirrors the contract of
+// trickymind1324/axon-infer src/model/llama.h:87-110 (load, forward, forward_prefill,
+// forward_one, forward_batch, new_cache) and the op order of LlamaModel::run
+// (src/model/llama.cpp:315-639), with every weight, activation and KV cache resident in HBM.
+// What crosses to the host per forward: the token ids and row positions in (a few bytes per
+// row) and the logits out.
+//
+// Where the reference calls the table per column chunk and per (sequence, head), this model
+// issues whole-matrix launches through the coarse entries of include/axon_hip.h: norm + Q8_0
+// quantize, fused q|k|v and gate|up matvecs, rope + bias + KV write, one ragged attention
+// launch per layer, residual adds fused into the wo and down matvecs.
+
+#include "expected.h"
+#include "gguf.h"
+#include "kernels.h"
+
+#include <cstddef>
+#include <cstdint>
+#include <memory>
+#include <span>
+#include <string>
+#include <vector>
+
+namespace axon::model {
+
+struct LoadOptions {
+  std::size_t max_seq = 512;    // rows per prefill call (llama.h:24-43)
+  std::size_t max_ctx = 4096;   // positions per cache, clamped to the training context
+  std::size_t max_batch = 1;    // rows per forward_batch call
+  std::size_t max_caches = 0;   // KV slots on the device (0: max_batch + 1)
+  bool exact_activations = false;
+  kernels::KernelSet kernels = kernels::KernelSet::Hip;
+};
+
+struct Config {
+  std::string arch;
+  std::uint32_t n_layer = 0, n_embd = 0, n_head = 0, n_head_kv = 0, n_ff = 0, n_ctx_train = 0;
+  std::uint32_t n_vocab = 0, head_dim = 0, rotary_dim = 0;
+  float rope_theta = 10000.0f, rms_eps = 1e-5f;
+  kernels::RopeStyle rope_style = kernels::RopeStyle::Normal;
+  bool tie_embeddings = false, attn_bias = false, llama3 = false;
+  std::uint32_t n_embd_q() const { return n_head * head_dim; }
+  std::uint32_t n_embd_kv() const { return n_head_kv * head_dim; }
+};
+
+// A bound weight: its GGUF view on the host and its copy in HBM.
+struct Tensor {
+  DType type = DType::F32;
+  std::uint64_t ne0 = 0, ne1 = 1;
+  std::size_t row_bytes = 0, total_bytes = 0;
+  const std::byte* host = nullptr;
+  void* dev = nullptr;
+};
+
+struct Layer {
+  Tensor attn_norm, wq, wk, wv, wo, ffn_norm, w_gate, w_up, w_down;
+  bool bias = false;
+  Tensor bq, bk, bv;
+};
+
+// One sequence's KV cache: a slot of the device pool, laid out per layer as K rows then V rows
+// [max_ctx][n_head_kv * head_dim] (src/model/kv_cache.cpp:15-18).
+class KVCache {
+public:
+  KVCache(int slot, std::size_t max_ctx) : slot_(slot), max_ctx_(max_ctx) {}
+  int slot() const { return slot_; }
+  std::size_t pos() const { return pos_; }
+  std::size_t max_ctx() const { return max_ctx_; }
+  void clear() { pos_ = 0; }
+  bool truncate(std::size_t pos);
+  void advance(std::size_t n) { pos_ += n; }
+
+private:
+  int slot_;
+  std::size_t max_ctx_;
+  std::size_t pos_ = 0;
+};
+
+class LlamaModel {
+public:
+  static Expected<std::unique_ptr<LlamaModel>> load(const std::string& path, LoadOptions options);
+  ~LlamaModel();
+
+  // llama.h:87-110. The returned span points into a host buffer owned by the model, valid
+  // until the next forward call; logits are [rows][n_vocab].
+  Expected<std::span<const float>> forward(std::span<const std::int32_t> tokens);
+  Expected<std::span<const float>> forward_prefill(KVCache& cache, std::span<const std::int32_t> tokens);
+  Expected<std::span<const float>> forward_one(KVCache& cache, std::int32_t token);
+  Expected<std::span<const float>> forward_batch(std::span<KVCache* const> caches,
+                                                 std::span<const std::int32_t> tokens);
+  // The same passes with the logits left in HBM (logits_device()), for callers that reduce
+  // them on the device or time the forward pass alone.
+  Expected<std::size_t> forward_batch_device(std::span<KVCache* const> caches, std::span<const std::int32_t> tokens);
+  const float* logits_device() const { return logits_; }
+
+  // A fresh cache in a free device slot, or an error when every slot is taken.
+  Expected<std::unique_ptr<KVCache>> new_cache();
+  void release_cache(const KVCache& cache);
+  // Copies rows [0, n) of layer l's K or V of a cache to the host (tests).
+  Expected<std::vector<float>> read_cache(const KVCache& cache, std::size_t layer, bool values, std::size_t n);
+
+  const Config& config() const { return cfg_; }
+  const kernels::KernelTable& table() const { return *kernels_; }
+  std::size_t weight_bytes_per_token() const { return weight_bytes_; }
+  std::size_t device_bytes() const { return device_bytes_; }
+  std::size_t max_ctx() const { return max_ctx_; }
+  std::size_t max_seq() const { return max_seq_; }
+  std::size_t max_batch() const { return max_batch_; }
+
+private:
+  LlamaModel() = default;
+  struct Row {
+    std::int32_t token;
+    std::int32_t pos;
+    int slot;
+  };
+  Expected<std::size_t> run(std::span<const Row> rows, bool copy_logits);
+  Expected<std::vector<Row>> batch_rows(std::span<KVCache* const> caches, std::span<const std::int32_t> tokens) const;
+  Error device_error(const char* what) const;
+  int mm(const Tensor& w, const float* x, const void* xq, float* y, std::size_t n, bool accumulate);
+  bool q8_path(const Tensor& w) const;
+
+  std::unique_ptr<GgufFile> file_;
+  Config cfg_;
+  const kernels::KernelTable* kernels_ = nullptr;
+  std::vector<Layer> layers_;
+  Tensor token_embd_, output_norm_, output_, rope_freqs_;
+  bool have_rope_freqs_ = false;
+  std::size_t max_seq_ = 0, max_ctx_ = 0, max_batch_ = 0, max_rows_ = 0, n_slots_ = 0;
+  bool exact_ = false;
+  std::size_t weight_bytes_ = 0, device_bytes_ = 0;
+
+  // Device memory.
+  void* weights_ = nullptr;
+  float* rope_table_ = nullptr;
+  float* kv_ = nullptr;
+  std::size_t slot_elems_ = 0;
+  float *x_ = nullptr, *h_ = nullptr, *q_ = nullptr, *k_ = nullptr, *v_ = nullptr, *attn_ = nullptr;
+  float *gate_ = nullptr, *up_ = nullptr, *tmp_ = nullptr, *logits_ = nullptr, *scores_ = nullptr;
+  void* xq_ = nullptr;
+  void* rowinfo_ = nullptr;      // device: ids[R] | pos[R] | n_vis[R] | (8-aligned) cache_off[R]
+  void* rowinfo_host_ = nullptr; // pinned staging of the same
+  std::size_t scores_floats_ = 0;
+  std::vector<float> logits_host_;
+  std::vector<bool> slot_used_;
+};
+
+}  // namespace axon::model

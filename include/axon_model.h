@@ -1,0 +1,65 @@
+/*
+ * axon_model — C ABI of the device-resident forward pass (libaxon_host.so), the caller of the
+ * hip table. Mirrors trickymind1324/axon-infer's LlamaModel (src/model/llama.h:87-110):
+ * load a GGUF file, open per-sequence KV caches, run forward / forward_prefill / forward_one /
+ * forward_batch, read logits [rows][n_vocab] on the host. Weights, activations and KV caches
+ * live in HBM; caches are slots of one device pool, named by int ids.
+ *
+ * Every function returns 0 or a negative status; axon_model_last_error() holds the message
+ * (the reference's Expected error, src/model/llama.cpp:322-351 and 269-302).
+ */
+#ifndef AXON_MODEL_H
+#define AXON_MODEL_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct axon_model axon_model;
+
+/* LoadOptions (src/model/llama.h:24-43). max_caches: KV slots in the device pool
+ * (0: max_batch + 1). kernels: "hip" or "auto" (anything else is Unsupported here). */
+typedef struct {
+  size_t max_seq;
+  size_t max_ctx;
+  size_t max_batch;
+  size_t max_caches;
+  int exact_activations;
+  const char* kernels;
+} axon_model_options;
+
+typedef struct {
+  uint32_t n_layer, n_embd, n_head, n_head_kv, n_ff, n_vocab, head_dim, rotary_dim;
+  size_t max_seq, max_ctx, max_batch;
+  size_t weight_bytes_per_token; /* llama.cpp:151-167 */
+  size_t device_bytes;
+  size_t kv_bytes_per_position;  /* both K and V, all layers, one sequence */
+} axon_model_info;
+
+const char* axon_model_last_error(void);
+int axon_model_load(const char* path, const axon_model_options* options, axon_model** out);
+void axon_model_free(axon_model* model);
+int axon_model_get_info(const axon_model* model, axon_model_info* out);
+/* The name of the kernel table the model runs on ("hip"). */
+const char* axon_model_table_name(const axon_model* model);
+
+/* KVCache (src/model/kv_cache.h:17-73): new (a free slot), free, position, truncate. */
+int axon_model_cache_new(axon_model* model, int* cache);
+int axon_model_cache_free(axon_model* model, int cache);
+int axon_model_cache_pos(axon_model* model, int cache, size_t* pos);
+int axon_model_cache_truncate(axon_model* model, int cache, size_t pos);
+/* Rows [0, n) of layer l's keys (values = 0) or values (1) of a cache, to the host. */
+int axon_model_cache_read(axon_model* model, int cache, size_t layer, int values, size_t n, float* out);
+
+/* The passes. logits: host [n][n_vocab], or NULL to leave them in HBM (timing). */
+int axon_model_forward(axon_model* model, const int32_t* tokens, size_t n, float* logits);
+int axon_model_forward_prefill(axon_model* model, int cache, const int32_t* tokens, size_t n, float* logits);
+int axon_model_forward_batch(axon_model* model, const int* caches, const int32_t* tokens, size_t n, float* logits);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

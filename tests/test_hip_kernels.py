@@ -4,8 +4,7 @@ Integer paths (Q8_0 activation quantization, per-block int32 sums, every matmul 
 activations) and the float chains the kernels keep in the scalar table's order (float matmuls,
 RMSNorm, embedding rows) must be bit-identical. Entries whose only difference is the rounding of
 a transcendental (exp in softmax / SiLU / attention, cos and sin in the table-less RoPE) are held
-to a few ulp; Q6_K, which regroups its float sum, to 1e-5 of sum |w x| (the north star's float
-matmul bound). Patterned on the reference's cross-table tests (tests/unit/test_kernels_neon.cpp,
+to a few ulp. Patterned on the reference's cross-table tests (tests/unit/test_kernels_neon.cpp,
 test_kernels_attention_neon.cpp) and its fixture tests (test_dtype_quant.cpp,
 test_kernels_quant.cpp, test_kernels_norm_act.cpp, test_kernels_rope.cpp,
 test_kernels_attention.cpp, test_kernels_embedding.cpp)."""
@@ -166,21 +165,34 @@ def test_float_matmul_fixtures(h, name):
     assert np.max(np.abs(got - want)) <= 1e-5 * max(1.0, np.max(np.abs(want)))
 
 
-# ---- Q6_K: float path, 1e-5 of sum |w x| ------------------------------------------------------
+# ---- Q6_K: float path, bit-exact (the dequantized value is exact in float) -----------------
 
-@pytest.mark.parametrize("n_in,n_out,n_rows", [(256, 9, 1), (2048, 300, 1), (2048, 64, 3), (2048, 40, 9)])
-def test_q6_k_within_float_budget(h, o, n_in, n_out, n_rows):
+@pytest.mark.parametrize("n_in,n_out,n_rows", [(256, 9, 1), (2048, 300, 1), (2048, 64, 3), (2048, 40, 9),
+                                               (768, 70, 2), (8192, 65, 1)])
+def test_q6_k_bit_exact(h, o, n_in, n_out, n_rows):
     w = random_weights("q6_k", n_out, n_in, n_in + n_out)
     x = random_floats(n_rows * n_in, 9)
-    deq = dequantize("q6_k", w, n_out, n_in)
     if n_rows == 1:
-        got, want = h.matmul("q6_k", w, x, n_out, n_in), o.matmul("q6_k", w, x, n_out, n_in)
-        assert relative_error(got, want, deq, x) < 1e-5
+        assert np.array_equal(h.matmul("q6_k", w, x, n_out, n_in), o.matmul("q6_k", w, x, n_out, n_in))
     else:
-        got = h.matmul("q6_k", w, x, n_out, n_in, n_rows=n_rows).reshape(n_rows, n_out)
-        want = o.matmul("q6_k", w, x, n_out, n_in, n_rows=n_rows).reshape(n_rows, n_out)
-        for r in range(n_rows):
-            assert relative_error(got[r], want[r], deq, x[r * n_in:(r + 1) * n_in]) < 1e-5
+        got = h.matmul("q6_k", w, x, n_out, n_in, n_rows=n_rows, y_stride=n_out + 1)
+        want = o.matmul("q6_k", w, x, n_out, n_in, n_rows=n_rows, y_stride=n_out + 1)
+        assert np.array_equal(got, want)
+
+
+def test_q6_k_unaligned_weights(h, o):
+    # A weight pointer 2 bytes off a 4-byte boundary flips which super-blocks start aligned.
+    import axon_hip as H
+    n_in, n_out = 1280, 33
+    w = random_weights("q6_k", n_out, n_in, 5)
+    x = random_floats(n_in, 6)
+    raw = np.frombuffer(w.tobytes(), np.uint8)
+    buf = H.DeviceBuffer(raw.size + 16)
+    buf.upload(raw, offset=2)
+    dx = H.DeviceBuffer.of(x)
+    y = H.DeviceBuffer(n_out * 4)
+    H.call("matmul_q6_k", buf.at(2), dx, y, n_out, n_in)
+    assert np.array_equal(y.download(np.float32), o.matmul("q6_k", w, x, n_out, n_in))
 
 
 def test_q6_k_fixture(h):
