@@ -212,6 +212,9 @@ def host() -> C.CDLL:
         L.axon_model_forward.argtypes = [C.c_void_p, C.c_void_p, C.c_size_t, C.c_void_p]
         L.axon_model_forward_prefill.argtypes = [C.c_void_p, C.c_int, C.c_void_p, C.c_size_t, C.c_void_p]
         L.axon_model_forward_batch.argtypes = [C.c_void_p, C.c_void_p, C.c_void_p, C.c_size_t, C.c_void_p]
+        L.axon_model_probe.argtypes = [C.c_void_p, C.c_int, C.c_int]
+        L.axon_model_probe_read.argtypes = [C.c_void_p, C.POINTER(C.c_double), C.POINTER(C.c_size_t),
+                                            C.POINTER(C.c_double)]
         _host = L
     return _host
 
@@ -291,3 +294,12 @@ class Model:
         _mcheck(host().axon_model_forward_batch(self.h, cs.ctypes.data, t.ctypes.data, len(t),
                                                out.ctypes.data if out is not None else None), "forward_batch")
         return out
+
+    def probe(self, weight_type: int, enable: bool = True) -> None:
+        _mcheck(host().axon_model_probe(self.h, weight_type, int(enable)), "probe")
+
+    def probe_read(self):
+        """(device ms, launches, algorithmic bytes) of the probed launches since the last read."""
+        ms, n, b = C.c_double(0), C.c_size_t(0), C.c_double(0)
+        _mcheck(host().axon_model_probe_read(self.h, C.byref(ms), C.byref(n), C.byref(b)), "probe_read")
+        return ms.value, n.value, b.value

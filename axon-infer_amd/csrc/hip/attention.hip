@@ -147,6 +147,161 @@ __global__ __launch_bounds__(kThreads) void attention_kernel(AttnArgs a) {
   }
 }
 
+// ---- Decode-shaped launches: scores and value mix as two kernels ----------------------------
+// With few query rows the one-workgroup-per-(row, kv head) kernel above runs on a handful of
+// CUs and its value loop waits on memory. These two kernels spread the same arithmetic wider:
+//   attn_scores_kernel  one lane per (row, position), every head of the kv group, written to
+//                       a global score buffer S[row][head][max_vis];
+//   attn_mix_kernel     one workgroup per (row, kv head, slice of kDc head dims): softmax of the
+//                       group's score rows (identical in every slice), then the value mix, each
+//                       lane owning one (head, dim) and walking positions in order over value
+//                       tiles staged in LDS by the whole workgroup.
+// Every float operation and its order are those of the fused kernel.
+
+constexpr uint32_t kDc = 16;    // head dims per mix workgroup
+constexpr uint32_t kTile = 128; // positions per staged value tile
+
+template <bool F16>
+__global__ __launch_bounds__(kThreads) void attn_scores_kernel(AttnArgs a) {
+  extern __shared__ __attribute__((aligned(16))) float qs[];  // [group][hd]
+  const uint32_t r = blockIdx.x;
+  const uint32_t g = blockIdx.y;
+  const uint32_t tid = threadIdx.x;
+  const uint32_t hd = a.head_dim;
+  const uint32_t group = a.n_head / a.n_kv;
+  const uint32_t n_vis = a.n_vis != nullptr ? static_cast<uint32_t>(a.n_vis[r]) : static_cast<uint32_t>(a.n_past) + r + 1;
+  const uint32_t j0 = blockIdx.z * kThreads;
+  if (j0 >= n_vis) return;
+  const int64_t k_off = (a.k_off != nullptr ? a.k_off[r] : 0) + a.k_off_c;
+  const size_t kv_row = static_cast<size_t>(a.n_kv) * hd;
+  const float* q = a.q + static_cast<size_t>(r) * a.q_stride + static_cast<size_t>(g) * group * hd;
+  for (uint32_t i = tid; i < group * hd; i += kThreads) qs[i] = q[i];
+  __syncthreads();
+  const uint32_t j = j0 + tid;
+  if (j >= n_vis) return;
+  float* out = a.scratch + (static_cast<size_t>(r) * a.n_head + static_cast<size_t>(g) * group) * a.max_vis + j;
+  const size_t krow = k_off + j * kv_row + static_cast<size_t>(g) * hd;
+  const bool vec4 = !F16 && hd == 64 &&
+                    ((reinterpret_cast<uintptr_t>(reinterpret_cast<const float*>(a.kv) + krow) & 15u) == 0);
+  if (vec4) {
+    float kr[64];
+    const float4* kp = reinterpret_cast<const float4*>(reinterpret_cast<const float*>(a.kv) + krow);
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const float4 t = kp[i];
+      kr[4 * i] = t.x;
+      kr[4 * i + 1] = t.y;
+      kr[4 * i + 2] = t.z;
+      kr[4 * i + 3] = t.w;
+    }
+    for (uint32_t h = 0; h < group; ++h) {
+      float acc = 0.0f;
+#pragma unroll
+      for (int d = 0; d < 64; ++d) acc += qs[h * 64 + d] * kr[d];
+      out[static_cast<size_t>(h) * a.max_vis] = a.scale * acc;
+    }
+  } else {
+    for (uint32_t h = 0; h < group; ++h) {
+      float acc = 0.0f;
+      for (uint32_t d = 0; d < hd; ++d) acc += qs[h * hd + d] * kv_at<F16>(a.kv, krow + d);
+      out[static_cast<size_t>(h) * a.max_vis] = a.scale * acc;
+    }
+  }
+}
+
+template <bool F16>
+__global__ __launch_bounds__(kThreads) void attn_mix_kernel(AttnArgs a) {
+  extern __shared__ __attribute__((aligned(16))) float lds[];
+  __shared__ double red_d[kThreads / 64];
+  __shared__ float red_f[kThreads / 64];
+  const uint32_t r = blockIdx.x;
+  const uint32_t g = blockIdx.y;
+  const uint32_t d0 = blockIdx.z * kDc;
+  const uint32_t tid = threadIdx.x;
+  const uint32_t hd = a.head_dim;
+  const uint32_t group = a.n_head / a.n_kv;
+  const uint32_t n_vis = a.n_vis != nullptr ? static_cast<uint32_t>(a.n_vis[r]) : static_cast<uint32_t>(a.n_past) + r + 1;
+  const int64_t v_off = (a.v_off != nullptr ? a.v_off[r] : 0) + a.v_off_c;
+  const size_t kv_row = static_cast<size_t>(a.n_kv) * hd;
+  const uint32_t dc = min(kDc, hd - d0);
+
+  float* p = lds;                               // [group][n_vis]
+  float* vt = lds + group * n_vis;              // [2][kTile][kDc]
+  const float* s = a.scratch + (static_cast<size_t>(r) * a.n_head + static_cast<size_t>(g) * group) * a.max_vis;
+  for (uint32_t i = tid; i < group * n_vis; i += kThreads) {
+    const uint32_t h = i / n_vis;
+    p[i] = s[static_cast<size_t>(h) * a.max_vis + (i - h * n_vis)];
+  }
+  __syncthreads();
+  for (uint32_t h = 0; h < group; ++h) {
+    float* row = p + h * n_vis;
+    float m = -INFINITY;
+    for (uint32_t j = tid; j < n_vis; j += kThreads) m = fmaxf(m, row[j]);
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off, 64));
+    if ((tid & 63) == 0) red_f[tid >> 6] = m;
+    __syncthreads();
+    m = red_f[0];
+    for (int w = 1; w < kThreads / 64; ++w) m = fmaxf(m, red_f[w]);
+    double sum = 0.0;
+    for (uint32_t j = tid; j < n_vis; j += kThreads) {
+      const float e = exp_rounded(row[j] - m);
+      row[j] = e;
+      sum += static_cast<double>(e);
+    }
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) sum += __shfl_xor(sum, off, 64);
+    if ((tid & 63) == 0) red_d[tid >> 6] = sum;
+    __syncthreads();
+    sum = 0.0;
+    for (int w = 0; w < kThreads / 64; ++w) sum += red_d[w];
+    const float inv = static_cast<float>(1.0 / sum);
+    for (uint32_t j = tid; j < n_vis; j += kThreads) row[j] *= inv;
+    __syncthreads();
+  }
+
+  // Value tiles: tile t holds positions [t*kTile, t*kTile + kTile) x dims [d0, d0 + dc).
+  const uint32_t n_tiles = (n_vis + kTile - 1) / kTile;
+  const uint32_t per_tile = kTile * kDc;  // floats
+  auto fetch = [&](uint32_t t, float (&reg)[kTile * kDc / kThreads]) {
+#pragma unroll
+    for (uint32_t k = 0; k < kTile * kDc / kThreads; ++k) {
+      const uint32_t i = tid + k * kThreads;
+      const uint32_t jj = i / kDc;
+      const uint32_t dd = i - jj * kDc;
+      const uint32_t j = t * kTile + jj;
+      reg[k] = (j < n_vis && dd < dc) ? kv_at<F16>(a.kv, v_off + j * kv_row + static_cast<size_t>(g) * hd + d0 + dd) : 0.0f;
+    }
+  };
+  float reg[kTile * kDc / kThreads];
+  fetch(0, reg);
+#pragma unroll
+  for (uint32_t k = 0; k < kTile * kDc / kThreads; ++k) vt[tid + k * kThreads] = reg[k];
+  __syncthreads();
+  const bool lane_active = tid < group * kDc;
+  const uint32_t h = tid / kDc;
+  const uint32_t dd = tid - h * kDc;
+  float acc = 0.0f;
+  for (uint32_t t = 0; t < n_tiles; ++t) {
+    float* cur = vt + (t & 1) * per_tile;
+    float* nxt = vt + ((t + 1) & 1) * per_tile;
+    if (t + 1 < n_tiles) fetch(t + 1, reg);
+    if (lane_active && dd < dc) {
+      const float* pr = p + h * n_vis + t * kTile;
+      const uint32_t cnt = min(kTile, n_vis - t * kTile);
+      for (uint32_t jj = 0; jj < cnt; ++jj) acc += pr[jj] * cur[jj * kDc + dd];
+    }
+    if (t + 1 < n_tiles) {
+#pragma unroll
+      for (uint32_t k = 0; k < kTile * kDc / kThreads; ++k) nxt[tid + k * kThreads] = reg[k];
+    }
+    __syncthreads();
+  }
+  if (lane_active && dd < dc) {
+    a.out[static_cast<size_t>(r) * a.out_stride + static_cast<size_t>(g * group + h) * hd + d0 + dd] = acc;
+  }
+}
+
 bool scores_fit_lds(const AttnArgs& a) {
   const uint32_t group = a.n_head / a.n_kv;
   return static_cast<size_t>(group) * (a.head_dim + a.max_vis) * 4 <= kLdsScores;
@@ -154,8 +309,16 @@ bool scores_fit_lds(const AttnArgs& a) {
 
 }  // namespace
 
+// Decode-shaped launches (few rows, every head) take the two-kernel path when its LDS fits.
+bool use_split(const AttnArgs& a, uint32_t n_rows) {
+  const uint32_t group = a.n_head / a.n_kv;
+  const size_t lds = (static_cast<size_t>(group) * a.max_vis + 2 * kTile * kDc) * 4;
+  return a.split && a.head_begin == 0 && a.head_end == a.n_head && static_cast<size_t>(n_rows) * a.n_kv < 512 &&
+         lds <= 65536 && group * kDc <= kThreads;
+}
+
 size_t attention_scratch_floats(const AttnArgs& a, uint32_t n_rows) {
-  if (scores_fit_lds(a)) return 0;
+  if (scores_fit_lds(a) && !use_split(a, n_rows)) return 0;
   return static_cast<size_t>(n_rows) * a.n_head * a.max_vis;
 }
 
@@ -167,6 +330,20 @@ int attention_launch(const AttnArgs& a, uint32_t n_rows) {
     return fail(kInvalidArgument, "attention: heads [%u, %u) of %u", a.head_begin, a.head_end, a.n_head);
   if (a.head_begin == a.head_end) return kOk;
   const uint32_t group = a.n_head / a.n_kv;
+  if (a.scratch != nullptr && use_split(a, n_rows)) {
+    const dim3 sgrid(n_rows, a.n_kv, (a.max_vis + kThreads - 1) / kThreads);
+    const size_t slds = static_cast<size_t>(group) * a.head_dim * 4;
+    const dim3 mgrid(n_rows, a.n_kv, (a.head_dim + kDc - 1) / kDc);
+    const size_t mlds = (static_cast<size_t>(group) * a.max_vis + 2 * kTile * kDc) * 4;
+    if (a.f16) {
+      hipLaunchKernelGGL(attn_scores_kernel<true>, sgrid, dim3(kThreads), slds, stream(), a);
+      hipLaunchKernelGGL(attn_mix_kernel<true>, mgrid, dim3(kThreads), mlds, stream(), a);
+    } else {
+      hipLaunchKernelGGL(attn_scores_kernel<false>, sgrid, dim3(kThreads), slds, stream(), a);
+      hipLaunchKernelGGL(attn_mix_kernel<false>, mgrid, dim3(kThreads), mlds, stream(), a);
+    }
+    return check_launch("attention (split)");
+  }
   const dim3 grid(n_rows, a.n_kv);
   const bool lds_ok = scores_fit_lds(a);
   if (!lds_ok && a.scratch == nullptr) return fail(kInvalidArgument, "attention: %u positions need a score scratch", a.max_vis);

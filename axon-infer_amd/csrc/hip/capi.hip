@@ -573,6 +573,7 @@ static AttnArgs attn_from(const axon_hip_attention_rows_args* args) {
   a.f16 = args->f16;
   a.scratch = args->scratch;
   a.max_vis = args->max_vis;
+  a.split = 1;
   return a;
 }
 

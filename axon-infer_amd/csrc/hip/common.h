@@ -95,85 +95,77 @@ __device__ __forceinline__ float exp_rounded(float x) {
 // funnel-shifted into place.
 
 // Copies nbytes (a multiple of 2) from global src to LDS dst (16-byte aligned), using 16-, 4-
-// or 2-byte accesses, whichever the alignment of src and nbytes permits. Every thread of the
-// block must call it; it does not synchronise.
+// or 2-byte accesses, whichever the alignment of src and nbytes permits. Each thread issues up
+// to eight loads before its first LDS store, so a whole tile is in flight at once. Every
+// thread of the block must call it; it does not synchronise.
+template <typename T>
+__device__ __forceinline__ void stage_units(const T* __restrict__ s, T* d, uint32_t n, uint32_t tid,
+                                            uint32_t nthreads) {
+  for (uint32_t base = tid; base < n; base += 8 * nthreads) {
+    T v[8];
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      const uint32_t i = base + k * nthreads;
+      if (i < n) v[k] = __builtin_nontemporal_load(s + i);
+    }
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      const uint32_t i = base + k * nthreads;
+      if (i < n) d[i] = v[k];
+    }
+  }
+}
+
 __device__ __forceinline__ void stage_bytes(const uint8_t* __restrict__ src, uint8_t* dst,
                                             uint32_t nbytes, uint32_t tid, uint32_t nthreads) {
   const uintptr_t a = reinterpret_cast<uintptr_t>(src);
   if (((a | nbytes) & 15u) == 0) {
-    const u32x4* s = reinterpret_cast<const u32x4*>(src);
-    u32x4* d = reinterpret_cast<u32x4*>(dst);
-    const uint32_t n = nbytes >> 4;
-    uint32_t i = tid;
-    // Eight loads in flight per thread before the first LDS store.
-    for (; i + 7 * nthreads < n; i += 8 * nthreads) {
-      u32x4 v[8];
-#pragma unroll
-      for (int k = 0; k < 8; ++k) v[k] = __builtin_nontemporal_load(s + i + k * nthreads);
-#pragma unroll
-      for (int k = 0; k < 8; ++k) d[i + k * nthreads] = v[k];
-    }
-    for (; i < n; i += nthreads) d[i] = __builtin_nontemporal_load(s + i);
+    stage_units(reinterpret_cast<const u32x4*>(src), reinterpret_cast<u32x4*>(dst), nbytes >> 4, tid, nthreads);
   } else if (((a | nbytes) & 3u) == 0) {
-    const uint32_t* s = reinterpret_cast<const uint32_t*>(src);
-    uint32_t* d = reinterpret_cast<uint32_t*>(dst);
-    const uint32_t n = nbytes >> 2;
-    uint32_t i = tid;
-    for (; i + 7 * nthreads < n; i += 8 * nthreads) {
-      uint32_t v[8];
-#pragma unroll
-      for (int k = 0; k < 8; ++k) v[k] = __builtin_nontemporal_load(s + i + k * nthreads);
-#pragma unroll
-      for (int k = 0; k < 8; ++k) d[i + k * nthreads] = v[k];
-    }
-    for (; i < n; i += nthreads) d[i] = __builtin_nontemporal_load(s + i);
+    stage_units(reinterpret_cast<const uint32_t*>(src), reinterpret_cast<uint32_t*>(dst), nbytes >> 2, tid, nthreads);
   } else {
-    const uint16_t* s = reinterpret_cast<const uint16_t*>(src);
-    uint16_t* d = reinterpret_cast<uint16_t*>(dst);
-    const uint32_t n = nbytes >> 1;
-    for (uint32_t i = tid; i < n; i += nthreads) d[i] = s[i];
+    stage_units(reinterpret_cast<const uint16_t*>(src), reinterpret_cast<uint16_t*>(dst), nbytes >> 1, tid, nthreads);
   }
 }
 
 // Copies n_rows rows of row_bytes each from global src (rows src_pitch bytes apart) to LDS
 // dst (rows dst_pitch bytes apart), with 4-byte accesses when src, src_pitch, dst_pitch and
-// row_bytes allow it and 2-byte accesses otherwise. Does not synchronise.
+// row_bytes allow it and 2-byte accesses otherwise, eight loads in flight per thread. Does not
+// synchronise.
+template <typename T>
+__device__ __forceinline__ void stage_rows_units(const uint8_t* __restrict__ src, size_t src_pitch, uint8_t* dst,
+                                                 uint32_t dst_pitch, uint32_t n_rows, uint32_t per_row,
+                                                 uint32_t tid, uint32_t nthreads) {
+  const uint32_t n = per_row * n_rows;
+  for (uint32_t base = tid; base < n; base += 8 * nthreads) {
+    T v[8];
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      const uint32_t j = base + k * nthreads;
+      if (j < n) {
+        const uint32_t r = j / per_row;
+        v[k] = __builtin_nontemporal_load(reinterpret_cast<const T*>(src + r * src_pitch) + (j - r * per_row));
+      }
+    }
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      const uint32_t j = base + k * nthreads;
+      if (j < n) {
+        const uint32_t r = j / per_row;
+        reinterpret_cast<T*>(dst + r * dst_pitch)[j - r * per_row] = v[k];
+      }
+    }
+  }
+}
+
 __device__ __forceinline__ void stage_rows(const uint8_t* __restrict__ src, size_t src_pitch, uint8_t* dst,
                                            uint32_t dst_pitch, uint32_t n_rows, uint32_t row_bytes,
                                            uint32_t tid, uint32_t nthreads) {
   const uintptr_t a = reinterpret_cast<uintptr_t>(src);
   if (((a | src_pitch | dst_pitch | row_bytes) & 3u) == 0) {
-    const uint32_t per_row = row_bytes >> 2;
-    const uint32_t n = per_row * n_rows;
-    uint32_t i = tid;
-    for (; i + 7 * nthreads < n; i += 8 * nthreads) {
-      uint32_t v[8];
-#pragma unroll
-      for (int k = 0; k < 8; ++k) {
-        const uint32_t j = i + k * nthreads;
-        const uint32_t r = j / per_row;
-        v[k] = __builtin_nontemporal_load(reinterpret_cast<const uint32_t*>(src + r * src_pitch) + (j - r * per_row));
-      }
-#pragma unroll
-      for (int k = 0; k < 8; ++k) {
-        const uint32_t j = i + k * nthreads;
-        const uint32_t r = j / per_row;
-        reinterpret_cast<uint32_t*>(dst + r * dst_pitch)[j - r * per_row] = v[k];
-      }
-    }
-    for (; i < n; i += nthreads) {
-      const uint32_t r = i / per_row;
-      reinterpret_cast<uint32_t*>(dst + r * dst_pitch)[i - r * per_row] =
-          __builtin_nontemporal_load(reinterpret_cast<const uint32_t*>(src + r * src_pitch) + (i - r * per_row));
-    }
+    stage_rows_units<uint32_t>(src, src_pitch, dst, dst_pitch, n_rows, row_bytes >> 2, tid, nthreads);
   } else {
-    const uint32_t per_row = row_bytes >> 1;
-    const uint32_t n = per_row * n_rows;
-    for (uint32_t i = tid; i < n; i += nthreads) {
-      const uint32_t r = i / per_row;
-      reinterpret_cast<uint16_t*>(dst + r * dst_pitch)[i - r * per_row] =
-          reinterpret_cast<const uint16_t*>(src + r * src_pitch)[i - r * per_row];
-    }
+    stage_rows_units<uint16_t>(src, src_pitch, dst, dst_pitch, n_rows, row_bytes >> 1, tid, nthreads);
   }
 }
 

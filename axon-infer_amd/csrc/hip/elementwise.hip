@@ -88,15 +88,31 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(const float* __restrict__ 
     for (uint32_t i = threadIdx.x; i < n; i += blockDim.x) yr[i] = xr[i] * inv * w[i];
     return;
   }
-  // One half-wave per Q8_0 block of the normalised row.
+  // One half-wave per Q8_0 block of the normalised row; each half-wave first loads all of its
+  // blocks' inputs (up to eight at a time) so the loads are in flight together.
   const uint32_t nb = n / kQK;
   const uint32_t lane = threadIdx.x & 31;
+  const uint32_t halves = blockDim.x / 32;
   uint8_t* qr = yq + static_cast<size_t>(row) * nb * kBytesQ8_0;
-  for (uint32_t b = threadIdx.x >> 5; b < nb; b += blockDim.x / 32) {
-    const uint32_t i = b * kQK + lane;
-    const float v = xr[i] * inv * w[i];
-    if (y != nullptr) y[static_cast<size_t>(row) * n + i] = v;
-    quantize_block_lanes(v, lane, qr + b * kBytesQ8_0);
+  for (uint32_t b0 = threadIdx.x >> 5; b0 < nb; b0 += 8 * halves) {
+    float xv[8], wv[8];
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      const uint32_t b = b0 + k * halves;
+      if (b < nb) {
+        xv[k] = xr[b * kQK + lane];
+        wv[k] = w[b * kQK + lane];
+      }
+    }
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      const uint32_t b = b0 + k * halves;
+      if (b < nb) {
+        const float v = xv[k] * inv * wv[k];
+        if (y != nullptr) y[static_cast<size_t>(row) * n + b * kQK + lane] = v;
+        quantize_block_lanes(v, lane, qr + b * kBytesQ8_0);
+      }
+    }
   }
 }
 

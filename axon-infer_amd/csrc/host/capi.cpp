@@ -157,4 +157,18 @@ int axon_model_forward_batch(axon_model* model, const int* caches, const int32_t
   return copy_out(model->m->forward_batch(cs, std::span<const int32_t>(tokens, n)), logits);
 }
 
+int axon_model_probe(axon_model* model, int type, int enable) {
+  auto r = model->m->set_probe(type, enable != 0);
+  return r ? 0 : fail(r.error());
+}
+
+int axon_model_probe_read(axon_model* model, double* ms, size_t* launches, double* bytes) {
+  auto r = model->m->read_probe();
+  if (!r) return fail(r.error());
+  *ms = r->ms;
+  *launches = r->launches;
+  *bytes = r->bytes;
+  return 0;
+}
+
 }  // extern "C"

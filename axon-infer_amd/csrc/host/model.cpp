@@ -265,7 +265,9 @@ Expected<std::unique_ptr<LlamaModel>> LlamaModel::load(const std::string& path, 
   probe.n_kv = c.n_head_kv;
   probe.head_dim = c.head_dim;
   probe.max_vis = static_cast<std::uint32_t>(m->max_ctx_);
-  m->scores_floats_ = axon_hip_attention_scratch_floats(&probe, R);
+  m->scores_floats_ = 0;
+  for (std::size_t rows = 1; rows <= R; ++rows)
+    m->scores_floats_ = std::max(m->scores_floats_, axon_hip_attention_scratch_floats(&probe, rows));
   if (m->scores_floats_ != 0 &&
       axon_hip_malloc(reinterpret_cast<void**>(&m->scores_), m->scores_floats_ * 4) != AXON_HIP_OK)
     return m->device_error("attention scratch");
@@ -284,6 +286,55 @@ LlamaModel::~LlamaModel() {
     if (p != nullptr) axon_hip_free(p);
   }
   if (rowinfo_host_ != nullptr) axon_hip_host_free(rowinfo_host_);
+  for (void* e : probe_events_) axon_hip_event_destroy(e);
+}
+
+Expected<bool> LlamaModel::set_probe(int type, bool enable) {
+  if (!enable) {
+    probe_type_ = -1;
+    return true;
+  }
+  if (probe_events_.empty()) {
+    probe_events_.resize(2 * 8192, nullptr);
+    for (void*& e : probe_events_) {
+      if (axon_hip_event_create(&e) != AXON_HIP_OK) return device_error("probe events");
+    }
+  }
+  probe_type_ = type;
+  probe_used_ = 0;
+  probe_bytes_.clear();
+  return true;
+}
+
+void LlamaModel::probe_begin(const Tensor& w) {
+  if (static_cast<int>(w.type) != probe_type_ || 2 * probe_used_ + 2 > probe_events_.size()) return;
+  axon_hip_event_record(probe_events_[2 * probe_used_]);
+}
+
+void LlamaModel::probe_end(const Tensor& w, std::size_t n_rows, std::size_t n_out_total, bool accumulate) {
+  if (static_cast<int>(w.type) != probe_type_ || 2 * probe_used_ + 2 > probe_events_.size()) return;
+  axon_hip_event_record(probe_events_[2 * probe_used_ + 1]);
+  const double in_bytes = q8_path(w) ? static_cast<double>(n_rows) * (w.ne0 / 32) * sizeof(BlockQ8_0)
+                                     : static_cast<double>(n_rows) * w.ne0 * 4.0;
+  const double out_bytes = static_cast<double>(n_rows) * n_out_total * 4.0 * (accumulate ? 2 : 1);
+  probe_bytes_.push_back(static_cast<double>(w.row_bytes) * n_out_total + in_bytes + out_bytes);
+  ++probe_used_;
+}
+
+Expected<LlamaModel::ProbeTotals> LlamaModel::read_probe() {
+  ProbeTotals t;
+  if (axon_hip_synchronize() != AXON_HIP_OK) return device_error("synchronize");
+  for (std::size_t i = 0; i < probe_used_; ++i) {
+    float ms = 0;
+    if (axon_hip_event_elapsed_ms(probe_events_[2 * i], probe_events_[2 * i + 1], &ms) != AXON_HIP_OK)
+      return device_error("probe elapsed");
+    t.ms += ms;
+    t.bytes += probe_bytes_[i];
+  }
+  t.launches = probe_used_;
+  probe_used_ = 0;
+  probe_bytes_.clear();
+  return t;
 }
 
 Expected<std::unique_ptr<KVCache>> LlamaModel::new_cache() {
@@ -321,8 +372,13 @@ int LlamaModel::mm(const Tensor& w, const float* x, const void* xq, float* y, st
     const void* ws[1] = {w.dev};
     float* ys[1] = {y};
     const std::size_t no[1] = {n_out};
-    return axon_hip_matmul_q8_fused(static_cast<int>(w.type), xq, n, n_in, 1, ws, ys, no, no, accumulate ? 1 : 0);
+    probe_begin(w);
+    const int rc =
+        axon_hip_matmul_q8_fused(static_cast<int>(w.type), xq, n, n_in, 1, ws, ys, no, no, accumulate ? 1 : 0);
+    probe_end(w, n, n_out, accumulate);
+    return rc;
   }
+  probe_begin(w);
   float* out = accumulate ? tmp_ : y;
   const kernels::KernelTable& k = *kernels_;
   const bool one = n == 1;
@@ -363,6 +419,7 @@ int LlamaModel::mm(const Tensor& w, const float* x, const void* xq, float* y, st
     break;
   }
   }
+  probe_end(w, n, n_out, false);
   return accumulate ? axon_hip_add(y, tmp_, n * n_out) : AXON_HIP_OK;
 }
 
@@ -417,7 +474,9 @@ Expected<std::size_t> LlamaModel::run(std::span<const Row> rows, bool copy_logit
       const void* ws[3] = {L.wq.dev, L.wk.dev, L.wv.dev};
       float* ys[3] = {q_, k_, v_};
       const std::size_t no[3] = {dq, dkv, dkv};
+      probe_begin(L.wq);
       DEV(axon_hip_matmul_q8_fused(static_cast<int>(L.wq.type), xq_, n, d, 3, ws, ys, no, no, 0));
+      probe_end(L.wq, n, dq + 2 * dkv, false);
     } else {
       DEV(mm(L.wq, h_, xq_, q_, n, false));
       DEV(mm(L.wk, h_, xq_, k_, n, false));
@@ -480,7 +539,9 @@ Expected<std::size_t> LlamaModel::run(std::span<const Row> rows, bool copy_logit
       const void* ws[2] = {L.w_gate.dev, L.w_up.dev};
       float* ys[2] = {gate_, up_};
       const std::size_t no[2] = {ff, ff};
+      probe_begin(L.w_gate);
       DEV(axon_hip_matmul_q8_fused(static_cast<int>(L.w_gate.type), xq_, n, d, 2, ws, ys, no, no, 0));
+      probe_end(L.w_gate, n, 2 * ff, false);
     } else {
       DEV(mm(L.w_gate, h_, xq_, gate_, n, false));
       DEV(mm(L.w_up, h_, xq_, up_, n, false));

@@ -101,6 +101,18 @@ public:
   // Copies rows [0, n) of layer l's K or V of a cache to the host (tests).
   Expected<std::vector<float>> read_cache(const KVCache& cache, std::size_t layer, bool values, std::size_t n);
 
+  // Kernel-time probe: while enabled, every matmul launch on weights of `type` (one ggml type
+  // id) is bracketed by HIP events on the library stream. read_probe sums the bracketed device
+  // time, the launches and their algorithmic bytes (weights + Q8_0 or float input + output,
+  // the output counted twice when the launch accumulates into it).
+  Expected<bool> set_probe(int type, bool enable);
+  struct ProbeTotals {
+    double ms = 0;
+    std::size_t launches = 0;
+    double bytes = 0;
+  };
+  Expected<ProbeTotals> read_probe();
+
   const Config& config() const { return cfg_; }
   const kernels::KernelTable& table() const { return *kernels_; }
   std::size_t weight_bytes_per_token() const { return weight_bytes_; }
@@ -144,6 +156,13 @@ private:
   void* rowinfo_host_ = nullptr; // pinned staging of the same
   std::size_t scores_floats_ = 0;
   std::vector<float> logits_host_;
+  // Probe state (set_probe / read_probe).
+  int probe_type_ = -1;
+  std::vector<void*> probe_events_;
+  std::size_t probe_used_ = 0;
+  std::vector<double> probe_bytes_;
+  void probe_begin(const Tensor& w);
+  void probe_end(const Tensor& w, std::size_t n_rows, std::size_t n_out_total, bool accumulate);
   std::vector<bool> slot_used_;
 };
 

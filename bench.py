@@ -1,0 +1,290 @@
+#!/usr/bin/env python3
+"""Decode throughput of the hip kernel table on one MI355X, on the Llama-3.2-1B-shaped Q4_0 model
+(hidden 2048, 16 layers, 32/8 heads, FFN 8192, vocab 128256, tied Q6_K
+embedding/output, llama3 rope scaling; seeded random-init GGUF written by synth.py).
+
+Two workloads, both greedy:
+  decode-b1    one sequence: a 512-token prompt is prefilled (untimed), W warm-up decode steps,
+               then K timed decode steps. One step = forward_one on the device + the logits to
+               the host + argmax, as the reference's Engine::generate loop does per token
+               (src/engine/engine.cpp:50-58). value = K / seconds.
+  ragged-32    continuous batching of 32 sequences with contexts drawn U[64, 2048] from the seed:
+               eight cohorts of four join 16 steps apart, each sequence decodes 128 tokens. Joining
+               sequences are prefilled in their join step (timed apart, as src/engine/batch.cpp:71-85
+               runs the prefill chunk apart from forward_batch). tokens/s = decoded tokens over the
+               forward_batch time (logits to the host and argmax included).
+
+The line also carries:
+  roofline     the Q4_0 x Q8_0 matvec kernel (the dominant kernel by time), from a probe pass of the
+               same decode-b1 steps with HIP events around every such launch on the library stream:
+               achieved = algorithmic bytes (weights + activation blocks + outputs) / device time.
+  cpu_baseline the reference's own LlamaModel on its scalar table (oracle/_ref, compiled from the
+               reference sources) on the same GGUF, threads = the host's cores, on a bounded sample.
+
+Prints one JSON line. --gpus above 1 exits: this build measures one GPU.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+import numpy as np
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT / "axon-infer_amd"))
+sys.path.insert(0, str(ROOT / "tests"))
+
+HBM_PEAK_GBS = 8000.0
+METRIC = "decode tokens/s + HBM GB/s (% peak), Q4_0 1B model, batch 1 and 32 ragged"
+
+
+def log(msg: str) -> None:
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def greedy_decode(model, cache, first_logits, steps):
+    tok = int(np.argmax(first_logits[-1]))
+    for _ in range(steps):
+        logits = model.forward_prefill(cache, [tok])
+        tok = int(np.argmax(logits[-1]))
+    return tok
+
+
+def bench_decode_b1(H, model, n_vocab, steps, warmup, prompt_len, seed):
+    rng = np.random.default_rng(seed)
+    prompt = rng.integers(0, n_vocab, prompt_len).astype(np.int32)
+    cache = model.new_cache()
+    t0 = time.perf_counter()
+    first = model.forward_prefill(cache, prompt)
+    H.synchronize()
+    prefill_s = time.perf_counter() - t0
+    tok = greedy_decode(model, cache, first, warmup)
+    H.synchronize()
+    t0 = time.perf_counter()
+    logits = first
+    tok_last = tok
+    for _ in range(steps):
+        logits = model.forward_prefill(cache, [tok_last])
+        tok_last = int(np.argmax(logits[-1]))
+    H.synchronize()
+    elapsed = time.perf_counter() - t0
+    ctx_end = model.cache_pos(cache)
+    model.free_cache(cache)
+    return {"tokens_per_s": steps / elapsed, "ms_per_step": 1e3 * elapsed / steps, "prefill_tokens_per_s":
+            prompt_len / prefill_s, "context": [prompt_len + warmup, ctx_end]}
+
+
+def probe_pass(H, model, n_vocab, steps, prompt_len, seed, weight_type):
+    rng = np.random.default_rng(seed + 1)
+    prompt = rng.integers(0, n_vocab, prompt_len).astype(np.int32)
+    cache = model.new_cache()
+    first = model.forward_prefill(cache, prompt)
+    model.probe(weight_type, True)
+    model.probe_read()
+    greedy_decode(model, cache, first, steps)
+    ms, launches, nbytes = model.probe_read()
+    model.probe(weight_type, False)
+    model.free_cache(cache)
+    return ms, launches, nbytes
+
+
+def ragged_schedule(n_seq, cohort, gap, decode_steps):
+    return [(i // cohort) * gap for i in range(n_seq)], decode_steps
+
+
+def bench_ragged(H, model, n_vocab, seed, n_seq=32, decode_steps=128, cohort=4, gap=16):
+    rng = np.random.default_rng(seed + 7)
+    ctx = rng.integers(64, 2049, n_seq)
+    prompts = [rng.integers(0, n_vocab, int(c)).astype(np.int32) for c in ctx]
+    joins, _ = ragged_schedule(n_seq, cohort, gap, decode_steps)
+    caches = [None] * n_seq
+    next_tok = [0] * n_seq
+    done = [0] * n_seq
+    max_seq = model.info.max_seq
+    decode_s = prefill_s = 0.0
+    decoded = 0
+    step = 0
+    batch_sizes = []
+    while any(d < decode_steps for d in done):
+        t0 = time.perf_counter()
+        for i in range(n_seq):
+            if joins[i] == step:
+                c = model.new_cache()
+                p = prompts[i]
+                for s in range(0, len(p), max_seq):
+                    logits = model.forward_prefill(c, p[s:s + max_seq])
+                caches[i] = c
+                next_tok[i] = int(np.argmax(logits[-1]))
+        H.synchronize()
+        prefill_s += time.perf_counter() - t0
+        active = [i for i in range(n_seq) if caches[i] is not None and done[i] < decode_steps]
+        if active:
+            t0 = time.perf_counter()
+            logits = model.forward_batch([caches[i] for i in active], [next_tok[i] for i in active])
+            toks = np.argmax(logits, axis=1)
+            decode_s += time.perf_counter() - t0
+            for j, i in enumerate(active):
+                next_tok[i] = int(toks[j])
+                done[i] += 1
+                if done[i] == decode_steps:
+                    model.free_cache(caches[i])
+            decoded += len(active)
+            batch_sizes.append(len(active))
+        step += 1
+    return {"tokens_per_s": decoded / decode_s, "decoded_tokens": decoded, "steps": step,
+            "mean_batch": float(np.mean(batch_sizes)), "max_batch": int(max(batch_sizes)),
+            "prefill_tokens": int(ctx.sum()), "prefill_s": prefill_s, "decode_s": decode_s,
+            "contexts": {"min": int(ctx.min()), "mean": float(ctx.mean()), "max": int(ctx.max())}}
+
+
+def host_cores() -> int:
+    try:
+        return len(os.sched_getaffinity(0))
+    except AttributeError:
+        return os.cpu_count() or 1
+
+
+def cpu_baseline(path, n_vocab, seed, budget_s):
+    """The reference's LlamaModel (scalar table) on the host cores: batch-1 decode and one
+    32-sequence batched step over caches filled to the ragged contexts."""
+    from helpers import have_ref
+    if not have_ref():
+        return None, None
+    from helpers import RefModel, ref
+    import ctypes as C
+    cores = host_cores()
+    rng = np.random.default_rng(seed)
+    prompt = rng.integers(0, n_vocab, 8).astype(np.int32)
+    log(f"cpu baseline: reference scalar table, {cores} threads, loading")
+    r = RefModel(path, max_seq=32, max_ctx=2176, max_batch=32, n_threads=cores)
+    c = r.new_cache()
+    logits = r.forward_prefill(c, prompt)
+    tok = int(np.argmax(logits[-1]))
+    steps, t0 = 0, time.perf_counter()
+    while steps < 3 or (time.perf_counter() - t0 < budget_s and steps < 64):
+        logits = r.forward_prefill(c, [tok])
+        tok = int(np.argmax(logits[-1]))
+        steps += 1
+    dt = time.perf_counter() - t0
+    b1 = {"value": steps / dt, "unit": "tokens/s", "cores": cores, "kind": "reference",
+          "sample": f"{steps} greedy decode steps after an 8-token prompt (contexts 9..{8 + steps}), "
+                    f"reference LlamaModel on its scalar table, {cores} threads"}
+    log(f"cpu baseline b1: {b1['value']:.3f} tok/s")
+    # Ragged: 32 caches filled (zeros) to the ragged contexts, then batched decode steps.
+    ctx = np.random.default_rng(seed + 7).integers(64, 2049, 32)
+    from helpers import GGUF, ModelConfig
+    cfg = ModelConfig(GGUF(path))
+    lib = ref()
+    zeros = np.zeros(cfg.n_layer * 2 * int(ctx.max()) * cfg.n_head_kv * cfg.head_dim, np.float32)
+    ids = []
+    for n in ctx:
+        cid = r.new_cache()
+        lib.ref_cache_fill(C.c_void_p(r.h), cid, C.c_void_p(zeros.ctypes.data), C.c_size_t(int(n)))
+        ids.append(cid)
+    toks = rng.integers(0, n_vocab, 32).astype(np.int32)
+    steps, t0 = 0, time.perf_counter()
+    while steps < 1 or (time.perf_counter() - t0 < budget_s and steps < 8):
+        r.forward_batch(ids, toks)
+        steps += 1
+    dt = time.perf_counter() - t0
+    rg = {"value": 32 * steps / dt, "unit": "tokens/s", "cores": cores, "kind": "reference",
+          "sample": f"{steps} forward_batch steps of 32 sequences at contexts U[64, 2048] "
+                    f"(mean {float(ctx.mean()):.0f}; caches zero-filled), {cores} threads"}
+    log(f"cpu baseline ragged: {rg['value']:.3f} tok/s")
+    return b1, rg
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=128)
+    ap.add_argument("--warmup", type=int, default=8)
+    ap.add_argument("--seed", type=int, default=0)
+    ap.add_argument("--prompt", type=int, default=512)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--no-ragged", action="store_true", help="skip the 32-sequence workload")
+    ap.add_argument("--cpu-budget", type=float, default=12.0, help="seconds per CPU baseline sample")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py: this build runs on one GPU; --gpus {args.gpus} is not supported "
+              "(the path would shard by sequence, see DESIGN.md)", file=sys.stderr)
+        return 2
+
+    import axon_hip as H
+    import synth
+
+    spec = synth.LLAMA32_1B
+    log(f"model: {spec.name} (writing the seeded GGUF on first use)")
+    t0 = time.perf_counter()
+    path = synth.cached_model(spec)
+    log(f"model file {path} ready in {time.perf_counter() - t0:.1f}s")
+    H.init(0)
+    model = H.Model(path, max_seq=512, max_ctx=2048 + 128 + 64, max_batch=32, max_caches=34)
+    info = model.info
+    log(f"loaded on the {model.table_name} table: {info.device_bytes / 1e9:.2f} GB in HBM, "
+        f"{info.weight_bytes_per_token / 1e6:.2f} MB of weights per token")
+
+    b1 = bench_decode_b1(H, model, info.n_vocab, args.steps, args.warmup, args.prompt, args.seed)
+    log(f"decode-b1: {b1['tokens_per_s']:.1f} tok/s ({b1['ms_per_step']:.3f} ms/step)")
+
+    ms, launches, nbytes = probe_pass(H, model, info.n_vocab, min(args.steps, 32), args.prompt, args.seed, synth.Q4_0)
+    achieved = nbytes / (ms * 1e-3) / 1e9
+    q6_ms, q6_n, q6_b = probe_pass(H, model, info.n_vocab, min(args.steps, 32), args.prompt, args.seed, synth.Q6_K)
+    q6_gbs = q6_b / (q6_ms * 1e-3) / 1e9
+    log(f"Q4_0 matvec: {launches} launches, {achieved:.0f} GB/s; Q6_K: {q6_n} launches, {q6_gbs:.0f} GB/s")
+
+    kv_pos_bytes = info.kv_bytes_per_position
+    mean_ctx = 0.5 * (b1["context"][0] + b1["context"][1])
+    step_bytes = info.weight_bytes_per_token + kv_pos_bytes * mean_ctx
+    result = {
+        "metric": METRIC,
+        "value": round(b1["tokens_per_s"], 2),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(b1["ms_per_step"], 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int8",
+        "data": "synthetic",
+        "config": {"workload": "decode-b1: Llama-3.2-1B-shaped Q4_0 (tied Q6_K output), 512-token prompt, "
+                               "greedy, batch 1",
+                   "model": spec.name, "global_batch": 1, "seq_len": args.prompt, "parallelism": "none"},
+        "hbm_gbs_per_step": round(step_bytes / (b1["ms_per_step"] * 1e-3) / 1e9, 1),
+        "hbm_frac_per_step": round(step_bytes / (b1["ms_per_step"] * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+        "roofline": {"bound": "hbm", "kernel": "matvec_q8_kernel<Q4_0> (Q4_0 x Q8_0 dot4 matvec)",
+                     "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                     "launches": launches, "bytes_per_launch": round(nbytes / max(launches, 1)),
+                     "avg_us": round(1e3 * ms / max(launches, 1), 3)},
+        "roofline_q6_k": {"kernel": "matvec_q6k_kernel<1> (tied output, 128256 x 2048)",
+                          "achieved": round(q6_gbs, 1), "frac": round(q6_gbs / HBM_PEAK_GBS, 4),
+                          "avg_us": round(1e3 * q6_ms / max(q6_n, 1), 3)},
+        "prefill_tokens_per_s": round(b1["prefill_tokens_per_s"], 1),
+        "cpu_baseline": None,
+    }
+    if not args.no_ragged:
+        rg = bench_ragged(H, model, info.n_vocab, args.seed)
+        log(f"ragged-32: {rg['tokens_per_s']:.1f} tok/s over {rg['steps']} steps (mean batch {rg['mean_batch']:.1f})")
+        result["ragged32"] = {k: (round(v, 3) if isinstance(v, float) else v) for k, v in rg.items()}
+    model.close()
+    if not args.no_cpu:
+        b1c, rgc = cpu_baseline(path, info.n_vocab, args.seed, args.cpu_budget)
+        result["cpu_baseline"] = b1c
+        if b1c is not None:
+            result["vs_cpu"] = round(result["value"] / b1c["value"], 1)
+        if rgc is not None and "ragged32" in result:
+            result["ragged32"]["cpu_baseline"] = rgc
+            result["ragged32"]["vs_cpu"] = round(result["ragged32"]["tokens_per_s"] / rgc["value"], 1)
+    print(json.dumps(result), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -208,7 +208,8 @@ typedef struct {
   uint32_t max_vis;       /* >= every n_vis */
 } axon_hip_attention_rows_args;
 int axon_hip_attention_rows(const axon_hip_attention_rows_args* args, size_t n_rows);
-/* Floats of scratch axon_hip_attention_rows needs for n_rows rows (0: LDS suffices). */
+/* Floats of scratch axon_hip_attention_rows needs for n_rows rows (0: LDS suffices). Launches
+ * of few rows use a two-kernel path whose scores always go through the scratch. */
 size_t axon_hip_attention_scratch_floats(const axon_hip_attention_rows_args* args, size_t n_rows);
 
 /* embedding_row for a device array of token ids (llama.cpp:482-485). */
