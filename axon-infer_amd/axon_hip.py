@@ -164,7 +164,18 @@ class AttentionRowsArgs(C.Structure):
                 ("kv", C.c_void_p), ("k_off", C.c_void_p), ("v_off", C.c_void_p), ("n_vis", C.c_void_p),
                 ("k_layer_off", C.c_int64), ("v_layer_off", C.c_int64), ("n_past", C.c_int32),
                 ("n_head", C.c_uint32), ("n_kv", C.c_uint32), ("head_dim", C.c_uint32), ("scale", C.c_float),
-                ("f16", C.c_int), ("scratch", C.c_void_p), ("max_vis", C.c_uint32)]
+                ("f16", C.c_int), ("scratch", C.c_void_p), ("max_vis", C.c_uint32), ("outq", C.c_void_p)]
+
+
+class MatvecFusedArgs(C.Structure):
+    """axon_hip_matvec_fused_args (include/axon_hip.h)."""
+    _fields_ = [("type", C.c_int), ("n_seg", C.c_size_t), ("w", C.c_void_p * 3), ("n_out", C.c_size_t * 3),
+                ("n_rows", C.c_size_t), ("n_in", C.c_size_t), ("in_mode", C.c_int), ("xq", C.c_void_p),
+                ("x", C.c_void_p), ("x_stride", C.c_size_t), ("norm_w", C.c_void_p), ("eps", C.c_float),
+                ("out_mode", C.c_int), ("y", C.c_void_p * 3), ("y_stride", C.c_size_t * 3), ("bias", C.c_void_p * 3),
+                ("rope_table", C.c_void_p), ("rot_half", C.c_uint32), ("head_dim", C.c_uint32), ("pos", C.c_void_p),
+                ("cache_off", C.c_void_p), ("cache", C.c_void_p), ("k_layer_off", C.c_int64),
+                ("v_layer_off", C.c_int64)]
 
 
 def ptr_of(b) -> int:

@@ -158,8 +158,11 @@ __global__ __launch_bounds__(kThreads) void attention_kernel(AttnArgs a) {
 //                       tiles staged in LDS by the whole workgroup.
 // Every float operation and its order are those of the fused kernel.
 
-constexpr uint32_t kDc = 16;    // head dims per mix workgroup
-constexpr uint32_t kTile = 128; // positions per staged value tile
+// Head dims per mix workgroup: 8 (more workgroups, deeper tiles) or 32 (one whole Q8_0 block of
+// each head, so the epilogue can quantize the output). Either way a value tile is 2048 floats.
+constexpr uint32_t kTileFloats = 2048;
+
+__host__ __device__ inline uint32_t score_pitch(uint32_t max_vis) { return (max_vis + 3) & ~3u; }
 
 template <bool F16>
 __global__ __launch_bounds__(kThreads) void attn_scores_kernel(AttnArgs a) {
@@ -209,8 +212,9 @@ __global__ __launch_bounds__(kThreads) void attn_scores_kernel(AttnArgs a) {
   }
 }
 
-template <bool F16>
+template <bool F16, uint32_t kDc>
 __global__ __launch_bounds__(kThreads) void attn_mix_kernel(AttnArgs a) {
+  constexpr uint32_t kTile = kTileFloats / kDc;
   extern __shared__ __attribute__((aligned(16))) float lds[];
   __shared__ double red_d[kThreads / 64];
   __shared__ float red_f[kThreads / 64];
@@ -225,16 +229,18 @@ __global__ __launch_bounds__(kThreads) void attn_mix_kernel(AttnArgs a) {
   const size_t kv_row = static_cast<size_t>(a.n_kv) * hd;
   const uint32_t dc = min(kDc, hd - d0);
 
-  float* p = lds;                               // [group][n_vis]
-  float* vt = lds + group * n_vis;              // [2][kTile][kDc]
+  const uint32_t pitch = score_pitch(n_vis);
+  float* p = lds;                               // [group][pitch]
+  float* vt = lds + group * pitch;              // [2][kTile][kDc]
   const float* s = a.scratch + (static_cast<size_t>(r) * a.n_head + static_cast<size_t>(g) * group) * a.max_vis;
   for (uint32_t i = tid; i < group * n_vis; i += kThreads) {
     const uint32_t h = i / n_vis;
-    p[i] = s[static_cast<size_t>(h) * a.max_vis + (i - h * n_vis)];
+    const uint32_t j = i - h * n_vis;
+    p[h * pitch + j] = s[static_cast<size_t>(h) * a.max_vis + j];
   }
   __syncthreads();
   for (uint32_t h = 0; h < group; ++h) {
-    float* row = p + h * n_vis;
+    float* row = p + h * pitch;
     float m = -INFINITY;
     for (uint32_t j = tid; j < n_vis; j += kThreads) m = fmaxf(m, row[j]);
 #pragma unroll
@@ -261,11 +267,12 @@ __global__ __launch_bounds__(kThreads) void attn_mix_kernel(AttnArgs a) {
   }
 
   // Value tiles: tile t holds positions [t*kTile, t*kTile + kTile) x dims [d0, d0 + dc).
+  constexpr uint32_t kPer = kTile * kDc / kThreads;
   const uint32_t n_tiles = (n_vis + kTile - 1) / kTile;
   const uint32_t per_tile = kTile * kDc;  // floats
-  auto fetch = [&](uint32_t t, float (&reg)[kTile * kDc / kThreads]) {
+  auto fetch = [&](uint32_t t, float (&reg)[kPer]) {
 #pragma unroll
-    for (uint32_t k = 0; k < kTile * kDc / kThreads; ++k) {
+    for (uint32_t k = 0; k < kPer; ++k) {
       const uint32_t i = tid + k * kThreads;
       const uint32_t jj = i / kDc;
       const uint32_t dd = i - jj * kDc;
@@ -273,10 +280,10 @@ __global__ __launch_bounds__(kThreads) void attn_mix_kernel(AttnArgs a) {
       reg[k] = (j < n_vis && dd < dc) ? kv_at<F16>(a.kv, v_off + j * kv_row + static_cast<size_t>(g) * hd + d0 + dd) : 0.0f;
     }
   };
-  float reg[kTile * kDc / kThreads];
+  float reg[kPer];
   fetch(0, reg);
 #pragma unroll
-  for (uint32_t k = 0; k < kTile * kDc / kThreads; ++k) vt[tid + k * kThreads] = reg[k];
+  for (uint32_t k = 0; k < kPer; ++k) vt[tid + k * kThreads] = reg[k];
   __syncthreads();
   const bool lane_active = tid < group * kDc;
   const uint32_t h = tid / kDc;
@@ -287,18 +294,36 @@ __global__ __launch_bounds__(kThreads) void attn_mix_kernel(AttnArgs a) {
     float* nxt = vt + ((t + 1) & 1) * per_tile;
     if (t + 1 < n_tiles) fetch(t + 1, reg);
     if (lane_active && dd < dc) {
-      const float* pr = p + h * n_vis + t * kTile;
+      const float* pr = p + h * pitch + t * kTile;
       const uint32_t cnt = min(kTile, n_vis - t * kTile);
-      for (uint32_t jj = 0; jj < cnt; ++jj) acc += pr[jj] * cur[jj * kDc + dd];
+      if (cnt == kTile) {
+        // positions in order; scores read four at a time, values one per position
+#pragma unroll
+        for (uint32_t jj = 0; jj < kTile; jj += 4) {
+          const float4 pp = *reinterpret_cast<const float4*>(pr + jj);
+          acc += pp.x * cur[(jj + 0) * kDc + dd];
+          acc += pp.y * cur[(jj + 1) * kDc + dd];
+          acc += pp.z * cur[(jj + 2) * kDc + dd];
+          acc += pp.w * cur[(jj + 3) * kDc + dd];
+        }
+      } else {
+        for (uint32_t jj = 0; jj < cnt; ++jj) acc += pr[jj] * cur[jj * kDc + dd];
+      }
     }
     if (t + 1 < n_tiles) {
 #pragma unroll
-      for (uint32_t k = 0; k < kTile * kDc / kThreads; ++k) nxt[tid + k * kThreads] = reg[k];
+      for (uint32_t k = 0; k < kPer; ++k) nxt[tid + k * kThreads] = reg[k];
     }
     __syncthreads();
   }
   if (lane_active && dd < dc) {
-    a.out[static_cast<size_t>(r) * a.out_stride + static_cast<size_t>(g * group + h) * hd + d0 + dd] = acc;
+    const size_t col = static_cast<size_t>(g * group + h) * hd + d0 + dd;
+    a.out[static_cast<size_t>(r) * a.out_stride + col] = acc;
+    // The Q8_0 block of dims [d0, d0 + 32) of head h: one half-wave (wo's input, llama.cpp:401-417).
+    if (kDc == kQK && a.outq != nullptr) {
+      const size_t nbq = a.out_stride / kQK;
+      quantize_block_lanes(acc, dd, a.outq + (static_cast<size_t>(r) * nbq + col / kQK) * kBytesQ8_0);
+    }
   }
 }
 
@@ -312,9 +337,9 @@ bool scores_fit_lds(const AttnArgs& a) {
 // Decode-shaped launches (few rows, every head) take the two-kernel path when its LDS fits.
 bool use_split(const AttnArgs& a, uint32_t n_rows) {
   const uint32_t group = a.n_head / a.n_kv;
-  const size_t lds = (static_cast<size_t>(group) * a.max_vis + 2 * kTile * kDc) * 4;
+  const size_t lds = (static_cast<size_t>(group) * score_pitch(a.max_vis) + 2 * kTileFloats) * 4;
   return a.split && a.head_begin == 0 && a.head_end == a.n_head && static_cast<size_t>(n_rows) * a.n_kv < 512 &&
-         lds <= 65536 && group * kDc <= kThreads;
+         lds <= 65536 && group * 32 <= kThreads && a.head_dim % 32 == 0;
 }
 
 size_t attention_scratch_floats(const AttnArgs& a, uint32_t n_rows) {
@@ -333,16 +358,28 @@ int attention_launch(const AttnArgs& a, uint32_t n_rows) {
   if (a.scratch != nullptr && use_split(a, n_rows)) {
     const dim3 sgrid(n_rows, a.n_kv, (a.max_vis + kThreads - 1) / kThreads);
     const size_t slds = static_cast<size_t>(group) * a.head_dim * 4;
-    const dim3 mgrid(n_rows, a.n_kv, (a.head_dim + kDc - 1) / kDc);
-    const size_t mlds = (static_cast<size_t>(group) * a.max_vis + 2 * kTile * kDc) * 4;
+    const size_t mlds = (static_cast<size_t>(group) * score_pitch(a.max_vis) + 2 * kTileFloats) * 4;
+    // Quantized output: 32-dim slices (whole Q8_0 blocks); float output: 8-dim slices.
+    const bool q = a.outq != nullptr;
+    const dim3 mgrid(n_rows, a.n_kv, a.head_dim / (q ? 32 : 8));
     if (a.f16) {
       hipLaunchKernelGGL(attn_scores_kernel<true>, sgrid, dim3(kThreads), slds, stream(), a);
-      hipLaunchKernelGGL(attn_mix_kernel<true>, mgrid, dim3(kThreads), mlds, stream(), a);
+      if (q) hipLaunchKernelGGL((attn_mix_kernel<true, 32>), mgrid, dim3(kThreads), mlds, stream(), a);
+      else hipLaunchKernelGGL((attn_mix_kernel<true, 8>), mgrid, dim3(kThreads), mlds, stream(), a);
     } else {
       hipLaunchKernelGGL(attn_scores_kernel<false>, sgrid, dim3(kThreads), slds, stream(), a);
-      hipLaunchKernelGGL(attn_mix_kernel<false>, mgrid, dim3(kThreads), mlds, stream(), a);
+      if (q) hipLaunchKernelGGL((attn_mix_kernel<false, 32>), mgrid, dim3(kThreads), mlds, stream(), a);
+      else hipLaunchKernelGGL((attn_mix_kernel<false, 8>), mgrid, dim3(kThreads), mlds, stream(), a);
     }
     return check_launch("attention (split)");
+  }
+  if (a.outq != nullptr) {
+    // The fused kernel has no quantizing epilogue: quantize its output rows afterwards.
+    AttnArgs b = a;
+    b.outq = nullptr;
+    const int rc = attention_launch(b, n_rows);
+    if (rc != kOk) return rc;
+    return quantize_rows_launch(a.out, a.outq, a.n_head * a.head_dim, n_rows, a.out_stride);
   }
   const dim3 grid(n_rows, a.n_kv);
   const bool lds_ok = scores_fit_lds(a);

@@ -574,6 +574,7 @@ static AttnArgs attn_from(const axon_hip_attention_rows_args* args) {
   a.scratch = args->scratch;
   a.max_vis = args->max_vis;
   a.split = 1;
+  a.outq = static_cast<uint8_t*>(args->outq);
   return a;
 }
 
@@ -585,6 +586,54 @@ int axon_hip_attention_rows(const axon_hip_attention_rows_args* args, size_t n_r
 
 size_t axon_hip_attention_scratch_floats(const axon_hip_attention_rows_args* args, size_t n_rows) {
   return attention_scratch_floats(attn_from(args), static_cast<uint32_t>(n_rows));
+}
+
+int axon_hip_matvec_fused_supported(int type, int in_mode, size_t n_rows, size_t n_in, int silu) {
+  if ((type != Q8_0 && type != Q4_0 && type != Q4_1) || n_in % kQK != 0 || n_rows > 4 || n_in > (1u << 24)) return 0;
+  if (in_mode < kInQ8 || in_mode > kInNorm) return 0;
+  return matvec_fused_fits(type, in_mode, static_cast<uint32_t>(n_rows), static_cast<uint32_t>(n_in / kQK), silu != 0)
+             ? 1
+             : 0;
+}
+
+int axon_hip_matvec_fused(const axon_hip_matvec_fused_args* p) {
+  AXON_READY();
+  if (p->n_seg < 1 || p->n_seg > 3) return fail(kInvalidArgument, "matvec_fused: %zu segments", p->n_seg);
+  if (p->n_in % kQK != 0) return fail(kInvalidArgument, "matvec_fused: n_in %zu is not a multiple of 32", p->n_in);
+  if (p->out_mode < kOutStore || p->out_mode > kOutRope) return fail(kInvalidArgument, "matvec_fused: out_mode %d", p->out_mode);
+  if (p->in_mode < kInQ8 || p->in_mode > kInNorm) return fail(kInvalidArgument, "matvec_fused: in_mode %d", p->in_mode);
+  if (p->out_mode == kOutRope && (p->pos == nullptr || p->cache == nullptr || p->cache_off == nullptr ||
+                                  p->rope_table == nullptr || p->head_dim == 0 || p->rot_half * 2 > p->head_dim))
+    return fail(kInvalidArgument, "matvec_fused: the rope epilogue needs positions, a cache and a cos/sin table");
+  if (!fits_u32(p->n_rows) || !fits_u32(p->n_in) || !fits_u32(p->x_stride)) return fail(kInvalidArgument, "matvec_fused: sizes too large");
+  FusedArgs a{};
+  a.n_seg = static_cast<int>(p->n_seg);
+  for (size_t s = 0; s < p->n_seg; ++s) {
+    if (!fits_u32(p->n_out[s]) || !fits_u32(p->y_stride[s])) return fail(kInvalidArgument, "matvec_fused: sizes too large");
+    a.w[s] = static_cast<const uint8_t*>(p->w[s]);
+    a.n_out[s] = static_cast<uint32_t>(p->n_out[s]);
+    a.y[s] = p->y[s];
+    a.y_stride[s] = static_cast<uint32_t>(p->y_stride[s]);
+    a.bias[s] = p->bias[s];
+  }
+  a.nb = static_cast<uint32_t>(p->n_in / kQK);
+  a.m = static_cast<uint32_t>(p->n_rows);
+  a.in_mode = p->in_mode;
+  a.xq = static_cast<const uint8_t*>(p->xq);
+  a.x = p->x;
+  a.x_stride = static_cast<uint32_t>(p->x_stride);
+  a.norm_w = p->norm_w;
+  a.eps = p->eps;
+  a.out_mode = p->out_mode;
+  a.rope_table = p->rope_table;
+  a.rot_half = p->rot_half;
+  a.head_dim = p->head_dim;
+  a.pos = p->pos;
+  a.cache_off = p->cache_off;
+  a.cache = p->cache;
+  a.k_layer_off = p->k_layer_off;
+  a.v_layer_off = p->v_layer_off;
+  return matvec_fused_launch(p->type, a);
 }
 
 int axon_hip_embedding_rows(int type, const void* table, size_t n, const int32_t* ids, size_t n_rows, float* out) {

@@ -94,8 +94,8 @@ __device__ __forceinline__ float exp_rounded(float x) {
 // (coalesced across the workgroup), and blocks are then read out of LDS as aligned dwords and
 // funnel-shifted into place.
 
-// Copies nbytes (a multiple of 2) from global src to LDS dst (16-byte aligned), using 16-, 4-
-// or 2-byte accesses, whichever the alignment of src and nbytes permits. Each thread issues up
+// Copies nbytes (a multiple of 2) from global src to LDS dst (2-byte aligned), using 16-, 4-
+// or 2-byte accesses, whichever the alignment of src, dst and nbytes permits. Each thread issues up
 // to eight loads before its first LDS store, so a whole tile is in flight at once. Every
 // thread of the block must call it; it does not synchronise.
 template <typename T>
@@ -118,7 +118,7 @@ __device__ __forceinline__ void stage_units(const T* __restrict__ s, T* d, uint3
 
 __device__ __forceinline__ void stage_bytes(const uint8_t* __restrict__ src, uint8_t* dst,
                                             uint32_t nbytes, uint32_t tid, uint32_t nthreads) {
-  const uintptr_t a = reinterpret_cast<uintptr_t>(src);
+  const uintptr_t a = reinterpret_cast<uintptr_t>(src) | reinterpret_cast<uintptr_t>(dst);
   if (((a | nbytes) & 15u) == 0) {
     stage_units(reinterpret_cast<const u32x4*>(src), reinterpret_cast<u32x4*>(dst), nbytes >> 4, tid, nthreads);
   } else if (((a | nbytes) & 3u) == 0) {
@@ -211,6 +211,24 @@ __device__ __forceinline__ int32_t dot32(const int32_t (&a)[8], const int32_t (&
 #pragma unroll
   for (int i = 0; i < 8; ++i) s = __builtin_amdgcn_sdot4(a[i], b[i], s, false);
   return s;
+}
+
+// Q8_0 quantization of one 32-element block held one element per lane in a 32-lane half-wave
+// (src/core/dtype.cpp:338-354): amax, d = amax / 127 (IEEE division), id = 1 / d or 0,
+// fp16(d), q = int8(roundf(x * id)), ties away from zero. `lane` is 0..31 within the half.
+__device__ __forceinline__ void quantize_block_lanes(float x, uint32_t lane, uint8_t* block) {
+  float amax = fabsf(x);
+#pragma unroll
+  for (int off = 16; off > 0; off >>= 1) amax = fmaxf(amax, __shfl_xor(amax, off, 32));
+  const float d = amax / 127.0f;
+  const float id = d != 0.0f ? 1.0f / d : 0.0f;
+  const int32_t q = static_cast<int32_t>(roundf(x * id));
+  const int32_t q_next = __shfl_down(q, 1, 32);
+  if (lane == 0) *reinterpret_cast<uint16_t*>(block) = static_cast<uint16_t>(float_to_half_bits(d));
+  if ((lane & 1) == 0) {
+    *reinterpret_cast<uint16_t*>(block + 2 + lane) =
+        static_cast<uint16_t>((q & 0xff) | ((q_next & 0xff) << 8));
+  }
 }
 
 // ------------------------------------------------------------------------------------------

@@ -56,6 +56,7 @@ struct AttnArgs {
   float* scratch;            // global score scratch when the scores do not fit LDS (or null)
   uint32_t max_vis;          // upper bound of n_vis over the rows
   int split;                 // decode-shaped launches may take the two-kernel path (scratch sized for it)
+  uint8_t* outq;             // Q8_0 blocks of each output row as well (split path only), or null
 };
 int attention_launch(const AttnArgs& a, uint32_t n_rows);
 // Floats of global scratch attention_launch needs for these rows (0 when LDS suffices).

@@ -9,25 +9,6 @@ namespace axon_hip {
 
 namespace {
 
-// ------------------------------------------------------------------------------------------
-// Q8_0 quantization of one 32-element block held one element per lane in a 32-lane half-wave
-// (src/core/dtype.cpp:338-354): amax, d = amax / 127 (IEEE division), id = 1 / d or 0,
-// fp16(d), q = int8(roundf(x * id)), ties away from zero. `lane` is 0..31 within the half.
-__device__ __forceinline__ void quantize_block_lanes(float x, uint32_t lane, uint8_t* block) {
-  float amax = fabsf(x);
-#pragma unroll
-  for (int off = 16; off > 0; off >>= 1) amax = fmaxf(amax, __shfl_xor(amax, off, 32));
-  const float d = amax / 127.0f;
-  const float id = d != 0.0f ? 1.0f / d : 0.0f;
-  const int32_t q = static_cast<int32_t>(roundf(x * id));
-  const int32_t q_next = __shfl_down(q, 1, 32);
-  if (lane == 0) *reinterpret_cast<uint16_t*>(block) = static_cast<uint16_t>(float_to_half_bits(d));
-  if ((lane & 1) == 0) {
-    *reinterpret_cast<uint16_t*>(block + 2 + lane) =
-        static_cast<uint16_t>((q & 0xff) | ((q_next & 0xff) << 8));
-  }
-}
-
 // Double-precision sum over the workgroup (256 threads), result broadcast to all threads.
 __device__ __forceinline__ double block_sum_double(double v, double* red) {
 #pragma unroll
@@ -70,6 +51,67 @@ __global__ __launch_bounds__(256) void quantize_rows_kernel(const float* __restr
 // the scalar table's left-to-right double sum only in its last bits, which survive the
 // rounding to float only when the two sums straddle a float rounding boundary. Optionally
 // writes y, the Q8_0 blocks of y, or both. One workgroup per row.
+// Rows of up to 256 * 8 elements (every model here) take rmsnorm_regs_kernel: each thread
+// holds 8 consecutive elements in registers from one load to the quantized store, and the 4
+// threads of a 32-element block agree on its scale through shuffles.
+__global__ __launch_bounds__(256) void rmsnorm_regs_kernel(const float* __restrict__ x, const float* __restrict__ w,
+                                                           float* __restrict__ y, uint8_t* __restrict__ yq,
+                                                           uint32_t n, float eps) {
+  __shared__ double red[4];
+  const uint32_t row = blockIdx.x;
+  const uint32_t e0 = threadIdx.x * 8;
+  const bool has = e0 < n;
+  const float* xr = x + static_cast<size_t>(row) * n;
+  float xv[8], wv[8];
+  if (has) {
+    const float4 a = *reinterpret_cast<const float4*>(xr + e0);
+    const float4 b = *reinterpret_cast<const float4*>(xr + e0 + 4);
+    const float4 c = *reinterpret_cast<const float4*>(w + e0);
+    const float4 d = *reinterpret_cast<const float4*>(w + e0 + 4);
+    xv[0] = a.x; xv[1] = a.y; xv[2] = a.z; xv[3] = a.w; xv[4] = b.x; xv[5] = b.y; xv[6] = b.z; xv[7] = b.w;
+    wv[0] = c.x; wv[1] = c.y; wv[2] = c.z; wv[3] = c.w; wv[4] = d.x; wv[5] = d.y; wv[6] = d.z; wv[7] = d.w;
+  } else {
+#pragma unroll
+    for (int k = 0; k < 8; ++k) xv[k] = wv[k] = 0.0f;
+  }
+  double ss = 0.0;
+#pragma unroll
+  for (int k = 0; k < 8; ++k) {
+    const double v = static_cast<double>(xv[k]);
+    ss += v * v;
+  }
+  ss = block_sum_double(ss, red);
+  const float inv = static_cast<float>(1.0 / sqrt(ss / static_cast<double>(n) + static_cast<double>(eps)));
+  float v[8];
+  float amax = 0.0f;
+#pragma unroll
+  for (int k = 0; k < 8; ++k) {
+    v[k] = xv[k] * inv * wv[k];
+    amax = fmaxf(amax, fabsf(v[k]));
+  }
+  if (y != nullptr && has) {
+    float* yr = y + static_cast<size_t>(row) * n + e0;
+    *reinterpret_cast<float4*>(yr) = make_float4(v[0], v[1], v[2], v[3]);
+    *reinterpret_cast<float4*>(yr + 4) = make_float4(v[4], v[5], v[6], v[7]);
+  }
+  if (yq == nullptr) return;
+  // The block's 4 threads are adjacent lanes.
+  amax = fmaxf(amax, __shfl_xor(amax, 1, 64));
+  amax = fmaxf(amax, __shfl_xor(amax, 2, 64));
+  if (!has) return;
+  const float d = amax / 127.0f;
+  const float id = d != 0.0f ? 1.0f / d : 0.0f;
+  uint8_t* blk = yq + (static_cast<size_t>(row) * (n / kQK) + e0 / kQK) * kBytesQ8_0;
+  const uint32_t part = threadIdx.x & 3;
+  uint32_t q[8];
+#pragma unroll
+  for (int k = 0; k < 8; ++k) q[k] = static_cast<uint32_t>(static_cast<int32_t>(roundf(v[k] * id))) & 0xffu;
+  if (part == 0) *reinterpret_cast<uint16_t*>(blk) = static_cast<uint16_t>(float_to_half_bits(d));
+  uint16_t* qs = reinterpret_cast<uint16_t*>(blk + 2 + 8 * part);
+#pragma unroll
+  for (int k = 0; k < 4; ++k) qs[k] = static_cast<uint16_t>(q[2 * k] | (q[2 * k + 1] << 8));
+}
+
 __global__ __launch_bounds__(256) void rmsnorm_kernel(const float* __restrict__ x, const float* __restrict__ w,
                                                       float* __restrict__ y, uint8_t* __restrict__ yq,
                                                       uint32_t n, float eps) {
@@ -321,7 +363,14 @@ int quantize_rows_launch(const float* x, uint8_t* out, uint32_t n, uint32_t n_ro
 int rmsnorm_launch(const float* x, const float* w, float* y, uint8_t* yq, uint32_t n, uint32_t n_rows, float eps) {
   if (n == 0 || n_rows == 0) return kOk;
   if (yq != nullptr && n % kQK != 0) return fail(kInvalidArgument, "rmsnorm+quantize: n %u is not a multiple of 32", n);
-  hipLaunchKernelGGL(rmsnorm_kernel, dim3(n_rows), dim3(256), 0, stream(), x, w, y, yq, n, eps);
+  const bool regs = n % kQK == 0 && n <= 256 * 8 &&
+                    ((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(w) |
+                      reinterpret_cast<uintptr_t>(y)) & 15u) == 0;
+  if (regs) {
+    hipLaunchKernelGGL(rmsnorm_regs_kernel, dim3(n_rows), dim3(256), 0, stream(), x, w, y, yq, n, eps);
+  } else {
+    hipLaunchKernelGGL(rmsnorm_kernel, dim3(n_rows), dim3(256), 0, stream(), x, w, y, yq, n, eps);
+  }
   return check_launch("rmsnorm");
 }
 

@@ -26,6 +26,38 @@ struct MatvecArgs {
   int accumulate;     // y += W x instead of y = W x
 };
 
+// The fused decode matvec (matvec_fused.hip): input prologue and output epilogue modes.
+enum FusedIn : int { kInQ8 = 0, kInF32 = 1, kInNorm = 2 };
+enum FusedOut : int { kOutStore = 0, kOutAdd = 1, kOutSilu = 2, kOutRope = 3 };
+
+struct FusedArgs {
+  const uint8_t* w[3];
+  uint32_t n_out[3];
+  uint32_t wg_begin[3];  // filled by the launcher
+  int n_seg;
+  uint32_t nb, m;
+  uint32_t rows, lds_tile, lds_scratch;  // filled by the launcher
+  int in_mode;
+  const uint8_t* xq;      // kInQ8: [m][nb] blocks
+  const float* x;         // kInF32 / kInNorm: [m][x_stride] floats
+  uint32_t x_stride;
+  const float* norm_w;    // kInNorm
+  float eps;
+  int out_mode;
+  float* y[3];
+  uint32_t y_stride[3];
+  const float* bias[3];   // kOutRope: per segment, or null
+  const float* rope_table;
+  uint32_t rot_half, head_dim;
+  const int32_t* pos;     // per activation row (device)
+  const int64_t* cache_off;
+  float* cache;
+  int64_t k_layer_off, v_layer_off;
+};
+
+bool matvec_fused_fits(int type, int in_mode, uint32_t m, uint32_t nb, bool silu);
+int matvec_fused_launch(int type, FusedArgs& a);
+
 // Quantized weights (Q8_0 / Q4_0 / Q4_1) against Q8_0 activations, m <= 4 rows.
 int matvec_q8_launch(int type, MatvecArgs& a);
 // The most activation rows (1..4) one matvec launch takes at nb blocks per row.

@@ -1,0 +1,375 @@
+// The decode matvec with its neighbours folded in: one launch per weight group of a layer for
+// one to four activation rows (batch-1 and small-batch decode).
+//
+// Prologue (input), per workgroup, identical in every workgroup:
+//   kInQ8    the activation rows arrive as Q8_0 blocks (as matvec_q8.hip);
+//   kInF32   float rows, quantized here exactly as quantize_row_q8_0
+//            (trickymind1324/axon-infer src/core/dtype.cpp:338-354);
+//   kInNorm  float rows, RMSNorm'd (src/kernels/ref/rmsnorm.cpp:10-21) then quantized, as
+//            src/model/llama.cpp:500 and 598 do before the q|k|v and gate|up matmuls.
+// Body: the integer-exact block dots and the left-to-right float accumulation of
+// matvec_q8.hip (src/kernels/ref/quant.cpp:44-69, 161-181).
+// Epilogue (output):
+//   kOutStore / kOutAdd   y = acc / y += acc (the residual add, llama.cpp:594-595, 621-623);
+//   kOutSilu              segment 0 is gate and segment 1 up, the same rows in one workgroup:
+//                         h = gate / (1 + exp(-gate)) * up (src/kernels/ref/silu.cpp:8-13);
+//   kOutRope              segments q, k, v: bias (llama.cpp:507-511), then the Normal-style
+//                         rotation of pairs (2i, 2i+1) with host-built cos/sin
+//                         (src/kernels/ref/rope.cpp:13-37), q to its buffer, k and v into the
+//                         row's KV cache at its position (llama.cpp:493-497, 520-537).
+// Every workgroup recomputes the row norm and the Q8_0 blocks with the same reduction tree as
+// rmsnorm_regs_kernel, so all of them and the standalone kernels agree bit for bit.
+#include "common.h"
+#include "matvec.h"
+
+namespace axon_hip {
+
+namespace {
+
+constexpr int kThreads = 256;
+constexpr int kMaxChunks = 4;  // float activation chunks of 8 held per thread
+
+template <int T>
+constexpr int wbytes() {
+  return T == Q8_0 ? kBytesQ8_0 : T == Q4_0 ? kBytesQ4_0 : kBytesQ4_1;
+}
+
+template <int T>
+__device__ __forceinline__ int32_t fused_block_sumi(const uint8_t* tile, uint32_t off, const ActBlock& a, float& dw,
+                                                    float& mw) {
+  if constexpr (T == Q8_0) {
+    uint32_t w[9];
+    lds_read_unaligned<9>(tile, off, w);
+    int32_t q[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) q[i] = static_cast<int32_t>(__builtin_amdgcn_alignbit(w[i + 1], w[i], 16));
+    dw = half_bits_to_float(w[0] & 0xffffu);
+    mw = 0.0f;
+    return dot32(q, a.qs);
+  } else {
+    constexpr uint32_t head = T == Q4_0 ? 2 : 4;
+    uint32_t w[4];
+    lds_read_unaligned<4>(tile, off + head, w);
+    uint32_t h[1];
+    lds_read_unaligned<1>(tile, off, h);
+    int32_t s = 0;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      s = __builtin_amdgcn_sdot4(static_cast<int32_t>(w[i] & 0x0f0f0f0fu), a.qs[i], s, false);
+      s = __builtin_amdgcn_sdot4(static_cast<int32_t>((w[i] >> 4) & 0x0f0f0f0fu), a.qs[4 + i], s, false);
+    }
+    dw = half_bits_to_float(h[0] & 0xffffu);
+    if constexpr (T == Q4_0) {
+      mw = 0.0f;
+      return s - 8 * a.sum;
+    } else {
+      mw = half_bits_to_float(h[0] >> 16);
+      return s;
+    }
+  }
+}
+
+template <int T>
+__device__ __forceinline__ float fused_term(const uint8_t* tile, uint32_t off, const ActBlock& a) {
+  float dw, mw;
+  const int32_t sumi = fused_block_sumi<T>(tile, off, a, dw, mw);
+  if constexpr (T == Q4_1) {
+    return static_cast<float>(sumi) * dw * a.d + mw * a.d * static_cast<float>(a.sum);
+  } else {
+    return static_cast<float>(sumi) * dw * a.d;
+  }
+}
+
+// Quantizes 8 consecutive elements held by this thread; the 4 adjacent lanes (part 0..3) hold
+// one 32-element block. Writes the thread's 2 dwords of quants, and lane part 0 the scale (as
+// the fp16 value the block would store) and the quant sum.
+__device__ __forceinline__ void quantize8_to_act(const float (&v)[8], uint32_t part, ActBlock& blk) {
+  float amax = 0.0f;
+#pragma unroll
+  for (int k = 0; k < 8; ++k) amax = fmaxf(amax, fabsf(v[k]));
+  amax = fmaxf(amax, __shfl_xor(amax, 1, 64));
+  amax = fmaxf(amax, __shfl_xor(amax, 2, 64));
+  const float d = amax / 127.0f;
+  const float id = d != 0.0f ? 1.0f / d : 0.0f;
+  uint32_t q[8];
+  int32_t s = 0;
+#pragma unroll
+  for (int k = 0; k < 8; ++k) {
+    const int32_t qi = static_cast<int32_t>(roundf(v[k] * id));
+    s += qi;
+    q[k] = static_cast<uint32_t>(qi) & 0xffu;
+  }
+  s += __shfl_xor(s, 1, 64);
+  s += __shfl_xor(s, 2, 64);
+  blk.qs[2 * part] = static_cast<int32_t>(q[0] | (q[1] << 8) | (q[2] << 16) | (q[3] << 24));
+  blk.qs[2 * part + 1] = static_cast<int32_t>(q[4] | (q[5] << 8) | (q[6] << 16) | (q[7] << 24));
+  if (part == 0) {
+    blk.d = half_bits_to_float(float_to_half_bits(d));
+    blk.sum = s;
+  }
+}
+
+template <int T>
+__global__ __launch_bounds__(kThreads) void matvec_fused_kernel(FusedArgs args) {
+  extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+  __shared__ double red[kThreads / 64];
+  constexpr int bs = wbytes<T>();
+  const uint32_t tid = threadIdx.x;
+  const uint32_t nb = args.nb;
+  const uint32_t n_in = nb * kQK;
+  const uint32_t M = args.m;
+  const uint32_t R = args.rows;
+  const uint32_t row_bytes = nb * bs;
+  const bool silu = args.out_mode == kOutSilu;
+
+  // Segment and rows of this workgroup. The SiLU pairing runs gate and up rows together.
+  uint32_t wg = blockIdx.x;
+  int s = 0;
+  if (!silu && args.n_seg > 1 && wg >= args.wg_begin[1]) s = 1;
+  if (!silu && args.n_seg > 2 && wg >= args.wg_begin[2]) s = 2;
+  const uint32_t r0 = (wg - args.wg_begin[s]) * R;
+  const uint32_t nr = min(R, args.n_out[s] - r0);
+  const uint32_t n_wrows = silu ? 2 * nr : nr;  // weight rows staged
+  const uint32_t pitch_rows = silu ? R : 0;     // tile row of up row r is pitch_rows + r
+
+  ActBlock* act = reinterpret_cast<ActBlock*>(smem);
+  uint8_t* tile = smem + args.lds_tile;
+  float* terms = reinterpret_cast<float*>(smem + args.lds_scratch);
+  uint8_t* raw = smem + args.lds_scratch;
+  const uint32_t tpitch = nb + 1;
+
+  // ---- float activations: this thread's 8-element chunks, loaded before the weight tile ----
+  // Thread t owns chunk c = t + 256 k (elements 8c .. 8c + 7) of every row; kMaxChunks bounds
+  // rows x chunks per thread (checked by the launcher).
+  const uint32_t n_chunks = n_in / 8;
+  const uint32_t cpt = (n_chunks + kThreads - 1) / kThreads;  // chunks per thread and row
+  float xv[kMaxChunks][8];
+  float wv[kMaxChunks][8];
+  if (args.in_mode != kInQ8) {
+#pragma unroll
+    for (int i = 0; i < kMaxChunks; ++i) {
+      const uint32_t m = i / cpt;
+      const uint32_t c = tid + (i - m * cpt) * kThreads;
+      if (m < M && c < n_chunks) {
+        const float4* xr = reinterpret_cast<const float4*>(args.x + static_cast<size_t>(m) * args.x_stride + c * 8);
+        const float4 a = xr[0], b = xr[1];
+        xv[i][0] = a.x; xv[i][1] = a.y; xv[i][2] = a.z; xv[i][3] = a.w;
+        xv[i][4] = b.x; xv[i][5] = b.y; xv[i][6] = b.z; xv[i][7] = b.w;
+        if (args.in_mode == kInNorm) {
+          const float4* wr = reinterpret_cast<const float4*>(args.norm_w + c * 8);
+          const float4 e = wr[0], f = wr[1];
+          wv[i][0] = e.x; wv[i][1] = e.y; wv[i][2] = e.z; wv[i][3] = e.w;
+          wv[i][4] = f.x; wv[i][5] = f.y; wv[i][6] = f.z; wv[i][7] = f.w;
+        }
+      }
+    }
+  }
+
+  // ---- weight tile (and Q8_0 activation blocks) into LDS ------------------------------------
+  const uint32_t xthreads = args.in_mode == kInQ8 ? 64u : 0u;
+  if (tid >= xthreads) {
+    stage_bytes(args.w[s] + static_cast<size_t>(r0) * row_bytes, tile, nr * row_bytes, tid - xthreads,
+                kThreads - xthreads);
+    if (silu) {
+      stage_bytes(args.w[1] + static_cast<size_t>(r0) * row_bytes, tile + static_cast<size_t>(pitch_rows) * row_bytes,
+                  nr * row_bytes, tid - xthreads, kThreads - xthreads);
+    }
+  } else {
+    stage_bytes(args.xq, raw, M * nb * kBytesQ8_0, tid, xthreads);
+  }
+
+  // ---- activation prologue ------------------------------------------------------------------
+  if (args.in_mode == kInQ8) {
+    __syncthreads();
+    for (uint32_t i = tid; i < M * nb; i += kThreads) act[i] = unpack_q8_0_lds(raw, i * kBytesQ8_0);
+  } else {
+    const uint32_t part = tid & 3;
+    for (uint32_t m = 0; m < M; ++m) {
+      float inv = 1.0f;
+      if (args.in_mode == kInNorm) {
+        // The sum of squares in double with rmsnorm_regs_kernel's tree: 8 elements per thread
+        // in order, then the wave butterfly, then the waves in order (one chunk per thread).
+        double ss = 0.0;
+#pragma unroll
+        for (int i = 0; i < kMaxChunks; ++i) {
+          if (i / cpt == m && tid + (i - m * cpt) * kThreads < n_chunks) {
+#pragma unroll
+            for (int k = 0; k < 8; ++k) {
+              const double v = static_cast<double>(xv[i][k]);
+              ss += v * v;
+            }
+          }
+        }
+#pragma unroll
+        for (int off = 32; off > 0; off >>= 1) ss += __shfl_xor(ss, off, 64);
+        if ((tid & 63) == 0) red[tid >> 6] = ss;
+        __syncthreads();
+        ss = 0.0;
+        for (int w = 0; w < kThreads / 64; ++w) ss += red[w];
+        __syncthreads();
+        inv = static_cast<float>(1.0 / sqrt(ss / static_cast<double>(n_in) + static_cast<double>(args.eps)));
+      }
+#pragma unroll
+      for (int i = 0; i < kMaxChunks; ++i) {
+        const uint32_t c = tid + (i - m * cpt) * kThreads;
+        if (i / cpt == m && c < n_chunks) {
+          float v[8];
+#pragma unroll
+          for (int k = 0; k < 8; ++k) v[k] = args.in_mode == kInNorm ? xv[i][k] * inv * wv[i][k] : xv[i][k];
+          quantize8_to_act(v, part, act[m * nb + c / 4]);
+        }
+      }
+    }
+  }
+  __syncthreads();
+
+  // ---- body: block terms, then the ordered chains --------------------------------------------
+  const uint32_t pairs = n_wrows * nb;
+  for (uint32_t p = tid; p < pairs; p += kThreads) {
+    const uint32_t r = p / nb;
+    const uint32_t b = p - r * nb;
+    const uint32_t trow = (silu && r >= nr) ? pitch_rows + (r - nr) : r;
+    for (uint32_t m = 0; m < M; ++m) {
+      terms[(m * 2 * R + trow) * tpitch + b] = fused_term<T>(tile, trow * row_bytes + b * bs, act[m * nb + b]);
+    }
+  }
+  __syncthreads();
+  float* outv = reinterpret_cast<float*>(tile);  // [M][2R], the tile is no longer needed
+  if (tid < M * n_wrows) {
+    const uint32_t m = tid / n_wrows;
+    const uint32_t r = tid - m * n_wrows;
+    const uint32_t trow = (silu && r >= nr) ? pitch_rows + (r - nr) : r;
+    const float* t = terms + (m * 2 * R + trow) * tpitch;
+    float acc = 0.0f;
+    for (uint32_t b = 0; b < nb; ++b) acc += t[b];
+    outv[m * 2 * R + trow] = acc;
+  }
+  __syncthreads();
+
+  // ---- epilogue -----------------------------------------------------------------------------
+  if (args.out_mode == kOutStore || args.out_mode == kOutAdd) {
+    if (tid < M * nr) {
+      const uint32_t m = tid / nr;
+      const uint32_t r = tid - m * nr;
+      const float acc = outv[m * 2 * R + r];
+      float* y = args.y[s] + static_cast<size_t>(m) * args.y_stride[s] + r0 + r;
+      *y = args.out_mode == kOutAdd ? *y + acc : acc;
+    }
+  } else if (silu) {
+    if (tid < M * nr) {
+      const uint32_t m = tid / nr;
+      const uint32_t r = tid - m * nr;
+      const float g = outv[m * 2 * R + r];
+      const float u = outv[m * 2 * R + pitch_rows + r];
+      args.y[0][static_cast<size_t>(m) * args.y_stride[0] + r0 + r] = g / (1.0f + exp_rounded(-g)) * u;
+    }
+  } else {
+    // kOutRope: one thread per (row, pair of outputs).
+    const uint32_t np = nr / 2;
+    if (tid < M * np) {
+      const uint32_t m = tid / np;
+      const uint32_t pr = tid - m * np;
+      const uint32_t o = r0 + 2 * pr;  // even: the pair (o, o + 1) lies in one head
+      float x0 = outv[m * 2 * R + 2 * pr];
+      float x1 = outv[m * 2 * R + 2 * pr + 1];
+      if (args.bias[s] != nullptr) {
+        x0 = x0 + args.bias[s][o];
+        x1 = x1 + args.bias[s][o + 1];
+      }
+      const int32_t pos = args.pos[m];
+      if (s < 2) {
+        const uint32_t i = (o % args.head_dim) / 2;
+        if (i < args.rot_half) {
+          const float2 cs = reinterpret_cast<const float2*>(args.rope_table)[static_cast<size_t>(pos) * args.rot_half + i];
+          const float a0 = x0, a1 = x1;
+          x0 = a0 * cs.x - a1 * cs.y;
+          x1 = a0 * cs.y + a1 * cs.x;
+        }
+      }
+      if (s == 0) {
+        float* q = args.y[0] + static_cast<size_t>(m) * args.y_stride[0] + o;
+        q[0] = x0;
+        q[1] = x1;
+      } else {
+        const size_t kv_row = args.n_out[1];
+        float* c = args.cache + args.cache_off[m] + (s == 1 ? args.k_layer_off : args.v_layer_off) +
+                   static_cast<size_t>(pos) * kv_row + o;
+        c[0] = x0;
+        c[1] = x1;
+      }
+    }
+  }
+}
+
+size_t fused_lds(int bs, uint32_t m, uint32_t nb, uint32_t rows, bool silu, size_t* act_out, size_t* tile_out) {
+  const size_t row_bytes = static_cast<size_t>(nb) * bs;
+  const uint32_t wrows = silu ? 2 * rows : rows;
+  const size_t act = (static_cast<size_t>(m) * nb * sizeof(ActBlock) + 15) & ~size_t(15);
+  const size_t tile = std::max<size_t>((wrows * row_bytes + 16 + 15) & ~size_t(15), static_cast<size_t>(m) * 2 * rows * 4);
+  const size_t raw = static_cast<size_t>(m) * nb * kBytesQ8_0 + 16;
+  const size_t terms = static_cast<size_t>(m) * 2 * rows * (nb + 1) * 4;
+  *act_out = act;
+  *tile_out = tile;
+  return act + tile + std::max(raw, terms);
+}
+
+}  // namespace
+
+bool matvec_fused_fits(int type, int in_mode, uint32_t m, uint32_t nb, bool silu) {
+  const int bs = type == Q8_0 ? kBytesQ8_0 : type == Q4_0 ? kBytesQ4_0 : kBytesQ4_1;
+  size_t act, tile;
+  if (m < 1 || m > 4 || fused_lds(bs, m, nb, silu ? 1 : 2, silu, &act, &tile) > 65536) return false;
+  if (in_mode == kInQ8) return true;
+  const uint32_t cpt = ceil_div(nb * kQK / 8, kThreads);
+  // The norm prologue reproduces rmsnorm_regs_kernel's reduction only with one chunk per thread.
+  return m * cpt <= kMaxChunks && (in_mode != kInNorm || cpt == 1);
+}
+
+int matvec_fused_launch(int type, FusedArgs& a) {
+  if (a.m == 0) return kOk;
+  if (a.m > 4) return fail(kInvalidArgument, "matvec_fused: %u rows (at most 4)", a.m);
+  if (!matvec_fused_fits(type, a.in_mode, a.m, a.nb, a.out_mode == kOutSilu))
+    return fail(kUnsupported, "matvec_fused: %u rows of %u blocks do not fit one launch", a.m, a.nb);
+  if (a.in_mode != kInQ8 && ((reinterpret_cast<uintptr_t>(a.x) | (a.x_stride * 4u) |
+                              (a.in_mode == kInNorm ? reinterpret_cast<uintptr_t>(a.norm_w) : 0u)) & 15u))
+    return fail(kInvalidArgument, "matvec_fused: float activations must be 16-byte aligned");
+  const bool silu = a.out_mode == kOutSilu;
+  const bool rope = a.out_mode == kOutRope;
+  if (silu && (a.n_seg != 2 || a.n_out[0] != a.n_out[1])) return fail(kInvalidArgument, "matvec_fused: SiLU pairs need gate and up of one size");
+  if (rope && (a.n_seg != 3 || a.n_out[1] != a.n_out[2] || (a.n_out[0] | a.n_out[1] | a.head_dim) & 1))
+    return fail(kInvalidArgument, "matvec_fused: q|k|v rope epilogue shapes");
+  const int bs = type == Q8_0 ? kBytesQ8_0 : type == Q4_0 ? kBytesQ4_0 : kBytesQ4_1;
+  const size_t row_bytes = static_cast<size_t>(a.nb) * bs;
+  uint32_t total_out = 0;
+  for (int s = 0; s < (silu ? 1 : a.n_seg); ++s) total_out += a.n_out[s];
+  uint32_t rows = static_cast<uint32_t>(std::max<size_t>(1, (silu ? 8192 : 16384) / row_bytes));
+  rows = std::min<uint32_t>(rows, std::max<uint32_t>(1, total_out / 512));
+  rows = std::min<uint32_t>(rows, (silu ? 128 : 256) / a.m);
+  if (rope) rows = std::max<uint32_t>(2, rows & ~1u);
+  for (;;) {
+    size_t act = 0, tile = 0;
+    const size_t lds = fused_lds(bs, a.m, a.nb, rows, silu, &act, &tile);
+    if (lds <= 65536) {
+      a.rows = rows;
+      a.lds_tile = static_cast<uint32_t>(act);
+      a.lds_scratch = static_cast<uint32_t>(act + tile);
+      uint32_t wg = 0;
+      for (int s = 0; s < a.n_seg; ++s) {
+        a.wg_begin[s] = wg;
+        if (!silu || s == 0) wg += static_cast<uint32_t>(ceil_div(a.n_out[s], rows));
+      }
+      if (silu) a.wg_begin[1] = 0;
+      switch (type) {
+      case Q8_0: hipLaunchKernelGGL(matvec_fused_kernel<Q8_0>, dim3(wg), dim3(kThreads), lds, stream(), a); break;
+      case Q4_0: hipLaunchKernelGGL(matvec_fused_kernel<Q4_0>, dim3(wg), dim3(kThreads), lds, stream(), a); break;
+      case Q4_1: hipLaunchKernelGGL(matvec_fused_kernel<Q4_1>, dim3(wg), dim3(kThreads), lds, stream(), a); break;
+      default: return fail(kUnsupported, "matvec_fused: weight type %d", type);
+      }
+      return check_launch("matvec_fused");
+    }
+    if (rows <= (rope ? 2u : 1u)) return fail(kUnsupported, "matvec_fused: %u blocks x %u rows exceed LDS", a.nb, a.m);
+    rows = rope ? std::max<uint32_t>(2, (rows / 2) & ~1u) : rows / 2;
+  }
+}
+
+}  // namespace axon_hip

@@ -140,11 +140,16 @@ __global__ __launch_bounds__(kThreads) void matvec_q8_kernel(MatvecArgs args) {
   float* terms = reinterpret_cast<float*>(scratch);
   const uint32_t tpitch = nb + 1;  // odd pitch: the chain lanes read distinct banks
 
-  if (tid < 64) {
-    stage_bytes(args.xq, scratch, M * nb * kBytesQ8_0, tid, 64);
+  // The activation blocks and the weight tile are copied side by side, by waves split in
+  // proportion to their bytes, so both streams are in flight at once.
+  const uint32_t xbytes = M * nb * kBytesQ8_0;
+  const uint32_t tbytes = nr * row_bytes;
+  const uint32_t xwaves = min(3u, max(1u, (4 * xbytes + (xbytes + tbytes) / 2) / (xbytes + tbytes)));
+  const uint32_t xthreads = 64 * xwaves;
+  if (tid < xthreads) {
+    stage_bytes(args.xq, scratch, xbytes, tid, xthreads);
   } else {
-    stage_bytes(seg.w + static_cast<size_t>(r0) * row_bytes, tile, nr * row_bytes, tid - 64,
-                kThreads - 64);
+    stage_bytes(seg.w + static_cast<size_t>(r0) * row_bytes, tile, tbytes, tid - xthreads, kThreads - xthreads);
   }
   __syncthreads();
   for (uint32_t i = tid; i < M * nb; i += kThreads) act[i] = unpack_q8_0_lds(scratch, i * kBytesQ8_0);

@@ -458,6 +458,20 @@ Expected<std::size_t> LlamaModel::run(std::span<const Row> rows, bool copy_logit
   } while (0)
 
   DEV(axon_hip_embedding_rows(static_cast<int>(token_embd_.type), token_embd_.dev, d, d_ids, n, x_));
+  // Decode-sized calls (up to four rows) fold the norms, quantizations, RoPE, KV write and
+  // SiLU into the matvec launches (axon_hip_matvec_fused); other calls run them apart.
+  const bool fuse = n <= 4 && !exact_;
+  const auto fused_ok = [&](const Tensor& w, int in_mode, std::size_t n_in, bool silu) {
+    return fuse && q8_path(w) && axon_hip_matvec_fused_supported(static_cast<int>(w.type), in_mode, n, n_in, silu) == 1;
+  };
+  const auto fused_args = [&](const Tensor& w) {
+    axon_hip_matvec_fused_args fa{};
+    fa.type = static_cast<int>(w.type);
+    fa.n_rows = n;
+    fa.n_in = w.ne0;
+    fa.eps = eps;
+    return fa;
+  };
   for (std::size_t l = 0; l < c.n_layer; ++l) {
     const Layer& L = layers_[l];
     const std::int64_t k_layer = static_cast<std::int64_t>(2 * l) * max_ctx_ * dkv;
@@ -466,47 +480,83 @@ Expected<std::size_t> LlamaModel::run(std::span<const Row> rows, bool copy_logit
     // attention block (llama.cpp:500-595)
     const bool qkv_q8 = q8_path(L.wq) && q8_path(L.wk) && q8_path(L.wv) && L.wq.type == L.wk.type &&
                         L.wk.type == L.wv.type;
-    const bool need_q8 = q8_path(L.wq) || q8_path(L.wk) || q8_path(L.wv);
-    const bool need_f = !q8_path(L.wq) || !q8_path(L.wk) || !q8_path(L.wv);
-    DEV(axon_hip_rmsnorm_rows(x_, static_cast<const float*>(L.attn_norm.dev), need_f ? h_ : nullptr,
-                              need_q8 ? xq_ : nullptr, d, n, eps));
-    if (qkv_q8) {
-      const void* ws[3] = {L.wq.dev, L.wk.dev, L.wv.dev};
-      float* ys[3] = {q_, k_, v_};
-      const std::size_t no[3] = {dq, dkv, dkv};
+    if (qkv_q8 && c.rope_style == kernels::RopeStyle::Normal && fused_ok(L.wq, 2, d, false)) {
+      // attn_norm, quantize, q|k|v, bias, RoPE and the KV write in one launch.
+      axon_hip_matvec_fused_args fa = fused_args(L.wq);
+      fa.n_seg = 3;
+      fa.w[0] = L.wq.dev;
+      fa.w[1] = L.wk.dev;
+      fa.w[2] = L.wv.dev;
+      fa.n_out[0] = dq;
+      fa.n_out[1] = dkv;
+      fa.n_out[2] = dkv;
+      fa.in_mode = 2;
+      fa.x = x_;
+      fa.x_stride = d;
+      fa.norm_w = static_cast<const float*>(L.attn_norm.dev);
+      fa.out_mode = 3;
+      fa.y[0] = q_;
+      fa.y_stride[0] = dq;
+      if (L.bias) {
+        fa.bias[0] = static_cast<const float*>(L.bq.dev);
+        fa.bias[1] = static_cast<const float*>(L.bk.dev);
+        fa.bias[2] = static_cast<const float*>(L.bv.dev);
+      }
+      fa.rope_table = rope_table_;
+      fa.rot_half = c.rotary_dim / 2;
+      fa.head_dim = c.head_dim;
+      fa.pos = d_pos;
+      fa.cache_off = d_coff;
+      fa.cache = kv_;
+      fa.k_layer_off = k_layer;
+      fa.v_layer_off = v_layer;
       probe_begin(L.wq);
-      DEV(axon_hip_matmul_q8_fused(static_cast<int>(L.wq.type), xq_, n, d, 3, ws, ys, no, no, 0));
+      DEV(axon_hip_matvec_fused(&fa));
       probe_end(L.wq, n, dq + 2 * dkv, false);
     } else {
-      DEV(mm(L.wq, h_, xq_, q_, n, false));
-      DEV(mm(L.wk, h_, xq_, k_, n, false));
-      DEV(mm(L.wv, h_, xq_, v_, n, false));
+      const bool need_q8 = q8_path(L.wq) || q8_path(L.wk) || q8_path(L.wv);
+      const bool need_f = !q8_path(L.wq) || !q8_path(L.wk) || !q8_path(L.wv);
+      DEV(axon_hip_rmsnorm_rows(x_, static_cast<const float*>(L.attn_norm.dev), need_f ? h_ : nullptr,
+                                need_q8 ? xq_ : nullptr, d, n, eps));
+      if (qkv_q8) {
+        const void* ws[3] = {L.wq.dev, L.wk.dev, L.wv.dev};
+        float* ys[3] = {q_, k_, v_};
+        const std::size_t no[3] = {dq, dkv, dkv};
+        probe_begin(L.wq);
+        DEV(axon_hip_matmul_q8_fused(static_cast<int>(L.wq.type), xq_, n, d, 3, ws, ys, no, no, 0));
+        probe_end(L.wq, n, dq + 2 * dkv, false);
+      } else {
+        DEV(mm(L.wq, h_, xq_, q_, n, false));
+        DEV(mm(L.wk, h_, xq_, k_, n, false));
+        DEV(mm(L.wv, h_, xq_, v_, n, false));
+      }
+      axon_hip_rope_rows_args ra{};
+      ra.q = q_;
+      ra.k = k_;
+      ra.v = v_;
+      if (L.bias) {
+        ra.bq = static_cast<const float*>(L.bq.dev);
+        ra.bk = static_cast<const float*>(L.bk.dev);
+        ra.bv = static_cast<const float*>(L.bv.dev);
+      }
+      ra.pos = d_pos;
+      ra.q_stride = static_cast<std::uint32_t>(dq);
+      ra.k_stride = static_cast<std::uint32_t>(dkv);
+      ra.n_head = c.n_head;
+      ra.n_kv = c.n_head_kv;
+      ra.head_dim = c.head_dim;
+      ra.rotary_dim = c.rotary_dim;
+      ra.neox = c.rope_style == kernels::RopeStyle::NeoX ? 1 : 0;
+      ra.theta = c.rope_theta;
+      ra.table = rope_table_;
+      ra.cache = kv_;
+      ra.cache_off = d_coff;
+      ra.k_layer_off = k_layer;
+      ra.v_layer_off = v_layer;
+      DEV(axon_hip_rope_rows(&ra, n));
     }
-    axon_hip_rope_rows_args ra{};
-    ra.q = q_;
-    ra.k = k_;
-    ra.v = v_;
-    if (L.bias) {
-      ra.bq = static_cast<const float*>(L.bq.dev);
-      ra.bk = static_cast<const float*>(L.bk.dev);
-      ra.bv = static_cast<const float*>(L.bv.dev);
-    }
-    ra.pos = d_pos;
-    ra.q_stride = static_cast<std::uint32_t>(dq);
-    ra.k_stride = static_cast<std::uint32_t>(dkv);
-    ra.n_head = c.n_head;
-    ra.n_kv = c.n_head_kv;
-    ra.head_dim = c.head_dim;
-    ra.rotary_dim = c.rotary_dim;
-    ra.neox = c.rope_style == kernels::RopeStyle::NeoX ? 1 : 0;
-    ra.theta = c.rope_theta;
-    ra.table = rope_table_;
-    ra.cache = kv_;
-    ra.cache_off = d_coff;
-    ra.k_layer_off = k_layer;
-    ra.v_layer_off = v_layer;
-    DEV(axon_hip_rope_rows(&ra, n));
 
+    const bool wo_fused = fused_ok(L.wo, 1, dq, false);
     axon_hip_attention_rows_args aa{};
     aa.q = q_;
     aa.out = attn_;
@@ -524,13 +574,64 @@ Expected<std::size_t> LlamaModel::run(std::span<const Row> rows, bool copy_logit
     aa.scale = scale;
     aa.scratch = scores_;
     aa.max_vis = max_vis;
+    // wo's Q8_0 input: quantized in the attention epilogue, or inside the fused wo launch.
+    aa.outq = q8_path(L.wo) && !wo_fused ? xq_ : nullptr;
     DEV(axon_hip_attention_rows(&aa, n));
 
-    if (q8_path(L.wo)) DEV(axon_hip_quantize_rows_q8_0(attn_, xq_, dq, n, dq));
-    DEV(mm(L.wo, attn_, xq_, x_, n, true));
+    if (wo_fused) {
+      axon_hip_matvec_fused_args fa = fused_args(L.wo);
+      fa.n_seg = 1;
+      fa.w[0] = L.wo.dev;
+      fa.n_out[0] = d;
+      fa.in_mode = 1;
+      fa.x = attn_;
+      fa.x_stride = dq;
+      fa.out_mode = 1;
+      fa.y[0] = x_;
+      fa.y_stride[0] = d;
+      probe_begin(L.wo);
+      DEV(axon_hip_matvec_fused(&fa));
+      probe_end(L.wo, n, d, true);
+    } else {
+      DEV(mm(L.wo, attn_, xq_, x_, n, true));
+    }
 
     // feed-forward block (llama.cpp:598-623)
     const bool gu_q8 = q8_path(L.w_gate) && q8_path(L.w_up) && L.w_gate.type == L.w_up.type;
+    if (gu_q8 && fused_ok(L.w_gate, 2, d, true) && fused_ok(L.w_down, 1, ff, false)) {
+      // ffn_norm, quantize, gate|up and SiLU * up in one launch; quantize, down and the
+      // residual add in the next.
+      axon_hip_matvec_fused_args fa = fused_args(L.w_gate);
+      fa.n_seg = 2;
+      fa.w[0] = L.w_gate.dev;
+      fa.w[1] = L.w_up.dev;
+      fa.n_out[0] = ff;
+      fa.n_out[1] = ff;
+      fa.in_mode = 2;
+      fa.x = x_;
+      fa.x_stride = d;
+      fa.norm_w = static_cast<const float*>(L.ffn_norm.dev);
+      fa.out_mode = 2;
+      fa.y[0] = gate_;
+      fa.y_stride[0] = ff;
+      probe_begin(L.w_gate);
+      DEV(axon_hip_matvec_fused(&fa));
+      probe_end(L.w_gate, n, 2 * ff, false);
+      axon_hip_matvec_fused_args fd = fused_args(L.w_down);
+      fd.n_seg = 1;
+      fd.w[0] = L.w_down.dev;
+      fd.n_out[0] = d;
+      fd.in_mode = 1;
+      fd.x = gate_;
+      fd.x_stride = ff;
+      fd.out_mode = 1;
+      fd.y[0] = x_;
+      fd.y_stride[0] = d;
+      probe_begin(L.w_down);
+      DEV(axon_hip_matvec_fused(&fd));
+      probe_end(L.w_down, n, d, true);
+      continue;
+    }
     const bool ff_q8 = q8_path(L.w_gate) || q8_path(L.w_up);
     const bool ff_f = !q8_path(L.w_gate) || !q8_path(L.w_up);
     DEV(axon_hip_rmsnorm_rows(x_, static_cast<const float*>(L.ffn_norm.dev), ff_f ? h_ : nullptr,
@@ -553,10 +654,27 @@ Expected<std::size_t> LlamaModel::run(std::span<const Row> rows, bool copy_logit
     }
     DEV(mm(L.w_down, gate_, xq_, x_, n, true));
   }
-  const bool out_q8 = q8_path(output_);
-  DEV(axon_hip_rmsnorm_rows(x_, static_cast<const float*>(output_norm_.dev), out_q8 ? nullptr : h_,
-                            out_q8 ? xq_ : nullptr, d, n, eps));
-  DEV(mm(output_, h_, xq_, logits_, n, false));
+  if (fused_ok(output_, 2, d, false)) {
+    axon_hip_matvec_fused_args fa = fused_args(output_);
+    fa.n_seg = 1;
+    fa.w[0] = output_.dev;
+    fa.n_out[0] = c.n_vocab;
+    fa.in_mode = 2;
+    fa.x = x_;
+    fa.x_stride = d;
+    fa.norm_w = static_cast<const float*>(output_norm_.dev);
+    fa.out_mode = 0;
+    fa.y[0] = logits_;
+    fa.y_stride[0] = c.n_vocab;
+    probe_begin(output_);
+    DEV(axon_hip_matvec_fused(&fa));
+    probe_end(output_, n, c.n_vocab, false);
+  } else {
+    const bool out_q8 = q8_path(output_);
+    DEV(axon_hip_rmsnorm_rows(x_, static_cast<const float*>(output_norm_.dev), out_q8 ? nullptr : h_,
+                              out_q8 ? xq_ : nullptr, d, n, eps));
+    DEV(mm(output_, h_, xq_, logits_, n, false));
+  }
   if (copy_logits) {
     logits_host_.resize(n * c.n_vocab);
     DEV(axon_hip_memcpy_d2h(logits_host_.data(), logits_, logits_host_.size() * 4));

@@ -206,11 +206,46 @@ typedef struct {
   int f16;                /* the cache holds fp16 bit patterns */
   float* scratch;         /* device score scratch for contexts beyond LDS, or NULL */
   uint32_t max_vis;       /* >= every n_vis */
+  void* outq;             /* also the Q8_0 blocks of each output row (wo's input), or NULL */
 } axon_hip_attention_rows_args;
 int axon_hip_attention_rows(const axon_hip_attention_rows_args* args, size_t n_rows);
 /* Floats of scratch axon_hip_attention_rows needs for n_rows rows (0: LDS suffices). Launches
  * of few rows use a two-kernel path whose scores always go through the scratch. */
 size_t axon_hip_attention_scratch_floats(const axon_hip_attention_rows_args* args, size_t n_rows);
+
+/* The decode matvec with its neighbours fused in, for 1..4 activation rows of quantized
+ * weights (one type for every segment). Input: in_mode 0 Q8_0 blocks (xq), 1 float rows (x,
+ * quantized in the kernel as quantize_row_q8_0 does), 2 float rows RMSNorm'd with norm_w and eps
+ * first (llama.cpp:500, 598). Output: out_mode 0 y = W x, 1 y += W x (residual), 2 segments gate
+ * and up -> y[0] = silu(gate) * up (llama.cpp:600-620), 3 segments q, k, v -> bias, Normal-style
+ * RoPE from the cos/sin table at pos[row], q into y[0], k and v into the row's cache slot at
+ * cache + cache_off[row] + {k,v}_layer_off + pos * n_out[1] (llama.cpp:493-537). */
+typedef struct {
+  int type;
+  size_t n_seg;
+  const void* w[3];
+  size_t n_out[3];
+  size_t n_rows, n_in;
+  int in_mode;
+  const void* xq;
+  const float* x;
+  size_t x_stride;
+  const float* norm_w;
+  float eps;
+  int out_mode;
+  float* y[3];
+  size_t y_stride[3];
+  const float* bias[3];
+  const float* rope_table;
+  uint32_t rot_half, head_dim;
+  const int32_t* pos;
+  const int64_t* cache_off;
+  float* cache;
+  int64_t k_layer_off, v_layer_off;
+} axon_hip_matvec_fused_args;
+int axon_hip_matvec_fused(const axon_hip_matvec_fused_args* args);
+/* 1 when axon_hip_matvec_fused takes this shape (rows, row length, input mode, SiLU pairing). */
+int axon_hip_matvec_fused_supported(int type, int in_mode, size_t n_rows, size_t n_in, int silu);
 
 /* embedding_row for a device array of token ids (llama.cpp:482-485). */
 int axon_hip_embedding_rows(int type, const void* table, size_t n, const int32_t* ids, size_t n_rows, float* out);
