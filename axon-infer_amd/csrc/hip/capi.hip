@@ -183,6 +183,17 @@ int attention_heads(const float* q, const void* k, const void* v, float* out, fl
 
 hipStream_t stream() { return g_stream; }
 
+namespace {
+thread_local hipEvent_t g_probe_start = nullptr;
+thread_local hipEvent_t g_probe_stop = nullptr;
+}  // namespace
+
+void take_probe(hipEvent_t* start, hipEvent_t* stop) {
+  *start = g_probe_start;
+  *stop = g_probe_stop;
+  g_probe_start = g_probe_stop = nullptr;
+}
+
 int fail(int code, const char* fmt, ...) {
   va_list ap;
   va_start(ap, fmt);
@@ -310,6 +321,14 @@ int axon_hip_event_record(void* event) {
   AXON_READY();
   const hipError_t e = hipEventRecord(static_cast<hipEvent_t>(event), g_stream);
   return e == hipSuccess ? kOk : hip_fail(e, "hipEventRecord");
+}
+
+int axon_hip_probe_next_launch(void* start, void* stop) {
+  AXON_READY();
+  if ((start == nullptr) != (stop == nullptr)) return fail(kInvalidArgument, "probe: both events or neither");
+  g_probe_start = static_cast<hipEvent_t>(start);
+  g_probe_stop = static_cast<hipEvent_t>(stop);
+  return kOk;
 }
 
 int axon_hip_event_elapsed_ms(void* start, void* stop, float* ms) {

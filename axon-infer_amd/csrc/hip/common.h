@@ -6,6 +6,7 @@
 #pragma once
 
 #include <hip/hip_runtime.h>
+#include <hip/hip_ext.h>
 
 #include <cstddef>
 #include <cstdint>
@@ -238,5 +239,22 @@ hipStream_t stream();
 int fail(int code, const char* fmt, ...);
 int check_launch(const char* what);
 inline size_t ceil_div(size_t a, size_t b) { return (a + b - 1) / b; }
+
+// Kernel-time probe: hands out (and clears) the event pair armed by axon_hip_probe_next_launch.
+void take_probe(hipEvent_t* start, hipEvent_t* stop);
+
+// Launches on the library stream. When a probe is armed, the launch goes through
+// hipExtLaunchKernel with the probe's events, which then carry the dispatch's own start and end
+// timestamps (the kernel duration a profiler reports, without the event packets' overhead).
+template <typename... Params, typename... Args>
+inline void launch(void (*kernel)(Params...), dim3 grid, dim3 block, size_t lds, Args... args) {
+  hipEvent_t start = nullptr, stop = nullptr;
+  take_probe(&start, &stop);
+  if (start != nullptr) {
+    hipExtLaunchKernelGGL(kernel, grid, block, static_cast<uint32_t>(lds), stream(), start, stop, 0u, args...);
+  } else {
+    hipLaunchKernelGGL(kernel, grid, block, lds, stream(), args...);
+  }
+}
 
 }  // namespace axon_hip

@@ -172,9 +172,9 @@ int matmul_q8_mfma_launch(int type, MatvecArgs& a) {
   const size_t lds = lds_of(kc);
   const dim3 grid(static_cast<uint32_t>(ceil_div(n_out, kTileN)), static_cast<uint32_t>(ceil_div(a.m, kTileM)));
   switch (type) {
-  case Q8_0: hipLaunchKernelGGL(mfma_q8_kernel<Q8_0>, grid, dim3(kThreads), lds, stream(), a, kc); break;
-  case Q4_0: hipLaunchKernelGGL(mfma_q8_kernel<Q4_0>, grid, dim3(kThreads), lds, stream(), a, kc); break;
-  case Q4_1: hipLaunchKernelGGL(mfma_q8_kernel<Q4_1>, grid, dim3(kThreads), lds, stream(), a, kc); break;
+  case Q8_0: launch(mfma_q8_kernel<Q8_0>, grid, dim3(kThreads), lds, a, kc); break;
+  case Q4_0: launch(mfma_q8_kernel<Q4_0>, grid, dim3(kThreads), lds, a, kc); break;
+  case Q4_1: launch(mfma_q8_kernel<Q4_1>, grid, dim3(kThreads), lds, a, kc); break;
   default: return fail(kUnsupported, "matmul rows: weight type %d has no Q8_0-activation path", type);
   }
   return check_launch("mfma_q8");

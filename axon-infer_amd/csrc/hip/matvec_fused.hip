@@ -360,9 +360,9 @@ int matvec_fused_launch(int type, FusedArgs& a) {
       }
       if (silu) a.wg_begin[1] = 0;
       switch (type) {
-      case Q8_0: hipLaunchKernelGGL(matvec_fused_kernel<Q8_0>, dim3(wg), dim3(kThreads), lds, stream(), a); break;
-      case Q4_0: hipLaunchKernelGGL(matvec_fused_kernel<Q4_0>, dim3(wg), dim3(kThreads), lds, stream(), a); break;
-      case Q4_1: hipLaunchKernelGGL(matvec_fused_kernel<Q4_1>, dim3(wg), dim3(kThreads), lds, stream(), a); break;
+      case Q8_0: launch(matvec_fused_kernel<Q8_0>, dim3(wg), dim3(kThreads), lds, a); break;
+      case Q4_0: launch(matvec_fused_kernel<Q4_0>, dim3(wg), dim3(kThreads), lds, a); break;
+      case Q4_1: launch(matvec_fused_kernel<Q4_1>, dim3(wg), dim3(kThreads), lds, a); break;
       default: return fail(kUnsupported, "matvec_fused: weight type %d", type);
       }
       return check_launch("matvec_fused");

@@ -145,10 +145,10 @@ int matvec_q6k_launch(MatvecArgs& a, uint32_t n_in) {
     g.seg[0].y = base.seg[0].y + static_cast<size_t>(done) * base.seg[0].y_stride;
     const dim3 grid(static_cast<uint32_t>(ceil_div(n_out, kThreads)));
     switch (mm) {
-    case 4: hipLaunchKernelGGL(matvec_q6k_kernel<4>, grid, dim3(kThreads), lds, stream(), g, n_in); break;
-    case 3: hipLaunchKernelGGL(matvec_q6k_kernel<3>, grid, dim3(kThreads), lds, stream(), g, n_in); break;
-    case 2: hipLaunchKernelGGL(matvec_q6k_kernel<2>, grid, dim3(kThreads), lds, stream(), g, n_in); break;
-    default: hipLaunchKernelGGL(matvec_q6k_kernel<1>, grid, dim3(kThreads), lds, stream(), g, n_in); break;
+    case 4: launch(matvec_q6k_kernel<4>, grid, dim3(kThreads), lds, g, n_in); break;
+    case 3: launch(matvec_q6k_kernel<3>, grid, dim3(kThreads), lds, g, n_in); break;
+    case 2: launch(matvec_q6k_kernel<2>, grid, dim3(kThreads), lds, g, n_in); break;
+    default: launch(matvec_q6k_kernel<1>, grid, dim3(kThreads), lds, g, n_in); break;
     }
     const int rc = check_launch("matvec_q6k");
     if (rc != kOk) return rc;

@@ -186,9 +186,9 @@ int block_sums_launch(int type, const void* w_row, const void* xq, uint32_t n_bl
   const uint8_t* w = static_cast<const uint8_t*>(w_row);
   const uint8_t* x = static_cast<const uint8_t*>(xq);
   switch (type) {
-  case Q8_0: hipLaunchKernelGGL(block_sums_kernel<Q8_0>, dim3(1), dim3(kThreads), lds, stream(), w, x, n_blocks, sumi, sumx); break;
-  case Q4_0: hipLaunchKernelGGL(block_sums_kernel<Q4_0>, dim3(1), dim3(kThreads), lds, stream(), w, x, n_blocks, sumi, sumx); break;
-  case Q4_1: hipLaunchKernelGGL(block_sums_kernel<Q4_1>, dim3(1), dim3(kThreads), lds, stream(), w, x, n_blocks, sumi, sumx); break;
+  case Q8_0: launch(block_sums_kernel<Q8_0>, dim3(1), dim3(kThreads), lds, w, x, n_blocks, sumi, sumx); break;
+  case Q4_0: launch(block_sums_kernel<Q4_0>, dim3(1), dim3(kThreads), lds, w, x, n_blocks, sumi, sumx); break;
+  case Q4_1: launch(block_sums_kernel<Q4_1>, dim3(1), dim3(kThreads), lds, w, x, n_blocks, sumi, sumx); break;
   default: return fail(kUnsupported, "block_sums: weight type %d", type);
   }
   return check_launch("block_sums");
@@ -244,13 +244,13 @@ int matvec_q8_launch(int type, MatvecArgs& a) {
       if (wg == 0) return kOk;
       switch (type) {
       case Q8_0:
-        hipLaunchKernelGGL(matvec_q8_kernel<Q8_0>, dim3(wg), dim3(kThreads), lds, stream(), a);
+        launch(matvec_q8_kernel<Q8_0>, dim3(wg), dim3(kThreads), lds, a);
         break;
       case Q4_0:
-        hipLaunchKernelGGL(matvec_q8_kernel<Q4_0>, dim3(wg), dim3(kThreads), lds, stream(), a);
+        launch(matvec_q8_kernel<Q4_0>, dim3(wg), dim3(kThreads), lds, a);
         break;
       case Q4_1:
-        hipLaunchKernelGGL(matvec_q8_kernel<Q4_1>, dim3(wg), dim3(kThreads), lds, stream(), a);
+        launch(matvec_q8_kernel<Q4_1>, dim3(wg), dim3(kThreads), lds, a);
         break;
       default:
         return fail(kUnsupported, "matvec: weight type %d has no Q8_0-activation path", type);

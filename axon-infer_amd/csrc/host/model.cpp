@@ -308,12 +308,12 @@ Expected<bool> LlamaModel::set_probe(int type, bool enable) {
 
 void LlamaModel::probe_begin(const Tensor& w) {
   if (static_cast<int>(w.type) != probe_type_ || 2 * probe_used_ + 2 > probe_events_.size()) return;
-  axon_hip_event_record(probe_events_[2 * probe_used_]);
+  axon_hip_probe_next_launch(probe_events_[2 * probe_used_], probe_events_[2 * probe_used_ + 1]);
 }
 
 void LlamaModel::probe_end(const Tensor& w, std::size_t n_rows, std::size_t n_out_total, bool accumulate) {
   if (static_cast<int>(w.type) != probe_type_ || 2 * probe_used_ + 2 > probe_events_.size()) return;
-  axon_hip_event_record(probe_events_[2 * probe_used_ + 1]);
+  axon_hip_probe_next_launch(nullptr, nullptr);
   const double in_bytes = q8_path(w) ? static_cast<double>(n_rows) * (w.ne0 / 32) * sizeof(BlockQ8_0)
                                      : static_cast<double>(n_rows) * w.ne0 * 4.0;
   const double out_bytes = static_cast<double>(n_rows) * n_out_total * 4.0 * (accumulate ? 2 : 1);

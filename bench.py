@@ -15,9 +15,12 @@ Two workloads, both greedy:
                forward_batch time (logits to the host and argmax included).
 
 The line also carries:
-  roofline     the Q4_0 x Q8_0 matvec kernel (the dominant kernel by time), from a probe pass of the
-               same decode-b1 steps with HIP events around every such launch on the library stream:
-               achieved = algorithmic bytes (weights + activation blocks + outputs) / device time.
+  roofline     the Q4_0 decode matvec kernel (matvec_fused_kernel<Q4_0>: q|k|v, wo, gate|up and
+               down of every layer; the dominant kernel by time), from a probe pass of the same
+               decode-b1 steps in which each such launch records its own dispatch start and end on
+               HIP events (hipExtLaunchKernel, on the library stream): achieved = algorithmic bytes
+               (weight rows + activations + outputs) / summed kernel time. The Q6_K output matvec
+               is probed the same way (roofline_q6_k).
   cpu_baseline the reference's own LlamaModel on its scalar table (oracle/_ref, compiled from the
                reference sources) on the same GGUF, threads = the host's cores, on a bounded sample.
 
@@ -258,7 +261,7 @@ def main() -> int:
                    "model": spec.name, "global_batch": 1, "seq_len": args.prompt, "parallelism": "none"},
         "hbm_gbs_per_step": round(step_bytes / (b1["ms_per_step"] * 1e-3) / 1e9, 1),
         "hbm_frac_per_step": round(step_bytes / (b1["ms_per_step"] * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
-        "roofline": {"bound": "hbm", "kernel": "matvec_q8_kernel<Q4_0> (Q4_0 x Q8_0 dot4 matvec)",
+        "roofline": {"bound": "hbm", "kernel": "matvec_fused_kernel<Q4_0> (decode matvec: q|k|v+rope, wo+add, gate|up+silu, down+add)",
                      "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
                      "launches": launches, "bytes_per_launch": round(nbytes / max(launches, 1)),

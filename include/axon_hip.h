@@ -68,6 +68,10 @@ int axon_hip_event_create(void** event);
 int axon_hip_event_record(void* event);
 int axon_hip_event_elapsed_ms(void* start, void* stop, float* ms);
 int axon_hip_event_destroy(void* event);
+/* Measurement only: the next matmul kernel launched on this thread records its own start and end
+ * on these events (hipExtLaunchKernel), so their elapsed time is the kernel's duration as a
+ * profiler reports it. Both NULL disarms. */
+int axon_hip_probe_next_launch(void* start, void* stop);
 /* Captures the entries called between begin and end into a replayable graph. */
 int axon_hip_graph_begin(void);
 int axon_hip_graph_end(void** graph);

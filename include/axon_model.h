@@ -59,9 +59,10 @@ int axon_model_forward(axon_model* model, const int32_t* tokens, size_t n, float
 int axon_model_forward_prefill(axon_model* model, int cache, const int32_t* tokens, size_t n, float* logits);
 int axon_model_forward_batch(axon_model* model, const int* caches, const int32_t* tokens, size_t n, float* logits);
 
-/* Kernel-time probe (measurement only): while enabled, every matmul launch on weights of ggml
- * type `type` is bracketed by HIP events on the library stream; probe_read returns the summed
- * device milliseconds, the launch count and the launches' algorithmic bytes, and resets. */
+/* Kernel-time probe (measurement only): while enabled, the kernel of every matmul on weights of
+ * ggml type `type` records its dispatch's start and end on HIP events (axon_hip_probe_next_launch);
+ * probe_read returns the summed kernel milliseconds, the launch count and the launches'
+ * algorithmic bytes, and resets. */
 int axon_model_probe(axon_model* model, int type, int enable);
 int axon_model_probe_read(axon_model* model, double* ms, size_t* launches, double* bytes);
 
