@@ -233,6 +233,123 @@ __device__ __forceinline__ void quantize_block_lanes(float x, uint32_t lane, uin
 }
 
 // ------------------------------------------------------------------------------------------
+// Whole-row work for one 256-thread workgroup, shared by the standalone kernels and the fused
+// matvec's prologue, so that both produce the same bits.
+
+// Sum over the 256 threads of a workgroup in a fixed order: the wave butterfly, then the four
+// waves in order. red: 4 doubles of LDS. Every thread gets the sum.
+__device__ __forceinline__ double block_sum_double_256(double v, double* red) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+  __syncthreads();
+  double s = 0.0;
+#pragma unroll
+  for (int w = 0; w < 4; ++w) s += red[w];
+  __syncthreads();
+  return s;
+}
+
+// Quantizes the 8 consecutive floats v of this thread, one quarter of a 32-element block whose
+// other quarters sit in the 3 adjacent lanes (part = lane & 3), as quantize_row_q8_0 does: the
+// thread's 8 quants go to blk + 2 + 8 * part, part 0 also writes the fp16 scale. active:
+// whether this thread's elements exist (the shuffles still need every lane).
+__device__ __forceinline__ void quantize8_store(const float (&v)[8], bool active, uint8_t* blk, uint32_t part) {
+  float amax = 0.0f;
+#pragma unroll
+  for (int k = 0; k < 8; ++k) amax = fmaxf(amax, fabsf(v[k]));
+  amax = fmaxf(amax, __shfl_xor(amax, 1, 64));
+  amax = fmaxf(amax, __shfl_xor(amax, 2, 64));
+  if (!active) return;
+  const float d = amax / 127.0f;
+  const float id = d != 0.0f ? 1.0f / d : 0.0f;
+  uint32_t q[8];
+#pragma unroll
+  for (int k = 0; k < 8; ++k) q[k] = static_cast<uint32_t>(static_cast<int32_t>(roundf(v[k] * id))) & 0xffu;
+  if (part == 0) *reinterpret_cast<uint16_t*>(blk) = static_cast<uint16_t>(float_to_half_bits(d));
+  uint16_t* qs = reinterpret_cast<uint16_t*>(blk + 2 + 8 * part);
+#pragma unroll
+  for (int k = 0; k < 4; ++k) qs[k] = static_cast<uint16_t>(q[2 * k] | (q[2 * k + 1] << 8));
+}
+
+// rmsnorm (src/kernels/ref/rmsnorm.cpp:10-21) of one row of n <= 2048 floats (n % 32 == 0;
+// x, w, y 16-byte aligned) by a 256-thread workgroup: thread t holds elements 8t..8t+7 in
+// registers; y = x * inv * w (or not stored when y is null) and its Q8_0 blocks into yq (or
+// not when null).
+__device__ __forceinline__ void rmsnorm_row_256(const float* xr, const float* w, float* yr, uint8_t* yq, uint32_t n,
+                                                float eps, double* red) {
+  const uint32_t e0 = threadIdx.x * 8;
+  const bool has = e0 < n;
+  float xv[8], wv[8];
+  if (has) {
+    const float4 a = *reinterpret_cast<const float4*>(xr + e0);
+    const float4 b = *reinterpret_cast<const float4*>(xr + e0 + 4);
+    const float4 c = *reinterpret_cast<const float4*>(w + e0);
+    const float4 d = *reinterpret_cast<const float4*>(w + e0 + 4);
+    xv[0] = a.x; xv[1] = a.y; xv[2] = a.z; xv[3] = a.w; xv[4] = b.x; xv[5] = b.y; xv[6] = b.z; xv[7] = b.w;
+    wv[0] = c.x; wv[1] = c.y; wv[2] = c.z; wv[3] = c.w; wv[4] = d.x; wv[5] = d.y; wv[6] = d.z; wv[7] = d.w;
+  } else {
+#pragma unroll
+    for (int k = 0; k < 8; ++k) xv[k] = wv[k] = 0.0f;
+  }
+  double ss = 0.0;
+#pragma unroll
+  for (int k = 0; k < 8; ++k) {
+    const double v = static_cast<double>(xv[k]);
+    ss += v * v;
+  }
+  ss = block_sum_double_256(ss, red);
+  const float inv = static_cast<float>(1.0 / sqrt(ss / static_cast<double>(n) + static_cast<double>(eps)));
+  float v[8];
+#pragma unroll
+  for (int k = 0; k < 8; ++k) v[k] = xv[k] * inv * wv[k];
+  if (yr != nullptr && has) {
+    *reinterpret_cast<float4*>(yr + e0) = make_float4(v[0], v[1], v[2], v[3]);
+    *reinterpret_cast<float4*>(yr + e0 + 4) = make_float4(v[4], v[5], v[6], v[7]);
+  }
+  if (yq != nullptr) quantize8_store(v, has, yq + (e0 / kQK) * kBytesQ8_0, threadIdx.x & 3);
+}
+
+// ------------------------------------------------------------------------------------------
+// LDS-DMA: global memory straight into LDS without passing through registers.
+
+using LdsPtr = __attribute__((address_space(3))) void*;
+// A generic pointer into a __shared__ object as an LDS address.
+__device__ __forceinline__ LdsPtr as_lds(const void* p) { return (LdsPtr)(const_cast<void*>(p)); }
+constexpr uint32_t kRawBufferWord3 = 0x00020000u;  // gfx9 raw buffer descriptor: 32-bit data
+
+// Copies `bytes` from global src to LDS dst with buffer loads that write LDS directly: 16-byte
+// units when src, dst and bytes are multiples of 16, else 4-byte units (all three must be
+// multiples of 4). Threads [0, nthreads) of the block take part in whole waves (tid and
+// nthreads multiples of 64 at wave starts). The copies complete asynchronously: s_waitcnt
+// vmcnt(0) on every copying wave, then a barrier, before anyone reads dst.
+__device__ __forceinline__ void dma_to_lds(const uint8_t* src, uint8_t* dst, uint32_t bytes, uint32_t tid,
+                                           uint32_t nthreads) {
+  const __amdgpu_buffer_rsrc_t rsrc = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<uint8_t*>(src), 0, static_cast<int>(bytes), static_cast<int>(kRawBufferWord3));
+  const uint32_t lane = tid & 63u;
+  const uint32_t wave0 = tid & ~63u;
+  if (((reinterpret_cast<uintptr_t>(src) | reinterpret_cast<uintptr_t>(dst) | bytes) & 15u) == 0) {
+    const uint32_t units = bytes >> 4;
+    for (uint32_t base = wave0; base < units; base += nthreads) {
+      if (base + lane < units) {
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, as_lds(dst + base * 16u), 16, (base + lane) * 16u, 0, 0, 0);
+      }
+    }
+  } else {
+    const uint32_t units = bytes >> 2;
+    for (uint32_t base = wave0; base < units; base += nthreads) {
+      if (base + lane < units) {
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, as_lds(dst + base * 4u), 4, (base + lane) * 4u, 0, 0, 0);
+      }
+    }
+  }
+}
+
+// Waits for every outstanding memory operation of this wave, LDS-DMA copies included.
+__device__ __forceinline__ void wait_memory() { __builtin_amdgcn_s_waitcnt(0); }
+
+// ------------------------------------------------------------------------------------------
 // Host-side plumbing shared by the translation units.
 
 hipStream_t stream();

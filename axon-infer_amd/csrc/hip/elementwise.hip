@@ -58,58 +58,9 @@ __global__ __launch_bounds__(256) void rmsnorm_regs_kernel(const float* __restri
                                                            float* __restrict__ y, uint8_t* __restrict__ yq,
                                                            uint32_t n, float eps) {
   __shared__ double red[4];
-  const uint32_t row = blockIdx.x;
-  const uint32_t e0 = threadIdx.x * 8;
-  const bool has = e0 < n;
-  const float* xr = x + static_cast<size_t>(row) * n;
-  float xv[8], wv[8];
-  if (has) {
-    const float4 a = *reinterpret_cast<const float4*>(xr + e0);
-    const float4 b = *reinterpret_cast<const float4*>(xr + e0 + 4);
-    const float4 c = *reinterpret_cast<const float4*>(w + e0);
-    const float4 d = *reinterpret_cast<const float4*>(w + e0 + 4);
-    xv[0] = a.x; xv[1] = a.y; xv[2] = a.z; xv[3] = a.w; xv[4] = b.x; xv[5] = b.y; xv[6] = b.z; xv[7] = b.w;
-    wv[0] = c.x; wv[1] = c.y; wv[2] = c.z; wv[3] = c.w; wv[4] = d.x; wv[5] = d.y; wv[6] = d.z; wv[7] = d.w;
-  } else {
-#pragma unroll
-    for (int k = 0; k < 8; ++k) xv[k] = wv[k] = 0.0f;
-  }
-  double ss = 0.0;
-#pragma unroll
-  for (int k = 0; k < 8; ++k) {
-    const double v = static_cast<double>(xv[k]);
-    ss += v * v;
-  }
-  ss = block_sum_double(ss, red);
-  const float inv = static_cast<float>(1.0 / sqrt(ss / static_cast<double>(n) + static_cast<double>(eps)));
-  float v[8];
-  float amax = 0.0f;
-#pragma unroll
-  for (int k = 0; k < 8; ++k) {
-    v[k] = xv[k] * inv * wv[k];
-    amax = fmaxf(amax, fabsf(v[k]));
-  }
-  if (y != nullptr && has) {
-    float* yr = y + static_cast<size_t>(row) * n + e0;
-    *reinterpret_cast<float4*>(yr) = make_float4(v[0], v[1], v[2], v[3]);
-    *reinterpret_cast<float4*>(yr + 4) = make_float4(v[4], v[5], v[6], v[7]);
-  }
-  if (yq == nullptr) return;
-  // The block's 4 threads are adjacent lanes.
-  amax = fmaxf(amax, __shfl_xor(amax, 1, 64));
-  amax = fmaxf(amax, __shfl_xor(amax, 2, 64));
-  if (!has) return;
-  const float d = amax / 127.0f;
-  const float id = d != 0.0f ? 1.0f / d : 0.0f;
-  uint8_t* blk = yq + (static_cast<size_t>(row) * (n / kQK) + e0 / kQK) * kBytesQ8_0;
-  const uint32_t part = threadIdx.x & 3;
-  uint32_t q[8];
-#pragma unroll
-  for (int k = 0; k < 8; ++k) q[k] = static_cast<uint32_t>(static_cast<int32_t>(roundf(v[k] * id))) & 0xffu;
-  if (part == 0) *reinterpret_cast<uint16_t*>(blk) = static_cast<uint16_t>(float_to_half_bits(d));
-  uint16_t* qs = reinterpret_cast<uint16_t*>(blk + 2 + 8 * part);
-#pragma unroll
-  for (int k = 0; k < 4; ++k) qs[k] = static_cast<uint16_t>(q[2 * k] | (q[2 * k + 1] << 8));
+  const size_t row = blockIdx.x;
+  rmsnorm_row_256(x + row * n, w, y != nullptr ? y + row * n : nullptr,
+                  yq != nullptr ? yq + row * (n / kQK) * kBytesQ8_0 : nullptr, n, eps, red);
 }
 
 __global__ __launch_bounds__(256) void rmsnorm_kernel(const float* __restrict__ x, const float* __restrict__ w,

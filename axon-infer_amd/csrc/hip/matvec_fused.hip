@@ -1,12 +1,16 @@
 // The decode matvec with its neighbours folded in: one launch per weight group of a layer for
 // one to four activation rows (batch-1 and small-batch decode).
 //
-// Prologue (input), per workgroup, identical in every workgroup:
-//   kInQ8    the activation rows arrive as Q8_0 blocks (as matvec_q8.hip);
-//   kInF32   float rows, quantized here exactly as quantize_row_q8_0
+// Input:
+//   kInQ8    the activation rows arrive as Q8_0 blocks;
+//   kInF32   float rows, quantized in every workgroup exactly as quantize_row_q8_0
 //            (trickymind1324/axon-infer src/core/dtype.cpp:338-354);
 //   kInNorm  float rows, RMSNorm'd (src/kernels/ref/rmsnorm.cpp:10-21) then quantized, as
 //            src/model/llama.cpp:500 and 598 do before the q|k|v and gate|up matmuls.
+// matvec_dma_kernel copies the weight rows (and Q8_0 blocks) straight into LDS with LDS-DMA
+// buffer loads: no staging registers, so many workgroups stay resident, every copy of the
+// launch is in flight at once, and the float prologue runs while the weights arrive.
+// matvec_fused_kernel stages through registers for rows that are not 4-byte multiples.
 // Body: the integer-exact block dots and the left-to-right float accumulation of
 // matvec_q8.hip (src/kernels/ref/quant.cpp:44-69, 161-181).
 // Epilogue (output):
@@ -17,8 +21,8 @@
 //                         rotation of pairs (2i, 2i+1) with host-built cos/sin
 //                         (src/kernels/ref/rope.cpp:13-37), q to its buffer, k and v into the
 //                         row's KV cache at its position (llama.cpp:493-497, 520-537).
-// Every workgroup recomputes the row norm and the Q8_0 blocks with the same reduction tree as
-// rmsnorm_regs_kernel, so all of them and the standalone kernels agree bit for bit.
+// The float prologues recompute the row norm and the Q8_0 blocks in every workgroup with the
+// same reduction tree as rmsnorm_regs_kernel, so all paths agree bit for bit.
 #include "common.h"
 #include "matvec.h"
 
@@ -109,136 +113,58 @@ __device__ __forceinline__ void quantize8_to_act(const float (&v)[8], uint32_t p
   }
 }
 
+// Where a workgroup's weight rows are. The SiLU pairing runs gate and up rows together: up
+// row r sits at tile row pitch_rows + r.
+struct WgRows {
+  int s;
+  uint32_t r0, nr, n_wrows, pitch_rows;
+  bool silu;
+};
+
+__device__ __forceinline__ WgRows wg_rows(const FusedArgs& args) {
+  WgRows g;
+  g.silu = args.out_mode == kOutSilu;
+  const uint32_t wg = blockIdx.x;
+  g.s = 0;
+  if (!g.silu && args.n_seg > 1 && wg >= args.wg_begin[1]) g.s = 1;
+  if (!g.silu && args.n_seg > 2 && wg >= args.wg_begin[2]) g.s = 2;
+  g.r0 = (wg - args.wg_begin[g.s]) * args.rows;
+  g.nr = min(args.rows, args.n_out[g.s] - g.r0);
+  g.n_wrows = g.silu ? 2 * g.nr : g.nr;
+  g.pitch_rows = g.silu ? args.rows : 0;
+  return g;
+}
+
+// Block terms, ordered chains and the epilogue, once the weight tile and the activation blocks
+// are in LDS. Reuses the tile for the chain results.
 template <int T>
-__global__ __launch_bounds__(kThreads) void matvec_fused_kernel(FusedArgs args) {
-  extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
-  __shared__ double red[kThreads / 64];
+__device__ __forceinline__ void fused_body(const FusedArgs& args, const WgRows& g, uint8_t* tile, const ActBlock* act,
+                                           float* terms) {
   constexpr int bs = wbytes<T>();
   const uint32_t tid = threadIdx.x;
   const uint32_t nb = args.nb;
-  const uint32_t n_in = nb * kQK;
   const uint32_t M = args.m;
   const uint32_t R = args.rows;
   const uint32_t row_bytes = nb * bs;
-  const bool silu = args.out_mode == kOutSilu;
-
-  // Segment and rows of this workgroup. The SiLU pairing runs gate and up rows together.
-  uint32_t wg = blockIdx.x;
-  int s = 0;
-  if (!silu && args.n_seg > 1 && wg >= args.wg_begin[1]) s = 1;
-  if (!silu && args.n_seg > 2 && wg >= args.wg_begin[2]) s = 2;
-  const uint32_t r0 = (wg - args.wg_begin[s]) * R;
-  const uint32_t nr = min(R, args.n_out[s] - r0);
-  const uint32_t n_wrows = silu ? 2 * nr : nr;  // weight rows staged
-  const uint32_t pitch_rows = silu ? R : 0;     // tile row of up row r is pitch_rows + r
-
-  ActBlock* act = reinterpret_cast<ActBlock*>(smem);
-  uint8_t* tile = smem + args.lds_tile;
-  float* terms = reinterpret_cast<float*>(smem + args.lds_scratch);
-  uint8_t* raw = smem + args.lds_scratch;
   const uint32_t tpitch = nb + 1;
-
-  // ---- float activations: this thread's 8-element chunks, loaded before the weight tile ----
-  // Thread t owns chunk c = t + 256 k (elements 8c .. 8c + 7) of every row; kMaxChunks bounds
-  // rows x chunks per thread (checked by the launcher).
-  const uint32_t n_chunks = n_in / 8;
-  const uint32_t cpt = (n_chunks + kThreads - 1) / kThreads;  // chunks per thread and row
-  float xv[kMaxChunks][8];
-  float wv[kMaxChunks][8];
-  if (args.in_mode != kInQ8) {
-#pragma unroll
-    for (int i = 0; i < kMaxChunks; ++i) {
-      const uint32_t m = i / cpt;
-      const uint32_t c = tid + (i - m * cpt) * kThreads;
-      if (m < M && c < n_chunks) {
-        const float4* xr = reinterpret_cast<const float4*>(args.x + static_cast<size_t>(m) * args.x_stride + c * 8);
-        const float4 a = xr[0], b = xr[1];
-        xv[i][0] = a.x; xv[i][1] = a.y; xv[i][2] = a.z; xv[i][3] = a.w;
-        xv[i][4] = b.x; xv[i][5] = b.y; xv[i][6] = b.z; xv[i][7] = b.w;
-        if (args.in_mode == kInNorm) {
-          const float4* wr = reinterpret_cast<const float4*>(args.norm_w + c * 8);
-          const float4 e = wr[0], f = wr[1];
-          wv[i][0] = e.x; wv[i][1] = e.y; wv[i][2] = e.z; wv[i][3] = e.w;
-          wv[i][4] = f.x; wv[i][5] = f.y; wv[i][6] = f.z; wv[i][7] = f.w;
-        }
-      }
-    }
-  }
-
-  // ---- weight tile (and Q8_0 activation blocks) into LDS ------------------------------------
-  const uint32_t xthreads = args.in_mode == kInQ8 ? 64u : 0u;
-  if (tid >= xthreads) {
-    stage_bytes(args.w[s] + static_cast<size_t>(r0) * row_bytes, tile, nr * row_bytes, tid - xthreads,
-                kThreads - xthreads);
-    if (silu) {
-      stage_bytes(args.w[1] + static_cast<size_t>(r0) * row_bytes, tile + static_cast<size_t>(pitch_rows) * row_bytes,
-                  nr * row_bytes, tid - xthreads, kThreads - xthreads);
-    }
-  } else {
-    stage_bytes(args.xq, raw, M * nb * kBytesQ8_0, tid, xthreads);
-  }
-
-  // ---- activation prologue ------------------------------------------------------------------
-  if (args.in_mode == kInQ8) {
-    __syncthreads();
-    for (uint32_t i = tid; i < M * nb; i += kThreads) act[i] = unpack_q8_0_lds(raw, i * kBytesQ8_0);
-  } else {
-    const uint32_t part = tid & 3;
-    for (uint32_t m = 0; m < M; ++m) {
-      float inv = 1.0f;
-      if (args.in_mode == kInNorm) {
-        // The sum of squares in double with rmsnorm_regs_kernel's tree: 8 elements per thread
-        // in order, then the wave butterfly, then the waves in order (one chunk per thread).
-        double ss = 0.0;
-#pragma unroll
-        for (int i = 0; i < kMaxChunks; ++i) {
-          if (i / cpt == m && tid + (i - m * cpt) * kThreads < n_chunks) {
-#pragma unroll
-            for (int k = 0; k < 8; ++k) {
-              const double v = static_cast<double>(xv[i][k]);
-              ss += v * v;
-            }
-          }
-        }
-#pragma unroll
-        for (int off = 32; off > 0; off >>= 1) ss += __shfl_xor(ss, off, 64);
-        if ((tid & 63) == 0) red[tid >> 6] = ss;
-        __syncthreads();
-        ss = 0.0;
-        for (int w = 0; w < kThreads / 64; ++w) ss += red[w];
-        __syncthreads();
-        inv = static_cast<float>(1.0 / sqrt(ss / static_cast<double>(n_in) + static_cast<double>(args.eps)));
-      }
-#pragma unroll
-      for (int i = 0; i < kMaxChunks; ++i) {
-        const uint32_t c = tid + (i - m * cpt) * kThreads;
-        if (i / cpt == m && c < n_chunks) {
-          float v[8];
-#pragma unroll
-          for (int k = 0; k < 8; ++k) v[k] = args.in_mode == kInNorm ? xv[i][k] * inv * wv[i][k] : xv[i][k];
-          quantize8_to_act(v, part, act[m * nb + c / 4]);
-        }
-      }
-    }
-  }
-  __syncthreads();
-
-  // ---- body: block terms, then the ordered chains --------------------------------------------
-  const uint32_t pairs = n_wrows * nb;
+  const uint32_t nr = g.nr;
+  const int s = g.s;
+  const uint32_t r0 = g.r0;
+  const uint32_t pairs = g.n_wrows * nb;
   for (uint32_t p = tid; p < pairs; p += kThreads) {
     const uint32_t r = p / nb;
     const uint32_t b = p - r * nb;
-    const uint32_t trow = (silu && r >= nr) ? pitch_rows + (r - nr) : r;
+    const uint32_t trow = (g.silu && r >= nr) ? g.pitch_rows + (r - nr) : r;
     for (uint32_t m = 0; m < M; ++m) {
       terms[(m * 2 * R + trow) * tpitch + b] = fused_term<T>(tile, trow * row_bytes + b * bs, act[m * nb + b]);
     }
   }
   __syncthreads();
   float* outv = reinterpret_cast<float*>(tile);  // [M][2R], the tile is no longer needed
-  if (tid < M * n_wrows) {
-    const uint32_t m = tid / n_wrows;
-    const uint32_t r = tid - m * n_wrows;
-    const uint32_t trow = (silu && r >= nr) ? pitch_rows + (r - nr) : r;
+  if (tid < M * g.n_wrows) {
+    const uint32_t m = tid / g.n_wrows;
+    const uint32_t r = tid - m * g.n_wrows;
+    const uint32_t trow = (g.silu && r >= nr) ? g.pitch_rows + (r - nr) : r;
     const float* t = terms + (m * 2 * R + trow) * tpitch;
     float acc = 0.0f;
     for (uint32_t b = 0; b < nb; ++b) acc += t[b];
@@ -246,7 +172,6 @@ __global__ __launch_bounds__(kThreads) void matvec_fused_kernel(FusedArgs args) 
   }
   __syncthreads();
 
-  // ---- epilogue -----------------------------------------------------------------------------
   if (args.out_mode == kOutStore || args.out_mode == kOutAdd) {
     if (tid < M * nr) {
       const uint32_t m = tid / nr;
@@ -255,13 +180,13 @@ __global__ __launch_bounds__(kThreads) void matvec_fused_kernel(FusedArgs args) 
       float* y = args.y[s] + static_cast<size_t>(m) * args.y_stride[s] + r0 + r;
       *y = args.out_mode == kOutAdd ? *y + acc : acc;
     }
-  } else if (silu) {
+  } else if (g.silu) {
     if (tid < M * nr) {
       const uint32_t m = tid / nr;
       const uint32_t r = tid - m * nr;
-      const float g = outv[m * 2 * R + r];
-      const float u = outv[m * 2 * R + pitch_rows + r];
-      args.y[0][static_cast<size_t>(m) * args.y_stride[0] + r0 + r] = g / (1.0f + exp_rounded(-g)) * u;
+      const float gt = outv[m * 2 * R + r];
+      const float u = outv[m * 2 * R + g.pitch_rows + r];
+      args.y[0][static_cast<size_t>(m) * args.y_stride[0] + r0 + r] = gt / (1.0f + exp_rounded(-gt)) * u;
     }
   } else {
     // kOutRope: one thread per (row, pair of outputs).
@@ -301,6 +226,131 @@ __global__ __launch_bounds__(kThreads) void matvec_fused_kernel(FusedArgs args) 
   }
 }
 
+// The float prologue, row by row: thread t loads chunks c = t + 256 k (elements 8c .. 8c + 7)
+// of the row (at most kMaxChunks per thread, checked by the launcher), RMSNorm's them
+// (kInNorm, one chunk per thread) with rmsnorm_row_256's reduction tree and quantizes them
+// into act.
+__device__ __forceinline__ void float_prologue(const FusedArgs& args, ActBlock* act, double* red) {
+  const uint32_t tid = threadIdx.x;
+  const uint32_t nb = args.nb;
+  const uint32_t n_in = nb * kQK;
+  const uint32_t n_chunks = n_in / 8;
+  const uint32_t part = tid & 3;
+  const bool norm = args.in_mode == kInNorm;
+  for (uint32_t m = 0; m < args.m; ++m) {
+    float xv[kMaxChunks][8];
+    float wv[8];
+    const float* xr = args.x + static_cast<size_t>(m) * args.x_stride;
+#pragma unroll
+    for (int i = 0; i < kMaxChunks; ++i) {
+      const uint32_t c = tid + i * kThreads;
+      if (c < n_chunks) {
+        const float4 a = reinterpret_cast<const float4*>(xr + c * 8)[0];
+        const float4 b = reinterpret_cast<const float4*>(xr + c * 8)[1];
+        xv[i][0] = a.x; xv[i][1] = a.y; xv[i][2] = a.z; xv[i][3] = a.w;
+        xv[i][4] = b.x; xv[i][5] = b.y; xv[i][6] = b.z; xv[i][7] = b.w;
+      }
+    }
+    float inv = 1.0f;
+    if (norm) {
+      // One chunk per thread: the sum of squares in double with rmsnorm_row_256's tree (8
+      // elements per thread in order, the wave butterfly, the waves in order).
+      const bool has = tid < n_chunks;
+      double ss = 0.0;
+      if (has) {
+        const float4 e = reinterpret_cast<const float4*>(args.norm_w + tid * 8)[0];
+        const float4 f = reinterpret_cast<const float4*>(args.norm_w + tid * 8)[1];
+        wv[0] = e.x; wv[1] = e.y; wv[2] = e.z; wv[3] = e.w; wv[4] = f.x; wv[5] = f.y; wv[6] = f.z; wv[7] = f.w;
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+          const double v = static_cast<double>(xv[0][k]);
+          ss += v * v;
+        }
+      }
+      ss = block_sum_double_256(ss, red);
+      inv = static_cast<float>(1.0 / sqrt(ss / static_cast<double>(n_in) + static_cast<double>(args.eps)));
+    }
+#pragma unroll
+    for (int i = 0; i < kMaxChunks; ++i) {
+      const uint32_t c = tid + i * kThreads;
+      if (c < n_chunks) {
+        float v[8];
+#pragma unroll
+        for (int k = 0; k < 8; ++k) v[k] = norm ? xv[0][k] * inv * wv[k] : xv[i][k];
+        quantize8_to_act(v, part, act[m * nb + c / 4]);
+      }
+    }
+  }
+}
+
+// Rows of a multiple of 4 bytes: the weight rows and Q8_0 blocks go straight into LDS by DMA;
+// a float prologue runs while they arrive.
+template <int T>
+__global__ __launch_bounds__(kThreads) void matvec_dma_kernel(FusedArgs args) {
+  extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+  __shared__ double red[kThreads / 64];
+  constexpr int bs = wbytes<T>();
+  const uint32_t tid = threadIdx.x;
+  const WgRows g = wg_rows(args);
+  const uint32_t row_bytes = args.nb * bs;
+  ActBlock* act = reinterpret_cast<ActBlock*>(smem);
+  uint8_t* tile = smem + args.lds_tile;
+  uint8_t* raw = smem + args.lds_scratch;
+  dma_to_lds(args.w[g.s] + static_cast<size_t>(g.r0) * row_bytes, tile, g.nr * row_bytes, tid, kThreads);
+  if (g.silu) {
+    dma_to_lds(args.w[1] + static_cast<size_t>(g.r0) * row_bytes, tile + static_cast<size_t>(g.pitch_rows) * row_bytes,
+               g.nr * row_bytes, tid, kThreads);
+  }
+  if (args.in_mode == kInQ8) {
+    dma_to_lds(args.xq, raw, args.m * args.nb * kBytesQ8_0, tid, kThreads);
+  } else {
+    float_prologue(args, act, red);
+  }
+  wait_memory();
+  __syncthreads();
+  if (args.in_mode == kInQ8) {
+    for (uint32_t i = tid; i < args.m * args.nb; i += kThreads) act[i] = unpack_q8_0_lds(raw, i * kBytesQ8_0);
+    __syncthreads();
+  }
+  fused_body<T>(args, g, tile, act, reinterpret_cast<float*>(raw));
+}
+
+// Rows of any even byte count: the same with the weights staged through registers.
+template <int T>
+__global__ __launch_bounds__(kThreads) void matvec_fused_kernel(FusedArgs args) {
+  extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+  __shared__ double red[kThreads / 64];
+  constexpr int bs = wbytes<T>();
+  const uint32_t tid = threadIdx.x;
+  const uint32_t nb = args.nb;
+  const uint32_t M = args.m;
+  const uint32_t row_bytes = nb * bs;
+  const WgRows g = wg_rows(args);
+  ActBlock* act = reinterpret_cast<ActBlock*>(smem);
+  uint8_t* tile = smem + args.lds_tile;
+  uint8_t* raw = smem + args.lds_scratch;
+  const uint32_t xthreads = args.in_mode == kInQ8 ? 64u : 0u;
+  if (tid >= xthreads) {
+    stage_bytes(args.w[g.s] + static_cast<size_t>(g.r0) * row_bytes, tile, g.nr * row_bytes, tid - xthreads,
+                kThreads - xthreads);
+    if (g.silu) {
+      stage_bytes(args.w[1] + static_cast<size_t>(g.r0) * row_bytes,
+                  tile + static_cast<size_t>(g.pitch_rows) * row_bytes, g.nr * row_bytes, tid - xthreads,
+                  kThreads - xthreads);
+    }
+  } else {
+    stage_bytes(args.xq, raw, M * nb * kBytesQ8_0, tid, xthreads);
+  }
+  if (args.in_mode == kInQ8) {
+    __syncthreads();
+    for (uint32_t i = tid; i < M * nb; i += kThreads) act[i] = unpack_q8_0_lds(raw, i * kBytesQ8_0);
+  } else {
+    float_prologue(args, act, red);
+  }
+  __syncthreads();
+  fused_body<T>(args, g, tile, act, reinterpret_cast<float*>(raw));
+}
+
 size_t fused_lds(int bs, uint32_t m, uint32_t nb, uint32_t rows, bool silu, size_t* act_out, size_t* tile_out) {
   const size_t row_bytes = static_cast<size_t>(nb) * bs;
   const uint32_t wrows = silu ? 2 * rows : rows;
@@ -318,11 +368,11 @@ size_t fused_lds(int bs, uint32_t m, uint32_t nb, uint32_t rows, bool silu, size
 bool matvec_fused_fits(int type, int in_mode, uint32_t m, uint32_t nb, bool silu) {
   const int bs = type == Q8_0 ? kBytesQ8_0 : type == Q4_0 ? kBytesQ4_0 : kBytesQ4_1;
   size_t act, tile;
-  if (m < 1 || m > 4 || fused_lds(bs, m, nb, silu ? 1 : 2, silu, &act, &tile) > 65536) return false;
+  if (m < 1 || m > 4 || fused_lds(bs, m, nb, silu ? 1 : 2, silu, &act, &tile) > 65536 - 256) return false;
   if (in_mode == kInQ8) return true;
   const uint32_t cpt = ceil_div(nb * kQK / 8, kThreads);
-  // The norm prologue reproduces rmsnorm_regs_kernel's reduction only with one chunk per thread.
-  return m * cpt <= kMaxChunks && (in_mode != kInNorm || cpt == 1);
+  // The norm prologue reproduces rmsnorm_row_256's reduction only with one chunk per thread.
+  return cpt <= kMaxChunks && (in_mode != kInNorm || cpt == 1);
 }
 
 int matvec_fused_launch(int type, FusedArgs& a) {
@@ -340,16 +390,25 @@ int matvec_fused_launch(int type, FusedArgs& a) {
     return fail(kInvalidArgument, "matvec_fused: q|k|v rope epilogue shapes");
   const int bs = type == Q8_0 ? kBytesQ8_0 : type == Q4_0 ? kBytesQ4_0 : kBytesQ4_1;
   const size_t row_bytes = static_cast<size_t>(a.nb) * bs;
+  // LDS-DMA needs 4-byte multiples for every copy: the rows, the weight bases and the blocks.
+  uintptr_t bases = a.in_mode == kInQ8 ? reinterpret_cast<uintptr_t>(a.xq) : 0u;
+  for (int s = 0; s < a.n_seg; ++s) bases |= reinterpret_cast<uintptr_t>(a.w[s]);
+  const bool dma = row_bytes % 4 == 0 && (bases & 3u) == 0 &&
+                   (a.in_mode != kInQ8 || (static_cast<size_t>(a.m) * a.nb * kBytesQ8_0) % 4 == 0);
   uint32_t total_out = 0;
   for (int s = 0; s < (silu ? 1 : a.n_seg); ++s) total_out += a.n_out[s];
-  uint32_t rows = static_cast<uint32_t>(std::max<size_t>(1, (silu ? 8192 : 16384) / row_bytes));
+  // About 20 KB of weights per workgroup: under a thousand workgroups for the largest decode
+  // matrices (all resident at once), at least 512 for the smallest (below).
+  const size_t tile_target = dma ? (silu ? 10240 : 20480) : (silu ? 8192 : 16384);
+  uint32_t rows = static_cast<uint32_t>(std::max<size_t>(1, tile_target / row_bytes));
   rows = std::min<uint32_t>(rows, std::max<uint32_t>(1, total_out / 512));
   rows = std::min<uint32_t>(rows, (silu ? 128 : 256) / a.m);
   if (rope) rows = std::max<uint32_t>(2, rows & ~1u);
+  constexpr size_t kLdsLimit = 65536 - 256;  // the kernels' static LDS sits beside the dynamic part
   for (;;) {
     size_t act = 0, tile = 0;
     const size_t lds = fused_lds(bs, a.m, a.nb, rows, silu, &act, &tile);
-    if (lds <= 65536) {
+    if (lds <= kLdsLimit) {
       a.rows = rows;
       a.lds_tile = static_cast<uint32_t>(act);
       a.lds_scratch = static_cast<uint32_t>(act + tile);
@@ -359,11 +418,20 @@ int matvec_fused_launch(int type, FusedArgs& a) {
         if (!silu || s == 0) wg += static_cast<uint32_t>(ceil_div(a.n_out[s], rows));
       }
       if (silu) a.wg_begin[1] = 0;
-      switch (type) {
-      case Q8_0: launch(matvec_fused_kernel<Q8_0>, dim3(wg), dim3(kThreads), lds, a); break;
-      case Q4_0: launch(matvec_fused_kernel<Q4_0>, dim3(wg), dim3(kThreads), lds, a); break;
-      case Q4_1: launch(matvec_fused_kernel<Q4_1>, dim3(wg), dim3(kThreads), lds, a); break;
-      default: return fail(kUnsupported, "matvec_fused: weight type %d", type);
+      if (dma) {
+        switch (type) {
+        case Q8_0: launch(matvec_dma_kernel<Q8_0>, dim3(wg), dim3(kThreads), lds, a); break;
+        case Q4_0: launch(matvec_dma_kernel<Q4_0>, dim3(wg), dim3(kThreads), lds, a); break;
+        case Q4_1: launch(matvec_dma_kernel<Q4_1>, dim3(wg), dim3(kThreads), lds, a); break;
+        default: return fail(kUnsupported, "matvec_fused: weight type %d", type);
+        }
+      } else {
+        switch (type) {
+        case Q8_0: launch(matvec_fused_kernel<Q8_0>, dim3(wg), dim3(kThreads), lds, a); break;
+        case Q4_0: launch(matvec_fused_kernel<Q4_0>, dim3(wg), dim3(kThreads), lds, a); break;
+        case Q4_1: launch(matvec_fused_kernel<Q4_1>, dim3(wg), dim3(kThreads), lds, a); break;
+        default: return fail(kUnsupported, "matvec_fused: weight type %d", type);
+        }
       }
       return check_launch("matvec_fused");
     }

@@ -10,9 +10,15 @@
 // bit-identical to the scalar table's.
 //
 // One lane owns one output row and walks it in element order with its super-block in
-// registers: the lane loads the next 210-byte super-block (53 dwords) while it works on the
-// current one, so the row streams from HBM under the arithmetic. Activation rows sit in LDS
-// and are read as broadcasts.
+// registers. Two ways to get the super-blocks there:
+//  * q6k_stream_kernel (rows a multiple of 4 bytes, i.e. an even super-block count: every
+//    model shape): a wave's 64 rows move one super-block column at a time through the wave's
+//    own LDS tile, copied row by row by LDS-DMA buffer loads (contiguous 212-byte runs); each
+//    lane then reads its own window. The next column's copies are in flight while the lanes
+//    work on the current one. The column's activations travel the same way and are read as
+//    LDS broadcasts.
+//  * matvec_q6k_kernel (any 2-byte-aligned rows): each lane fetches its own super-blocks with
+//    per-lane loads, double-buffered in registers.
 #include "common.h"
 #include "matvec.h"
 
@@ -121,6 +127,129 @@ __global__ __launch_bounds__(kThreads) void matvec_q6k_kernel(MatvecArgs args, u
   for (int m = 0; m < MM; ++m) seg.y[static_cast<size_t>(m) * seg.y_stride + row] = acc[m];
 }
 
+
+// One super-block window (53 dwords, whole) of this lane's row in element order: the same
+// arithmetic as q6k_superblock, with the super-block's activations at x[m * 256 + e] (LDS).
+template <int MM>
+__device__ __forceinline__ void q6k_window(const uint32_t (&w)[kWin], uint32_t sh, const float* x,
+                                           float (&acc)[MM]) {
+  const uint32_t bits = 8 * sh;
+  auto dw = [&](int o) { return __builtin_amdgcn_alignbit(w[o / 4 + 1], w[o / 4], bits); };
+  const float d = half_bits_to_float(sh ? (w[kWin - 1] >> 16) : (w[kWin - 1] & 0xffffu));
+  uint32_t sc[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) sc[i] = dw(192 + 4 * i);
+#pragma unroll
+  for (int n = 0; n < 2; ++n) {
+#pragma unroll
+    for (int qi = 0; qi < 4; ++qi) {
+#pragma unroll
+      for (int half = 0; half < 2; ++half) {
+        const int si = n * 8 + qi * 2 + half;
+        const float scale = static_cast<float>(static_cast<int8_t>((sc[si >> 2] >> (8 * (si & 3))) & 0xffu));
+        const float ds = d * scale;       // exact
+        const float neg32 = -32.0f * ds;  // exact
+#pragma unroll
+        for (int l4 = 0; l4 < 4; ++l4) {
+          const int l = 16 * half + 4 * l4;
+          const uint32_t lw = dw(64 * n + 32 * (qi & 1) + l);
+          const uint32_t hw = dw(128 + 32 * n + l);
+          const uint32_t q = ((lw >> (4 * (qi >> 1))) & 0x0f0f0f0fu) | (((hw >> (2 * qi)) & 0x03030303u) << 4);
+          const uint32_t e0 = 128 * n + 32 * qi + l;
+#pragma unroll
+          for (int m = 0; m < MM; ++m) {
+            const float4 x4 = *reinterpret_cast<const float4*>(x + m * kQKK + e0);
+            const float xv[4] = {x4.x, x4.y, x4.z, x4.w};
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              const float v = fmaf(ds, static_cast<float>((q >> (8 * e)) & 0xffu), neg32);  // (d*scale)*(q-32)
+              acc[m] += v * xv[e];
+            }
+          }
+        }
+      }
+    }
+  }
+}
+
+// Rows of an even super-block count: the window of super-block c starts at byte
+// 210c - 2 (c odd) or 210c (c even), a multiple of 4, and its 212 bytes stay inside the row.
+//
+// One wave per workgroup, one output row per lane. Per super-block column the wave copies its
+// rows' windows straight from HBM into its LDS tile [64][53] with LDS-DMA buffer loads (load
+// k: lanes 0..52 move row k's 53 dwords, 212 contiguous bytes), and the column's activations
+// into a double-buffered LDS chunk the same way. Each lane reads its window into registers, the
+// wave issues the next column's copies into the same tile, and the lanes work on the window
+// while those copies are in flight. Every LDS access stays inside the wave, so waits on the
+// wave's own counters order them; no workgroup barrier is needed.
+constexpr int kStreamRows = 64;
+
+
+__device__ __forceinline__ void wait_all() {
+  __builtin_amdgcn_s_waitcnt(0);
+  __builtin_amdgcn_wave_barrier();
+}
+
+template <int MM>
+__global__ __launch_bounds__(kStreamRows) void q6k_stream_kernel(MatvecArgs args, uint32_t n_in) {
+  extern __shared__ __attribute__((aligned(16))) uint32_t tile[];  // [64 rows][kWin], then x [2][MM][256]
+  float* xc = reinterpret_cast<float*>(tile + kStreamRows * kWin);
+  const uint32_t lane = threadIdx.x;
+  const uint32_t nsb = args.nb;
+  const uint32_t row_bytes = nsb * kBytesQ6_K;
+  const MatvecSeg seg = args.seg[0];
+  const uint32_t row0 = blockIdx.x * kStreamRows;
+  const uint32_t rows = min(static_cast<uint32_t>(kStreamRows), seg.n_out - row0);
+  const __amdgpu_buffer_rsrc_t wsrc = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<uint8_t*>(seg.w) + static_cast<size_t>(row0) * row_bytes, 0, static_cast<int>(rows * row_bytes),
+      static_cast<int>(kRawBufferWord3));
+  const __amdgpu_buffer_rsrc_t xsrc = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<uint8_t*>(args.xq), 0, static_cast<int>(MM * n_in * 4), static_cast<int>(kRawBufferWord3));
+  const uint32_t voff = 4 * lane;
+  auto window_start = [](uint32_t c) { return c * kBytesQ6_K - 2 * (c & 1); };
+  // Copies of column c: rows below `rows` only (uniform), lanes below 53 for the windows.
+  // Rows past the last one re-copy the last row (uniform clamp, no branch per row).
+  const uint32_t last_off = (rows - 1) * row_bytes;
+  auto copy_column = [&](uint32_t c) {
+    uint32_t soff = window_start(c);
+    if (lane < kWin) {
+#pragma unroll
+      for (int k = 0; k < kStreamRows; ++k) {
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(wsrc, as_lds(tile + k * kWin), 4, voff,
+                                                 min(soff, last_off + window_start(c)), 0, 0);
+        soff += row_bytes;
+      }
+    }
+    float* xb = xc + (c & 1) * MM * kQKK;
+#pragma unroll
+    for (int m = 0; m < MM; ++m) {
+#pragma unroll
+      for (int p = 0; p < kQKK / 64; ++p) {
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(
+            xsrc, as_lds(xb + m * kQKK + 64 * p), 4, voff,
+            4 * (m * n_in + c * kQKK + 64 * p), 0, 0);
+      }
+    }
+  };
+  copy_column(0);
+  float acc[MM];
+#pragma unroll
+  for (int m = 0; m < MM; ++m) acc[m] = 0.0f;
+  for (uint32_t c = 0; c < nsb; ++c) {
+    wait_all();  // column c is in LDS; the previous column's activation reads are done
+    uint32_t w[kWin];
+#pragma unroll
+    for (int j = 0; j < kWin; ++j) w[j] = tile[lane * kWin + j];
+    wait_all();  // every lane holds its window: the tile may be refilled
+    if (c + 1 < nsb) copy_column(c + 1);
+    q6k_window<MM>(w, 2 * (c & 1), xc + (c & 1) * MM * kQKK, acc);
+  }
+  if (lane < rows) {
+#pragma unroll
+    for (int m = 0; m < MM; ++m) seg.y[static_cast<size_t>(m) * seg.y_stride + row0 + lane] = acc[m];
+  }
+}
+
 }  // namespace
 
 int matvec_q6k_launch(MatvecArgs& a, uint32_t n_in) {
@@ -133,6 +262,31 @@ int matvec_q6k_launch(MatvecArgs& a, uint32_t n_in) {
     return fail(kInvalidArgument, "matmul_q6_k: activations must be 4-byte aligned");
   const MatvecArgs base = a;
   const float* x = reinterpret_cast<const float*>(a.xq);
+  const uint32_t nsb = n_in / kQKK;
+  const bool stream_ok = nsb % 2 == 0 && (reinterpret_cast<uintptr_t>(a.seg[0].w) & 3u) == 0 &&
+                         (reinterpret_cast<uintptr_t>(a.xq) & 15u) == 0 &&
+                         static_cast<size_t>(kStreamRows) * nsb * kBytesQ6_K < (size_t(1) << 31);
+  if (stream_ok) {
+    const dim3 grid(static_cast<uint32_t>(ceil_div(n_out, kStreamRows)));
+    for (uint32_t done = 0; done < base.m;) {
+      const uint32_t mm = std::min<uint32_t>(4, base.m - done);
+      MatvecArgs g = base;
+      g.m = mm;
+      g.xq = reinterpret_cast<const uint8_t*>(x + static_cast<size_t>(done) * n_in);
+      g.seg[0].y = base.seg[0].y + static_cast<size_t>(done) * base.seg[0].y_stride;
+      const size_t lds = static_cast<size_t>(kStreamRows) * kWin * 4 + 2 * static_cast<size_t>(mm) * kQKK * 4;
+      switch (mm) {
+      case 4: launch(q6k_stream_kernel<4>, grid, dim3(kStreamRows), lds, g, n_in); break;
+      case 3: launch(q6k_stream_kernel<3>, grid, dim3(kStreamRows), lds, g, n_in); break;
+      case 2: launch(q6k_stream_kernel<2>, grid, dim3(kStreamRows), lds, g, n_in); break;
+      default: launch(q6k_stream_kernel<1>, grid, dim3(kStreamRows), lds, g, n_in); break;
+      }
+      const int rc = check_launch("q6k_stream");
+      if (rc != kOk) return rc;
+      done += mm;
+    }
+    return kOk;
+  }
   uint32_t done = 0;
   while (done < base.m) {
     uint32_t mm = std::min<uint32_t>(4, base.m - done);

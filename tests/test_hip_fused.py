@@ -240,6 +240,77 @@ def test_norm_qkv_rope_matches_unfused(H, o, kind, n_rows, d, n_head, n_kv, hd, 
         assert np.max(np.abs(got_q[i] - want)) <= 2e-6 * max(1.0, float(np.max(np.abs(want)))), i
 
 
+def quantized_rows(o, x_rows):
+    return np.concatenate([o.quantize_row_q8_0(r) for r in x_rows])
+
+
+@pytest.mark.parametrize("kind", KINDS)
+@pytest.mark.parametrize("n_rows", [1, 2, 3, 4])
+@pytest.mark.parametrize("n_in,n_out,out_mode", [(2048, 2048, 0), (2048, 1153, 1), (8192, 2048, 1), (576, 576, 1),
+                                                  (896, 300, 0)])
+@pytest.mark.parametrize("misalign", [0, 2])
+def test_q8_input_matches_unfused(H, o, kind, n_rows, n_in, n_out, out_mode, misalign):
+    """in_mode 0: Q8_0 activation blocks in, store or residual add out. Aligned blocks take the
+    LDS-DMA kernel; blocks 2 bytes off a 4-byte boundary take the staged kernel."""
+    if not supported(H, kind, 0, n_rows, n_in):
+        pytest.skip("shape outside the fused kernel")
+    x = random_floats(n_rows * n_in, n_in + 5 * n_rows, 2.0).reshape(n_rows, n_in)
+    xq = quantized_rows(o, x)
+    w = random_weights(kind, n_out, n_in, n_in + n_out)
+    res = random_floats(n_rows * n_out, n_out + 3, 1.0).reshape(n_rows, n_out)
+    raw = xq.tobytes()
+    dxq = H.DeviceBuffer(len(raw) + 16)
+    dxq.upload(np.frombuffer(raw, np.uint8), offset=misalign)
+    dw = H.DeviceBuffer.of(w)
+    y = H.DeviceBuffer.of(res)
+    fused(H, type=TYPE_ID[kind], n_seg=1, w=[dw], n_out=[n_out], n_rows=n_rows, n_in=n_in, in_mode=0,
+          xq=dxq.ptr + misalign, out_mode=out_mode, y=[y], y_stride=[n_out])
+    got = y.download(np.float32).reshape(n_rows, n_out)
+    want = oracle_rows(o, kind, w, x, n_out, n_in) + (res if out_mode == 1 else 0)
+    assert np.array_equal(got, want)
+
+
+@pytest.mark.parametrize("kind", KINDS)
+@pytest.mark.parametrize("n_rows", [1, 3, 4])
+def test_q8_input_silu_and_rope_match_unfused(H, o, kind, n_rows):
+    n_in, ff = 2048, 8192
+    x = random_floats(n_rows * n_in, 17 + n_rows, 2.0).reshape(n_rows, n_in)
+    dxq = H.DeviceBuffer.of(quantized_rows(o, x))
+    wg, wu = random_weights(kind, ff, n_in, 5), random_weights(kind, ff, n_in, 6)
+    dwg, dwu = H.DeviceBuffer.of(wg), H.DeviceBuffer.of(wu)
+    h = H.DeviceBuffer(n_rows * ff * 4)
+    fused(H, type=TYPE_ID[kind], n_seg=2, w=[dwg, dwu], n_out=[ff, ff], n_rows=n_rows, n_in=n_in, in_mode=0,
+          xq=dxq, out_mode=2, y=[h], y_stride=[ff])
+    gate, up = (H.DeviceBuffer(n_rows * ff * 4) for _ in range(2))
+    unfused_matmul(H, kind, dxq, n_rows, n_in, [dwg, dwu], [gate, up], [ff, ff], [ff, ff], False)
+    out = H.DeviceBuffer(n_rows * ff * 4)
+    H.call("silu_mul_rows", gate, up, out, None, ff, n_rows)
+    assert np.array_equal(h.download(np.float32), out.download(np.float32))
+
+    n_head, n_kv, hd, max_ctx = 32, 8, 64, 16
+    dq, dkv = n_head * hd, n_kv * hd
+    ws = [random_weights(kind, nn, n_in, 30 + i) for i, nn in enumerate((dq, dkv, dkv))]
+    dws = [H.DeviceBuffer.of(w) for w in ws]
+    pos = (np.arange(n_rows) * 3 + 1).astype(np.int32)
+    coff = (np.arange(n_rows) * 2 * max_ctx * dkv).astype(np.int64)
+    table = rope_table(max_ctx, hd, 500000.0)
+    dpos, dcoff, dtab = H.DeviceBuffer.of(pos), H.DeviceBuffer.of(coff), H.DeviceBuffer.of(table)
+    pool0 = np.zeros(n_rows * 2 * max_ctx * dkv, np.float32)
+    pool, pool2 = H.DeviceBuffer.of(pool0), H.DeviceBuffer.of(pool0)
+    q = H.DeviceBuffer(n_rows * dq * 4)
+    fused(H, type=TYPE_ID[kind], n_seg=3, w=dws, n_out=[dq, dkv, dkv], n_rows=n_rows, n_in=n_in, in_mode=0, xq=dxq,
+          out_mode=3, y=[q], y_stride=[dq], rope_table=dtab, rot_half=hd // 2, head_dim=hd, pos=dpos,
+          cache_off=dcoff, cache=pool, k_layer_off=0, v_layer_off=max_ctx * dkv)
+    q2, k2, v2 = (H.DeviceBuffer(n_rows * nn * 4) for nn in (dq, dkv, dkv))
+    unfused_matmul(H, kind, dxq, n_rows, n_in, dws, [q2, k2, v2], [dq, dkv, dkv], [dq, dkv, dkv], False)
+    ra = H.RopeRowsArgs(q=q2.ptr, k=k2.ptr, v=v2.ptr, pos=dpos.ptr, q_stride=dq, k_stride=dkv, n_head=n_head,
+                        n_kv=n_kv, head_dim=hd, rotary_dim=hd, neox=0, theta=500000.0, table=dtab.ptr,
+                        cache=pool2.ptr, cache_off=dcoff.ptr, k_layer_off=0, v_layer_off=max_ctx * dkv)
+    H.check(H.lib().axon_hip_rope_rows(C.byref(ra), C.c_size_t(n_rows)), "rope_rows")
+    assert np.array_equal(q.download(np.float32), q2.download(np.float32))
+    assert np.array_equal(pool.download(np.float32), pool2.download(np.float32))
+
+
 def test_rejects_bad_arguments(H):
     """Shapes the kernel cannot hold come back as errors, never as launches."""
     w = H.DeviceBuffer(64 * 34)
@@ -252,5 +323,6 @@ def test_rejects_bad_arguments(H):
         with pytest.raises(H.HipError):
             fused(H, **{**base, **bad})
     assert not supported(H, "q8_0", 2, 1, 4096)      # the norm prologue holds one chunk per thread
-    assert not supported(H, "q8_0", 1, 2, 8192)      # two rows of 8192 floats exceed the registers
+    assert supported(H, "q8_0", 1, 2, 8192)          # float rows are quantized one at a time
+    assert not supported(H, "q8_0", 1, 1, 16384)     # a row of 16384 floats exceeds the registers
     assert supported(H, "q4_0", 1, 1, 8192)
