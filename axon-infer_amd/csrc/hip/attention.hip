@@ -327,6 +327,214 @@ __global__ __launch_bounds__(kThreads) void attn_mix_kernel(AttnArgs a) {
   }
 }
 
+// ---- Decode-shaped launches, 64-dim heads of an fp32 cache --------------------------------
+//   attn_scores64_kernel  one workgroup per (row, kv head, 64 positions): the 64 K rows go into
+//                         LDS by DMA, wave h computes query head h's scores, one lane per
+//                         position, each dot over d in order.
+//   attn_mix64_kernel     one wave per (row, query head): the softmax statistics, then the
+//                         value mix with lane = dim, positions in order, V streaming through a
+//                         ring of LDS tiles that DMA keeps kRing tiles ahead.
+// The float operations and their order are the fused kernel's, and the double sum of the
+// softmax follows the fused kernel's 256-thread tree (each lane carries the partial sums of
+// threads lane, lane + 64, lane + 128, lane + 192).
+constexpr uint32_t kKPitch = 68;  // floats per K row in LDS (64 + 4: conflict-free b128 reads)
+
+__global__ __launch_bounds__(1024) void attn_scores64_kernel(AttnArgs a) {
+  extern __shared__ __attribute__((aligned(16))) float lds[];  // K [64][kKPitch], q [group][64]
+  const uint32_t r = blockIdx.x;
+  const uint32_t g = blockIdx.y;
+  const uint32_t j0 = blockIdx.z * 64;
+  const uint32_t n_vis = a.n_vis != nullptr ? static_cast<uint32_t>(a.n_vis[r]) : static_cast<uint32_t>(a.n_past) + r + 1;
+  if (j0 >= n_vis) return;
+  const uint32_t tid = threadIdx.x;
+  const uint32_t lane = tid & 63u;
+  const uint32_t wave = tid >> 6;
+  const uint32_t group = a.n_head / a.n_kv;
+  const uint32_t rows = min(64u, n_vis - j0);
+  const size_t kv_row = static_cast<size_t>(a.n_kv) * 64;
+  const int64_t k_off = (a.k_off != nullptr ? a.k_off[r] : 0) + a.k_off_c;
+  float* kt = lds;
+  float* qs = lds + 64 * kKPitch;
+  // K rows j0 .. j0 + 63 of kv head g (rows past n_vis repeat the last one): one dword DMA per
+  // row, waves taking rows in turn.
+  const float* kbase = reinterpret_cast<const float*>(a.kv) + k_off + static_cast<size_t>(j0) * kv_row + g * 64;
+  const __amdgpu_buffer_rsrc_t rsrc = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<float*>(kbase), 0, static_cast<int>((static_cast<size_t>(rows - 1) * kv_row + 64) * 4),
+      static_cast<int>(kRawBufferWord3));
+  for (uint32_t i = wave; i < 64; i += group) {
+    const uint32_t row = min(i, rows - 1);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, as_lds(kt + i * kKPitch), 4, 4 * lane,
+                                             static_cast<int>(row * kv_row * 4), 0, 0);
+  }
+  const float* q = a.q + static_cast<size_t>(r) * a.q_stride + static_cast<size_t>(g) * group * 64;
+  for (uint32_t i = tid; i < group * 64; i += blockDim.x) qs[i] = q[i];
+  wait_memory();
+  __syncthreads();
+  const uint32_t j = j0 + lane;
+  if (j >= n_vis) return;
+  const float* kr = kt + lane * kKPitch;
+  const float* qh = qs + wave * 64;
+  float acc = 0.0f;
+#pragma unroll
+  for (int d = 0; d < 64; d += 4) {
+    const float4 k4 = *reinterpret_cast<const float4*>(kr + d);
+    const float4 q4 = *reinterpret_cast<const float4*>(qh + d);
+    acc += q4.x * k4.x;
+    acc += q4.y * k4.y;
+    acc += q4.z * k4.z;
+    acc += q4.w * k4.w;
+  }
+  a.scratch[(static_cast<size_t>(r) * a.n_head + g * group + wave) * a.max_vis + j] = a.scale * acc;
+}
+
+constexpr uint32_t kMixTile = 32;  // positions per V tile (8 KB)
+constexpr uint32_t kRing = 6;      // V tiles in flight (kRing * 8 DMA ops <= vmcnt's 63)
+// The probabilities of one head's row (rows of more positions take the other paths).
+constexpr uint32_t kMixMaxVis = 2304;
+
+// The V ring is filled by LDS-DMA issued from inline assembly, and its waits are explicit:
+// the compiler's own wait counting, which cannot tell the copies into one ring slot from those
+// into another across loop iterations, would otherwise drain every copy before each tile.
+typedef int RsrcWords __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ RsrcWords raw_buffer_words(const void* base, uint32_t bytes) {
+  const uint64_t a = reinterpret_cast<uint64_t>(base);
+  RsrcWords w;
+  w.x = static_cast<int>(a & 0xffffffffu);
+  w.y = static_cast<int>((a >> 32) & 0xffffu);  // stride 0
+  w.z = static_cast<int>(bytes);
+  w.w = static_cast<int>(kRawBufferWord3);
+  return w;
+}
+
+// 4 bytes per lane from rsrc + voffset to LDS at lds + 4 * lane (lds uniform).
+__device__ __forceinline__ void lds_dma4(RsrcWords rsrc, uint32_t voffset, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %2\n\tbuffer_load_dword %0, %1, 0 offen lds" : : "v"(voffset), "s"(rsrc), "s"(lds)
+               : "memory");
+}
+
+// 16 bytes per lane from rsrc + voffset to LDS at lds + 16 * lane (lds uniform).
+__device__ __forceinline__ void lds_dma16(RsrcWords rsrc, uint32_t voffset, uint32_t lds) {
+  // m0 is set and consumed inside the statement; the compiler reserves it and keeps nothing in
+  // it across statements of this kernel.
+  asm volatile("s_mov_b32 m0, %2\n\tbuffer_load_dwordx4 %0, %1, 0 offen lds" : : "v"(voffset), "s"(rsrc), "s"(lds)
+               : "memory");
+}
+
+__global__ __launch_bounds__(64) void attn_mix64_kernel(AttnArgs a) {
+  __shared__ __attribute__((aligned(16))) float ring[kRing * kMixTile * 64];
+  __shared__ __attribute__((aligned(16))) float p[kMixMaxVis];
+  const uint32_t r = blockIdx.x;
+  const uint32_t h = blockIdx.y;
+  const uint32_t lane = threadIdx.x;
+  const uint32_t group = a.n_head / a.n_kv;
+  const uint32_t g = h / group;
+  const uint32_t n_vis = a.n_vis != nullptr ? static_cast<uint32_t>(a.n_vis[r]) : static_cast<uint32_t>(a.n_past) + r + 1;
+  const size_t kv_row = static_cast<size_t>(a.n_kv) * 64;
+  const int64_t v_off = (a.v_off != nullptr ? a.v_off[r] : 0) + a.v_off_c;
+  const float* s = a.scratch + (static_cast<size_t>(r) * a.n_head + h) * a.max_vis;
+
+  // V tile t = rows t*32 .. t*32+31 (rows past n_vis repeat the last one): 8 copies of 4 rows
+  // (64 lanes x 16 bytes = 1 KB contiguous in LDS) into ring slot t % kRing.
+  const float* vbase = reinterpret_cast<const float*>(a.kv) + v_off + g * 64;
+  const RsrcWords rsrc =
+      raw_buffer_words(vbase, static_cast<uint32_t>((static_cast<size_t>(n_vis - 1) * kv_row + 64) * 4));
+  const uint32_t ring_lds = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(as_lds(ring)));
+  const uint32_t n_tiles = (n_vis + kMixTile - 1) / kMixTile;
+  // The head's scores into p first (64 per copy), so that the softmax reads LDS.
+  const RsrcWords ssrc = raw_buffer_words(s, n_vis * 4);
+  const uint32_t p_lds = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(as_lds(p)));
+  for (uint32_t j0 = 0; j0 < n_vis; j0 += 64) lds_dma4(ssrc, 4 * (j0 + lane), p_lds + 4 * j0);
+  auto copy_tile = [&](uint32_t t) {
+    const uint32_t dst = ring_lds + (t % kRing) * kMixTile * 64 * 4;
+#pragma unroll
+    for (uint32_t k = 0; k < kMixTile / 4; ++k) {
+      const uint32_t row = min(t * kMixTile + 4 * k + lane / 16, n_vis - 1);
+      lds_dma16(rsrc, static_cast<uint32_t>(row * kv_row * 4 + (lane % 16) * 16), dst + 4 * k * 64 * 4);
+    }
+  };
+  for (uint32_t t = 0; t < kRing; ++t) copy_tile(t);
+
+  // Softmax in p while the V tiles arrive (the score copies are older than the 48 tile copies):
+  // max, e_j = exp(s_j - max) with the double sum of the fused kernel's tree, p_j = e_j *
+  // float(1 / sum). Lanes read back only the positions they copied until the max is known.
+  asm volatile("s_waitcnt vmcnt(48)" ::: "memory");
+  float m = -INFINITY;
+  for (uint32_t j = lane; j < n_vis; j += 64) m = fmaxf(m, p[j]);
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off, 64));
+  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+  double part[4] = {0.0, 0.0, 0.0, 0.0};
+#pragma unroll
+  for (int w = 0; w < 4; ++w) {
+    for (uint32_t j = lane + 64 * w; j < n_vis; j += 256) {
+      const float e = exp_rounded(p[j] - m);
+      p[j] = e;
+      part[w] += static_cast<double>(e);
+    }
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) part[w] += __shfl_xor(part[w], off, 64);
+  }
+  double sum = 0.0;
+#pragma unroll
+  for (int w = 0; w < 4; ++w) sum += part[w];
+  const float inv = static_cast<float>(1.0 / sum);
+  for (uint32_t j = lane; j < n_vis; j += 64) p[j] = p[j] * inv;
+
+  // Value mix, positions in order, software-pipelined: while tile t is mixed from registers,
+  // the LDS reads of tile t + 1 are in flight. Tile t's slot takes tile t + kRing as soon as
+  // its registers are loaded (copies past the last tile re-read the last row, never used).
+  // Before tile t + 1 is read from LDS its 8 copies are the oldest of the kRing * 8 in flight.
+  float acc = 0.0f;
+  float va[kMixTile], pa[kMixTile], vb[kMixTile], pb[kMixTile];
+  auto load_tile = [&](uint32_t t, float (&v)[kMixTile], float (&pp)[kMixTile]) {
+    const float* vt = ring + (t % kRing) * kMixTile * 64;
+    const float* pt = p + t * kMixTile;
+#pragma unroll
+    for (uint32_t i = 0; i < kMixTile; ++i) v[i] = vt[i * 64 + lane];
+#pragma unroll
+    for (uint32_t i = 0; i < kMixTile; i += 4) {
+      const float4 q4 = *reinterpret_cast<const float4*>(pt + i);
+      pp[i] = q4.x;
+      pp[i + 1] = q4.y;
+      pp[i + 2] = q4.z;
+      pp[i + 3] = q4.w;
+    }
+  };
+  auto mix_tile = [&](const float (&v)[kMixTile], const float (&pp)[kMixTile], uint32_t t) {
+    const uint32_t cnt = min(kMixTile, n_vis - t * kMixTile);
+#pragma unroll
+    for (uint32_t i = 0; i < kMixTile; ++i) {
+      if (i < cnt) acc += pp[i] * v[i];
+    }
+  };
+  // One step: tile t's registers are loaded into (v, pp); refill its slot, start reading tile
+  // t + 1 into (vn, pn), then mix tile t.
+  auto step = [&](uint32_t t, float (&v)[kMixTile], float (&pp)[kMixTile], float (&vn)[kMixTile],
+                  float (&pn)[kMixTile]) {
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    copy_tile(t + kRing);
+    if (t + 1 < n_tiles) {
+      asm volatile("s_waitcnt vmcnt(40)" ::: "memory");
+      load_tile(t + 1, vn, pn);
+    }
+    mix_tile(v, pp, t);
+  };
+  asm volatile("s_waitcnt vmcnt(40)" ::: "memory");
+  load_tile(0, va, pa);
+  for (uint32_t t = 0; t < n_tiles; t += 2) {
+    step(t, va, pa, vb, pb);
+    if (t + 1 < n_tiles) step(t + 1, vb, pb, va, pa);
+  }
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // no copy outlives the wave
+  const size_t col = static_cast<size_t>(h) * 64 + lane;
+  a.out[static_cast<size_t>(r) * a.out_stride + col] = acc;
+  if (a.outq != nullptr) {
+    const size_t nbq = a.out_stride / kQK;
+    quantize_block_lanes(acc, lane & 31u, a.outq + (static_cast<size_t>(r) * nbq + col / kQK) * kBytesQ8_0);
+  }
+}
+
 bool scores_fit_lds(const AttnArgs& a) {
   const uint32_t group = a.n_head / a.n_kv;
   return static_cast<size_t>(group) * (a.head_dim + a.max_vis) * 4 <= kLdsScores;
@@ -355,6 +563,14 @@ int attention_launch(const AttnArgs& a, uint32_t n_rows) {
     return fail(kInvalidArgument, "attention: heads [%u, %u) of %u", a.head_begin, a.head_end, a.n_head);
   if (a.head_begin == a.head_end) return kOk;
   const uint32_t group = a.n_head / a.n_kv;
+  if (a.scratch != nullptr && use_split(a, n_rows) && a.head_dim == 64 && !a.f16 && group <= 16 &&
+      a.max_vis <= kMixMaxVis) {
+    const dim3 sgrid(n_rows, a.n_kv, (a.max_vis + 63) / 64);
+    const size_t slds = (64 * kKPitch + static_cast<size_t>(group) * 64) * 4;
+    hipLaunchKernelGGL(attn_scores64_kernel, sgrid, dim3(group * 64), slds, stream(), a);
+    hipLaunchKernelGGL(attn_mix64_kernel, dim3(n_rows, a.n_head), dim3(64), 0, stream(), a);
+    return check_launch("attention (decode)");
+  }
   if (a.scratch != nullptr && use_split(a, n_rows)) {
     const dim3 sgrid(n_rows, a.n_kv, (a.max_vis + kThreads - 1) / kThreads);
     const size_t slds = static_cast<size_t>(group) * a.head_dim * 4;

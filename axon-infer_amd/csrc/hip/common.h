@@ -40,14 +40,12 @@ enum Status : int {
 // so that NaN payloads, signed zeros and subnormals come out bit for bit as the scalar table
 // produces them (trickymind1324/axon-infer src/core/dtype.cpp:198-272).
 
+// The hardware conversion is exact for every finite half (subnormals included: half denormals
+// are on); infinities and NaNs take the bit-level form so NaN payloads pass through unchanged.
 __device__ __forceinline__ float half_bits_to_float(uint32_t h) {
-  const uint32_t sign = (h & 0x8000u) << 16;
-  const uint32_t e = (h >> 10) & 0x1fu;
-  const uint32_t m = h & 0x3ffu;
-  if (e == 0x1fu) return __uint_as_float(sign | 0x7f800000u | (m << 13));
-  if (e != 0) return __uint_as_float(sign | ((e + 112u) << 23) | (m << 13));
-  // Zero or subnormal: m * 2^-24 is exact in binary32 (a normal number there).
-  return __uint_as_float(sign | __float_as_uint(static_cast<float>(m) * 0x1p-24f));
+  const float f = static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(h)));
+  const uint32_t special = ((h & 0x8000u) << 16) | 0x7f800000u | ((h & 0x3ffu) << 13);
+  return ((h >> 10) & 0x1fu) == 0x1fu ? __uint_as_float(special) : f;
 }
 
 // Round to nearest even, overflow to infinity, gradual underflow, NaN kept non-zero.
@@ -348,6 +346,10 @@ __device__ __forceinline__ void dma_to_lds(const uint8_t* src, uint8_t* dst, uin
 
 // Waits for every outstanding memory operation of this wave, LDS-DMA copies included.
 __device__ __forceinline__ void wait_memory() { __builtin_amdgcn_s_waitcnt(0); }
+
+// s_waitcnt immediates (gfx9 encoding: vmcnt in bits 3:0 and 15:14, expcnt 6:4, lgkmcnt 11:8).
+constexpr int waitcnt_vm(int n) { return (n & 15) | ((n >> 4) << 14) | (7 << 4) | (15 << 8); }
+constexpr int kWaitLgkm0 = 15 | (3 << 14) | (7 << 4);  // LDS reads and writes of this wave done
 
 // ------------------------------------------------------------------------------------------
 // Host-side plumbing shared by the translation units.

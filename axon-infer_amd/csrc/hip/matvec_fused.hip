@@ -113,6 +113,45 @@ __device__ __forceinline__ void quantize8_to_act(const float (&v)[8], uint32_t p
   }
 }
 
+// Terms rows are 16-byte aligned (a multiple of 4 floats) so the chains read them four at a time.
+__host__ __device__ constexpr uint32_t term_pitch(uint32_t nb) { return (nb + 3) & ~3u; }
+
+// t[0] + t[1] + ... + t[n-1], left to right, from 16-byte aligned LDS: rounds of sixteen terms,
+// the next round's reads in flight while this round's adds run (reads stay within the rows'
+// padding; only the first n terms are added).
+__device__ __forceinline__ void load16(const float* t, float4 (&v)[4]) {
+#pragma unroll
+  for (int k = 0; k < 4; ++k) v[k] = reinterpret_cast<const float4*>(t)[k];
+}
+__device__ __forceinline__ void add16(const float4 (&v)[4], float& acc) {
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    acc += v[k].x;
+    acc += v[k].y;
+    acc += v[k].z;
+    acc += v[k].w;
+  }
+}
+__device__ __forceinline__ float ordered_sum(const float* t, uint32_t n) {
+  float acc = 0.0f;
+  const uint32_t full = n & ~15u;
+  float4 a[4], b[4];
+  uint32_t i = 0;
+  if (full != 0) load16(t, a);
+  for (; i + 32 <= full; i += 32) {
+    load16(t + i + 16, b);
+    add16(a, acc);
+    if (i + 48 <= full) load16(t + i + 32, a);
+    add16(b, acc);
+  }
+  if (i < full) {
+    add16(a, acc);
+    i += 16;
+  }
+  for (; i < n; ++i) acc += t[i];
+  return acc;
+}
+
 // Where a workgroup's weight rows are. The SiLU pairing runs gate and up rows together: up
 // row r sits at tile row pitch_rows + r.
 struct WgRows {
@@ -146,17 +185,25 @@ __device__ __forceinline__ void fused_body(const FusedArgs& args, const WgRows& 
   const uint32_t M = args.m;
   const uint32_t R = args.rows;
   const uint32_t row_bytes = nb * bs;
-  const uint32_t tpitch = nb + 1;
+  const uint32_t tpitch = term_pitch(nb);
   const uint32_t nr = g.nr;
   const int s = g.s;
   const uint32_t r0 = g.r0;
-  const uint32_t pairs = g.n_wrows * nb;
-  for (uint32_t p = tid; p < pairs; p += kThreads) {
-    const uint32_t r = p / nb;
-    const uint32_t b = p - r * nb;
-    const uint32_t trow = (g.silu && r >= nr) ? g.pitch_rows + (r - nr) : r;
-    for (uint32_t m = 0; m < M; ++m) {
-      terms[(m * 2 * R + trow) * tpitch + b] = fused_term<T>(tile, trow * row_bytes + b * bs, act[m * nb + b]);
+  // Each thread keeps one block column b (its activation block read once per row of x) and
+  // walks the weight rows of that column: with nb <= 256 the threads form floor(256 / nb) row
+  // groups, otherwise columns b, b + 256, ... each take every row.
+  const uint32_t groups = nb <= kThreads ? kThreads / nb : 1;
+  const uint32_t col0 = nb <= kThreads ? tid % nb : tid;
+  const uint32_t rg = nb <= kThreads ? tid / nb : 0;
+  if (rg < groups) {
+    for (uint32_t b = col0; b < nb; b += kThreads) {
+      for (uint32_t m = 0; m < M; ++m) {
+        const ActBlock a = act[m * nb + b];
+        for (uint32_t r = rg; r < g.n_wrows; r += groups) {
+          const uint32_t trow = (g.silu && r >= nr) ? g.pitch_rows + (r - nr) : r;
+          terms[(m * 2 * R + trow) * tpitch + b] = fused_term<T>(tile, trow * row_bytes + b * bs, a);
+        }
+      }
     }
   }
   __syncthreads();
@@ -165,10 +212,7 @@ __device__ __forceinline__ void fused_body(const FusedArgs& args, const WgRows& 
     const uint32_t m = tid / g.n_wrows;
     const uint32_t r = tid - m * g.n_wrows;
     const uint32_t trow = (g.silu && r >= nr) ? g.pitch_rows + (r - nr) : r;
-    const float* t = terms + (m * 2 * R + trow) * tpitch;
-    float acc = 0.0f;
-    for (uint32_t b = 0; b < nb; ++b) acc += t[b];
-    outv[m * 2 * R + trow] = acc;
+    outv[m * 2 * R + trow] = ordered_sum(terms + (m * 2 * R + trow) * tpitch, nb);
   }
   __syncthreads();
 
@@ -357,7 +401,7 @@ size_t fused_lds(int bs, uint32_t m, uint32_t nb, uint32_t rows, bool silu, size
   const size_t act = (static_cast<size_t>(m) * nb * sizeof(ActBlock) + 15) & ~size_t(15);
   const size_t tile = std::max<size_t>((wrows * row_bytes + 16 + 15) & ~size_t(15), static_cast<size_t>(m) * 2 * rows * 4);
   const size_t raw = static_cast<size_t>(m) * nb * kBytesQ8_0 + 16;
-  const size_t terms = static_cast<size_t>(m) * 2 * rows * (nb + 1) * 4;
+  const size_t terms = static_cast<size_t>(m) * 2 * rows * term_pitch(nb) * 4 + 64;
   *act_out = act;
   *tile_out = tile;
   return act + tile + std::max(raw, terms);

@@ -556,7 +556,7 @@ Expected<std::size_t> LlamaModel::run(std::span<const Row> rows, bool copy_logit
       DEV(axon_hip_rope_rows(&ra, n));
     }
 
-    const bool wo_fused = fused_ok(L.wo, 1, dq, false);
+    const bool wo_fused = fused_ok(L.wo, 0, dq, false);
     axon_hip_attention_rows_args aa{};
     aa.q = q_;
     aa.out = attn_;
@@ -574,8 +574,8 @@ Expected<std::size_t> LlamaModel::run(std::span<const Row> rows, bool copy_logit
     aa.scale = scale;
     aa.scratch = scores_;
     aa.max_vis = max_vis;
-    // wo's Q8_0 input: quantized in the attention epilogue, or inside the fused wo launch.
-    aa.outq = q8_path(L.wo) && !wo_fused ? xq_ : nullptr;
+    // wo's Q8_0 input, quantized in the attention epilogue.
+    aa.outq = q8_path(L.wo) ? xq_ : nullptr;
     DEV(axon_hip_attention_rows(&aa, n));
 
     if (wo_fused) {
@@ -583,9 +583,8 @@ Expected<std::size_t> LlamaModel::run(std::span<const Row> rows, bool copy_logit
       fa.n_seg = 1;
       fa.w[0] = L.wo.dev;
       fa.n_out[0] = d;
-      fa.in_mode = 1;
-      fa.x = attn_;
-      fa.x_stride = dq;
+      fa.in_mode = 0;
+      fa.xq = xq_;
       fa.out_mode = 1;
       fa.y[0] = x_;
       fa.y_stride[0] = d;
