@@ -223,6 +223,8 @@ def host() -> C.CDLL:
         L.axon_model_forward.argtypes = [C.c_void_p, C.c_void_p, C.c_size_t, C.c_void_p]
         L.axon_model_forward_prefill.argtypes = [C.c_void_p, C.c_int, C.c_void_p, C.c_size_t, C.c_void_p]
         L.axon_model_forward_batch.argtypes = [C.c_void_p, C.c_void_p, C.c_void_p, C.c_size_t, C.c_void_p]
+        L.axon_model_greedy.argtypes = [C.c_void_p, C.c_void_p, C.c_void_p, C.c_float, C.c_int, C.c_void_p,
+                                        C.c_size_t]
         L.axon_model_probe.argtypes = [C.c_void_p, C.c_int, C.c_int]
         L.axon_model_probe_read.argtypes = [C.c_void_p, C.POINTER(C.c_double), C.POINTER(C.c_size_t),
                                             C.POINTER(C.c_double)]
@@ -285,10 +287,11 @@ class Model:
     def _logits(self, n: int, want: bool):
         return np.zeros((n, self.n_vocab), np.float32) if want else None
 
-    def forward(self, tokens) -> np.ndarray:
+    def forward(self, tokens, logits: bool = True):
         t = np.ascontiguousarray(tokens, np.int32)
-        out = self._logits(len(t), True)
-        _mcheck(host().axon_model_forward(self.h, t.ctypes.data, len(t), out.ctypes.data), "forward")
+        out = self._logits(len(t), logits)
+        _mcheck(host().axon_model_forward(self.h, t.ctypes.data, len(t),
+                                         out.ctypes.data if out is not None else None), "forward")
         return out
 
     def forward_prefill(self, cache: int, tokens, logits: bool = True):
@@ -305,6 +308,20 @@ class Model:
         _mcheck(host().axon_model_forward_batch(self.h, cs.ctypes.data, t.ctypes.data, len(t),
                                                out.ctypes.data if out is not None else None), "forward_batch")
         return out
+
+    def greedy(self, n: int, recent=None, repeat_penalty: float = 1.0, repeat_last_n: int = 64) -> np.ndarray:
+        """Sampler::sample at temperature zero over the last pass's n rows, on the device
+        (src/sampling/sampler.cpp:67-102): the repetition penalty over recent[i], row i's token
+        history, then the first maximum. Consumes the pass's logits."""
+        ids = np.empty(n, np.int32)
+        rec = lens = None
+        if recent is not None:
+            arrs = [np.ascontiguousarray(r, np.int32) for r in recent]
+            rec = (C.c_void_p * n)(*[a.ctypes.data if len(a) else None for a in arrs])
+            lens = (C.c_size_t * n)(*[len(a) for a in arrs])
+        _mcheck(host().axon_model_greedy(self.h, rec, lens, repeat_penalty, repeat_last_n, ids.ctypes.data, n),
+                "greedy")
+        return ids
 
     def probe(self, weight_type: int, enable: bool = True) -> None:
         _mcheck(host().axon_model_probe(self.h, weight_type, int(enable)), "probe")

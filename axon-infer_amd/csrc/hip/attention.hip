@@ -399,26 +399,45 @@ typedef int RsrcWords __attribute__((ext_vector_type(4)));
 
 __device__ __forceinline__ RsrcWords raw_buffer_words(const void* base, uint32_t bytes) {
   const uint64_t a = reinterpret_cast<uint64_t>(base);
+  // The descriptor lives in scalar registers: every lane holds the same words.
   RsrcWords w;
-  w.x = static_cast<int>(a & 0xffffffffu);
-  w.y = static_cast<int>((a >> 32) & 0xffffu);  // stride 0
-  w.z = static_cast<int>(bytes);
+  w.x = __builtin_amdgcn_readfirstlane(static_cast<int>(a & 0xffffffffu));
+  w.y = __builtin_amdgcn_readfirstlane(static_cast<int>((a >> 32) & 0xffffu));  // stride 0
+  w.z = __builtin_amdgcn_readfirstlane(static_cast<int>(bytes));
   w.w = static_cast<int>(kRawBufferWord3);
   return w;
 }
 
 // 4 bytes per lane from rsrc + voffset to LDS at lds + 4 * lane (lds uniform).
 __device__ __forceinline__ void lds_dma4(RsrcWords rsrc, uint32_t voffset, uint32_t lds) {
+  lds = __builtin_amdgcn_readfirstlane(lds);
   asm volatile("s_mov_b32 m0, %2\n\tbuffer_load_dword %0, %1, 0 offen lds" : : "v"(voffset), "s"(rsrc), "s"(lds)
                : "memory");
 }
 
+// 16 bytes per lane from rsrc + voffset + soffset to LDS at lds + 16 * lane (soffset and lds
+// uniform).
+__device__ __forceinline__ void lds_dma16_so(RsrcWords rsrc, uint32_t voffset, uint32_t soffset, uint32_t lds) {
+  lds = __builtin_amdgcn_readfirstlane(lds);
+  soffset = __builtin_amdgcn_readfirstlane(soffset);
+  asm volatile("s_mov_b32 m0, %3\n\tbuffer_load_dwordx4 %0, %1, %2 offen lds"
+               : : "v"(voffset), "s"(rsrc), "s"(soffset), "s"(lds) : "memory");
+}
+
 // 16 bytes per lane from rsrc + voffset to LDS at lds + 16 * lane (lds uniform).
 __device__ __forceinline__ void lds_dma16(RsrcWords rsrc, uint32_t voffset, uint32_t lds) {
+  lds = __builtin_amdgcn_readfirstlane(lds);
   // m0 is set and consumed inside the statement; the compiler reserves it and keeps nothing in
   // it across statements of this kernel.
   asm volatile("s_mov_b32 m0, %2\n\tbuffer_load_dwordx4 %0, %1, 0 offen lds" : : "v"(voffset), "s"(rsrc), "s"(lds)
                : "memory");
+}
+
+// s_waitcnt vmcnt(N) as a statement the compiler does not move memory accesses across.
+template <int N>
+__device__ __forceinline__ void wait_vm() {
+  static_assert(N >= 0 && N <= 63, "vmcnt is six bits");
+  asm volatile("s_waitcnt vmcnt(%0)" : : "n"(N) : "memory");
 }
 
 __global__ __launch_bounds__(64) void attn_mix64_kernel(AttnArgs a) {
@@ -535,6 +554,150 @@ __global__ __launch_bounds__(64) void attn_mix64_kernel(AttnArgs a) {
   }
 }
 
+// One workgroup per (row, kv head) for groups of G = 1, 2, 4 or 8 query heads: wave w owns
+// query head g * G + w (lane = dim), its softmax in its own row of p, and one G-th of the copies
+// of every V tile, which all G waves then mix. The V rows of the group are streamed once.
+constexpr uint32_t kGRing = 3;  // V tiles in flight
+
+// Rows of p hold whole 64-position copies (the last copy of a row writes up to 63 past n_vis).
+__host__ __device__ inline uint32_t mixg_pitch(uint32_t max_vis) { return (max_vis + 63) & ~63u; }
+
+size_t mixg_lds(uint32_t group, uint32_t max_vis) {
+  return (static_cast<size_t>(kGRing) * kMixTile * 64 + static_cast<size_t>(group) * mixg_pitch(max_vis)) * 4;
+}
+
+template <int G>
+__global__ __launch_bounds__(G * 64) void attn_mixg_kernel(AttnArgs a) {
+  constexpr uint32_t kOps = 8 / G;  // copies per wave per tile (a tile is 8 copies of 1 KB)
+  extern __shared__ __attribute__((aligned(16))) float lds[];
+  float* ring = lds;                                  // [kGRing][kMixTile][64]
+  const uint32_t pitch = mixg_pitch(a.max_vis);
+  const uint32_t tid = threadIdx.x;
+  const uint32_t lane = tid & 63u;
+  const uint32_t w = tid >> 6;
+  float* p = lds + kGRing * kMixTile * 64 + w * pitch;  // this head's probabilities
+  const uint32_t r = blockIdx.x;
+  const uint32_t g = blockIdx.y;
+  const uint32_t h = g * G + w;
+  const uint32_t n_vis = a.n_vis != nullptr ? static_cast<uint32_t>(a.n_vis[r]) : static_cast<uint32_t>(a.n_past) + r + 1;
+  const size_t kv_row = static_cast<size_t>(a.n_kv) * 64;
+  const int64_t v_off = (a.v_off != nullptr ? a.v_off[r] : 0) + a.v_off_c;
+  const float* s = a.scratch + (static_cast<size_t>(r) * a.n_head + h) * a.max_vis;
+
+  const float* vbase = reinterpret_cast<const float*>(a.kv) + v_off + g * 64;
+  const RsrcWords rsrc =
+      raw_buffer_words(vbase, static_cast<uint32_t>((static_cast<size_t>(n_vis - 1) * kv_row + 64) * 4));
+  const uint32_t ring_lds = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(as_lds(ring)));
+  const uint32_t n_tiles = (n_vis + kMixTile - 1) / kMixTile;
+  // This head's scores into its row of p (64 per copy), older than every V copy.
+  const RsrcWords ssrc = raw_buffer_words(s, n_vis * 4);
+  const uint32_t p_lds = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(as_lds(p)));
+  for (uint32_t j0 = 0; j0 < n_vis; j0 += 64) lds_dma4(ssrc, 4 * (j0 + lane), p_lds + 4 * j0);
+  // Copy k (0..7) of tile t moves rows t*32 + 4k .. t*32 + 4k + 3; wave w issues k = w, w + G, ...
+  // A tile wholly below n_vis takes this lane's fixed offsets plus a uniform tile offset;
+  // others (the last tile, and the copies past it that keep the wait counts uniform) clamp each
+  // row to the last one.
+  const uint32_t row_bytes = static_cast<uint32_t>(kv_row * 4);
+  uint32_t lane_off[kOps];
+#pragma unroll
+  for (uint32_t i = 0; i < kOps; ++i) lane_off[i] = (4 * (w + i * G) + lane / 16) * row_bytes + (lane % 16) * 16;
+  auto copy_tile = [&](uint32_t t) {
+    const uint32_t dst = ring_lds + (t % kGRing) * kMixTile * 64 * 4;
+    if ((t + 1) * kMixTile <= n_vis) {
+#pragma unroll
+      for (uint32_t i = 0; i < kOps; ++i) {
+        lds_dma16_so(rsrc, lane_off[i], t * kMixTile * row_bytes, dst + 4 * (w + i * G) * 64 * 4);
+      }
+    } else {
+#pragma unroll
+      for (uint32_t i = 0; i < kOps; ++i) {
+        const uint32_t k = w + i * G;
+        const uint32_t row = min(t * kMixTile + 4 * k + lane / 16, n_vis - 1);
+        lds_dma16(rsrc, row * row_bytes + (lane % 16) * 16, dst + 4 * k * 64 * 4);
+      }
+    }
+  };
+  for (uint32_t t = 0; t < kGRing; ++t) copy_tile(t);
+
+  // Softmax of this head in p (the fused kernel's operations and double-sum tree).
+  wait_vm<kGRing * kOps>();
+  float m = -INFINITY;
+  for (uint32_t j = lane; j < n_vis; j += 64) m = fmaxf(m, p[j]);
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off, 64));
+  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+  double part[4] = {0.0, 0.0, 0.0, 0.0};
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    for (uint32_t j = lane + 64 * q; j < n_vis; j += 256) {
+      const float e = exp_rounded(p[j] - m);
+      p[j] = e;
+      part[q] += static_cast<double>(e);
+    }
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) part[q] += __shfl_xor(part[q], off, 64);
+  }
+  double sum = 0.0;
+#pragma unroll
+  for (int q = 0; q < 4; ++q) sum += part[q];
+  const float inv = static_cast<float>(1.0 / sum);
+  for (uint32_t j = lane; j < n_vis; j += 64) p[j] = p[j] * inv;
+
+  // Value mix, positions in order; tile t + 1 is read from LDS while tile t is mixed from
+  // registers. A slot is refilled once every wave has read it.
+  float acc = 0.0f;
+  float va[kMixTile], pa[kMixTile], vb[kMixTile], pb[kMixTile];
+  auto load_tile = [&](uint32_t t, float (&v)[kMixTile], float (&pp)[kMixTile]) {
+    const float* vt = ring + (t % kGRing) * kMixTile * 64;
+    const float* pt = p + t * kMixTile;
+#pragma unroll
+    for (uint32_t i = 0; i < kMixTile; ++i) v[i] = vt[i * 64 + lane];
+#pragma unroll
+    for (uint32_t i = 0; i < kMixTile; i += 4) {
+      const float4 q4 = *reinterpret_cast<const float4*>(pt + i);
+      pp[i] = q4.x;
+      pp[i + 1] = q4.y;
+      pp[i + 2] = q4.z;
+      pp[i + 3] = q4.w;
+    }
+  };
+  auto mix_tile = [&](const float (&v)[kMixTile], const float (&pp)[kMixTile], uint32_t t) {
+    const uint32_t cnt = min(kMixTile, n_vis - t * kMixTile);
+    if (cnt == kMixTile) {
+#pragma unroll
+      for (uint32_t i = 0; i < kMixTile; ++i) acc += pp[i] * v[i];
+    } else {
+      for (uint32_t i = 0; i < cnt; ++i) acc += pp[i] * v[i];
+    }
+  };
+  auto step = [&](uint32_t t, float (&v)[kMixTile], float (&pp)[kMixTile], float (&vn)[kMixTile],
+                  float (&pn)[kMixTile]) {
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    __syncthreads();  // every wave has tile t in registers: its slot takes tile t + kGRing
+    copy_tile(t + kGRing);
+    if (t + 1 < n_tiles) {
+      wait_vm<(kGRing - 1) * kOps>();  // this wave's copies of tile t + 1 landed
+      __syncthreads();                 // everyone's
+      load_tile(t + 1, vn, pn);
+    }
+    mix_tile(v, pp, t);
+  };
+  wait_vm<(kGRing - 1) * kOps>();
+  __syncthreads();
+  load_tile(0, va, pa);
+  for (uint32_t t = 0; t < n_tiles; t += 2) {
+    step(t, va, pa, vb, pb);
+    if (t + 1 < n_tiles) step(t + 1, vb, pb, va, pa);
+  }
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // no copy outlives the workgroup
+  const size_t col = static_cast<size_t>(h) * 64 + lane;
+  a.out[static_cast<size_t>(r) * a.out_stride + col] = acc;
+  if (a.outq != nullptr) {
+    const size_t nbq = a.out_stride / kQK;
+    quantize_block_lanes(acc, lane & 31u, a.outq + (static_cast<size_t>(r) * nbq + col / kQK) * kBytesQ8_0);
+  }
+}
+
 bool scores_fit_lds(const AttnArgs& a) {
   const uint32_t group = a.n_head / a.n_kv;
   return static_cast<size_t>(group) * (a.head_dim + a.max_vis) * 4 <= kLdsScores;
@@ -568,7 +731,16 @@ int attention_launch(const AttnArgs& a, uint32_t n_rows) {
     const dim3 sgrid(n_rows, a.n_kv, (a.max_vis + 63) / 64);
     const size_t slds = (64 * kKPitch + static_cast<size_t>(group) * 64) * 4;
     hipLaunchKernelGGL(attn_scores64_kernel, sgrid, dim3(group * 64), slds, stream(), a);
-    hipLaunchKernelGGL(attn_mix64_kernel, dim3(n_rows, a.n_head), dim3(64), 0, stream(), a);
+    const size_t glds = mixg_lds(group, a.max_vis);
+    const dim3 ggrid(n_rows, a.n_kv);
+    if (glds <= 65536 && (group == 1 || group == 2 || group == 4 || group == 8)) {
+      if (group == 1) hipLaunchKernelGGL(attn_mixg_kernel<1>, ggrid, dim3(64), glds, stream(), a);
+      if (group == 2) hipLaunchKernelGGL(attn_mixg_kernel<2>, ggrid, dim3(128), glds, stream(), a);
+      if (group == 4) hipLaunchKernelGGL(attn_mixg_kernel<4>, ggrid, dim3(256), glds, stream(), a);
+      if (group == 8) hipLaunchKernelGGL(attn_mixg_kernel<8>, ggrid, dim3(512), glds, stream(), a);
+    } else {
+      hipLaunchKernelGGL(attn_mix64_kernel, dim3(n_rows, a.n_head), dim3(64), 0, stream(), a);
+    }
     return check_launch("attention (decode)");
   }
   if (a.scratch != nullptr && use_split(a, n_rows)) {

@@ -553,6 +553,26 @@ int axon_hip_add(float* x, const float* y, size_t n) {
   return add_launch(x, y, n);
 }
 
+int axon_hip_repeat_penalty_rows(float* x, size_t n, size_t n_rows, size_t stride, const int32_t* recent,
+                                 const uint32_t* recent_len, size_t recent_stride, float penalty) {
+  AXON_READY();
+  if (!fits_u32(n) || !fits_u32(n_rows) || stride < n)
+    return fail(kInvalidArgument, "repeat_penalty: %zu x %zu, stride %zu", n_rows, n, stride);
+  if (n_rows != 0 && recent_stride != 0 && (recent == nullptr || recent_len == nullptr))
+    return fail(kInvalidArgument, "repeat_penalty: recent ids and lengths are required");
+  return repeat_penalty_launch(x, static_cast<uint32_t>(n), static_cast<uint32_t>(n_rows), stride, recent, recent_len,
+                               recent_stride, penalty);
+}
+
+size_t axon_hip_argmax_scratch_words(size_t n_rows) { return argmax_scratch_words(static_cast<uint32_t>(n_rows)); }
+
+int axon_hip_argmax_rows(const float* x, size_t n, size_t n_rows, size_t stride, uint64_t* scratch, int32_t* out) {
+  AXON_READY();
+  if (!fits_u32(n) || !fits_u32(n_rows) || stride < n) return fail(kInvalidArgument, "argmax: %zu x %zu, stride %zu", n_rows, n, stride);
+  if (scratch == nullptr || out == nullptr) return fail(kInvalidArgument, "argmax: scratch and output are required");
+  return argmax_rows_launch(x, static_cast<uint32_t>(n), static_cast<uint32_t>(n_rows), stride, scratch, out);
+}
+
 int axon_hip_matmul_q8_fused(int type, const void* xq, size_t n_rows, size_t n_in, size_t n_seg,
                              const void* const* w, float* const* y, const size_t* n_out, const size_t* y_stride,
                              int accumulate) {

@@ -31,6 +31,13 @@ int rmsnorm_launch(const float* x, const float* w, float* y, uint8_t* yq, uint32
 int silu_mul_launch(const float* gate, const float* up, float* out, uint8_t* outq, uint32_t n, uint32_t n_rows);
 int softmax_launch(float* x, uint32_t n);
 int add_launch(float* x, const float* y, size_t n);
+// Greedy selection (sampling.hip). repeat_penalty rescales each row's distinct recent ids in
+// place; argmax_rows takes the first maximum of each row, with argmax_scratch_words words of
+// scratch.
+int repeat_penalty_launch(float* x, uint32_t n, uint32_t n_rows, size_t stride, const int32_t* recent,
+                          const uint32_t* recent_len, size_t recent_stride, float penalty);
+size_t argmax_scratch_words(uint32_t n_rows);
+int argmax_rows_launch(const float* x, uint32_t n, uint32_t n_rows, size_t stride, uint64_t* scratch, int32_t* out);
 int rope_rows_launch(const RopeRowsArgs& a, uint32_t n_rows);
 int embedding_launch(int type, const uint8_t* table, uint32_t n, const int32_t* ids, int64_t id0, uint32_t n_rows,
                      float* out);

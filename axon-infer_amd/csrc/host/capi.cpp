@@ -135,12 +135,20 @@ int axon_model_cache_read(axon_model* model, int cache, size_t layer, int values
 }
 
 int axon_model_forward(axon_model* model, const int32_t* tokens, size_t n, float* logits) {
+  if (logits == nullptr) {
+    auto r = model->m->forward_device(std::span<const int32_t>(tokens, n));
+    return r ? 0 : fail(r.error());
+  }
   return copy_out(model->m->forward(std::span<const int32_t>(tokens, n)), logits);
 }
 
 int axon_model_forward_prefill(axon_model* model, int cache, const int32_t* tokens, size_t n, float* logits) {
   axon::model::KVCache* c = find(model, cache);
   if (c == nullptr) return fail("forward_prefill: unknown cache " + std::to_string(cache));
+  if (logits == nullptr) {
+    auto r = model->m->forward_prefill_device(*c, std::span<const int32_t>(tokens, n));
+    return r ? 0 : fail(r.error());
+  }
   return copy_out(model->m->forward_prefill(*c, std::span<const int32_t>(tokens, n)), logits);
 }
 
@@ -155,6 +163,22 @@ int axon_model_forward_batch(axon_model* model, const int* caches, const int32_t
     return r ? 0 : fail(r.error());
   }
   return copy_out(model->m->forward_batch(cs, std::span<const int32_t>(tokens, n)), logits);
+}
+
+int axon_model_greedy(axon_model* model, const int32_t* const* recent, const size_t* recent_len, float repeat_penalty,
+                      int repeat_last_n, int32_t* ids, size_t n) {
+  if (ids == nullptr && n != 0) return fail("greedy: ids is NULL");
+  std::vector<std::span<const int32_t>> windows;
+  if (recent != nullptr) {
+    if (recent_len == nullptr) return fail("greedy: recent_len is NULL");
+    windows.resize(n);
+    for (size_t i = 0; i < n; ++i) {
+      if (recent[i] == nullptr && recent_len[i] != 0) return fail("greedy: recent[" + std::to_string(i) + "] is NULL");
+      windows[i] = std::span<const int32_t>(recent[i], recent_len[i]);
+    }
+  }
+  auto r = model->m->greedy(std::span<int32_t>(ids, n), windows, repeat_penalty, repeat_last_n);
+  return r ? 0 : fail(r.error());
 }
 
 int axon_model_probe(axon_model* model, int type, int enable) {

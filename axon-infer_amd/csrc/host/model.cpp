@@ -253,6 +253,14 @@ Expected<std::unique_ptr<LlamaModel>> LlamaModel::load(const std::string& path, 
   if (axon_hip_malloc(&m->xq_, R * (widest / 32) * sizeof(BlockQ8_0) + 64) != AXON_HIP_OK)
     return m->device_error("activation blocks");
   const std::size_t info_bytes = align_up(12 * R, 8) + 8 * R;
+  if (axon_hip_malloc(reinterpret_cast<void**>(&m->argmax_scratch_), axon_hip_argmax_scratch_words(R) * 8) !=
+          AXON_HIP_OK ||
+      axon_hip_malloc(reinterpret_cast<void**>(&m->ids_), R * 4) != AXON_HIP_OK)
+    return m->device_error("argmax scratch");
+  const std::size_t window_bytes = R * (kMaxPenaltyWindow + 1) * 4;
+  if (axon_hip_malloc(&m->window_, window_bytes) != AXON_HIP_OK ||
+      axon_hip_host_malloc(&m->window_host_, window_bytes) != AXON_HIP_OK)
+    return m->device_error("penalty windows");
   if (axon_hip_malloc(&m->rowinfo_, info_bytes) != AXON_HIP_OK ||
       axon_hip_host_malloc(&m->rowinfo_host_, info_bytes) != AXON_HIP_OK)
     return m->device_error("row table");
@@ -281,11 +289,13 @@ LlamaModel::~LlamaModel() {
   for (void* p : {static_cast<void*>(x_), static_cast<void*>(h_), static_cast<void*>(q_), static_cast<void*>(k_),
                   static_cast<void*>(v_), static_cast<void*>(attn_), static_cast<void*>(gate_),
                   static_cast<void*>(up_), static_cast<void*>(tmp_), static_cast<void*>(logits_),
-                  static_cast<void*>(scores_), xq_, rowinfo_, static_cast<void*>(kv_),
+                  static_cast<void*>(scores_), static_cast<void*>(argmax_scratch_), static_cast<void*>(ids_), window_,
+                  xq_, rowinfo_, static_cast<void*>(kv_),
                   static_cast<void*>(rope_table_), weights_}) {
     if (p != nullptr) axon_hip_free(p);
   }
   if (rowinfo_host_ != nullptr) axon_hip_host_free(rowinfo_host_);
+  if (window_host_ != nullptr) axon_hip_host_free(window_host_);
   for (void* e : probe_events_) axon_hip_event_destroy(e);
 }
 
@@ -433,6 +443,7 @@ Expected<std::size_t> LlamaModel::run(std::span<const Row> rows, bool copy_logit
   std::int32_t* pos = ids + R;
   std::int32_t* nvis = pos + R;
   auto* coff = reinterpret_cast<std::int64_t*>(static_cast<std::byte*>(rowinfo_host_) + align_up(12 * R, 8));
+  last_rows_ = 0;
   // The previous call's row table may still be in flight when its logits stayed on the device.
   if (axon_hip_synchronize() != AXON_HIP_OK) return device_error("synchronize");
   std::uint32_t max_vis = 0;
@@ -680,10 +691,64 @@ Expected<std::size_t> LlamaModel::run(std::span<const Row> rows, bool copy_logit
   }
 #undef DEV
   (void)R;
+  last_rows_ = n;
+  return n;
+}
+
+Expected<std::size_t> LlamaModel::greedy(std::span<std::int32_t> ids,
+                                         std::span<const std::span<const std::int32_t>> recent,
+                                         float repeat_penalty, int repeat_last_n) {
+  const std::size_t n = last_rows_;
+  if (n == 0) return make_error(ErrorCode::InvalidArgument, "greedy: no logits from a forward pass");
+  if (ids.size() != n)
+    return make_error(ErrorCode::InvalidArgument,
+                      "greedy: " + std::to_string(ids.size()) + " ids for " + std::to_string(n) + " rows of logits");
+  if (!recent.empty() && recent.size() != n)
+    return make_error(ErrorCode::InvalidArgument,
+                      "greedy: " + std::to_string(recent.size()) + " recent windows for " + std::to_string(n) + " rows");
+  last_rows_ = 0;
+  // sampler.cpp:73: the penalty runs when it is not 1 and the window is not empty.
+  std::size_t width = 0;
+  if (repeat_penalty != 1.0F && repeat_last_n > 0) {
+    for (const auto& r : recent) width = std::max(width, std::min(r.size(), static_cast<std::size_t>(repeat_last_n)));
+  }
+  if (width > kMaxPenaltyWindow)
+    return make_error(ErrorCode::InvalidArgument, "greedy: a penalty window of " + std::to_string(width) +
+                                                      " ids exceeds " + std::to_string(kMaxPenaltyWindow));
+  if (width != 0) {
+    // Row r's window is the last min(len, repeat_last_n) ids of its history, packed [n][width].
+    auto* win = static_cast<std::int32_t*>(window_host_);
+    auto* len = reinterpret_cast<std::uint32_t*>(win + n * width);
+    for (std::size_t r = 0; r < n; ++r) {
+      const std::size_t w = std::min(recent[r].size(), static_cast<std::size_t>(repeat_last_n));
+      std::copy(recent[r].end() - static_cast<std::ptrdiff_t>(w), recent[r].end(), win + r * width);
+      len[r] = static_cast<std::uint32_t>(w);
+    }
+    auto* dwin = static_cast<std::int32_t*>(window_);
+    auto* dlen = reinterpret_cast<std::uint32_t*>(dwin + n * width);
+    if (axon_hip_memcpy_h2d_async(window_, window_host_, n * (width + 1) * 4) != AXON_HIP_OK ||
+        axon_hip_repeat_penalty_rows(logits_, cfg_.n_vocab, n, cfg_.n_vocab, dwin, dlen, width, repeat_penalty) !=
+            AXON_HIP_OK)
+      return device_error("greedy: repetition penalty");
+  }
+  if (axon_hip_argmax_rows(logits_, cfg_.n_vocab, n, cfg_.n_vocab, argmax_scratch_, ids_) != AXON_HIP_OK)
+    return device_error("greedy");
+  // A synchronous copy on the library stream: the staging above is free again when it returns.
+  if (axon_hip_memcpy_d2h(ids.data(), ids_, n * 4) != AXON_HIP_OK) return device_error("greedy");
   return n;
 }
 
 Expected<std::span<const float>> LlamaModel::forward(std::span<const std::int32_t> tokens) {
+  return forward_rows(tokens, true);
+}
+
+Expected<std::size_t> LlamaModel::forward_device(std::span<const std::int32_t> tokens) {
+  auto r = forward_rows(tokens, false);
+  if (!r) return r.error();
+  return tokens.size();
+}
+
+Expected<std::span<const float>> LlamaModel::forward_rows(std::span<const std::int32_t> tokens, bool copy_logits) {
   if (tokens.empty()) return make_error(ErrorCode::InvalidArgument, "forward: empty token sequence");
   if (tokens.size() > max_seq_)
     return make_error(ErrorCode::InvalidArgument, "forward: " + std::to_string(tokens.size()) + " tokens exceed max_seq");
@@ -693,12 +758,13 @@ Expected<std::span<const float>> LlamaModel::forward(std::span<const std::int32_
       return make_error(ErrorCode::InvalidArgument, "forward: token id " + std::to_string(tokens[i]) + " outside the vocabulary");
     rows[i] = Row{tokens[i], static_cast<std::int32_t>(i), static_cast<int>(n_slots_)};
   }
-  auto r = run(rows, true);
+  auto r = run(rows, copy_logits);
   if (!r) return r.error();
   return std::span<const float>(logits_host_);
 }
 
-Expected<std::span<const float>> LlamaModel::forward_prefill(KVCache& cache, std::span<const std::int32_t> tokens) {
+Expected<std::vector<LlamaModel::Row>> LlamaModel::prefill_rows(const KVCache& cache,
+                                                                 std::span<const std::int32_t> tokens) const {
   if (tokens.empty()) return make_error(ErrorCode::InvalidArgument, "forward: empty token sequence");
   if (tokens.size() > max_seq_)
     return make_error(ErrorCode::InvalidArgument, "forward: " + std::to_string(tokens.size()) + " tokens exceed max_seq");
@@ -712,10 +778,25 @@ Expected<std::span<const float>> LlamaModel::forward_prefill(KVCache& cache, std
       return make_error(ErrorCode::InvalidArgument, "forward: token id " + std::to_string(tokens[i]) + " outside the vocabulary");
     rows[i] = Row{tokens[i], static_cast<std::int32_t>(cache.pos() + i), cache.slot()};
   }
-  auto r = run(rows, true);
+  return rows;
+}
+
+Expected<std::span<const float>> LlamaModel::forward_prefill(KVCache& cache, std::span<const std::int32_t> tokens) {
+  auto rows = prefill_rows(cache, tokens);
+  if (!rows) return rows.error();
+  auto r = run(*rows, true);
   if (!r) return r.error();
   cache.advance(tokens.size());
   return std::span<const float>(logits_host_);
+}
+
+Expected<std::size_t> LlamaModel::forward_prefill_device(KVCache& cache, std::span<const std::int32_t> tokens) {
+  auto rows = prefill_rows(cache, tokens);
+  if (!rows) return rows.error();
+  auto r = run(*rows, false);
+  if (!r) return r.error();
+  cache.advance(tokens.size());
+  return *r;
 }
 
 Expected<std::span<const float>> LlamaModel::forward_one(KVCache& cache, std::int32_t token) {

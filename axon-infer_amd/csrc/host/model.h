@@ -92,8 +92,18 @@ public:
                                                  std::span<const std::int32_t> tokens);
   // The same passes with the logits left in HBM (logits_device()), for callers that reduce
   // them on the device or time the forward pass alone.
+  Expected<std::size_t> forward_device(std::span<const std::int32_t> tokens);
+  Expected<std::size_t> forward_prefill_device(KVCache& cache, std::span<const std::int32_t> tokens);
   Expected<std::size_t> forward_batch_device(std::span<KVCache* const> caches, std::span<const std::int32_t> tokens);
   const float* logits_device() const { return logits_; }
+  // Sampler::sample at temperature zero (src/sampling/sampler.cpp:67-102) over the last pass's
+  // logits, on the device: the repetition penalty over each row's recent tokens (recent[r], the
+  // sequence's tail, prompt included; empty spans or penalty 1 turn it off), then the first
+  // maximum. One id per row of that pass into `ids`, whose size must be that row count. Only the
+  // ids cross to the host. The pass's logits are consumed: the penalty rescales them in place.
+  static constexpr std::size_t kMaxPenaltyWindow = 4096;
+  Expected<std::size_t> greedy(std::span<std::int32_t> ids, std::span<const std::span<const std::int32_t>> recent = {},
+                               float repeat_penalty = 1.0F, int repeat_last_n = 64);
 
   // A fresh cache in a free device slot, or an error when every slot is taken.
   Expected<std::unique_ptr<KVCache>> new_cache();
@@ -129,6 +139,8 @@ private:
     int slot;
   };
   Expected<std::size_t> run(std::span<const Row> rows, bool copy_logits);
+  Expected<std::span<const float>> forward_rows(std::span<const std::int32_t> tokens, bool copy_logits);
+  Expected<std::vector<Row>> prefill_rows(const KVCache& cache, std::span<const std::int32_t> tokens) const;
   Expected<std::vector<Row>> batch_rows(std::span<KVCache* const> caches, std::span<const std::int32_t> tokens) const;
   Error device_error(const char* what) const;
   int mm(const Tensor& w, const float* x, const void* xq, float* y, std::size_t n, bool accumulate);
@@ -155,6 +167,11 @@ private:
   void* rowinfo_ = nullptr;      // device: ids[R] | pos[R] | n_vis[R] | (8-aligned) cache_off[R]
   void* rowinfo_host_ = nullptr; // pinned staging of the same
   std::size_t scores_floats_ = 0;
+  std::uint64_t* argmax_scratch_ = nullptr;
+  std::int32_t* ids_ = nullptr;
+  void* window_ = nullptr;       // device: recent ids [R][kMaxPenaltyWindow] | lengths [R]
+  void* window_host_ = nullptr;  // pinned staging of the same
+  std::size_t last_rows_ = 0;  // rows of the last pass's logits, 0 after a failed pass
   std::vector<float> logits_host_;
   // Probe state (set_probe / read_probe).
   int probe_type_ = -1;

@@ -5,14 +5,17 @@ embedding/output, llama3 rope scaling; seeded random-init GGUF written by synth.
 
 Two workloads, both greedy:
   decode-b1    one sequence: a 512-token prompt is prefilled (untimed), W warm-up decode steps,
-               then K timed decode steps. One step = forward_one on the device + the logits to
-               the host + argmax, as the reference's Engine::generate loop does per token
-               (src/engine/engine.cpp:50-58). value = K / seconds.
+               then K timed decode steps. One step = forward_one on the device + the greedy
+               choice (Sampler::sample at temperature zero, src/sampling/sampler.cpp:67-102) made
+               on the device, only the token id crossing to the host: the reference's
+               Engine::generate step (src/engine/engine.cpp:50-58) with the sampler moved next to
+               the logits. value = K / seconds. The same steps with the [n_vocab] logits copied to
+               the host and argmax'd there are reported as decode_b1_host_argmax.
   ragged-32    continuous batching of 32 sequences with contexts drawn U[64, 2048] from the seed:
                eight cohorts of four join 16 steps apart, each sequence decodes 128 tokens. Joining
                sequences are prefilled in their join step (timed apart, as src/engine/batch.cpp:71-85
                runs the prefill chunk apart from forward_batch). tokens/s = decoded tokens over the
-               forward_batch time (logits to the host and argmax included).
+               forward_batch time (device greedy choice and the ids to the host included).
 
 The line also carries:
   roofline     the Q4_0 decode matvec kernel (matvec_fused_kernel<Q4_0>: q|k|v, wo, gate|up and
@@ -49,8 +52,20 @@ def log(msg: str) -> None:
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
 
-def greedy_decode(model, cache, first_logits, steps):
-    tok = int(np.argmax(first_logits[-1]))
+def prefill_greedy(model, cache, tokens):
+    """Prefill with the logits left in HBM; the last row's greedy id, chosen on the device."""
+    model.forward_prefill(cache, tokens, logits=False)
+    return int(model.greedy(len(tokens))[-1])
+
+
+def greedy_decode(model, cache, tok, steps):
+    for _ in range(steps):
+        model.forward_prefill(cache, [tok], logits=False)
+        tok = int(model.greedy(1)[0])
+    return tok
+
+
+def host_argmax_decode(model, cache, tok, steps):
     for _ in range(steps):
         logits = model.forward_prefill(cache, [tok])
         tok = int(np.argmax(logits[-1]))
@@ -62,33 +77,37 @@ def bench_decode_b1(H, model, n_vocab, steps, warmup, prompt_len, seed):
     prompt = rng.integers(0, n_vocab, prompt_len).astype(np.int32)
     cache = model.new_cache()
     t0 = time.perf_counter()
-    first = model.forward_prefill(cache, prompt)
-    H.synchronize()
+    tok = prefill_greedy(model, cache, prompt)
     prefill_s = time.perf_counter() - t0
-    tok = greedy_decode(model, cache, first, warmup)
+    tok = greedy_decode(model, cache, tok, warmup)
     H.synchronize()
     t0 = time.perf_counter()
-    logits = first
-    tok_last = tok
-    for _ in range(steps):
-        logits = model.forward_prefill(cache, [tok_last])
-        tok_last = int(np.argmax(logits[-1]))
+    tok = greedy_decode(model, cache, tok, steps)
     H.synchronize()
     elapsed = time.perf_counter() - t0
     ctx_end = model.cache_pos(cache)
+    # The same step with the logits row copied to the host and argmax'd there (the reference's
+    # placement of the sampler), over the next steps of the same sequence.
+    host_steps = min(steps, 64)
+    t0 = time.perf_counter()
+    host_argmax_decode(model, cache, tok, host_steps)
+    H.synchronize()
+    host_s = time.perf_counter() - t0
     model.free_cache(cache)
     return {"tokens_per_s": steps / elapsed, "ms_per_step": 1e3 * elapsed / steps, "prefill_tokens_per_s":
-            prompt_len / prefill_s, "context": [prompt_len + warmup, ctx_end]}
+            prompt_len / prefill_s, "context": [prompt_len + warmup, ctx_end],
+            "host_argmax": {"tokens_per_s": round(host_steps / host_s, 2),
+                            "ms_per_step": round(1e3 * host_s / host_steps, 4), "steps": host_steps}}
 
 
 def probe_pass(H, model, n_vocab, steps, prompt_len, seed, weight_type):
     rng = np.random.default_rng(seed + 1)
     prompt = rng.integers(0, n_vocab, prompt_len).astype(np.int32)
     cache = model.new_cache()
-    first = model.forward_prefill(cache, prompt)
+    tok = prefill_greedy(model, cache, prompt)
     model.probe(weight_type, True)
     model.probe_read()
-    greedy_decode(model, cache, first, steps)
+    greedy_decode(model, cache, tok, steps)
     ms, launches, nbytes = model.probe_read()
     model.probe(weight_type, False)
     model.free_cache(cache)
@@ -119,16 +138,16 @@ def bench_ragged(H, model, n_vocab, seed, n_seq=32, decode_steps=128, cohort=4, 
                 c = model.new_cache()
                 p = prompts[i]
                 for s in range(0, len(p), max_seq):
-                    logits = model.forward_prefill(c, p[s:s + max_seq])
+                    tok = prefill_greedy(model, c, p[s:s + max_seq])
                 caches[i] = c
-                next_tok[i] = int(np.argmax(logits[-1]))
+                next_tok[i] = tok
         H.synchronize()
         prefill_s += time.perf_counter() - t0
         active = [i for i in range(n_seq) if caches[i] is not None and done[i] < decode_steps]
         if active:
             t0 = time.perf_counter()
-            logits = model.forward_batch([caches[i] for i in active], [next_tok[i] for i in active])
-            toks = np.argmax(logits, axis=1)
+            model.forward_batch([caches[i] for i in active], [next_tok[i] for i in active], logits=False)
+            toks = model.greedy(len(active))
             decode_s += time.perf_counter() - t0
             for j, i in enumerate(active):
                 next_tok[i] = int(toks[j])
@@ -270,6 +289,7 @@ def main() -> int:
                           "achieved": round(q6_gbs, 1), "frac": round(q6_gbs / HBM_PEAK_GBS, 4),
                           "avg_us": round(1e3 * q6_ms / max(q6_n, 1), 3)},
         "prefill_tokens_per_s": round(b1["prefill_tokens_per_s"], 1),
+        "decode_b1_host_argmax": b1["host_argmax"],
         "cpu_baseline": None,
     }
     if not args.no_ragged:

@@ -160,6 +160,18 @@ int axon_hip_quantize_rows_q8_0(const float* x, void* out, size_t n, size_t n_ro
 int axon_hip_silu_mul_rows(const float* gate, const float* up, float* out, void* outq, size_t n, size_t n_rows);
 /* x += y (add_rows, llama.cpp:122-126). */
 int axon_hip_add(float* x, const float* y, size_t n);
+/* Greedy selection on the device (src/sampling/sampler.cpp:100-102 with the repetition penalty
+ * off): out[r] = std::ranges::max_element over row r of x (rows stride floats apart): the first
+ * maximum; NaN is skipped, but a NaN first element selects 0. n >= 1. scratch: device words,
+ * axon_hip_argmax_scratch_words(n_rows) of them. */
+size_t axon_hip_argmax_scratch_words(size_t n_rows);
+/* The repetition penalty in place (src/sampling/sampler.cpp:73-97): for each row r, every distinct
+ * id in [0, n) among recent[r * recent_stride + i], i < min(recent_len[r], recent_stride), gets
+ * logit > 0 ? logit / penalty : logit * penalty, once. recent and recent_len are device arrays
+ * holding each row's window (the last repeat_last_n ids), which the caller cuts. */
+int axon_hip_repeat_penalty_rows(float* x, size_t n, size_t n_rows, size_t stride, const int32_t* recent,
+                                 const uint32_t* recent_len, size_t recent_stride, float penalty);
+int axon_hip_argmax_rows(const float* x, size_t n, size_t n_rows, size_t stride, uint64_t* scratch, int32_t* out);
 /* Y_s[n_rows][n_out_s] (+)= X W_s^T for up to three weights of one type sharing one Q8_0
  * input (mm_fused, llama.cpp:425-472). w[s], y[s] device pointers in host arrays. Rows below
  * 16 run the v_dot4 matvec, 16 and more the int8 MFMA tiles. accumulate adds into y (the

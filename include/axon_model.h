@@ -54,10 +54,21 @@ int axon_model_cache_truncate(axon_model* model, int cache, size_t pos);
 /* Rows [0, n) of layer l's keys (values = 0) or values (1) of a cache, to the host. */
 int axon_model_cache_read(axon_model* model, int cache, size_t layer, int values, size_t n, float* out);
 
-/* The passes. logits: host [n][n_vocab], or NULL to leave them in HBM (timing). */
+/* The passes. logits: host [n][n_vocab], or NULL to leave them in HBM for axon_model_greedy (or
+ * for timing the pass alone). */
 int axon_model_forward(axon_model* model, const int32_t* tokens, size_t n, float* logits);
 int axon_model_forward_prefill(axon_model* model, int cache, const int32_t* tokens, size_t n, float* logits);
 int axon_model_forward_batch(axon_model* model, const int* caches, const int32_t* tokens, size_t n, float* logits);
+
+/* Sampler::sample at temperature zero on the device (src/sampling/sampler.cpp:67-102) over the
+ * last pass's logits, which may have stayed in HBM (logits NULL): the repetition penalty over
+ * each row's recent tokens, then std::ranges::max_element per row. recent: n host pointers to
+ * each row's token history (prompt included) with recent_len[i] ids, or NULL for no penalty;
+ * the window is its last repeat_last_n ids (at most 4096), and repeat_penalty 1 turns it off.
+ * n must be the pass's row count. The pass's logits are consumed (rescaled in place); only the
+ * n ids cross to the host. */
+int axon_model_greedy(axon_model* model, const int32_t* const* recent, const size_t* recent_len, float repeat_penalty,
+                      int repeat_last_n, int32_t* ids, size_t n);
 
 /* Kernel-time probe (measurement only): while enabled, the kernel of every matmul on weights of
  * ggml type `type` records its dispatch's start and end on HIP events (axon_hip_probe_next_launch);

@@ -291,24 +291,28 @@ static int by_logit_desc(const void* pa, const void* pb) {
   return a < b ? -1 : (a > b);
 }
 
+void ora_repeat_penalty(float* sl, size_t n, const int32_t* recent, size_t n_recent, float penalty,
+                        int repeat_last_n, uint8_t* touched) {
+  if (penalty == 1.0f || repeat_last_n <= 0 || n_recent == 0) return;
+  const size_t window = n_recent < (size_t)repeat_last_n ? n_recent : (size_t)repeat_last_n;
+  const int32_t* tail = recent + (n_recent - window);
+  for (size_t t = 0; t < window; ++t) {
+    const int32_t id = tail[t];
+    if (id < 0 || (size_t)id >= n || touched[id]) continue;
+    touched[id] = 1;
+    float* logit = &sl[id];
+    *logit = *logit > 0.0f ? *logit / penalty : *logit * penalty;
+  }
+  for (size_t t = 0; t < window; ++t)
+    if (tail[t] >= 0 && (size_t)tail[t] < n) touched[tail[t]] = 0;
+}
+
 int32_t ora_sample(const ora_sampler_config* c, ora_rng* rng, const float* logits, int32_t n_vocab,
                    const int32_t* recent, size_t n_recent, float* sl, int32_t* order, double* probs,
                    uint8_t* touched) {
   const size_t n = (size_t)n_vocab;
   memcpy(sl, logits, n * sizeof(float));
-  if (c->repeat_penalty != 1.0f && c->repeat_last_n > 0 && n_recent > 0) {
-    const size_t window = n_recent < (size_t)c->repeat_last_n ? n_recent : (size_t)c->repeat_last_n;
-    const int32_t* tail = recent + (n_recent - window);
-    for (size_t t = 0; t < window; ++t) {
-      const int32_t id = tail[t];
-      if (id < 0 || (size_t)id >= n || touched[id]) continue;
-      touched[id] = 1;
-      float* logit = &sl[id];
-      *logit = *logit > 0.0f ? *logit / c->repeat_penalty : *logit * c->repeat_penalty;
-    }
-    for (size_t t = 0; t < window; ++t)
-      if (tail[t] >= 0 && (size_t)tail[t] < n) touched[tail[t]] = 0;
-  }
+  ora_repeat_penalty(sl, n, recent, n_recent, c->repeat_penalty, c->repeat_last_n, touched);
   if (c->temperature <= 0.0f) {
     size_t best = 0;
     for (size_t i = 1; i < n; ++i)

@@ -21,6 +21,10 @@
  *   model forward ........... fixtures model/synthetic-2l*.logits (F32 GGUF, 1e-4) and
  *                             the reference's own LlamaModel built under oracle/_ref
  *   all table entries ....... bit-exact against the reference's own scalar table (oracle/_ref)
+ *   sampler (rng, penalty, greedy, top-k/top-p/min-p draws) ... the reference's sampler test
+ *                             cases (test_sampler.cpp:35-135), np.argmax (first maximum) on NaN-free
+ *                             rows, hand-worked NaN rows, and the reference's own Sampler
+ *                             (oracle/_ref) draw for draw on random rows, windows and seeds
  */
 #ifndef AXON_ORACLE_H
 #define AXON_ORACLE_H
@@ -177,6 +181,12 @@ typedef struct {
 int32_t ora_sample(const ora_sampler_config* c, ora_rng* rng, const float* logits, int32_t n_vocab,
                    const int32_t* recent, size_t n_recent, float* scratch_logits,
                    int32_t* scratch_order, double* scratch_probs, uint8_t* scratch_touched);
+
+/* The repetition penalty alone (sampler.cpp:73-97), in place on n logits: each distinct id in
+ * [0, n) of the last min(n_recent, repeat_last_n) ids, once, when penalty != 1 and
+ * repeat_last_n > 0. touched: n zeroed bytes, left zeroed. ora_sample runs it first. */
+void ora_repeat_penalty(float* logits, size_t n, const int32_t* recent, size_t n_recent, float penalty,
+                        int repeat_last_n, uint8_t* touched);
 
 #ifdef __cplusplus
 }

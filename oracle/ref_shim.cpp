@@ -6,6 +6,7 @@
 #include "kernels/kernels.h"
 #include "model/kv_cache.h"
 #include "model/llama.h"
+#include "axon/sampler.h"
 
 #include <cstddef>
 #include <cstdint>
@@ -170,6 +171,24 @@ int ref_forward_batch(void* h, const int* cache_ids, const std::int32_t* tokens,
     caches[i] = m->caches[cache_ids[i]].get();
   }
   return copy_logits(m->model->forward_batch(caches, std::span<const std::int32_t>(tokens, n)), logits);
+}
+
+// `draws` calls of Sampler::sample (src/sampling/sampler.cpp:160-183) with one configuration,
+// seed and row of logits, into out[draws].
+void ref_sample(const float* logits, size_t n, const std::int32_t* recent, size_t n_recent, float temperature,
+                int top_k, float top_p, float min_p, float repeat_penalty, int repeat_last_n, std::uint64_t seed,
+                size_t draws, std::int32_t* out) {
+  axon::SamplerConfig cfg;
+  cfg.temperature = temperature;
+  cfg.top_k = top_k;
+  cfg.top_p = top_p;
+  cfg.min_p = min_p;
+  cfg.repeat_penalty = repeat_penalty;
+  cfg.repeat_last_n = repeat_last_n;
+  cfg.seed = seed;
+  axon::Sampler sampler(cfg, static_cast<std::int32_t>(n));
+  for (size_t i = 0; i < draws; ++i)
+    out[i] = sampler.sample(std::span<const float>(logits, n), std::span<const std::int32_t>(recent, n_recent));
 }
 
 }  // extern "C"
