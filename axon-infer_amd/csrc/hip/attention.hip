@@ -698,6 +698,279 @@ __global__ __launch_bounds__(G * 64) void attn_mixg_kernel(AttnArgs a) {
   }
 }
 
+// One workgroup per (row, kv head, 32-dim half of the head), for decode rows of an fp32 cache
+// with 64-dim heads. Against attn_mixg_kernel it changes where the work runs, not the float
+// operations or their order:
+//   - V streams through a deep LDS ring (up to 96 KB) filled by LDS-DMA, only the half of each
+//     V row this workgroup mixes (128 bytes). A copy moves 8 positions (64 lanes x 16 bytes), a
+//     tile is 4 copies (32 positions), issued by the first min(G, 4) waves. Only tiles below
+//     n_vis are copied; the waits count the copies actually issued.
+//   - Two waves per head run the softmax: wave (head, s) holds the double partial sums
+//     part[2s] and part[2s + 1] of the fixed tree (part[q] takes positions lane + 64 q + 256 k,
+//     k ascending), on registers, and the head's max and sum meet in LDS. The sum is
+//     part[0] + part[1] + part[2] + part[3] in that order, as everywhere else.
+//   - The chains run on ceil(G / 2) waves, wave c holding heads 2c (lanes 0..31) and 2c + 1
+//     (lanes 32..63) of one dim each, so one LDS read of a V value serves two heads. They run
+//     over half a ring at a time between one wait and two barriers, and form the 32 products of
+//     tile t + 1 while they add those of tile t (each product rounds to float before its add,
+//     so the bits are those of acc += p * v).
+constexpr uint32_t kDTile = 32;                // positions per tile (4 KB)
+constexpr uint32_t kSPer = kMixMaxVis / 256;   // positions per lane per partial sum
+
+template <int G>
+struct MixD {
+  static constexpr uint32_t kCw = G < 4 ? G : 4;              // copying waves
+  static constexpr uint32_t kCmax = (4 + kCw - 1) / kCw;      // most copies per wave per tile
+  static constexpr uint32_t kBudget = 163840 - G * kMixMaxVis * 4 - 512;  // LDS beside p
+  static constexpr uint32_t kR0 = (kBudget < 98304 ? kBudget : 98304) / (kDTile * 128);
+  // Tiles in flight, even (two halves). A wave holds at most kMixMaxVis / 128 score copies and
+  // kRing * kCmax V copies outstanding, within the 63 that vmcnt counts (and the 31 that
+  // wait_vm_upto waits on).
+  static constexpr uint32_t kRing = (kR0 * kCmax > 27 ? 27 / kCmax : kR0) & ~1u;
+};
+
+template <int G>
+size_t mixd_lds(uint32_t max_vis) {
+  return static_cast<size_t>(MixD<G>::kRing) * kDTile * 128 + static_cast<size_t>(G) * mixg_pitch(max_vis) * 4 + 512;
+}
+
+// s_waitcnt vmcnt(n) for a wave-uniform n; counts above 31 wait for 31 (a stricter wait).
+__device__ __forceinline__ void wait_vm_upto(uint32_t n) {
+  n = __builtin_amdgcn_readfirstlane(n);
+#define AXON_WAIT_CASE(k) \
+  case k: wait_vm<k>(); return;
+  switch (n) {
+    AXON_WAIT_CASE(0) AXON_WAIT_CASE(1) AXON_WAIT_CASE(2) AXON_WAIT_CASE(3) AXON_WAIT_CASE(4) AXON_WAIT_CASE(5)
+    AXON_WAIT_CASE(6) AXON_WAIT_CASE(7) AXON_WAIT_CASE(8) AXON_WAIT_CASE(9) AXON_WAIT_CASE(10) AXON_WAIT_CASE(11)
+    AXON_WAIT_CASE(12) AXON_WAIT_CASE(13) AXON_WAIT_CASE(14) AXON_WAIT_CASE(15) AXON_WAIT_CASE(16)
+    AXON_WAIT_CASE(17) AXON_WAIT_CASE(18) AXON_WAIT_CASE(19) AXON_WAIT_CASE(20) AXON_WAIT_CASE(21)
+    AXON_WAIT_CASE(22) AXON_WAIT_CASE(23) AXON_WAIT_CASE(24) AXON_WAIT_CASE(25) AXON_WAIT_CASE(26)
+    AXON_WAIT_CASE(27) AXON_WAIT_CASE(28) AXON_WAIT_CASE(29) AXON_WAIT_CASE(30)
+    default: wait_vm<31>(); return;
+  }
+#undef AXON_WAIT_CASE
+}
+
+template <int G>
+__global__ __launch_bounds__(G * 128) void attn_mixd_kernel(AttnArgs a) {
+  using M = MixD<G>;
+  constexpr uint32_t kR = M::kRing;
+  constexpr uint32_t kCw = M::kCw;
+  constexpr uint32_t kH = kR / 2;
+  static_assert(kR >= 4 && kR * M::kCmax <= 27, "ring depth");
+  extern __shared__ __attribute__((aligned(16))) float lds[];
+  float* ring = lds;                                   // [kR][kDTile][32]
+  float* pbase = lds + kR * kDTile * 32;               // [G][pitch]
+  const uint32_t pitch = mixg_pitch(a.max_vis);
+  float* red_m = pbase + G * pitch;                       // [G][2] maxima (64 bytes)
+  double* red_s = reinterpret_cast<double*>(red_m + 16);  // [G][4] partial sums (256 bytes)
+  const uint32_t tid = threadIdx.x;
+  const uint32_t lane = tid & 63u;
+  const uint32_t w = tid >> 6;
+  const uint32_t r = blockIdx.x;
+  const uint32_t g = blockIdx.y;
+  const uint32_t half = blockIdx.z;
+  const uint32_t n_vis = a.n_vis != nullptr ? static_cast<uint32_t>(a.n_vis[r]) : static_cast<uint32_t>(a.n_past) + r + 1;
+  const size_t kv_row = static_cast<size_t>(a.n_kv) * 64;
+  const int64_t v_off = (a.v_off != nullptr ? a.v_off[r] : 0) + a.v_off_c;
+
+  // Softmax role: head sh, partial sums 2 ss and 2 ss + 1.
+  const uint32_t sh = w >> 1, ss = w & 1u;
+  float* p = pbase + sh * pitch;
+  const float* s = a.scratch + (static_cast<size_t>(r) * a.n_head + g * G + sh) * a.max_vis;
+  const uint32_t p_lds = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(as_lds(p)));
+  const RsrcWords ssrc = raw_buffer_words(s, n_vis * 4);
+  // This wave's score groups (64 positions each): j0 = 64 (2 ss + i % 2) + 256 (i / 2).
+  for (uint32_t i = 0;; ++i) {
+    const uint32_t j0 = 64 * (2 * ss + (i & 1u)) + 256 * (i >> 1);
+    if (j0 >= n_vis) break;
+    lds_dma4(ssrc, 4 * (j0 + lane), p_lds + 4 * j0);
+  }
+
+  const float* vbase = reinterpret_cast<const float*>(a.kv) + v_off + g * 64 + half * 32;
+  const RsrcWords rsrc =
+      raw_buffer_words(vbase, static_cast<uint32_t>((static_cast<size_t>(n_vis - 1) * kv_row + 32) * 4));
+  const uint32_t ring_lds = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(as_lds(ring)));
+  const uint32_t n_tiles = (n_vis + kDTile - 1) / kDTile;
+  // Copy k (0..3) of a tile moves its positions 8k .. 8k + 7 (lane / 8 picks the position,
+  // lane % 8 the 16 bytes); wave w < kCw issues k = w, w + kCw, ... A tile wholly below n_vis
+  // takes this lane's fixed offsets plus a uniform tile offset; the last tile clamps each
+  // position to the last one.
+  const uint32_t copies = w < kCw ? (4 - w + kCw - 1) / kCw : 0;  // this wave's copies per tile
+  const uint32_t row_bytes = static_cast<uint32_t>(kv_row * 4);
+  const uint32_t lane_row = lane / 8, lane_byte = (lane % 8) * 16;
+  auto copy_tile = [&](uint32_t t) {
+    if (t >= n_tiles) return;
+    const uint32_t dst = ring_lds + (t % kR) * kDTile * 128;
+    const bool whole = (t + 1) * kDTile <= n_vis;
+    for (uint32_t k = w; k < 4 && w < kCw; k += kCw) {
+      if (whole) {
+        lds_dma16_so(rsrc, (8 * k + lane_row) * row_bytes + lane_byte, t * kDTile * row_bytes, dst + k * 1024);
+      } else {
+        const uint32_t row = min(t * kDTile + 8 * k + lane_row, n_vis - 1);
+        lds_dma16(rsrc, row * row_bytes + lane_byte, dst + k * 1024);
+      }
+    }
+  };
+  for (uint32_t t = 0; t < kR; ++t) copy_tile(t);
+  // Waiting for tile u leaves the copies of the tiles issued after it outstanding.
+  auto wait_tile = [&](uint32_t u, uint32_t issued) { wait_vm_upto(issued > u + 1 ? (issued - u - 1) * copies : 0); };
+
+  // Softmax. x[2 k + i] holds position lane + 64 (2 ss + i) + 256 k; positions past n_vis hold
+  // -inf, whose exponential adds an exact zero to the double sums.
+  wait_vm_upto(min(n_tiles, kR) * copies);  // the scores, older than every V copy
+  float x[2 * kSPer];
+#pragma unroll
+  for (uint32_t k = 0; k < kSPer; ++k) {
+#pragma unroll
+    for (uint32_t i = 0; i < 2; ++i) {
+      const uint32_t j0 = 64 * (2 * ss + i) + 256 * k;
+      if (j0 < n_vis) {
+        const float v = p[j0 + lane];
+        x[2 * k + i] = j0 + lane < n_vis ? v : -INFINITY;
+      }
+    }
+  }
+  float m = -INFINITY;
+#pragma unroll
+  for (uint32_t k = 0; k < kSPer; ++k) {
+#pragma unroll
+    for (uint32_t i = 0; i < 2; ++i) {
+      if (64 * (2 * ss + i) + 256 * k < n_vis) m = fmaxf(m, x[2 * k + i]);
+    }
+  }
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off, 64));
+  if (lane == 0) red_m[2 * sh + ss] = m;
+  __syncthreads();
+  m = fmaxf(red_m[2 * sh], red_m[2 * sh + 1]);
+  double part[2] = {0.0, 0.0};
+#pragma unroll
+  for (uint32_t k = 0; k < kSPer; ++k) {
+#pragma unroll
+    for (uint32_t i = 0; i < 2; ++i) {
+      if (64 * (2 * ss + i) + 256 * k < n_vis) {
+        x[2 * k + i] = exp_rounded(x[2 * k + i] - m);
+        part[i] += static_cast<double>(x[2 * k + i]);
+      }
+    }
+  }
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) {
+    part[0] += __shfl_xor(part[0], off, 64);
+    part[1] += __shfl_xor(part[1], off, 64);
+  }
+  if (lane == 0) {
+    red_s[4 * sh + 2 * ss] = part[0];
+    red_s[4 * sh + 2 * ss + 1] = part[1];
+  }
+  __syncthreads();
+  double sum = 0.0;
+#pragma unroll
+  for (int q = 0; q < 4; ++q) sum += red_s[4 * sh + q];
+  const float inv = static_cast<float>(1.0 / sum);
+#pragma unroll
+  for (uint32_t k = 0; k < kSPer; ++k) {
+#pragma unroll
+    for (uint32_t i = 0; i < 2; ++i) {
+      const uint32_t j0 = 64 * (2 * ss + i) + 256 * k;
+      if (j0 < n_vis) p[j0 + lane] = x[2 * k + i] * inv;
+    }
+  }
+
+  // Value mix, positions in order, half a ring at a time.
+  constexpr uint32_t kChains = (G + 1) / 2;  // chain waves
+  const uint32_t d = lane & 31u;
+  const uint32_t hl = 2 * w + (lane >> 5);  // this lane's head within the group
+  const bool chain = w < kChains;
+  const bool live = hl < G;
+  const float* ph = pbase + (live ? hl : 2 * w) * pitch;  // its probabilities
+  float acc = 0.0f;
+  float va[kDTile], pa[kDTile], vb[kDTile], pb[kDTile];
+  auto load_tile = [&](uint32_t t, float (&v)[kDTile], float (&pp)[kDTile]) {
+    const float* vt = ring + (t % kR) * kDTile * 32 + d;
+    const float* pt = ph + t * kDTile;
+#pragma unroll
+    for (uint32_t i = 0; i < kDTile; ++i) v[i] = vt[i * 32];
+#pragma unroll
+    for (uint32_t i = 0; i < kDTile; i += 4) {
+      const float4 q4 = *reinterpret_cast<const float4*>(pt + i);
+      pp[i] = q4.x;
+      pp[i + 1] = q4.y;
+      pp[i + 2] = q4.z;
+      pp[i + 3] = q4.w;
+    }
+  };
+  auto mul_tile = [&](float (&v)[kDTile], const float (&pp)[kDTile]) {
+#pragma unroll
+    for (uint32_t i = 0; i < kDTile; ++i) v[i] = pp[i] * v[i];
+  };
+  auto add_tile = [&](const float (&prod)[kDTile], uint32_t t) {
+    const uint32_t cnt = min(kDTile, n_vis - t * kDTile);
+    if (cnt == kDTile) {
+#pragma unroll
+      for (uint32_t i = 0; i < kDTile; ++i) acc += prod[i];
+    } else {
+      for (uint32_t i = 0; i < cnt; ++i) acc += prod[i];
+    }
+  };
+  uint32_t issued = min(n_tiles, kR);
+  for (uint32_t t0 = 0; t0 < n_tiles; t0 += kH) {
+    const uint32_t t1 = min(n_tiles, t0 + kH);
+    wait_tile(t1 - 1, issued);
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    __syncthreads();  // everyone's copies of [t0, t1), and (first time) every p write
+    if (chain) {
+      // Tile t + 1 is read while tile t's products are added, and its products are formed
+      // after them, so neither the LDS reads nor the multiplies stall the adds.
+      load_tile(t0, va, pa);
+      mul_tile(va, pa);
+      for (uint32_t t = t0; t < t1; t += 2) {
+        if (t + 1 < t1) load_tile(t + 1, vb, pb);
+        add_tile(va, t);
+        if (t + 1 < t1) {
+          mul_tile(vb, pb);
+          if (t + 2 < t1) load_tile(t + 2, va, pa);
+          add_tile(vb, t + 1);
+          if (t + 2 < t1) mul_tile(va, pa);
+        }
+      }
+    }
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    __syncthreads();  // every wave is done with the half [t0, t1)
+    for (uint32_t t = t0 + kR; t < t1 + kR; ++t) copy_tile(t);
+    issued = min(n_tiles, t1 + kR);
+  }
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // no copy outlives the workgroup
+  if (chain && live) {
+    const size_t col = static_cast<size_t>(g * G + hl) * 64 + half * 32 + d;
+    a.out[static_cast<size_t>(r) * a.out_stride + col] = acc;
+    if (a.outq != nullptr) {
+      const size_t nbq = a.out_stride / kQK;
+      quantize_block_lanes(acc, d, a.outq + (static_cast<size_t>(r) * nbq + col / kQK) * kBytesQ8_0);
+    }
+  }
+}
+
+// Dynamic LDS above 64 KB must be granted per kernel; 0 when the device cannot.
+template <int G>
+size_t mixd_lds_granted(uint32_t max_vis) {
+  static int limit = -1;
+  if (limit < 0) {
+    int dev = 0, v = 0;
+    limit = (hipGetDevice(&dev) == hipSuccess &&
+             hipDeviceGetAttribute(&v, hipDeviceAttributeMaxSharedMemoryPerBlock, dev) == hipSuccess)
+                ? v
+                : 65536;
+    const int want = static_cast<int>(mixd_lds<G>(kMixMaxVis));
+    if (hipFuncSetAttribute(reinterpret_cast<const void*>(attn_mixd_kernel<G>),
+                            hipFuncAttributeMaxDynamicSharedMemorySize, std::min(want, limit)) != hipSuccess)
+      limit = 65536;
+  }
+  const size_t need = mixd_lds<G>(max_vis);
+  return need <= static_cast<size_t>(limit) ? need : 0;
+}
+
 bool scores_fit_lds(const AttnArgs& a) {
   const uint32_t group = a.n_head / a.n_kv;
   return static_cast<size_t>(group) * (a.head_dim + a.max_vis) * 4 <= kLdsScores;
@@ -733,7 +1006,17 @@ int attention_launch(const AttnArgs& a, uint32_t n_rows) {
     hipLaunchKernelGGL(attn_scores64_kernel, sgrid, dim3(group * 64), slds, stream(), a);
     const size_t glds = mixg_lds(group, a.max_vis);
     const dim3 ggrid(n_rows, a.n_kv);
-    if (glds <= 65536 && (group == 1 || group == 2 || group == 4 || group == 8)) {
+    const dim3 dgrid(n_rows, a.n_kv, 2);
+    size_t dlds = 0;
+    if (group == 4 && (dlds = mixd_lds_granted<4>(a.max_vis)) != 0) {
+      hipLaunchKernelGGL(attn_mixd_kernel<4>, dgrid, dim3(512), dlds, stream(), a);
+    } else if (group == 8 && (dlds = mixd_lds_granted<8>(a.max_vis)) != 0) {
+      hipLaunchKernelGGL(attn_mixd_kernel<8>, dgrid, dim3(1024), dlds, stream(), a);
+    } else if (group == 3 && (dlds = mixd_lds_granted<3>(a.max_vis)) != 0) {
+      hipLaunchKernelGGL(attn_mixd_kernel<3>, dgrid, dim3(384), dlds, stream(), a);
+    } else if (group == 7 && (dlds = mixd_lds_granted<7>(a.max_vis)) != 0) {
+      hipLaunchKernelGGL(attn_mixd_kernel<7>, dgrid, dim3(896), dlds, stream(), a);
+    } else if (glds <= 65536 && (group == 1 || group == 2 || group == 4 || group == 8)) {
       if (group == 1) hipLaunchKernelGGL(attn_mixg_kernel<1>, ggrid, dim3(64), glds, stream(), a);
       if (group == 2) hipLaunchKernelGGL(attn_mixg_kernel<2>, ggrid, dim3(128), glds, stream(), a);
       if (group == 4) hipLaunchKernelGGL(attn_mixg_kernel<4>, ggrid, dim3(256), glds, stream(), a);
