@@ -715,13 +715,16 @@ __global__ __launch_bounds__(G * 64) void attn_mixg_kernel(AttnArgs a) {
 //     tile t + 1 while they add those of tile t (each product rounds to float before its add,
 //     so the bits are those of acc += p * v).
 constexpr uint32_t kDTile = 32;                // positions per tile (4 KB)
+// Rows of p hold whole 64-position copies; 4 more floats put the two heads a chain wave reads
+// in different LDS banks.
+__host__ __device__ inline uint32_t mixd_pitch(uint32_t max_vis) { return ((max_vis + 63) & ~63u) + 4; }
 constexpr uint32_t kSPer = kMixMaxVis / 256;   // positions per lane per partial sum
 
 template <int G>
 struct MixD {
   static constexpr uint32_t kCw = G < 4 ? G : 4;              // copying waves
   static constexpr uint32_t kCmax = (4 + kCw - 1) / kCw;      // most copies per wave per tile
-  static constexpr uint32_t kBudget = 163840 - G * kMixMaxVis * 4 - 512;  // LDS beside p
+  static constexpr uint32_t kBudget = 163840 - G * (kMixMaxVis + 4) * 4 - 512;  // LDS beside p
   static constexpr uint32_t kR0 = (kBudget < 98304 ? kBudget : 98304) / (kDTile * 128);
   // Tiles in flight, even (two halves). A wave holds at most kMixMaxVis / 128 score copies and
   // kRing * kCmax V copies outstanding, within the 63 that vmcnt counts (and the 31 that
@@ -731,7 +734,7 @@ struct MixD {
 
 template <int G>
 size_t mixd_lds(uint32_t max_vis) {
-  return static_cast<size_t>(MixD<G>::kRing) * kDTile * 128 + static_cast<size_t>(G) * mixg_pitch(max_vis) * 4 + 512;
+  return static_cast<size_t>(MixD<G>::kRing) * kDTile * 128 + static_cast<size_t>(G) * mixd_pitch(max_vis) * 4 + 512;
 }
 
 // s_waitcnt vmcnt(n) for a wave-uniform n; counts above 31 wait for 31 (a stricter wait).
@@ -761,7 +764,7 @@ __global__ __launch_bounds__(G * 128) void attn_mixd_kernel(AttnArgs a) {
   extern __shared__ __attribute__((aligned(16))) float lds[];
   float* ring = lds;                                   // [kR][kDTile][32]
   float* pbase = lds + kR * kDTile * 32;               // [G][pitch]
-  const uint32_t pitch = mixg_pitch(a.max_vis);
+  const uint32_t pitch = mixd_pitch(a.max_vis);
   float* red_m = pbase + G * pitch;                       // [G][2] maxima (64 bytes)
   double* red_s = reinterpret_cast<double*>(red_m + 16);  // [G][4] partial sums (256 bytes)
   const uint32_t tid = threadIdx.x;

@@ -27,6 +27,12 @@ The line also carries:
   cpu_baseline the reference's own LlamaModel on its scalar table (oracle/_ref, compiled from the
                reference sources) on the same GGUF, threads = the host's cores, on a bounded sample.
 
+  traffic      HBM bytes per launch of that kernel, from two rocprofv3 counter passes over
+               `bench.py --traffic-probe` (FETCH_SIZE, then WRITE_SIZE, KiB per dispatch), each
+               scaled by what the same counter reads for a device-to-device copy of 256 MiB in the
+               same process; `bench.py --traffic-summary FETCH_CSV WRITE_CSV` reduces the two
+               counter files to profiles/traffic_matvec_q4_0.json, which this line reports.
+
 Prints one JSON line. --gpus above 1 exits: this build measures one GPU.
 """
 from __future__ import annotations
@@ -45,6 +51,9 @@ sys.path.insert(0, str(ROOT / "axon-infer_amd"))
 sys.path.insert(0, str(ROOT / "tests"))
 
 HBM_PEAK_GBS = 8000.0
+TRAFFIC_FILE = ROOT / "profiles" / "traffic_matvec_q4_0.json"
+COPY_BYTES = 256 << 20
+MATVEC_KERNEL = "matvec_dma_kernel<2>"  # Q4_0 is ggml type 2
 METRIC = "decode tokens/s + HBM GB/s (% peak), Q4_0 1B model, batch 1 and 32 ragged"
 
 
@@ -163,6 +172,64 @@ def bench_ragged(H, model, n_vocab, seed, n_seq=32, decode_steps=128, cohort=4, 
             "contexts": {"min": int(ctx.min()), "mean": float(ctx.mean()), "max": int(ctx.max())}}
 
 
+def traffic_probe(H, model, n_vocab, steps, prompt_len, seed):
+    """The workload of the counter passes: one device-to-device copy of COPY_BYTES (the
+    calibration), then a prefill and `steps` greedy decode steps of decode-b1."""
+    src, dst = H.DeviceBuffer(COPY_BYTES), H.DeviceBuffer(COPY_BYTES)
+    src.fill(1)
+    H.call("memcpy_d2d", dst, src, COPY_BYTES)
+    H.synchronize()
+    src.free()
+    dst.free()
+    rng = np.random.default_rng(seed + 3)
+    cache = model.new_cache()
+    tok = prefill_greedy(model, cache, rng.integers(0, n_vocab, prompt_len).astype(np.int32))
+    greedy_decode(model, cache, tok, steps)
+    H.synchronize()
+    model.free_cache(cache)
+
+
+def _counter_rows(path):
+    """(kernel name, counter name, value) of every dispatch in a rocprofv3 counter CSV."""
+    import csv
+    with open(path, newline="") as f:
+        for row in csv.DictReader(f):
+            keys = {k.lower(): k for k in row}
+            yield (row[keys["kernel_name"]], row[keys["counter_name"]], float(row[keys["counter_value"]]))
+
+
+def traffic_summary(fetch_csv, write_csv):
+    """Per-dispatch FETCH_SIZE and WRITE_SIZE (KiB) of the Q4_0 decode matvec, each scaled by
+    the counter's reading for the calibration copy (COPY_BYTES read and written)."""
+    def per_kernel(path, counter):
+        copy, mv = [], []
+        for name, cname, value in _counter_rows(path):
+            if cname != counter:
+                continue
+            if "copyBuffer" in name:
+                copy.append(value)
+            elif MATVEC_KERNEL in name.replace(" ", ""):
+                mv.append(value)
+        if not copy or not mv:
+            raise SystemExit(f"{path}: no {counter} rows for the copy ({len(copy)}) or {MATVEC_KERNEL} ({len(mv)})")
+        return max(copy), mv
+    fcopy, fmv = per_kernel(fetch_csv, "FETCH_SIZE")
+    wcopy, wmv = per_kernel(write_csv, "WRITE_SIZE")
+    f_scale = COPY_BYTES / (fcopy * 1024.0)
+    w_scale = COPY_BYTES / (wcopy * 1024.0)
+    fetch = float(np.mean(fmv)) * 1024.0 * f_scale
+    write = float(np.mean(wmv)) * 1024.0 * w_scale
+    out = {"kernel": MATVEC_KERNEL, "dispatches": len(fmv),
+           "fetch_bytes_per_launch": round(fetch), "write_bytes_per_launch": round(write),
+           "traffic_bytes_per_launch": round(fetch + write),
+           "copy_bytes": COPY_BYTES, "copy_fetch_kib": fcopy, "copy_write_kib": wcopy,
+           "fetch_scale": round(f_scale, 4), "write_scale": round(w_scale, 4),
+           "counters": [str(fetch_csv), str(write_csv)]}
+    TRAFFIC_FILE.write_text(json.dumps(out, indent=1) + "\n")
+    print(json.dumps(out))
+    return 0
+
+
 def host_cores() -> int:
     try:
         return len(os.sched_getaffinity(0))
@@ -230,7 +297,13 @@ def main() -> int:
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-ragged", action="store_true", help="skip the 32-sequence workload")
     ap.add_argument("--cpu-budget", type=float, default=12.0, help="seconds per CPU baseline sample")
+    ap.add_argument("--traffic-probe", action="store_true",
+                    help="run the workload of the FETCH_SIZE / WRITE_SIZE counter passes and exit")
+    ap.add_argument("--traffic-summary", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"),
+                    help=f"reduce the two counter passes to {TRAFFIC_FILE.relative_to(ROOT)} and exit")
     args = ap.parse_args()
+    if args.traffic_summary:
+        return traffic_summary(*args.traffic_summary)
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU; --gpus {args.gpus} is not supported "
               "(the path would shard by sequence, see DESIGN.md)", file=sys.stderr)
@@ -249,6 +322,11 @@ def main() -> int:
     info = model.info
     log(f"loaded on the {model.table_name} table: {info.device_bytes / 1e9:.2f} GB in HBM, "
         f"{info.weight_bytes_per_token / 1e6:.2f} MB of weights per token")
+    if args.traffic_probe:
+        traffic_probe(H, model, info.n_vocab, min(args.steps, 16), args.prompt, args.seed)
+        model.close()
+        log("traffic probe done")
+        return 0
 
     b1 = bench_decode_b1(H, model, info.n_vocab, args.steps, args.warmup, args.prompt, args.seed)
     log(f"decode-b1: {b1['tokens_per_s']:.1f} tok/s ({b1['ms_per_step']:.3f} ms/step)")
@@ -280,7 +358,7 @@ def main() -> int:
                    "model": spec.name, "global_batch": 1, "seq_len": args.prompt, "parallelism": "none"},
         "hbm_gbs_per_step": round(step_bytes / (b1["ms_per_step"] * 1e-3) / 1e9, 1),
         "hbm_frac_per_step": round(step_bytes / (b1["ms_per_step"] * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
-        "roofline": {"bound": "hbm", "kernel": "matvec_fused_kernel<Q4_0> (decode matvec: q|k|v+rope, wo+add, gate|up+silu, down+add)",
+        "roofline": {"bound": "hbm", "kernel": "matvec_dma_kernel<Q4_0> (decode matvec: q|k|v+rope, wo+add, gate|up+silu, down+add)",
                      "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
                      "launches": launches, "bytes_per_launch": round(nbytes / max(launches, 1)),
@@ -292,6 +370,12 @@ def main() -> int:
         "decode_b1_host_argmax": b1["host_argmax"],
         "cpu_baseline": None,
     }
+    if TRAFFIC_FILE.exists():
+        t = json.loads(TRAFFIC_FILE.read_text())
+        result["roofline"]["traffic"] = t["traffic_bytes_per_launch"]
+        result["roofline"]["traffic_over_algorithmic"] = round(
+            t["traffic_bytes_per_launch"] / max(result["roofline"]["bytes_per_launch"], 1), 3)
+        result["roofline"]["traffic_source"] = str(TRAFFIC_FILE.relative_to(ROOT))
     if not args.no_ragged:
         rg = bench_ragged(H, model, info.n_vocab, args.seed)
         log(f"ragged-32: {rg['tokens_per_s']:.1f} tok/s over {rg['steps']} steps (mean batch {rg['mean_batch']:.1f})")
