@@ -392,53 +392,10 @@ constexpr uint32_t kRing = 6;      // V tiles in flight (kRing * 8 DMA ops <= vm
 // The probabilities of one head's row (rows of more positions take the other paths).
 constexpr uint32_t kMixMaxVis = 2304;
 
-// The V ring is filled by LDS-DMA issued from inline assembly, and its waits are explicit:
-// the compiler's own wait counting, which cannot tell the copies into one ring slot from those
-// into another across loop iterations, would otherwise drain every copy before each tile.
-typedef int RsrcWords __attribute__((ext_vector_type(4)));
-
-__device__ __forceinline__ RsrcWords raw_buffer_words(const void* base, uint32_t bytes) {
-  const uint64_t a = reinterpret_cast<uint64_t>(base);
-  // The descriptor lives in scalar registers: every lane holds the same words.
-  RsrcWords w;
-  w.x = __builtin_amdgcn_readfirstlane(static_cast<int>(a & 0xffffffffu));
-  w.y = __builtin_amdgcn_readfirstlane(static_cast<int>((a >> 32) & 0xffffu));  // stride 0
-  w.z = __builtin_amdgcn_readfirstlane(static_cast<int>(bytes));
-  w.w = static_cast<int>(kRawBufferWord3);
-  return w;
-}
-
-// 4 bytes per lane from rsrc + voffset to LDS at lds + 4 * lane (lds uniform).
-__device__ __forceinline__ void lds_dma4(RsrcWords rsrc, uint32_t voffset, uint32_t lds) {
-  lds = __builtin_amdgcn_readfirstlane(lds);
-  asm volatile("s_mov_b32 m0, %2\n\tbuffer_load_dword %0, %1, 0 offen lds" : : "v"(voffset), "s"(rsrc), "s"(lds)
-               : "memory");
-}
-
-// 16 bytes per lane from rsrc + voffset + soffset to LDS at lds + 16 * lane (soffset and lds
-// uniform).
-__device__ __forceinline__ void lds_dma16_so(RsrcWords rsrc, uint32_t voffset, uint32_t soffset, uint32_t lds) {
-  lds = __builtin_amdgcn_readfirstlane(lds);
-  soffset = __builtin_amdgcn_readfirstlane(soffset);
-  asm volatile("s_mov_b32 m0, %3\n\tbuffer_load_dwordx4 %0, %1, %2 offen lds"
-               : : "v"(voffset), "s"(rsrc), "s"(soffset), "s"(lds) : "memory");
-}
-
-// 16 bytes per lane from rsrc + voffset to LDS at lds + 16 * lane (lds uniform).
-__device__ __forceinline__ void lds_dma16(RsrcWords rsrc, uint32_t voffset, uint32_t lds) {
-  lds = __builtin_amdgcn_readfirstlane(lds);
-  // m0 is set and consumed inside the statement; the compiler reserves it and keeps nothing in
-  // it across statements of this kernel.
-  asm volatile("s_mov_b32 m0, %2\n\tbuffer_load_dwordx4 %0, %1, 0 offen lds" : : "v"(voffset), "s"(rsrc), "s"(lds)
-               : "memory");
-}
-
-// s_waitcnt vmcnt(N) as a statement the compiler does not move memory accesses across.
-template <int N>
-__device__ __forceinline__ void wait_vm() {
-  static_assert(N >= 0 && N <= 63, "vmcnt is six bits");
-  asm volatile("s_waitcnt vmcnt(%0)" : : "n"(N) : "memory");
-}
+// The V rings are filled by LDS-DMA issued from inline assembly (common.h), and their waits
+// are explicit: the compiler's own wait counting, which cannot tell the copies into one ring
+// slot from those into another across loop iterations, would otherwise drain every copy before
+// each tile.
 
 __global__ __launch_bounds__(64) void attn_mix64_kernel(AttnArgs a) {
   __shared__ __attribute__((aligned(16))) float ring[kRing * kMixTile * 64];
@@ -737,22 +694,6 @@ size_t mixd_lds(uint32_t max_vis) {
   return static_cast<size_t>(MixD<G>::kRing) * kDTile * 128 + static_cast<size_t>(G) * mixd_pitch(max_vis) * 4 + 512;
 }
 
-// s_waitcnt vmcnt(n) for a wave-uniform n; counts above 31 wait for 31 (a stricter wait).
-__device__ __forceinline__ void wait_vm_upto(uint32_t n) {
-  n = __builtin_amdgcn_readfirstlane(n);
-#define AXON_WAIT_CASE(k) \
-  case k: wait_vm<k>(); return;
-  switch (n) {
-    AXON_WAIT_CASE(0) AXON_WAIT_CASE(1) AXON_WAIT_CASE(2) AXON_WAIT_CASE(3) AXON_WAIT_CASE(4) AXON_WAIT_CASE(5)
-    AXON_WAIT_CASE(6) AXON_WAIT_CASE(7) AXON_WAIT_CASE(8) AXON_WAIT_CASE(9) AXON_WAIT_CASE(10) AXON_WAIT_CASE(11)
-    AXON_WAIT_CASE(12) AXON_WAIT_CASE(13) AXON_WAIT_CASE(14) AXON_WAIT_CASE(15) AXON_WAIT_CASE(16)
-    AXON_WAIT_CASE(17) AXON_WAIT_CASE(18) AXON_WAIT_CASE(19) AXON_WAIT_CASE(20) AXON_WAIT_CASE(21)
-    AXON_WAIT_CASE(22) AXON_WAIT_CASE(23) AXON_WAIT_CASE(24) AXON_WAIT_CASE(25) AXON_WAIT_CASE(26)
-    AXON_WAIT_CASE(27) AXON_WAIT_CASE(28) AXON_WAIT_CASE(29) AXON_WAIT_CASE(30)
-    default: wait_vm<31>(); return;
-  }
-#undef AXON_WAIT_CASE
-}
 
 template <int G>
 __global__ __launch_bounds__(G * 128) void attn_mixd_kernel(AttnArgs a) {

@@ -344,6 +344,73 @@ __device__ __forceinline__ void dma_to_lds(const uint8_t* src, uint8_t* dst, uin
   }
 }
 
+// LDS-DMA from inline assembly. The compiler does not count these copies, so a kernel that
+// uses them waits for them itself (wait_vm, wait_vm_upto): vmcnt drains in issue order, so a
+// load issued before the copies can be waited for while the copies stay in flight, which the
+// compiler's own counting (that sees the copies) cannot express.
+typedef int RsrcWords __attribute__((ext_vector_type(4)));
+
+// A raw buffer descriptor of `bytes` from base, in scalar registers (every lane holds the same
+// words).
+__device__ __forceinline__ RsrcWords raw_buffer_words(const void* base, uint32_t bytes) {
+  const uint64_t a = reinterpret_cast<uint64_t>(base);
+  RsrcWords w;
+  w.x = __builtin_amdgcn_readfirstlane(static_cast<int>(a & 0xffffffffu));
+  w.y = __builtin_amdgcn_readfirstlane(static_cast<int>((a >> 32) & 0xffffu));  // stride 0
+  w.z = __builtin_amdgcn_readfirstlane(static_cast<int>(bytes));
+  w.w = static_cast<int>(kRawBufferWord3);
+  return w;
+}
+
+// 4 bytes per lane from rsrc + voffset to LDS at lds + 4 * lane (lds uniform).
+__device__ __forceinline__ void lds_dma4(RsrcWords rsrc, uint32_t voffset, uint32_t lds) {
+  lds = __builtin_amdgcn_readfirstlane(lds);
+  asm volatile("s_mov_b32 m0, %2\n\tbuffer_load_dword %0, %1, 0 offen lds" : : "v"(voffset), "s"(rsrc), "s"(lds)
+               : "memory");
+}
+
+// 16 bytes per lane from rsrc + voffset + soffset to LDS at lds + 16 * lane (soffset and lds
+// uniform).
+__device__ __forceinline__ void lds_dma16_so(RsrcWords rsrc, uint32_t voffset, uint32_t soffset, uint32_t lds) {
+  lds = __builtin_amdgcn_readfirstlane(lds);
+  soffset = __builtin_amdgcn_readfirstlane(soffset);
+  asm volatile("s_mov_b32 m0, %3\n\tbuffer_load_dwordx4 %0, %1, %2 offen lds"
+               : : "v"(voffset), "s"(rsrc), "s"(soffset), "s"(lds) : "memory");
+}
+
+// 16 bytes per lane from rsrc + voffset to LDS at lds + 16 * lane (lds uniform).
+__device__ __forceinline__ void lds_dma16(RsrcWords rsrc, uint32_t voffset, uint32_t lds) {
+  lds = __builtin_amdgcn_readfirstlane(lds);
+  // m0 is set and consumed inside the statement; the compiler reserves it and keeps nothing in
+  // it across statements of this kernel.
+  asm volatile("s_mov_b32 m0, %2\n\tbuffer_load_dwordx4 %0, %1, 0 offen lds" : : "v"(voffset), "s"(rsrc), "s"(lds)
+               : "memory");
+}
+
+// s_waitcnt vmcnt(N) as a statement the compiler does not move memory accesses across.
+template <int N>
+__device__ __forceinline__ void wait_vm() {
+  static_assert(N >= 0 && N <= 63, "vmcnt is six bits");
+  asm volatile("s_waitcnt vmcnt(%0)" : : "n"(N) : "memory");
+}
+
+// s_waitcnt vmcnt(n) for a wave-uniform n; counts above 31 wait for 31 (a stricter wait).
+__device__ __forceinline__ void wait_vm_upto(uint32_t n) {
+  n = __builtin_amdgcn_readfirstlane(n);
+#define AXON_WAIT_CASE(k) \
+  case k: wait_vm<k>(); return;
+  switch (n) {
+    AXON_WAIT_CASE(0) AXON_WAIT_CASE(1) AXON_WAIT_CASE(2) AXON_WAIT_CASE(3) AXON_WAIT_CASE(4) AXON_WAIT_CASE(5)
+    AXON_WAIT_CASE(6) AXON_WAIT_CASE(7) AXON_WAIT_CASE(8) AXON_WAIT_CASE(9) AXON_WAIT_CASE(10) AXON_WAIT_CASE(11)
+    AXON_WAIT_CASE(12) AXON_WAIT_CASE(13) AXON_WAIT_CASE(14) AXON_WAIT_CASE(15) AXON_WAIT_CASE(16)
+    AXON_WAIT_CASE(17) AXON_WAIT_CASE(18) AXON_WAIT_CASE(19) AXON_WAIT_CASE(20) AXON_WAIT_CASE(21)
+    AXON_WAIT_CASE(22) AXON_WAIT_CASE(23) AXON_WAIT_CASE(24) AXON_WAIT_CASE(25) AXON_WAIT_CASE(26)
+    AXON_WAIT_CASE(27) AXON_WAIT_CASE(28) AXON_WAIT_CASE(29) AXON_WAIT_CASE(30)
+    default: wait_vm<31>(); return;
+  }
+#undef AXON_WAIT_CASE
+}
+
 // Waits for every outstanding memory operation of this wave, LDS-DMA copies included.
 __device__ __forceinline__ void wait_memory() { __builtin_amdgcn_s_waitcnt(0); }
 
