@@ -175,7 +175,7 @@ class MatvecFusedArgs(C.Structure):
                 ("out_mode", C.c_int), ("y", C.c_void_p * 3), ("y_stride", C.c_size_t * 3), ("bias", C.c_void_p * 3),
                 ("rope_table", C.c_void_p), ("rot_half", C.c_uint32), ("head_dim", C.c_uint32), ("pos", C.c_void_p),
                 ("cache_off", C.c_void_p), ("cache", C.c_void_p), ("k_layer_off", C.c_int64),
-                ("v_layer_off", C.c_int64)]
+                ("v_layer_off", C.c_int64), ("outq", C.c_void_p)]
 
 
 def ptr_of(b) -> int:

@@ -672,6 +672,9 @@ int axon_hip_matvec_fused(const axon_hip_matvec_fused_args* p) {
   a.cache = p->cache;
   a.k_layer_off = p->k_layer_off;
   a.v_layer_off = p->v_layer_off;
+  a.outq = static_cast<uint8_t*>(p->outq);
+  if (a.outq != nullptr && (a.out_mode != kOutSilu || a.n_out[0] % kQK != 0))
+    return fail(kInvalidArgument, "matvec_fused: Q8_0 output needs the SiLU epilogue and outputs in whole blocks");
   return matvec_fused_launch(p->type, a);
 }
 

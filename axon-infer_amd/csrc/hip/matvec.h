@@ -53,6 +53,7 @@ struct FusedArgs {
   const int64_t* cache_off;
   float* cache;
   int64_t k_layer_off, v_layer_off;
+  uint8_t* outq;          // kOutSilu: also [m][n_out / 32] Q8_0 blocks of the output, or null
 };
 
 bool matvec_fused_fits(int type, int in_mode, uint32_t m, uint32_t nb, bool silu);

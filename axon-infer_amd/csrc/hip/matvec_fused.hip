@@ -230,7 +230,14 @@ __device__ __forceinline__ void fused_body(const FusedArgs& args, const WgRows& 
       const uint32_t r = tid - m * nr;
       const float gt = outv[m * 2 * R + r];
       const float u = outv[m * 2 * R + g.pitch_rows + r];
-      args.y[0][static_cast<size_t>(m) * args.y_stride[0] + r0 + r] = gt / (1.0f + exp_rounded(-gt)) * u;
+      const float h = gt / (1.0f + exp_rounded(-gt)) * u;
+      args.y[0][static_cast<size_t>(m) * args.y_stride[0] + r0 + r] = h;
+      // Q8_0 blocks of h (the launcher gives each workgroup whole blocks: 32 rows, so the 32
+      // outputs of one block sit in 32 aligned lanes, r = lane % 32).
+      if (args.outq != nullptr) {
+        const size_t nbq = args.n_out[0] / kQK;
+        quantize_block_lanes(h, r & 31u, args.outq + (static_cast<size_t>(m) * nbq + (r0 + r) / kQK) * kBytesQ8_0);
+      }
     }
   } else {
     // kOutRope: one thread per (row, pair of outputs).
@@ -407,6 +414,28 @@ size_t fused_lds(int bs, uint32_t m, uint32_t nb, uint32_t rows, bool silu, size
   return act + tile + std::max(raw, terms);
 }
 
+// Dynamic LDS the decode matvec kernels may use once granted above the default 64 KB (asked
+// for once per instantiation), or 64 KB when the device does not grant more.
+template <typename K>
+size_t grant_lds(K kernel) {
+  int dev = 0, v = 0;
+  if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&v, hipDeviceAttributeMaxSharedMemoryPerBlock, dev) != hipSuccess ||
+      v <= 65536 || hipFuncSetAttribute(reinterpret_cast<const void*>(kernel), hipFuncAttributeMaxDynamicSharedMemorySize, v - 256) != hipSuccess)
+    return 65536;
+  return static_cast<size_t>(v);
+}
+
+size_t wide_lds_limit(int type, bool dma) {
+  static size_t limits[2][3] = {{0, 0, 0}, {0, 0, 0}};
+  const int t = type == Q8_0 ? 0 : type == Q4_0 ? 1 : 2;
+  size_t& l = limits[dma ? 1 : 0][t];
+  if (l == 0) {
+    if (dma) l = t == 0 ? grant_lds(matvec_dma_kernel<Q8_0>) : t == 1 ? grant_lds(matvec_dma_kernel<Q4_0>) : grant_lds(matvec_dma_kernel<Q4_1>);
+    else l = t == 0 ? grant_lds(matvec_fused_kernel<Q8_0>) : t == 1 ? grant_lds(matvec_fused_kernel<Q4_0>) : grant_lds(matvec_fused_kernel<Q4_1>);
+  }
+  return l;
+}
+
 }  // namespace
 
 bool matvec_fused_fits(int type, int in_mode, uint32_t m, uint32_t nb, bool silu) {
@@ -448,7 +477,10 @@ int matvec_fused_launch(int type, FusedArgs& a) {
   rows = std::min<uint32_t>(rows, std::max<uint32_t>(1, total_out / 512));
   rows = std::min<uint32_t>(rows, (silu ? 128 : 256) / a.m);
   if (rope) rows = std::max<uint32_t>(2, rows & ~1u);
-  constexpr size_t kLdsLimit = 65536 - 256;  // the kernels' static LDS sits beside the dynamic part
+  // A Q8_0 output needs whole blocks per workgroup: 32 rows, whose tile may exceed 64 KB of LDS.
+  const bool outq = a.outq != nullptr;
+  if (outq) rows = kQK;
+  const size_t kLdsLimit = (outq ? wide_lds_limit(type, dma) : 65536) - 256;  // static LDS beside it
   for (;;) {
     size_t act = 0, tile = 0;
     const size_t lds = fused_lds(bs, a.m, a.nb, rows, silu, &act, &tile);
@@ -479,7 +511,7 @@ int matvec_fused_launch(int type, FusedArgs& a) {
       }
       return check_launch("matvec_fused");
     }
-    if (rows <= (rope ? 2u : 1u)) return fail(kUnsupported, "matvec_fused: %u blocks x %u rows exceed LDS", a.nb, a.m);
+    if (outq || rows <= (rope ? 2u : 1u)) return fail(kUnsupported, "matvec_fused: %u blocks x %u rows exceed LDS", a.nb, a.m);
     rows = rope ? std::max<uint32_t>(2, (rows / 2) & ~1u) : rows / 2;
   }
 }

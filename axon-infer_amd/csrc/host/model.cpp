@@ -624,14 +624,24 @@ Expected<std::size_t> LlamaModel::run(std::span<const Row> rows, bool copy_logit
       fa.out_mode = 2;
       fa.y[0] = gate_;
       fa.y_stride[0] = ff;
+      // The SiLU epilogue also writes down's Q8_0 input when the launch shape allows it (whole
+      // blocks per workgroup in LDS); down then reads blocks instead of quantizing h itself.
+      const bool down_q8 = q8_path(L.w_down) && ff % 32 == 0 && fused_ok(L.w_down, 0, ff, false);
+      fa.outq = down_q8 ? xq_ : nullptr;
       probe_begin(L.w_gate);
-      DEV(axon_hip_matvec_fused(&fa));
+      int rc = axon_hip_matvec_fused(&fa);
+      if (rc == AXON_HIP_E_UNSUPPORTED && fa.outq != nullptr) {
+        fa.outq = nullptr;
+        rc = axon_hip_matvec_fused(&fa);
+      }
+      DEV(rc);
       probe_end(L.w_gate, n, 2 * ff, false);
       axon_hip_matvec_fused_args fd = fused_args(L.w_down);
       fd.n_seg = 1;
       fd.w[0] = L.w_down.dev;
       fd.n_out[0] = d;
-      fd.in_mode = 1;
+      fd.in_mode = fa.outq != nullptr ? 0 : 1;
+      fd.xq = xq_;
       fd.x = gate_;
       fd.x_stride = ff;
       fd.out_mode = 1;

@@ -258,6 +258,9 @@ typedef struct {
   const int64_t* cache_off;
   float* cache;
   int64_t k_layer_off, v_layer_off;
+  /* out_mode 2 only: also the Q8_0 blocks of every output row (down's input, llama.cpp:600-620,
+   * [n_rows][n_out[0] / 32] blocks), or NULL. Requires n_out[0] % 32 == 0. */
+  void* outq;
 } axon_hip_matvec_fused_args;
 int axon_hip_matvec_fused(const axon_hip_matvec_fused_args* args);
 /* 1 when axon_hip_matvec_fused takes this shape (rows, row length, input mode, SiLU pairing). */

@@ -168,6 +168,66 @@ def test_norm_silu_matches_unfused(H, o, kind, n_rows, n_in, ff):
     assert ulp_diff(got, want) <= 2
 
 
+@pytest.mark.parametrize("kind", KINDS)
+@pytest.mark.parametrize("n_rows", [1, 2, 4])
+@pytest.mark.parametrize("n_in,ff", [(576, 1536), (2048, 8192), (896, 4864)])
+def test_silu_q8_output_feeds_down(H, o, kind, n_rows, n_in, ff):
+    """The SiLU epilogue's Q8_0 output (outq): byte-identical to quantize_rows_q8_0 of its own
+    float output, with the float output unchanged; down over those blocks (in_mode 0) gives the
+    bits of down over the floats (in_mode 1), the residual add included."""
+    if not supported(H, kind, 2, n_rows, n_in, silu=True) or not supported(H, kind, 0, n_rows, ff):
+        pytest.skip("shape outside the fused kernel")
+    eps = 1e-6
+    x = random_floats(n_rows * n_in, ff + 3 * n_rows, 2.0).reshape(n_rows, n_in)
+    g = random_floats(n_in, n_in + 6, 1.0)
+    wg = random_weights(kind, ff, n_in, ff + 3)
+    wu = random_weights(kind, ff, n_in, ff + 4)
+    dx, dg, dwg, dwu = (H.DeviceBuffer.of(a) for a in (x, g, wg, wu))
+    args = dict(type=TYPE_ID[kind], n_seg=2, w=[dwg, dwu], n_out=[ff, ff], n_rows=n_rows, n_in=n_in, in_mode=2,
+                x=dx, x_stride=n_in, norm_w=dg, eps=eps, out_mode=2, y_stride=[ff])
+    h_plain = H.DeviceBuffer.of(np.full((n_rows, ff), -1.0, np.float32))
+    fused(H, y=[h_plain], **args)
+    h = H.DeviceBuffer.of(np.full((n_rows, ff), -1.0, np.float32))
+    hq = H.DeviceBuffer.of(np.full(n_rows * ff // 32 * 34 + 34, 0x5A, np.uint8))
+    try:
+        fused(H, y=[h], outq=hq, **args)
+    except H.HipError as e:
+        # 32 rows of gate and up per workgroup: Q8_0 weights at several rows exceed LDS; the
+        # model then hands h to down as floats.
+        assert "exceed LDS" in str(e)
+        pytest.skip("32-row gate|up tile does not fit LDS for this type and row count")
+    hf = h.download(np.float32).reshape(n_rows, ff)
+    assert np.array_equal(hf, h_plain.download(np.float32).reshape(n_rows, ff))
+    ref_q = H.DeviceBuffer(n_rows * ff // 32 * 34)
+    H.call("quantize_rows_q8_0", h, ref_q, ff, n_rows, ff)
+    got_q = hq.download(np.uint8)
+    assert got_q[:n_rows * ff // 32 * 34].tobytes() == ref_q.download(np.uint8).tobytes()
+    assert np.all(got_q[n_rows * ff // 32 * 34:] == 0x5A)      # nothing past the blocks
+    assert got_q[:ff // 32 * 34].tobytes() == o.quantize_row_q8_0(hf[0]).tobytes()
+    # down: 2048 or the model width outputs, residual add, from the blocks and from the floats
+    d = n_in
+    wd = random_weights(kind, d, ff, d + ff)
+    dwd = H.DeviceBuffer.of(wd)
+    res = random_floats(n_rows * d, d + 9, 1.0).reshape(n_rows, d)
+    y_q, y_f = H.DeviceBuffer.of(res), H.DeviceBuffer.of(res)
+    fused(H, type=TYPE_ID[kind], n_seg=1, w=[dwd], n_out=[d], n_rows=n_rows, n_in=ff, in_mode=0, xq=hq,
+          out_mode=1, y=[y_q], y_stride=[d])
+    fused(H, type=TYPE_ID[kind], n_seg=1, w=[dwd], n_out=[d], n_rows=n_rows, n_in=ff, in_mode=1, x=h,
+          x_stride=ff, out_mode=1, y=[y_f], y_stride=[d])
+    assert np.array_equal(y_q.download(np.float32), y_f.download(np.float32))
+
+
+def test_q8_output_needs_silu_and_whole_blocks(H):
+    dw = H.DeviceBuffer(64 * 34)
+    y, q = H.DeviceBuffer(256), H.DeviceBuffer(256)
+    with pytest.raises(H.HipError):
+        fused(H, type=TYPE_ID["q8_0"], n_seg=1, w=[dw], n_out=[64], n_rows=1, n_in=32, in_mode=0, xq=q,
+              out_mode=0, y=[y], y_stride=[64], outq=q)
+    with pytest.raises(H.HipError):
+        fused(H, type=TYPE_ID["q8_0"], n_seg=2, w=[dw, dw], n_out=[40, 40], n_rows=1, n_in=32, in_mode=0, xq=q,
+              out_mode=2, y=[y], y_stride=[40], outq=q)
+
+
 def rope_table(max_pos, rotary_dim, theta):
     i = np.arange(rotary_dim // 2, dtype=np.float64)
     inv = np.power(np.float64(theta), -2.0 * i / rotary_dim)
