@@ -116,39 +116,40 @@ __device__ __forceinline__ void quantize8_to_act(const float (&v)[8], uint32_t p
 // Terms rows are 16-byte aligned (a multiple of 4 floats) so the chains read them four at a time.
 __host__ __device__ constexpr uint32_t term_pitch(uint32_t nb) { return (nb + 3) & ~3u; }
 
-// t[0] + t[1] + ... + t[n-1], left to right, from 16-byte aligned LDS: rounds of sixteen terms,
-// the next round's reads in flight while this round's adds run (reads stay within the rows'
-// padding; only the first n terms are added).
-__device__ __forceinline__ void load16(const float* t, float4 (&v)[4]) {
-#pragma unroll
-  for (int k = 0; k < 4; ++k) v[k] = reinterpret_cast<const float4*>(t)[k];
-}
-__device__ __forceinline__ void add16(const float4 (&v)[4], float& acc) {
-#pragma unroll
-  for (int k = 0; k < 4; ++k) {
-    acc += v[k].x;
-    acc += v[k].y;
-    acc += v[k].z;
-    acc += v[k].w;
-  }
-}
+// t[0] + t[1] + ... + t[n-1], left to right, from 16-byte aligned LDS: 64 terms at a time are
+// read into registers and then added, so the dependent adds run back to back (a chain of adds
+// whose operands come straight from LDS costs about twice as much per add). The tail goes in
+// rounds of 16 reads that stay within the rows' padding; only the first n terms are added.
 __device__ __forceinline__ float ordered_sum(const float* t, uint32_t n) {
   float acc = 0.0f;
-  const uint32_t full = n & ~15u;
-  float4 a[4], b[4];
   uint32_t i = 0;
-  if (full != 0) load16(t, a);
-  for (; i + 32 <= full; i += 32) {
-    load16(t + i + 16, b);
-    add16(a, acc);
-    if (i + 48 <= full) load16(t + i + 32, a);
-    add16(b, acc);
+  for (; i + 64 <= n; i += 64) {
+    float4 v[16];
+#pragma unroll
+    for (int k = 0; k < 16; ++k) v[k] = reinterpret_cast<const float4*>(t + i)[k];
+#pragma unroll
+    for (int k = 0; k < 16; ++k) {
+      acc += v[k].x;
+      acc += v[k].y;
+      acc += v[k].z;
+      acc += v[k].w;
+    }
   }
-  if (i < full) {
-    add16(a, acc);
-    i += 16;
+  for (; i < n; i += 16) {
+    float v[16];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const float4 q = reinterpret_cast<const float4*>(t + i)[k];
+      v[4 * k] = q.x;
+      v[4 * k + 1] = q.y;
+      v[4 * k + 2] = q.z;
+      v[4 * k + 3] = q.w;
+    }
+#pragma unroll
+    for (uint32_t k = 0; k < 16; ++k) {
+      if (i + k < n) acc += v[k];
+    }
   }
-  for (; i < n; ++i) acc += t[i];
   return acc;
 }
 
