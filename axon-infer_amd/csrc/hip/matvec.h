@@ -37,6 +37,7 @@ struct FusedArgs {
   int n_seg;
   uint32_t nb, m;
   uint32_t rows, lds_tile, lds_scratch;  // filled by the launcher
+  uint32_t lds_stage;                    // filled by the launcher (staged-prologue kernel)
   int in_mode;
   const uint8_t* xq;      // kInQ8: [m][nb] blocks
   const float* x;         // kInF32 / kInNorm: [m][x_stride] floats

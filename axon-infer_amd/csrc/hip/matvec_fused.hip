@@ -367,6 +367,104 @@ __global__ __launch_bounds__(kThreads) void matvec_dma_kernel(FusedArgs args) {
   fused_body<T>(args, g, tile, act, reinterpret_cast<float*>(raw));
 }
 
+// One activation row RMSNorm'd in the prologue (q|k|v and gate|up at batch 1), rows of a
+// multiple of 4 bytes: matvec_dma_kernel with its copies ordered for latency. Every copy is
+// LDS-DMA issued from inline assembly, this wave's chunks of the activation row and of the norm
+// gains first, then the weights; vmcnt drains in issue order, so each wave waits for its own
+// two staging copies alone while its weight copies stay in flight, and the norm/quantize
+// prologue runs while the weights arrive. The prologue's operations are float_prologue's for one
+// row with one chunk per thread, in the same order. The staging area (norm1_stage_bytes) lies
+// past the shared layout: the row [256][8] and the gains [256][8].
+
+// dma_to_lds from inline assembly; returns this wave's number of copies (uniform in the wave).
+__device__ __forceinline__ uint32_t dma_to_lds_asm(const uint8_t* src, uint8_t* dst, uint32_t bytes, uint32_t tid,
+                                                   uint32_t nthreads) {
+  const RsrcWords rsrc = raw_buffer_words(src, bytes);
+  const uint32_t lane = tid & 63u;
+  const uint32_t wave0 = tid & ~63u;
+  const uint32_t dst_lds = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(as_lds(dst)));
+  const bool wide = ((reinterpret_cast<uintptr_t>(src) | reinterpret_cast<uintptr_t>(dst) | bytes) & 15u) == 0;
+  const uint32_t units = bytes / (wide ? 16u : 4u);
+  uint32_t n = 0;
+  for (uint32_t base = wave0; base < units; base += nthreads) {
+    if (base + lane < units) {
+      if (wide) lds_dma16(rsrc, (base + lane) * 16u, dst_lds + base * 16u);
+      else lds_dma4(rsrc, (base + lane) * 4u, dst_lds + base * 4u);
+    }
+    ++n;
+  }
+  return n;
+}
+
+constexpr uint32_t kNorm1Stage = 2 * kThreads * 32;  // row and gains, one 8-float chunk per thread
+constexpr size_t kNorm1MinWeights = 32 * 1024;        // weight bytes per workgroup that pay for staging
+
+template <int T>
+__global__ __launch_bounds__(kThreads) void matvec_norm1_kernel(FusedArgs args) {
+  extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+  __shared__ double red[kThreads / 64];
+  constexpr int bs = wbytes<T>();
+  const uint32_t tid = threadIdx.x;
+  const uint32_t lane = tid & 63u;
+  const uint32_t wave0 = tid & ~63u;
+  const WgRows g = wg_rows(args);
+  const uint32_t row_bytes = args.nb * bs;
+  ActBlock* act = reinterpret_cast<ActBlock*>(smem);
+  uint8_t* tile = smem + args.lds_tile;
+  uint8_t* raw = smem + args.lds_scratch;
+  const uint32_t n_in = args.nb * kQK;
+  const uint32_t n_chunks = n_in / 8;  // at most kThreads (the launcher checks)
+  float* xs = reinterpret_cast<float*>(smem + args.lds_stage);  // [256][8]
+  float* ws = xs + kThreads * 8;                                // [256][8]
+  // 1. Staging: wave w copies chunks wave0 .. wave0 + 63 (2 KB, two copies) of the row and of
+  // the gains. Reads past the row return zeros (raw buffer bounds) into the staging area.
+  if (wave0 < n_chunks) {
+    const RsrcWords xsrc = raw_buffer_words(args.x, n_in * 4);
+    const RsrcWords wsrc = raw_buffer_words(args.norm_w, n_in * 4);
+    const uint32_t xs_lds = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(as_lds(xs)));
+    const uint32_t ws_lds = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(as_lds(ws)));
+    lds_dma16(xsrc, wave0 * 32 + lane * 16, xs_lds + wave0 * 32);
+    lds_dma16(xsrc, wave0 * 32 + 1024 + lane * 16, xs_lds + wave0 * 32 + 1024);
+    lds_dma16(wsrc, wave0 * 32 + lane * 16, ws_lds + wave0 * 32);
+    lds_dma16(wsrc, wave0 * 32 + 1024 + lane * 16, ws_lds + wave0 * 32 + 1024);
+  }
+  // 2. The weight copies.
+  uint32_t copies = dma_to_lds_asm(args.w[g.s] + static_cast<size_t>(g.r0) * row_bytes, tile, g.nr * row_bytes, tid, kThreads);
+  if (g.silu) {
+    copies += dma_to_lds_asm(args.w[1] + static_cast<size_t>(g.r0) * row_bytes,
+                             tile + static_cast<size_t>(g.pitch_rows) * row_bytes, g.nr * row_bytes, tid, kThreads);
+  }
+  // 3. The prologue once this wave's staging copies (older than its weight copies) landed.
+  wait_vm_upto(copies);
+  const bool has = tid < n_chunks;
+  float xv[8], wv[8];
+#pragma unroll
+  for (int k = 0; k < 8; ++k) {
+    xv[k] = xs[tid * 8 + k];
+    wv[k] = ws[tid * 8 + k];
+  }
+  double ss = 0.0;
+  if (has) {
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      const double v = static_cast<double>(xv[k]);
+      ss += v * v;
+    }
+  }
+  ss = block_sum_double_256(ss, red);
+  const float inv = static_cast<float>(1.0 / sqrt(ss / static_cast<double>(n_in) + static_cast<double>(args.eps)));
+  if (has) {
+    float v[8];
+#pragma unroll
+    for (int k = 0; k < 8; ++k) v[k] = xv[k] * inv * wv[k];
+    quantize8_to_act(v, tid & 3, act[tid / 4]);
+  }
+  // 4. Every copy, then the body.
+  wait_vm<0>();
+  __syncthreads();
+  fused_body<T>(args, g, tile, act, reinterpret_cast<float*>(raw));
+}
+
 // Rows of any even byte count: the same with the weights staged through registers.
 template <int T>
 __global__ __launch_bounds__(kThreads) void matvec_fused_kernel(FusedArgs args) {
@@ -424,6 +522,16 @@ size_t grant_lds(K kernel) {
       v <= 65536 || hipFuncSetAttribute(reinterpret_cast<const void*>(kernel), hipFuncAttributeMaxDynamicSharedMemorySize, v - 256) != hipSuccess)
     return 65536;
   return static_cast<size_t>(v);
+}
+
+size_t norm1_lds_limit(int type) {
+  static size_t limits[3] = {0, 0, 0};
+  const int t = type == Q8_0 ? 0 : type == Q4_0 ? 1 : 2;
+  if (limits[t] == 0) {
+    limits[t] = t == 0 ? grant_lds(matvec_norm1_kernel<Q8_0>)
+                       : t == 1 ? grant_lds(matvec_norm1_kernel<Q4_0>) : grant_lds(matvec_norm1_kernel<Q4_1>);
+  }
+  return limits[t] - 256;
 }
 
 size_t wide_lds_limit(int type, bool dma) {
@@ -495,7 +603,24 @@ int matvec_fused_launch(int type, FusedArgs& a) {
         if (!silu || s == 0) wg += static_cast<uint32_t>(ceil_div(a.n_out[s], rows));
       }
       if (silu) a.wg_begin[1] = 0;
-      if (dma) {
+      // One RMSNorm'd row (one chunk per thread) under at least kNorm1MinWeights of weight copies
+      // per workgroup: the staged kernel, its staging after the layout. With fewer, the weights
+      // land before the prologue ends either way, and staging the row through LDS only adds its
+      // latency (q|k|v at 6 rows per workgroup: 6.16 us plain, 6.64 us staged; gate|up at
+      // 2 x 32 rows: 11.44 us plain, 10.88 us staged).
+      a.lds_stage = static_cast<uint32_t>((lds + 15) & ~size_t(15));
+      const size_t lds1 = a.lds_stage + kNorm1Stage;
+      const size_t wg_weights = rows * row_bytes * (silu ? 2 : 1);
+      const bool norm1 = dma && a.m == 1 && a.in_mode == kInNorm && a.nb * kQK / 8 <= kThreads &&
+                         wg_weights >= kNorm1MinWeights && lds1 <= norm1_lds_limit(type);
+      if (norm1) {
+        switch (type) {
+        case Q8_0: launch(matvec_norm1_kernel<Q8_0>, dim3(wg), dim3(kThreads), lds1, a); break;
+        case Q4_0: launch(matvec_norm1_kernel<Q4_0>, dim3(wg), dim3(kThreads), lds1, a); break;
+        case Q4_1: launch(matvec_norm1_kernel<Q4_1>, dim3(wg), dim3(kThreads), lds1, a); break;
+        default: return fail(kUnsupported, "matvec_fused: weight type %d", type);
+        }
+      } else if (dma) {
         switch (type) {
         case Q8_0: launch(matvec_dma_kernel<Q8_0>, dim3(wg), dim3(kThreads), lds, a); break;
         case Q4_0: launch(matvec_dma_kernel<Q4_0>, dim3(wg), dim3(kThreads), lds, a); break;

@@ -18,8 +18,9 @@ Two workloads, both greedy:
                forward_batch time (device greedy choice and the ids to the host included).
 
 The line also carries:
-  roofline     the Q4_0 decode matvec kernel (matvec_fused_kernel<Q4_0>: q|k|v, wo, gate|up and
-               down of every layer; the dominant kernel by time), from a probe pass of the same
+  roofline     the Q4_0 decode matvec (matvec_dma_kernel<Q4_0> for q|k|v, wo and down,
+               matvec_norm1_kernel<Q4_0> for gate|up, of every layer; the dominant kernels by
+               time), from a probe pass of the same
                decode-b1 steps in which each such launch records its own dispatch start and end on
                HIP events (hipExtLaunchKernel, on the library stream): achieved = algorithmic bytes
                (weight rows + activations + outputs) / summed kernel time. The Q6_K output matvec
@@ -53,7 +54,9 @@ sys.path.insert(0, str(ROOT / "tests"))
 HBM_PEAK_GBS = 8000.0
 TRAFFIC_FILE = ROOT / "profiles" / "traffic_matvec_q4_0.json"
 COPY_BYTES = 256 << 20
-MATVEC_KERNEL = "matvec_dma_kernel<2>"  # Q4_0 is ggml type 2
+# The Q4_0 decode matvec's two kernels (Q4_0 is ggml type 2): matvec_dma_kernel for q|k|v, wo
+# and down, matvec_norm1_kernel (the row RMSNorm'd while the weights arrive) for gate|up.
+MATVEC_KERNELS = ("matvec_dma_kernel<2>", "matvec_norm1_kernel<2>")
 METRIC = "decode tokens/s + HBM GB/s (% peak), Q4_0 1B model, batch 1 and 32 ragged"
 
 
@@ -208,10 +211,10 @@ def traffic_summary(fetch_csv, write_csv):
                 continue
             if "copyBuffer" in name:
                 copy.append(value)
-            elif MATVEC_KERNEL in name.replace(" ", ""):
+            elif any(k in name.replace(" ", "") for k in MATVEC_KERNELS):
                 mv.append(value)
         if not copy or not mv:
-            raise SystemExit(f"{path}: no {counter} rows for the copy ({len(copy)}) or {MATVEC_KERNEL} ({len(mv)})")
+            raise SystemExit(f"{path}: no {counter} rows for the copy ({len(copy)}) or {'/'.join(MATVEC_KERNELS)} ({len(mv)})")
         return max(copy), mv
     fcopy, fmv = per_kernel(fetch_csv, "FETCH_SIZE")
     wcopy, wmv = per_kernel(write_csv, "WRITE_SIZE")
@@ -219,7 +222,7 @@ def traffic_summary(fetch_csv, write_csv):
     w_scale = COPY_BYTES / (wcopy * 1024.0)
     fetch = float(np.mean(fmv)) * 1024.0 * f_scale
     write = float(np.mean(wmv)) * 1024.0 * w_scale
-    out = {"kernel": MATVEC_KERNEL, "dispatches": len(fmv),
+    out = {"kernel": " + ".join(MATVEC_KERNELS), "dispatches": len(fmv),
            "fetch_bytes_per_launch": round(fetch), "write_bytes_per_launch": round(write),
            "traffic_bytes_per_launch": round(fetch + write),
            "copy_bytes": COPY_BYTES, "copy_fetch_kib": fcopy, "copy_write_kib": wcopy,
@@ -358,7 +361,8 @@ def main() -> int:
                    "model": spec.name, "global_batch": 1, "seq_len": args.prompt, "parallelism": "none"},
         "hbm_gbs_per_step": round(step_bytes / (b1["ms_per_step"] * 1e-3) / 1e9, 1),
         "hbm_frac_per_step": round(step_bytes / (b1["ms_per_step"] * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
-        "roofline": {"bound": "hbm", "kernel": "matvec_dma_kernel<Q4_0> (decode matvec: q|k|v+rope, wo+add, gate|up+silu, down+add)",
+        "roofline": {"bound": "hbm", "kernel": "decode matvec <Q4_0>: matvec_dma_kernel (q|k|v+rope, wo+add, down+add) "
+                                                     "and matvec_norm1_kernel (gate|up+silu)",
                      "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
                      "launches": launches, "bytes_per_launch": round(nbytes / max(launches, 1)),
