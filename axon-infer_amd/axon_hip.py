@@ -156,7 +156,7 @@ class RopeRowsArgs(C.Structure):
                 ("k_stride", C.c_uint32), ("n_head", C.c_uint32), ("n_kv", C.c_uint32), ("head_dim", C.c_uint32),
                 ("rotary_dim", C.c_uint32), ("neox", C.c_int), ("theta", C.c_float), ("freq_factors", C.c_void_p),
                 ("table", C.c_void_p), ("cache", C.c_void_p), ("cache_off", C.c_void_p),
-                ("k_layer_off", C.c_int64), ("v_layer_off", C.c_int64)]
+                ("k_layer_off", C.c_int64), ("v_layer_off", C.c_int64), ("cache_f16", C.c_int)]
 
 
 class AttentionRowsArgs(C.Structure):
@@ -175,7 +175,7 @@ class MatvecFusedArgs(C.Structure):
                 ("out_mode", C.c_int), ("y", C.c_void_p * 3), ("y_stride", C.c_size_t * 3), ("bias", C.c_void_p * 3),
                 ("rope_table", C.c_void_p), ("rot_half", C.c_uint32), ("head_dim", C.c_uint32), ("pos", C.c_void_p),
                 ("cache_off", C.c_void_p), ("cache", C.c_void_p), ("k_layer_off", C.c_int64),
-                ("v_layer_off", C.c_int64), ("outq", C.c_void_p)]
+                ("v_layer_off", C.c_int64), ("outq", C.c_void_p), ("cache_f16", C.c_int)]
 
 
 def ptr_of(b) -> int:
@@ -187,7 +187,8 @@ def ptr_of(b) -> int:
 
 class ModelOptions(C.Structure):
     _fields_ = [("max_seq", C.c_size_t), ("max_ctx", C.c_size_t), ("max_batch", C.c_size_t),
-                ("max_caches", C.c_size_t), ("exact_activations", C.c_int), ("kernels", C.c_char_p)]
+                ("max_caches", C.c_size_t), ("exact_activations", C.c_int), ("kernels", C.c_char_p),
+                ("cache_type", C.c_int)]
 
 
 class ModelInfo(C.Structure):
@@ -195,7 +196,7 @@ class ModelInfo(C.Structure):
                 ("n_ff", C.c_uint32), ("n_vocab", C.c_uint32), ("head_dim", C.c_uint32), ("rotary_dim", C.c_uint32),
                 ("max_seq", C.c_size_t), ("max_ctx", C.c_size_t), ("max_batch", C.c_size_t),
                 ("weight_bytes_per_token", C.c_size_t), ("device_bytes", C.c_size_t),
-                ("kv_bytes_per_position", C.c_size_t)]
+                ("kv_bytes_per_position", C.c_size_t), ("cache_type", C.c_int)]
 
 
 _host = None
@@ -241,8 +242,14 @@ class Model:
     """LlamaModel on the hip table (src/model/llama.h:87-110): logits come back as numpy
     arrays [rows, n_vocab]; caches are int slot ids of the device KV pool."""
 
-    def __init__(self, path, max_seq=512, max_ctx=4096, max_batch=1, max_caches=0, exact=False, kernels="hip"):
-        o = ModelOptions(max_seq, max_ctx, max_batch, max_caches, int(exact), kernels.encode())
+    CACHE_TYPES = {"f32": 0, "f16": 1}  # CacheType (src/model/config.h:16)
+
+    def __init__(self, path, max_seq=512, max_ctx=4096, max_batch=1, max_caches=0, exact=False, kernels="hip",
+                 cache="f32"):
+        if cache not in self.CACHE_TYPES:
+            raise ValueError(f"cache type {cache!r}: f32 or f16")
+        o = ModelOptions(max_seq, max_ctx, max_batch, max_caches, int(exact), kernels.encode(),
+                         self.CACHE_TYPES[cache])
         h = C.c_void_p(0)
         _mcheck(host().axon_model_load(str(path).encode(), C.byref(o), C.byref(h)), f"load {path}")
         self.h = h

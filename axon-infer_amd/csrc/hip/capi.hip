@@ -670,6 +670,7 @@ int axon_hip_matvec_fused(const axon_hip_matvec_fused_args* p) {
   a.pos = p->pos;
   a.cache_off = p->cache_off;
   a.cache = p->cache;
+  a.cache_f16 = p->cache_f16 != 0;
   a.k_layer_off = p->k_layer_off;
   a.v_layer_off = p->v_layer_off;
   a.outq = static_cast<uint8_t*>(p->outq);

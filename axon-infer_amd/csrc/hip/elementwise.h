@@ -21,9 +21,10 @@ struct RopeRowsArgs {
   float theta;
   const float* freq_factors;  // device, rotary_dim/2 divisors, or null
   const float* table;         // device cos/sin pairs [pos][rotary_dim/2], or null
-  float* cache;               // KV pool base (or null: no cache write)
+  void* cache;                // KV pool base (or null: no cache write)
   const int64_t* cache_off;   // per-row element offset of the row's sequence in the pool
   int64_t k_layer_off, v_layer_off;  // element offsets of this layer's K and V regions
+  int cache_f16;              // the pool holds fp16 bit patterns (rows rounded in once)
 };
 
 int quantize_rows_launch(const float* x, uint8_t* out, uint32_t n, uint32_t n_rows, uint32_t x_stride);

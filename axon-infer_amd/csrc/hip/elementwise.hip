@@ -178,13 +178,23 @@ __global__ __launch_bounds__(256) void rope_rows_kernel(RopeRowsArgs a) {
   float* q = a.q != nullptr ? a.q + static_cast<size_t>(r) * a.q_stride : nullptr;
   float* k = a.k != nullptr ? a.k + static_cast<size_t>(r) * a.k_stride : nullptr;
   const float* v = a.v != nullptr ? a.v + static_cast<size_t>(r) * a.k_stride : nullptr;
+  // The row's cache slots: float elements, or fp16 bit patterns rounded in once.
   float* kc = nullptr;
   float* vc = nullptr;
+  uint16_t* kc16 = nullptr;
+  uint16_t* vc16 = nullptr;
   if (a.cache != nullptr) {
     const int64_t base = a.cache_off != nullptr ? a.cache_off[r] : 0;
     const size_t row = static_cast<size_t>(a.n_kv) * a.head_dim;
-    kc = a.cache + base + a.k_layer_off + static_cast<size_t>(pos) * row;
-    vc = a.cache + base + a.v_layer_off + static_cast<size_t>(pos) * row;
+    const size_t k_at = base + a.k_layer_off + static_cast<size_t>(pos) * row;
+    const size_t v_at = base + a.v_layer_off + static_cast<size_t>(pos) * row;
+    if (a.cache_f16) {
+      kc16 = static_cast<uint16_t*>(a.cache) + k_at;
+      vc16 = static_cast<uint16_t*>(a.cache) + v_at;
+    } else {
+      kc = static_cast<float*>(a.cache) + k_at;
+      vc = static_cast<float*>(a.cache) + v_at;
+    }
   }
   const uint32_t nq = a.q != nullptr ? a.n_head * a.head_dim : 0;
   const uint32_t nk = a.k != nullptr ? a.n_kv * a.head_dim : 0;
@@ -197,6 +207,7 @@ __global__ __launch_bounds__(256) void rope_rows_kernel(RopeRowsArgs a) {
     for (uint32_t i = threadIdx.x; i < nk; i += blockDim.x) {
       const float vv = a.bv != nullptr ? v[i] + a.bv[i] : v[i];
       if (vc != nullptr) vc[i] = vv;
+      else if (vc16 != nullptr) vc16[i] = static_cast<uint16_t>(float_to_half_bits(vv));
       else const_cast<float*>(v)[i] = vv;
     }
   }
@@ -229,9 +240,12 @@ __global__ __launch_bounds__(256) void rope_rows_kernel(RopeRowsArgs a) {
     head[ia] = x0 * c - x1 * s;
     head[ib] = x0 * s + x1 * c;
   }
-  if (kc != nullptr) {
+  if (kc != nullptr || kc16 != nullptr) {
     __syncthreads();
-    for (uint32_t i = threadIdx.x; i < nk; i += blockDim.x) kc[i] = k[i];
+    for (uint32_t i = threadIdx.x; i < nk; i += blockDim.x) {
+      if (kc != nullptr) kc[i] = k[i];
+      else kc16[i] = static_cast<uint16_t>(float_to_half_bits(k[i]));
+    }
   }
 }
 

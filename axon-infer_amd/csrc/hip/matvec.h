@@ -52,9 +52,10 @@ struct FusedArgs {
   uint32_t rot_half, head_dim;
   const int32_t* pos;     // per activation row (device)
   const int64_t* cache_off;
-  float* cache;
+  void* cache;            // kOutRope: float or fp16 elements (cache_f16)
   int64_t k_layer_off, v_layer_off;
   uint8_t* outq;          // kOutSilu: also [m][n_out / 32] Q8_0 blocks of the output, or null
+  int cache_f16;
 };
 
 bool matvec_fused_fits(int type, int in_mode, uint32_t m, uint32_t nb, bool silu);

@@ -269,10 +269,17 @@ __device__ __forceinline__ void fused_body(const FusedArgs& args, const WgRows& 
         q[1] = x1;
       } else {
         const size_t kv_row = args.n_out[1];
-        float* c = args.cache + args.cache_off[m] + (s == 1 ? args.k_layer_off : args.v_layer_off) +
-                   static_cast<size_t>(pos) * kv_row + o;
-        c[0] = x0;
-        c[1] = x1;
+        const size_t at = args.cache_off[m] + (s == 1 ? args.k_layer_off : args.v_layer_off) +
+                          static_cast<size_t>(pos) * kv_row + o;
+        if (args.cache_f16) {  // rounded in once (llama.cpp:525-532)
+          uint16_t* c = static_cast<uint16_t*>(args.cache) + at;
+          c[0] = static_cast<uint16_t>(float_to_half_bits(x0));
+          c[1] = static_cast<uint16_t>(float_to_half_bits(x1));
+        } else {
+          float* c = static_cast<float*>(args.cache) + at;
+          c[0] = x0;
+          c[1] = x1;
+        }
       }
     }
   }

@@ -13,6 +13,25 @@ namespace {
 
 std::string fmt_shape(std::uint64_t a, std::uint64_t b) { return std::to_string(a) + "x" + std::to_string(b); }
 
+// An fp16 bit pattern widened to float, exactly (subnormals are m * 2^-24).
+float half_to_float(std::uint16_t h) {
+  const std::uint32_t sign = static_cast<std::uint32_t>(h & 0x8000u) << 16;
+  const std::uint32_t e = (h >> 10) & 0x1fu, m = h & 0x3ffu;
+  std::uint32_t bits;
+  if (e == 0x1fu) {
+    bits = sign | 0x7f800000u | (m << 13);
+  } else if (e != 0) {
+    bits = sign | ((e + 112u) << 23) | (m << 13);
+  } else {
+    const float f = std::ldexp(static_cast<float>(m), -24);
+    std::memcpy(&bits, &f, 4);
+    bits |= sign;
+  }
+  float out;
+  std::memcpy(&out, &bits, 4);
+  return out;
+}
+
 bool matmul_type(DType t) {
   switch (t) {
   case DType::F32: case DType::F16: case DType::BF16: case DType::Q8_0: case DType::Q4_0: case DType::Q4_1:
@@ -132,6 +151,7 @@ Expected<std::unique_ptr<LlamaModel>> LlamaModel::load(const std::string& path, 
   m->max_rows_ = std::max(m->max_seq_, m->max_batch_);
   m->n_slots_ = options.max_caches != 0 ? options.max_caches : m->max_batch_ + 1;
   m->exact_ = options.exact_activations;
+  m->cache_type_ = options.cache;
 
   // Bind (weights.cpp:71-127).
   const std::uint64_t d = c.n_embd, dq = c.n_embd_q(), dkv = c.n_embd_kv(), ff = c.n_ff;
@@ -265,9 +285,14 @@ Expected<std::unique_ptr<LlamaModel>> LlamaModel::load(const std::string& path, 
       axon_hip_host_malloc(&m->rowinfo_host_, info_bytes) != AXON_HIP_OK)
     return m->device_error("row table");
   m->slot_elems_ = static_cast<std::size_t>(c.n_layer) * 2 * m->max_ctx_ * dkv;
-  const std::size_t pool = (m->n_slots_ + 1) * m->slot_elems_;  // +1: the cache-free forward's slot
-  if (axon_hip_malloc(reinterpret_cast<void**>(&m->kv_), pool * 4) != AXON_HIP_OK) return m->device_error("kv pool");
-  m->device_bytes_ += pool * 4;
+  const std::size_t pool = m->n_slots_ * m->slot_elems_ * m->kv_element_bytes();
+  if (axon_hip_malloc(&m->kv_, pool) != AXON_HIP_OK) return m->device_error("kv pool");
+  // The cache-free forward (llama.cpp:379-383) keeps its keys and values in float whatever
+  // the cache type, laid out as a slot of max_seq positions.
+  const std::size_t free_bytes = static_cast<std::size_t>(c.n_layer) * 2 * m->max_seq_ * dkv * 4;
+  if (axon_hip_malloc(reinterpret_cast<void**>(&m->kv_free_), free_bytes) != AXON_HIP_OK)
+    return m->device_error("kv (cache-free pass)");
+  m->device_bytes_ += pool + free_bytes;
   axon_hip_attention_rows_args probe{};
   probe.n_head = c.n_head;
   probe.n_kv = c.n_head_kv;
@@ -290,7 +315,7 @@ LlamaModel::~LlamaModel() {
                   static_cast<void*>(v_), static_cast<void*>(attn_), static_cast<void*>(gate_),
                   static_cast<void*>(up_), static_cast<void*>(tmp_), static_cast<void*>(logits_),
                   static_cast<void*>(scores_), static_cast<void*>(argmax_scratch_), static_cast<void*>(ids_), window_,
-                  xq_, rowinfo_, static_cast<void*>(kv_),
+                  xq_, rowinfo_, kv_, static_cast<void*>(kv_free_),
                   static_cast<void*>(rope_table_), weights_}) {
     if (p != nullptr) axon_hip_free(p);
   }
@@ -365,8 +390,16 @@ Expected<std::vector<float>> LlamaModel::read_cache(const KVCache& cache, std::s
   if (layer >= cfg_.n_layer || n > max_ctx_) return make_error(ErrorCode::InvalidArgument, "read_cache: out of range");
   const std::size_t dkv = cfg_.n_embd_kv();
   std::vector<float> out(n * dkv);
-  const float* src = kv_ + cache.slot() * slot_elems_ + (2 * layer + (values ? 1 : 0)) * max_ctx_ * dkv;
-  if (axon_hip_memcpy_d2h(out.data(), src, out.size() * 4) != AXON_HIP_OK) return device_error("read_cache");
+  const std::size_t at = cache.slot() * slot_elems_ + (2 * layer + (values ? 1 : 0)) * max_ctx_ * dkv;
+  if (cache_type_ == CacheType::F32) {
+    if (axon_hip_memcpy_d2h(out.data(), static_cast<const float*>(kv_) + at, out.size() * 4) != AXON_HIP_OK)
+      return device_error("read_cache");
+    return out;
+  }
+  std::vector<std::uint16_t> bits(n * dkv);
+  if (axon_hip_memcpy_d2h(bits.data(), static_cast<const std::uint16_t*>(kv_) + at, bits.size() * 2) != AXON_HIP_OK)
+    return device_error("read_cache");
+  for (std::size_t i = 0; i < bits.size(); ++i) out[i] = half_to_float(bits[i]);
   return out;
 }
 
@@ -444,6 +477,13 @@ Expected<std::size_t> LlamaModel::run(std::span<const Row> rows, bool copy_logit
   std::int32_t* nvis = pos + R;
   auto* coff = reinterpret_cast<std::int64_t*>(static_cast<std::byte*>(rowinfo_host_) + align_up(12 * R, 8));
   last_rows_ = 0;
+  // The cache-free forward's rows all name slot n_slots_: its keys and values go to the float
+  // area kv_free_ (max_seq positions per layer); cached passes use the pool in the cache type
+  // (llama.cpp:379-383, 520-563).
+  const bool free_pass = n > 0 && rows[0].slot == static_cast<int>(n_slots_);
+  void* const kv = free_pass ? static_cast<void*>(kv_free_) : kv_;
+  const int kv_f16 = !free_pass && cache_type_ == CacheType::F16 ? 1 : 0;
+  const std::size_t layer_ctx = free_pass ? max_seq_ : max_ctx_;
   // The previous call's row table may still be in flight when its logits stayed on the device.
   if (axon_hip_synchronize() != AXON_HIP_OK) return device_error("synchronize");
   std::uint32_t max_vis = 0;
@@ -451,7 +491,7 @@ Expected<std::size_t> LlamaModel::run(std::span<const Row> rows, bool copy_logit
     ids[i] = rows[i].token;
     pos[i] = rows[i].pos;
     nvis[i] = rows[i].pos + 1;
-    coff[i] = static_cast<std::int64_t>(rows[i].slot) * static_cast<std::int64_t>(slot_elems_);
+    coff[i] = free_pass ? 0 : static_cast<std::int64_t>(rows[i].slot) * static_cast<std::int64_t>(slot_elems_);
     max_vis = std::max<std::uint32_t>(max_vis, static_cast<std::uint32_t>(nvis[i]));
   }
   const std::size_t info_bytes = align_up(12 * R, 8) + 8 * R;
@@ -485,8 +525,8 @@ Expected<std::size_t> LlamaModel::run(std::span<const Row> rows, bool copy_logit
   };
   for (std::size_t l = 0; l < c.n_layer; ++l) {
     const Layer& L = layers_[l];
-    const std::int64_t k_layer = static_cast<std::int64_t>(2 * l) * max_ctx_ * dkv;
-    const std::int64_t v_layer = k_layer + static_cast<std::int64_t>(max_ctx_ * dkv);
+    const std::int64_t k_layer = static_cast<std::int64_t>(2 * l) * layer_ctx * dkv;
+    const std::int64_t v_layer = k_layer + static_cast<std::int64_t>(layer_ctx * dkv);
 
     // attention block (llama.cpp:500-595)
     const bool qkv_q8 = q8_path(L.wq) && q8_path(L.wk) && q8_path(L.wv) && L.wq.type == L.wk.type &&
@@ -518,7 +558,8 @@ Expected<std::size_t> LlamaModel::run(std::span<const Row> rows, bool copy_logit
       fa.head_dim = c.head_dim;
       fa.pos = d_pos;
       fa.cache_off = d_coff;
-      fa.cache = kv_;
+      fa.cache = kv;
+      fa.cache_f16 = kv_f16;
       fa.k_layer_off = k_layer;
       fa.v_layer_off = v_layer;
       probe_begin(L.wq);
@@ -560,7 +601,8 @@ Expected<std::size_t> LlamaModel::run(std::span<const Row> rows, bool copy_logit
       ra.neox = c.rope_style == kernels::RopeStyle::NeoX ? 1 : 0;
       ra.theta = c.rope_theta;
       ra.table = rope_table_;
-      ra.cache = kv_;
+      ra.cache = kv;
+      ra.cache_f16 = kv_f16;
       ra.cache_off = d_coff;
       ra.k_layer_off = k_layer;
       ra.v_layer_off = v_layer;
@@ -573,7 +615,8 @@ Expected<std::size_t> LlamaModel::run(std::span<const Row> rows, bool copy_logit
     aa.out = attn_;
     aa.q_stride = static_cast<std::uint32_t>(dq);
     aa.out_stride = static_cast<std::uint32_t>(dq);
-    aa.kv = kv_;
+    aa.kv = kv;
+    aa.f16 = kv_f16;
     aa.k_off = d_coff;
     aa.v_off = d_coff;
     aa.n_vis = d_nvis;

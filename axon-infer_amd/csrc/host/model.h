@@ -25,6 +25,10 @@
 
 namespace axon::model {
 
+// Key/value cache storage (src/model/config.h:16): F32 keeps cached decoding bit-identical to
+// the cache-free pass; F16 halves the cache and rounds each key and value once when written.
+enum class CacheType : std::uint8_t { F32, F16 };
+
 struct LoadOptions {
   std::size_t max_seq = 512;    // rows per prefill call (llama.h:24-43)
   std::size_t max_ctx = 4096;   // positions per cache, clamped to the training context
@@ -32,6 +36,7 @@ struct LoadOptions {
   std::size_t max_caches = 0;   // KV slots on the device (0: max_batch + 1)
   bool exact_activations = false;
   kernels::KernelSet kernels = kernels::KernelSet::Hip;
+  CacheType cache = CacheType::F32;  // llama.h:40-42
 };
 
 struct Config {
@@ -108,7 +113,7 @@ public:
   // A fresh cache in a free device slot, or an error when every slot is taken.
   Expected<std::unique_ptr<KVCache>> new_cache();
   void release_cache(const KVCache& cache);
-  // Copies rows [0, n) of layer l's K or V of a cache to the host (tests).
+  // Copies rows [0, n) of layer l's K or V of a cache to the host as floats (tests).
   Expected<std::vector<float>> read_cache(const KVCache& cache, std::size_t layer, bool values, std::size_t n);
 
   // Kernel-time probe: while enabled, every matmul launch on weights of `type` (one ggml type
@@ -130,6 +135,8 @@ public:
   std::size_t max_ctx() const { return max_ctx_; }
   std::size_t max_seq() const { return max_seq_; }
   std::size_t max_batch() const { return max_batch_; }
+  CacheType cache_type() const { return cache_type_; }
+  std::size_t kv_element_bytes() const { return cache_type_ == CacheType::F16 ? 2 : 4; }
 
 private:
   LlamaModel() = default;
@@ -154,12 +161,14 @@ private:
   bool have_rope_freqs_ = false;
   std::size_t max_seq_ = 0, max_ctx_ = 0, max_batch_ = 0, max_rows_ = 0, n_slots_ = 0;
   bool exact_ = false;
+  CacheType cache_type_ = CacheType::F32;
   std::size_t weight_bytes_ = 0, device_bytes_ = 0;
 
   // Device memory.
   void* weights_ = nullptr;
   float* rope_table_ = nullptr;
-  float* kv_ = nullptr;
+  void* kv_ = nullptr;        // n_slots_ cache slots of slot_elems_ elements (float or fp16)
+  float* kv_free_ = nullptr;  // the cache-free forward's keys and values: float, max_seq positions
   std::size_t slot_elems_ = 0;
   float *x_ = nullptr, *h_ = nullptr, *q_ = nullptr, *k_ = nullptr, *v_ = nullptr, *attn_ = nullptr;
   float *gate_ = nullptr, *up_ = nullptr, *tmp_ = nullptr, *logits_ = nullptr, *scores_ = nullptr;

@@ -196,9 +196,11 @@ typedef struct {
   float theta;
   const float* freq_factors; /* device, or NULL */
   const float* table;     /* device cos/sin pairs [pos][rotary_dim/2] built on the host, or NULL */
-  float* cache;           /* KV pool base, or NULL for no cache write */
+  void* cache;            /* KV pool base (float or fp16 elements), or NULL for no cache write */
   const int64_t* cache_off; /* per-row element offset of the row's sequence (device), or NULL */
   int64_t k_layer_off, v_layer_off;
+  int cache_f16;          /* the cache holds fp16 bit patterns: rows rounded in once, round to nearest
+                           * even (CacheType::F16, llama.cpp:525-532, 559-563) */
 } axon_hip_rope_rows_args;
 int axon_hip_rope_rows(const axon_hip_rope_rows_args* args, size_t n_rows);
 
@@ -256,11 +258,12 @@ typedef struct {
   uint32_t rot_half, head_dim;
   const int32_t* pos;
   const int64_t* cache_off;
-  float* cache;
+  void* cache;            /* float or fp16 elements (cache_f16) */
   int64_t k_layer_off, v_layer_off;
   /* out_mode 2 only: also the Q8_0 blocks of every output row (down's input, llama.cpp:600-620,
    * [n_rows][n_out[0] / 32] blocks), or NULL. Requires n_out[0] % 32 == 0. */
   void* outq;
+  int cache_f16;          /* out_mode 3: k and v rounded into an fp16 cache (llama.cpp:525-532) */
 } axon_hip_matvec_fused_args;
 int axon_hip_matvec_fused(const axon_hip_matvec_fused_args* args);
 /* 1 when axon_hip_matvec_fused takes this shape (rows, row length, input mode, SiLU pairing). */

@@ -29,6 +29,9 @@ typedef struct {
   size_t max_caches;
   int exact_activations;
   const char* kernels;
+  /* LoadOptions::cache (src/model/llama.h:40-42, CacheType src/model/config.h:16): 0 F32, 1 F16
+   * (keys and values rounded once into an fp16 cache; the cache-free forward stays float). */
+  int cache_type;
 } axon_model_options;
 
 typedef struct {
@@ -37,6 +40,7 @@ typedef struct {
   size_t weight_bytes_per_token; /* llama.cpp:151-167 */
   size_t device_bytes;
   size_t kv_bytes_per_position;  /* both K and V, all layers, one sequence */
+  int cache_type;                /* 0 F32, 1 F16 */
 } axon_model_info;
 
 const char* axon_model_last_error(void);
@@ -51,7 +55,8 @@ int axon_model_cache_new(axon_model* model, int* cache);
 int axon_model_cache_free(axon_model* model, int cache);
 int axon_model_cache_pos(axon_model* model, int cache, size_t* pos);
 int axon_model_cache_truncate(axon_model* model, int cache, size_t pos);
-/* Rows [0, n) of layer l's keys (values = 0) or values (1) of a cache, to the host. */
+/* Rows [0, n) of layer l's keys (values = 0) or values (1) of a cache, to the host as floats
+ * (fp16 elements widened exactly). */
 int axon_model_cache_read(axon_model* model, int cache, size_t layer, int values, size_t n, float* out);
 
 /* The passes. logits: host [n][n_vocab], or NULL to leave them in HBM for axon_model_greedy (or

@@ -138,11 +138,21 @@ static void rmsnorm_rows(const ora_model* m, const float* x, const ora_tensor* w
   for (size_t r = 0; r < seq; ++r) ora_rmsnorm(x + r * n, w->data, out + r * n, n, m->rms_eps);
 }
 
-static float* cache_k(const ora_model* m, ora_cache* c, size_t l) {
-  return c->base + (2 * l) * c->max_ctx * ((size_t)m->n_head_kv * m->head_dim);
+static size_t cache_at(const ora_model* m, const ora_cache* c, size_t l, int values) {
+  return (2 * l + (size_t)values) * c->max_ctx * ((size_t)m->n_head_kv * m->head_dim);
 }
-static float* cache_v(const ora_model* m, ora_cache* c, size_t l) {
-  return c->base + (2 * l + 1) * c->max_ctx * ((size_t)m->n_head_kv * m->head_dim);
+static float* cache_k(const ora_model* m, ora_cache* c, size_t l) { return (float*)c->base + cache_at(m, c, l, 0); }
+static float* cache_v(const ora_model* m, ora_cache* c, size_t l) { return (float*)c->base + cache_at(m, c, l, 1); }
+static uint16_t* cache_k16(const ora_model* m, ora_cache* c, size_t l) {
+  return (uint16_t*)c->base + cache_at(m, c, l, 0);
+}
+static uint16_t* cache_v16(const ora_model* m, ora_cache* c, size_t l) {
+  return (uint16_t*)c->base + cache_at(m, c, l, 1);
+}
+
+/* llama.cpp:525-532, 559-563: rows of float keys and values rounded once into an fp16 cache. */
+static void round_in(uint16_t* dst, const float* src, size_t n) {
+  for (size_t i = 0; i < n; ++i) dst[i] = ora_fp32_to_fp16(src[i]);
 }
 
 /* The one forward pass, llama.cpp:315-639. batch != NULL is forward_batch: row i is its own
@@ -164,6 +174,11 @@ static int run(const ora_model* m, const int32_t* tokens, size_t seq, ora_cache*
       if (batch[i]->pos + 1 > total) total = batch[i]->pos + 1;
     }
   }
+  /* llama.cpp:381-382: an fp16 cache stages the new keys and values in float (a.k, a.v). */
+  const int half_cache = (cache != NULL && cache->f16) || (batch != NULL && batch[0]->f16);
+  if (batch != NULL)
+    for (size_t i = 0; i < seq; ++i)
+      if (batch[i]->f16 != batch[0]->f16) return -4;
   acts a = carve(m, ws, seq, total);
   const float scale = 1.0f / sqrtf((float)hd);
 
@@ -172,7 +187,7 @@ static int run(const ora_model* m, const int32_t* tokens, size_t seq, ora_cache*
 
   for (size_t l = 0; l < m->n_layer; ++l) {
     const ora_layer* w = &m->layers[l];
-    const int direct = cache != NULL;
+    const int direct = cache != NULL && !half_cache;
     float* k_base = direct ? cache_k(m, cache, l) : a.k;
     float* v_base = direct ? cache_v(m, cache, l) : a.v;
     float* k_new = direct ? k_base + n_past * kv_row : a.k;
@@ -200,15 +215,33 @@ static int run(const ora_model* m, const int32_t* tokens, size_t seq, ora_cache*
        * (sequence, head) over that cache. */
       for (size_t i = 0; i < seq; ++i) {
         ora_cache* c = batch[i];
-        memcpy(cache_k(m, c, l) + c->pos * kv_row, k_new + i * kv_row, kv_row * sizeof(float));
-        memcpy(cache_v(m, c, l) + c->pos * kv_row, v_new + i * kv_row, kv_row * sizeof(float));
+        if (half_cache) {
+          round_in(cache_k16(m, c, l) + c->pos * kv_row, k_new + i * kv_row, kv_row);
+          round_in(cache_v16(m, c, l) + c->pos * kv_row, v_new + i * kv_row, kv_row);
+        } else {
+          memcpy(cache_k(m, c, l) + c->pos * kv_row, k_new + i * kv_row, kv_row * sizeof(float));
+          memcpy(cache_v(m, c, l) + c->pos * kv_row, v_new + i * kv_row, kv_row * sizeof(float));
+        }
       }
       for (size_t b = 0; b < seq; ++b) {
         ora_cache* c = batch[b];
         for (size_t h = 0; h < nh; ++h) {
-          ora_attention_kv_heads(a.q + b * q_row, cache_k(m, c, l), cache_v(m, c, l), a.attn + b * q_row,
-                                 a.scores, 1, c->pos, nh, nkv, hd, scale, h, h + 1);
+          if (half_cache)
+            ora_attention_kv_heads_f16(a.q + b * q_row, cache_k16(m, c, l), cache_v16(m, c, l),
+                                       a.attn + b * q_row, a.scores, 1, c->pos, nh, nkv, hd, scale, h, h + 1);
+          else
+            ora_attention_kv_heads(a.q + b * q_row, cache_k(m, c, l), cache_v(m, c, l), a.attn + b * q_row,
+                                   a.scores, 1, c->pos, nh, nkv, hd, scale, h, h + 1);
         }
+      }
+    } else if (half_cache) {
+      /* llama.cpp:557-563 then 566-590: the chunk's rows rounded in, then every row attends over
+       * the fp16 cache. */
+      round_in(cache_k16(m, cache, l) + n_past * kv_row, k_new, seq * kv_row);
+      round_in(cache_v16(m, cache, l) + n_past * kv_row, v_new, seq * kv_row);
+      for (size_t h = 0; h < nh; ++h) {
+        ora_attention_kv_heads_f16(a.q, cache_k16(m, cache, l), cache_v16(m, cache, l), a.attn, a.scores, seq,
+                                   n_past, nh, nkv, hd, scale, h, h + 1);
       }
     } else {
       /* llama.cpp:566-590: rows are computed independently, so all rows in one call. */

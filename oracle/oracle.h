@@ -143,12 +143,15 @@ typedef struct {
   const ora_layer* layers;
 } ora_model;
 
-/* A per-sequence F32 cache, laid out as src/model/kv_cache.cpp:15-18:
- * layer l's K rows at base + (2l) * max_ctx * row, V rows at base + (2l+1) * max_ctx * row. */
+/* A per-sequence cache, laid out as src/model/kv_cache.cpp:15-18: layer l's K rows at
+ * base + (2l) * max_ctx * row, V rows at base + (2l+1) * max_ctx * row (elements). f16 == 0:
+ * float elements (CacheType::F32); f16 == 1: fp16 bit patterns (CacheType::F16,
+ * src/model/kv_cache.h:34-43). The caches of one forward_batch call share one type. */
 typedef struct {
-  float* base;
+  void* base;
   size_t max_ctx;
   size_t pos;
+  int f16;
 } ora_cache;
 
 /* Scratch sized by ora_workspace_floats(model, n_tokens, ctx). */

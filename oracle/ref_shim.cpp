@@ -93,9 +93,11 @@ void ref_matmul_q4_1_q8_rows(const void* w, const void* x, float* y, size_t r, s
 
 // ---- LlamaModel (src/model/llama.h:83-153) ----
 // Returns a handle or null; the error message is copied into err.
-void* ref_model_load(const char* path, size_t max_seq, size_t max_ctx, size_t max_batch, int n_threads,
-                     int exact_activations, char* err, size_t err_len) {
+// LlamaModel::load on the scalar table; cache_f16 selects CacheType::F16 for every cache.
+void* ref_model_load_cache(const char* path, size_t max_seq, size_t max_ctx, size_t max_batch, int n_threads,
+                           int exact_activations, int cache_f16, char* err, size_t err_len) {
   axon::model::LoadOptions opts;
+  opts.cache = cache_f16 != 0 ? axon::model::CacheType::F16 : axon::model::CacheType::F32;
   opts.max_seq = max_seq;
   opts.max_ctx = max_ctx;
   opts.max_batch = max_batch;
@@ -115,13 +117,18 @@ void* ref_model_load(const char* path, size_t max_seq, size_t max_ctx, size_t ma
   return h;
 }
 
+void* ref_model_load(const char* path, size_t max_seq, size_t max_ctx, size_t max_batch, int n_threads,
+                     int exact_activations, char* err, size_t err_len) {
+  return ref_model_load_cache(path, max_seq, max_ctx, max_batch, n_threads, exact_activations, 0, err, err_len);
+}
+
 void ref_model_free(void* h) { delete static_cast<RefModel*>(h); }
 
 int ref_model_threads(void* h) { return static_cast<RefModel*>(h)->model->n_threads(); }
 
 size_t ref_model_weight_bytes(void* h) { return static_cast<RefModel*>(h)->model->weight_bytes_per_token(); }
 
-// A new F32 cache owned by the handle; returns its index.
+// A new cache of the model's type owned by the handle; returns its index.
 int ref_cache_new(void* h) {
   auto* m = static_cast<RefModel*>(h);
   m->caches.push_back(std::make_unique<axon::model::KVCache>(m->model->new_cache()));
@@ -140,6 +147,13 @@ void ref_cache_fill(void* h, int c, const float* rows, size_t n) {
   const size_t row = cache.row_floats();
   const size_t pos = cache.pos();
   for (size_t l = 0; l < cache.n_layer(); ++l) {
+    if (cache.type() == axon::model::CacheType::F16) {
+      for (size_t i = 0; i < n * row; ++i) {
+        cache.k16(l)[pos * row + i] = axon::fp32_to_fp16(rows[(l * 2 + 0) * n * row + i]);
+        cache.v16(l)[pos * row + i] = axon::fp32_to_fp16(rows[(l * 2 + 1) * n * row + i]);
+      }
+      continue;
+    }
     std::memcpy(cache.k(l) + pos * row, rows + (l * 2 + 0) * n * row, n * row * sizeof(float));
     std::memcpy(cache.v(l) + pos * row, rows + (l * 2 + 1) * n * row, n * row * sizeof(float));
   }

@@ -173,6 +173,9 @@ def ref() -> C.CDLL | None:
         lib.ref_model_load.restype = C.c_void_p
         lib.ref_model_load.argtypes = [C.c_char_p, C.c_size_t, C.c_size_t, C.c_size_t, C.c_int, C.c_int,
                                        C.c_char_p, C.c_size_t]
+        lib.ref_model_load_cache.restype = C.c_void_p
+        lib.ref_model_load_cache.argtypes = [C.c_char_p, C.c_size_t, C.c_size_t, C.c_size_t, C.c_int, C.c_int,
+                                             C.c_int, C.c_char_p, C.c_size_t]
         for f in ("ref_model_free", "ref_model_threads", "ref_cache_new"):
             getattr(lib, f).argtypes = [C.c_void_p]
         lib.ref_model_weight_bytes.restype = C.c_size_t
@@ -231,7 +234,7 @@ class OraModel(C.Structure):
 
 
 class OraCache(C.Structure):
-    _fields_ = [("base", C.c_void_p), ("max_ctx", C.c_size_t), ("pos", C.c_size_t)]
+    _fields_ = [("base", C.c_void_p), ("max_ctx", C.c_size_t), ("pos", C.c_size_t), ("f16", C.c_int)]
 
 
 class ModelConfig:
@@ -296,10 +299,11 @@ class OracleModel:
         self.m = m
         self.lib = oracle()
 
-    def new_cache(self, max_ctx: int):
+    def new_cache(self, max_ctx: int, f16: bool = False):
+        """A cache of float elements (CacheType::F32) or fp16 bit patterns (CacheType::F16)."""
         row = self.cfg.n_head_kv * self.cfg.head_dim
-        store = np.zeros(self.cfg.n_layer * 2 * max_ctx * row, dtype=np.float32)
-        c = OraCache(store.ctypes.data, max_ctx, 0)
+        store = np.zeros(self.cfg.n_layer * 2 * max_ctx * row, dtype=np.uint16 if f16 else np.float32)
+        c = OraCache(store.ctypes.data, max_ctx, 0, int(f16))
         c._store = store
         return c
 
@@ -333,12 +337,12 @@ class OracleModel:
 class RefModel:
     """The reference's own LlamaModel (scalar table) through oracle/_ref."""
 
-    def __init__(self, path: Path, max_seq=32, max_ctx=128, max_batch=1, n_threads=1, exact=False):
+    def __init__(self, path: Path, max_seq=32, max_ctx=128, max_batch=1, n_threads=1, exact=False, f16=False):
         self.lib = ref()
         assert self.lib is not None
         err = C.create_string_buffer(512)
-        self.h = self.lib.ref_model_load(str(path).encode(), max_seq, max_ctx, max_batch, n_threads, int(exact),
-                                         err, 512)
+        self.h = self.lib.ref_model_load_cache(str(path).encode(), max_seq, max_ctx, max_batch, n_threads,
+                                               int(exact), int(f16), err, 512)
         assert self.h, err.value.decode()
         self.n_vocab = ModelConfig(GGUF(path)).n_vocab
 

@@ -109,17 +109,19 @@ def test_synthetic_model_loads_in_oracle_and_reference(tmp_path):
 
 @pytest.mark.parametrize("cname,pyname", [("axon_hip_rope_rows_args", "RopeRowsArgs"),
                                           ("axon_hip_attention_rows_args", "AttentionRowsArgs"),
-                                          ("axon_hip_matvec_fused_args", "MatvecFusedArgs")])
+                                          ("axon_hip_matvec_fused_args", "MatvecFusedArgs"),
+                                          ("axon_model_options", "ModelOptions"),
+                                          ("axon_model_info", "ModelInfo")])
 def test_ctypes_structs_match_the_header_layout(tmp_path, cname, pyname):
     """The ctypes mirrors of the argument structs have the size and field offsets gcc gives the
-    declarations in include/axon_hip.h."""
+    declarations in include/axon_hip.h and include/axon_model.h."""
     import subprocess
     import axon_hip as H
     py = getattr(H, pyname)
     fields = [f[0] for f in py._fields_]
     src = tmp_path / "layout.c"
     body = "".join(f'  printf("%zu\\n", offsetof({cname}, {f}));\n' for f in fields)
-    src.write_text(f'#include <stddef.h>\n#include <stdio.h>\n#include "axon_hip.h"\n'
+    src.write_text(f'#include <stddef.h>\n#include <stdio.h>\n#include "axon_hip.h"\n#include "axon_model.h"\n'
                    f'int main(void) {{\n  printf("%zu\\n", sizeof({cname}));\n{body}  return 0;\n}}\n')
     exe = tmp_path / "layout"
     subprocess.run(["gcc", "-I", str(ROOT / "include"), str(src), "-o", str(exe)], check=True)

@@ -141,6 +141,49 @@ def test_model_forward_bit_exact_with_reference(name):
         assert np.array_equal(a[j], full[n])
 
 
+@pytest.mark.parametrize("name", MODELS)
+def test_f16_cache_model_bit_exact_with_reference(name):
+    """The oracle's fp16 cache (CacheType::F16: keys and values staged in float, rounded once
+    into the cache, attention through attention_kv_heads_f16; llama.cpp:379-383, 520-590)
+    against the reference's own LlamaModel loaded with LoadOptions::cache = F16: prefill
+    chunks, single steps and a ragged forward_batch, bit for bit."""
+    path = GOLDEN / "gguf" / name
+    tokens = golden("model/synthetic-2l.tokens.axt")
+    om = OracleModel(path)
+    rm = RefModel(path, max_seq=32, max_ctx=128, max_batch=4, f16=True)
+    # The cache-free pass keeps float keys and values (no cache, no rounding).
+    assert np.array_equal(om.forward(tokens), rm.forward(tokens))
+    oc = om.new_cache(128, f16=True)
+    rc = rm.new_cache()
+    for lo, hi in ((0, 5), (5, 8), (8, 9), (9, 16), (16, len(tokens))):
+        assert np.array_equal(om.forward(tokens[lo:hi], oc), rm.forward_prefill(rc, tokens[lo:hi]))
+    caches_o = [om.new_cache(128, f16=True) for _ in range(3)]
+    caches_r = [rm.new_cache() for _ in range(3)]
+    for j, n in enumerate((3, 9, 14)):
+        om.forward(tokens[:n], caches_o[j])
+        rm.forward_prefill(caches_r[j], tokens[:n])
+    nxt = np.array([tokens[3], tokens[9], tokens[14]], np.int32)
+    assert np.array_equal(om.forward_batch(nxt, caches_o), rm.forward_batch(caches_r, nxt))
+
+
+def test_f16_cache_rounds_keys_and_values_once():
+    """Layer 0's keys and values are computed from the same inputs with either cache, so the
+    fp16 cache must hold exactly numpy's round-to-nearest-even fp16 of the F32 cache's rows (an
+    independent restatement of the rounding), and nothing past the written positions."""
+    path = GOLDEN / "gguf" / "synthetic-2l.gguf"
+    tokens = golden("model/synthetic-2l.tokens.axt")[:6]
+    om = OracleModel(path)
+    c16 = om.new_cache(16, f16=True)
+    c32 = om.new_cache(16)
+    om.forward(tokens, c16)
+    om.forward(tokens, c32)
+    row = om.cfg.n_head_kv * om.cfg.head_dim
+    f32 = c32._store.reshape(om.cfg.n_layer, 2, 16, row)
+    f16 = c16._store.reshape(om.cfg.n_layer, 2, 16, row)
+    assert np.array_equal(f16[0, :, :6], f32[0, :, :6].astype(np.float16).view(np.uint16))
+    assert not f16[:, :, 6:].any()
+
+
 def test_f32_model_matches_numpy_fixture():
     # tests/unit/test_model_forward.cpp:40-54
     om = OracleModel(GOLDEN / "gguf" / "synthetic-2l.gguf")
