@@ -64,8 +64,9 @@ int ready() {
 
 bool fits_u32(size_t v) { return v <= 0xffffffffull; }
 
-// The Q8_0-activation path: groups of up to four rows on the dot4 matvec below 16 rows,
-// int8 MFMA tiles from 16 rows.
+// The Q8_0-activation path: groups of up to four rows on the dot4 matvec below 5 rows, the
+// few-rows MFMA kernel (every segment in one launch) from 5 to 64 rows, 64 x 64 MFMA tiles
+// beyond. All of them give the same bits for a row.
 int q8_matmul(int type, const void* xq, size_t n_rows, size_t n_in, size_t n_seg, const void* const* w,
               float* const* y, const size_t* n_out, const size_t* y_stride, int accumulate) {
   if (n_in % kQK != 0) return fail(kInvalidArgument, "quantized matmul: n_in %zu is not a multiple of 32", n_in);
@@ -79,6 +80,19 @@ int q8_matmul(int type, const void* xq, size_t n_rows, size_t n_in, size_t n_seg
   if (n_rows == 0) return kOk;
   const uint32_t nb = static_cast<uint32_t>(n_in / kQK);
   const size_t xrow = static_cast<size_t>(nb) * kBytesQ8_0;
+  if (n_rows >= 5 && n_rows <= kRowsMaxM) {
+    MatvecArgs a{};
+    for (size_t s = 0; s < n_seg; ++s) {
+      a.seg[s] = MatvecSeg{static_cast<const uint8_t*>(w[s]), y[s], static_cast<uint32_t>(n_out[s]),
+                           static_cast<uint32_t>(y_stride[s]), 0};
+    }
+    a.n_seg = static_cast<int>(n_seg);
+    a.xq = static_cast<const uint8_t*>(xq);
+    a.nb = nb;
+    a.m = static_cast<uint32_t>(n_rows);
+    a.accumulate = accumulate;
+    if (matmul_q8_rows_fits(type, a)) return matmul_q8_rows_launch(type, a);
+  }
   if (n_rows >= 16) {
     for (size_t s = 0; s < n_seg; ++s) {
       MatvecArgs a{};

@@ -69,5 +69,10 @@ uint32_t matvec_q8_max_rows(int type, uint32_t nb);
 int matvec_q6k_launch(MatvecArgs& a, uint32_t n_in);
 // int8 MFMA tiles for 16 or more Q8_0 activation rows.
 int matmul_q8_mfma_launch(int type, MatvecArgs& a);
+// int8 MFMA for 1..kRowsMaxM activation rows (batched decode): every segment in one grid, one
+// 16 x 16 tile per wave; the same outputs, bit for bit, as the other Q8_0-activation paths.
+constexpr uint32_t kRowsMaxM = 64;
+bool matmul_q8_rows_fits(int type, const MatvecArgs& a);
+int matmul_q8_rows_launch(int type, MatvecArgs& a);
 
 }  // namespace axon_hip

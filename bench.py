@@ -28,6 +28,9 @@ The line also carries:
   cpu_baseline the reference's own LlamaModel on its scalar table (oracle/_ref, compiled from the
                reference sources) on the same GGUF, threads = the host's cores, on a bounded sample.
 
+  f16_cache    decode-b1 and ragged-32 again with the KV cache held as fp16 (LoadOptions::cache
+               = F16): half the cache bytes per position (kv_bytes_per_position).
+
   traffic      HBM bytes per launch of that kernel, from two rocprofv3 counter passes over
                `bench.py --traffic-probe` (FETCH_SIZE, then WRITE_SIZE, KiB per dispatch), each
                scaled by what the same counter reads for a device-to-device copy of 256 MiB in the
@@ -299,6 +302,7 @@ def main() -> int:
     ap.add_argument("--prompt", type=int, default=512)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-ragged", action="store_true", help="skip the 32-sequence workload")
+    ap.add_argument("--no-f16", action="store_true", help="skip the fp16-cache runs")
     ap.add_argument("--cpu-budget", type=float, default=12.0, help="seconds per CPU baseline sample")
     ap.add_argument("--traffic-probe", action="store_true",
                     help="run the workload of the FETCH_SIZE / WRITE_SIZE counter passes and exit")
@@ -385,6 +389,21 @@ def main() -> int:
         log(f"ragged-32: {rg['tokens_per_s']:.1f} tok/s over {rg['steps']} steps (mean batch {rg['mean_batch']:.1f})")
         result["ragged32"] = {k: (round(v, 3) if isinstance(v, float) else v) for k, v in rg.items()}
     model.close()
+    if not args.no_f16:
+        # The same workloads over an fp16 KV cache (LoadOptions::cache = F16): half the cache
+        # bytes per position, keys and values rounded once on the way in.
+        m16 = H.Model(path, max_seq=512, max_ctx=2048 + 128 + 64, max_batch=32, max_caches=34, cache="f16")
+        b16 = bench_decode_b1(H, m16, info.n_vocab, args.steps, args.warmup, args.prompt, args.seed)
+        log(f"decode-b1 (f16 cache): {b16['tokens_per_s']:.1f} tok/s")
+        f16 = {"kv_bytes_per_position": m16.info.kv_bytes_per_position,
+               "decode_b1": {"tokens_per_s": round(b16["tokens_per_s"], 2), "ms_per_step": round(b16["ms_per_step"], 4)}}
+        if not args.no_ragged:
+            rg16 = bench_ragged(H, m16, info.n_vocab, args.seed)
+            log(f"ragged-32 (f16 cache): {rg16['tokens_per_s']:.1f} tok/s")
+            f16["ragged32"] = {"tokens_per_s": round(rg16["tokens_per_s"], 3), "decode_s": round(rg16["decode_s"], 3),
+                               "prefill_s": round(rg16["prefill_s"], 3)}
+        m16.close()
+        result["f16_cache"] = f16
     if not args.no_cpu:
         b1c, rgc = cpu_baseline(path, info.n_vocab, args.seed, args.cpu_budget)
         result["cpu_baseline"] = b1c
