@@ -158,47 +158,55 @@ __global__ __launch_bounds__(kThreads) void mfma_q8_kernel(MatvecArgs args, uint
 
 // ---- Few activation rows (batched decode): 5..64 rows -------------------------------------
 // The same MFMA sums and the same per-output expression, block after block in order, with the
-// work spread for latency rather than reuse: each wave owns one 16 weight rows x 16 activation
-// rows tile, a workgroup's four waves sit WN x WM over the weight and activation rows (4 x 1 up
-// to 16 rows, 2 x 2 up to 32, 1 x 4 up to 64), every segment of the call (q|k|v, gate|up) is one
-// grid, and the next K chunk is loaded into registers while the current one computes. Chunk
-// loads are raw buffer loads sized to the segment's and the activations' bytes: a load past
-// either returns zero and touches nothing (the last rows and the last partial chunk).
-constexpr uint32_t kRowsChunk = 16;  // blocks per K chunk
+// work spread for latency: a workgroup owns 16 weight rows x TM activation rows (TM 16 or 32),
+// every segment of the call (q|k|v, gate|up) is one grid, and each of the four waves runs the
+// tile's MFMAs but folds one of the four outputs a lane's MFMA result holds (wave w: activation
+// rows 4 kq + w), so a wave's float work per block is one output per M tile. MFMAs go in
+// batches of eight blocks ahead of their folds, which stay in block order.
+// K goes in chunks of kRowsChunk blocks. Each thread loads whole (row, block) items of the next
+// chunk into registers (from the 4-byte boundary at or below the block, enough dwords to cover
+// it) while the current chunk computes, then expands them once into 32 aligned int8 values and
+// the scales in LDS: Q8_0 quants as they are, Q4_0 nibbles as q - 8 ((b + 0x78) ^ 0x80 per
+// byte, so the MFMA sum is sumi itself), Q4_1 nibbles as q. The loads are raw buffer loads
+// sized to the segment's and the activations' bytes: a load past either returns zero and
+// touches nothing (the last rows, the last blocks, the last partial chunk).
+constexpr uint32_t kRowsChunk = 32;                 // blocks per K chunk
+constexpr uint32_t kRowsPitch = kRowsChunk * 8 + 4;  // dwords per expanded row (padded)
+constexpr uint32_t kRowsTN = 16;                    // weight rows per workgroup
 
 template <int T>
-__host__ __device__ constexpr uint32_t rows_wpitch() { return kRowsChunk * block_bytes<T>() + 4; }
-__host__ __device__ constexpr uint32_t rows_xpitch() { return kRowsChunk * kBytesQ8_0 + 4; }
-
-template <int T, int WN, int WM>
-__host__ __device__ constexpr size_t rows_lds() {
-  return static_cast<size_t>(16 * WN) * rows_wpitch<T>() + static_cast<size_t>(16 * WM) * rows_xpitch() +
-         static_cast<size_t>(kRowsChunk) * 16 * WM * 8 + static_cast<size_t>(kRowsChunk) * 16 * WN * 8;
+__host__ __device__ constexpr uint32_t item_dwords() {
+  return (block_bytes<T>() + 2 + 3) / 4;  // a 2-byte aligned block from its 4-byte boundary
 }
 
-template <int T, int WN, int WM>
-__global__ __launch_bounds__(kThreads) void mfma_rows_kernel(MatvecArgs args) {
-  static_assert(WN * WM == kThreads / 64, "four waves");
-  constexpr int bs = block_bytes<T>();
-  constexpr uint32_t TN = 16 * WN, TM = 16 * WM, KC = kRowsChunk;
-  constexpr uint32_t WPITCH = rows_wpitch<T>(), XPITCH = rows_xpitch();
-  constexpr uint32_t WU = KC * bs / 4, XU = KC * kBytesQ8_0 / 4;  // dwords per row chunk
-  constexpr uint32_t NW = (TN * WU + kThreads - 1) / kThreads;
-  constexpr uint32_t NX = (TM * XU + kThreads - 1) / kThreads;
-  static_assert((KC * bs) % 4 == 0 && (KC * kBytesQ8_0) % 4 == 0, "dword chunks");
+// LDS: expanded weights [16][kRowsPitch], expanded activations [TM][kRowsPitch] (dwords), then
+// per (row, block) scales: wd, wm [16][KC], xd, xs [TM][KC].
+template <int TM>
+__host__ __device__ constexpr size_t rows_lds() {
+  return (static_cast<size_t>(kRowsTN + TM) * kRowsPitch + static_cast<size_t>(kRowsTN + TM) * kRowsChunk * 2) * 4;
+}
 
-  extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
-  uint8_t* wt = smem;                                         // [TN][WPITCH] weight bytes
-  uint8_t* xt = wt + TN * WPITCH;                             // [TM][XPITCH] activation bytes
-  float* xd = reinterpret_cast<float*>(xt + TM * XPITCH);     // [KC][TM] activation scales
-  int32_t* xs = reinterpret_cast<int32_t*>(xd + KC * TM);     // [KC][TM] activation quant sums
-  float* wd = reinterpret_cast<float*>(xs + KC * TM);         // [KC][TN] weight scales
-  float* wmn = wd + KC * TN;                                  // [KC][TN] weight minimums (Q4_1)
+template <int T, int TM>
+__global__ __launch_bounds__(kThreads) void mfma_rows_kernel(MatvecArgs args) {
+  constexpr int bs = block_bytes<T>();
+  constexpr uint32_t TN = kRowsTN, KC = kRowsChunk, P = kRowsPitch;
+  constexpr uint32_t MT = TM / 16;                      // MFMA tiles along the activation rows
+  constexpr uint32_t WI = TN * KC / kThreads;           // weight items per thread per chunk
+  constexpr uint32_t XI = TM * KC / kThreads;           // activation items per thread per chunk
+  constexpr uint32_t WD = item_dwords<T>(), XD = item_dwords<Q8_0>();
+  static_assert(TN * KC % kThreads == 0 && TM * KC % kThreads == 0, "whole items per thread");
+
+  extern __shared__ __attribute__((aligned(16))) uint32_t lds_rows[];
+  uint32_t* wa = lds_rows;                               // [TN][P]
+  uint32_t* xa = wa + TN * P;                            // [TM][P]
+  float* wd = reinterpret_cast<float*>(xa + TM * P);     // [TN][KC]
+  float* wmn = wd + TN * KC;                             // [TN][KC] (Q4_1)
+  float* xd = wmn + TN * KC;                             // [TM][KC]
+  int32_t* xs = reinterpret_cast<int32_t*>(xd + TM * KC);  // [TM][KC] (Q4_1)
 
   const uint32_t tid = threadIdx.x;
   const uint32_t lane = tid & 63;
   const uint32_t wave = tid >> 6;
-  const uint32_t wn = wave % WN, wm = wave / WN;
   int s = 0;
   if (args.n_seg > 1 && blockIdx.x >= args.seg[1].wg_begin) s = 1;
   if (args.n_seg > 2 && blockIdx.x >= args.seg[2].wg_begin) s = 2;
@@ -206,8 +214,9 @@ __global__ __launch_bounds__(kThreads) void mfma_rows_kernel(MatvecArgs args) {
   const uint32_t n0 = (blockIdx.x - seg.wg_begin) * TN;
   const uint32_t m0 = blockIdx.y * TM;
   const uint32_t nn = min(TN, seg.n_out - n0);
-  const uint32_t mm = min(TM, args.m - m0);
+  const uint32_t mm = min(static_cast<uint32_t>(TM), args.m - m0);
   const uint32_t nb = args.nb;
+  const uint32_t n_chunks = (nb + KC - 1) / KC;
   const uint32_t w_pitch = nb * bs, x_pitch = nb * kBytesQ8_0;
   const __amdgpu_buffer_rsrc_t wsrc = __builtin_amdgcn_make_buffer_rsrc(
       const_cast<uint8_t*>(seg.w) + static_cast<size_t>(n0) * w_pitch, 0, static_cast<int>(nn * w_pitch),
@@ -216,140 +225,187 @@ __global__ __launch_bounds__(kThreads) void mfma_rows_kernel(MatvecArgs args) {
       const_cast<uint8_t*>(args.xq) + static_cast<size_t>(m0) * x_pitch, 0, static_cast<int>(mm * x_pitch),
       static_cast<int>(kRawBufferWord3));
 
-  uint32_t rw[NW], rx[NX];
-  auto load = [&](uint32_t b0) {
+  // Item i of a chunk: block i % KC of row i / KC (blocks fastest: consecutive threads read
+  // consecutive blocks of a row). The bases are 4-byte aligned (the launcher checks), so a
+  // block's byte offset and its 4-byte boundary differ by 0 or 2.
+  struct Raw {
+    uint32_t w[WI][WD];
+    uint32_t x[XI][XD];
+  };
+  auto load = [&](uint32_t c, Raw& r) {
+    const uint32_t b0 = c * KC;
 #pragma unroll
-    for (uint32_t k = 0; k < NW; ++k) {
-      const uint32_t j = tid + k * kThreads;
-      const uint32_t r = j / WU, c = j - r * WU;
-      rw[k] = j < TN * WU ? __builtin_amdgcn_raw_buffer_load_b32(wsrc, r * w_pitch + b0 * bs + 4 * c, 0, 0) : 0u;
+    for (uint32_t k = 0; k < WI; ++k) {
+      const uint32_t i = tid + k * kThreads;
+      const uint32_t row = i / KC, b = i - row * KC;
+      const uint32_t off = row * w_pitch + (b0 + b) * bs;
+#pragma unroll
+      for (uint32_t d = 0; d < WD; ++d)
+        r.w[k][d] = __builtin_amdgcn_raw_buffer_load_b32(wsrc, (off & ~3u) + 4 * d, 0, 0);
     }
 #pragma unroll
-    for (uint32_t k = 0; k < NX; ++k) {
-      const uint32_t j = tid + k * kThreads;
-      const uint32_t r = j / XU, c = j - r * XU;
-      rx[k] = j < TM * XU ? __builtin_amdgcn_raw_buffer_load_b32(xsrc, r * x_pitch + b0 * kBytesQ8_0 + 4 * c, 0, 0)
-                          : 0u;
+    for (uint32_t k = 0; k < XI; ++k) {
+      const uint32_t i = tid + k * kThreads;
+      const uint32_t row = i / KC, b = i - row * KC;
+      const uint32_t off = row * x_pitch + (b0 + b) * kBytesQ8_0;
+#pragma unroll
+      for (uint32_t d = 0; d < XD; ++d)
+        r.x[k][d] = __builtin_amdgcn_raw_buffer_load_b32(xsrc, (off & ~3u) + 4 * d, 0, 0);
     }
   };
-  auto store = [&]() {
+  auto expand = [&](uint32_t c, const Raw& r) {
+    const uint32_t b0 = c * KC;
 #pragma unroll
-    for (uint32_t k = 0; k < NW; ++k) {
-      const uint32_t j = tid + k * kThreads;
-      const uint32_t r = j / WU, c = j - r * WU;
-      if (j < TN * WU) *reinterpret_cast<uint32_t*>(wt + r * WPITCH + 4 * c) = rw[k];
+    for (uint32_t k = 0; k < WI; ++k) {
+      const uint32_t i = tid + k * kThreads;
+      const uint32_t row = i / KC, b = i - row * KC;
+      const uint32_t sh = (((b0 + b) * bs) & 3u) * 8;  // the row start is 4-byte aligned
+      // v: the block from its first byte (the fp16 scale(s), then the quants); its last dword
+      // holds only the block's last bytes, from the last loaded dword.
+      uint32_t v[WD];
+#pragma unroll
+      for (uint32_t d = 0; d < WD; ++d) v[d] = __builtin_amdgcn_alignbit(d + 1 < WD ? r.w[k][d + 1] : 0u, r.w[k][d], sh);
+      uint32_t q[8];
+      if constexpr (T == Q8_0) {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) q[j] = __builtin_amdgcn_alignbit(v[j + 1], v[j], 16);
+      } else {
+        constexpr uint32_t first = T == Q4_0 ? 0 : 1;  // the dword where the nibbles start
+        constexpr uint32_t bsh = T == Q4_0 ? 16 : 0;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const uint32_t n4 = bsh ? __builtin_amdgcn_alignbit(v[first + j + 1], v[first + j], bsh) : v[first + j];
+          q[j] = n4 & 0x0f0f0f0fu;             // elements 4j .. 4j+3: low nibbles
+          q[j + 4] = (n4 >> 4) & 0x0f0f0f0fu;  // elements 16+4j ..: high nibbles
+          if constexpr (T == Q4_0) {
+            // q - 8 as int8 per byte: a byte is at most 0x87 after the add, so no carry
+            // crosses bytes, and flipping bit 7 subtracts 128.
+            q[j] = (q[j] + 0x78787878u) ^ 0x80808080u;
+            q[j + 4] = (q[j + 4] + 0x78787878u) ^ 0x80808080u;
+          }
+        }
+      }
+      uint4* dst = reinterpret_cast<uint4*>(wa + row * P + b * 8);
+      dst[0] = make_uint4(q[0], q[1], q[2], q[3]);
+      dst[1] = make_uint4(q[4], q[5], q[6], q[7]);
+      wd[row * KC + b] = half_bits_to_float(v[0] & 0xffffu);
+      if constexpr (T == Q4_1) wmn[row * KC + b] = half_bits_to_float(v[0] >> 16);
     }
 #pragma unroll
-    for (uint32_t k = 0; k < NX; ++k) {
-      const uint32_t j = tid + k * kThreads;
-      const uint32_t r = j / XU, c = j - r * XU;
-      if (j < TM * XU) *reinterpret_cast<uint32_t*>(xt + r * XPITCH + 4 * c) = rx[k];
+    for (uint32_t k = 0; k < XI; ++k) {
+      const uint32_t i = tid + k * kThreads;
+      const uint32_t row = i / KC, b = i - row * KC;
+      const uint32_t sh = (((b0 + b) * kBytesQ8_0) & 3u) * 8;
+      uint32_t v[XD];
+#pragma unroll
+      for (uint32_t d = 0; d < XD; ++d) v[d] = __builtin_amdgcn_alignbit(d + 1 < XD ? r.x[k][d + 1] : 0u, r.x[k][d], sh);
+      uint32_t q[8];
+      int32_t sum = 0;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        q[j] = __builtin_amdgcn_alignbit(v[j + 1], v[j], 16);
+        if constexpr (T == Q4_1) sum = __builtin_amdgcn_sdot4(static_cast<int32_t>(q[j]), 0x01010101, sum, false);
+      }
+      uint4* dst = reinterpret_cast<uint4*>(xa + row * P + b * 8);
+      dst[0] = make_uint4(q[0], q[1], q[2], q[3]);
+      dst[1] = make_uint4(q[4], q[5], q[6], q[7]);
+      xd[row * KC + b] = half_bits_to_float(v[0] & 0xffffu);
+      if constexpr (T == Q4_1) xs[row * KC + b] = sum;
     }
   };
 
-  const uint32_t col = lane & 15;  // weight row (B) / activation row (A) within the wave's 16
+  const uint32_t col = lane & 15;  // weight row (B) within the tile's 16
   const uint32_t kq = lane >> 4;   // which 8 of a block's 32 elements this lane feeds
-  const uint32_t wr = wn * 16 + col;
-  const uint32_t ar = wm * 16 + col;
-  float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-
-  load(0);
-  for (uint32_t b0 = 0; b0 < nb; b0 += KC) {
-    const uint32_t cb = min(KC, nb - b0);
-    store();
-    __syncthreads();
-    for (uint32_t i = tid; i < TM * KC; i += kThreads) {
-      const uint32_t r = i / KC, b = i - r * KC;
-      if (b < cb) {
-        const ActBlock a = unpack_q8_0_lds(xt, r * XPITCH + b * kBytesQ8_0);
-        xd[b * TM + r] = a.d;
-        xs[b * TM + r] = a.sum;
-      }
-    }
-    for (uint32_t i = tid; i < TN * KC; i += kThreads) {
-      const uint32_t r = i / KC, b = i - r * KC;
-      if (b < cb) {
-        const uint32_t h = *reinterpret_cast<const uint16_t*>(wt + r * WPITCH + b * bs);
-        wd[b * TN + r] = half_bits_to_float(h);
-        if constexpr (T == Q4_1) {
-          wmn[b * TN + r] = half_bits_to_float(*reinterpret_cast<const uint16_t*>(wt + r * WPITCH + b * bs + 2));
-        }
-      }
-    }
-    __syncthreads();
-    if (b0 + KC < nb) load(b0 + KC);  // in flight while this chunk computes
-
-    for (uint32_t b = 0; b < cb; ++b) {
-      // B operand: weight row wr, elements 8*kq .. 8*kq+7 of block b.
-      int64_t bw;
-      {
-        const uint32_t off = wr * WPITCH + b * bs;
-        uint32_t q[2];
-        if constexpr (T == Q8_0) {
-          lds_read_unaligned<2>(wt, off + 2 + 8 * kq, q);
-          bw = static_cast<int64_t>((static_cast<uint64_t>(q[1]) << 32) | q[0]);
-        } else {
-          constexpr uint32_t qoff = T == Q4_0 ? 2 : 4;
-          lds_read_unaligned<2>(wt, off + qoff + 8 * (kq & 1), q);
-          const uint32_t sh = (kq >> 1) * 4;  // low nibbles for elements 0..15, high for 16..31
-          const uint32_t lo = (q[0] >> sh) & 0x0f0f0f0fu;
-          const uint32_t hi = (q[1] >> sh) & 0x0f0f0f0fu;
-          bw = static_cast<int64_t>((static_cast<uint64_t>(hi) << 32) | lo);
-        }
-      }
-      const float dw = wd[b * TN + wr];
-      // A operand: activation row ar, elements 8*kq .. 8*kq+7 of block b.
-      uint32_t qa[2];
-      lds_read_unaligned<2>(xt, ar * XPITCH + b * kBytesQ8_0 + 2 + 8 * kq, qa);
-      const int64_t ax = static_cast<int64_t>((static_cast<uint64_t>(qa[1]) << 32) | qa[0]);
-      i32x4 d = {0, 0, 0, 0};
-      d = __builtin_amdgcn_mfma_i32_16x16x32_i8(ax, bw, d, 0, 0, 0);
-      const float4 dx4 = *reinterpret_cast<const float4*>(xd + b * TM + wm * 16 + 4 * kq);
-      const int4 xs4 = *reinterpret_cast<const int4*>(xs + b * TM + wm * 16 + 4 * kq);
-      const float dxv[4] = {dx4.x, dx4.y, dx4.z, dx4.w};
-      const int32_t xsv[4] = {xs4.x, xs4.y, xs4.z, xs4.w};
+  // Wave w feeds activation row (col + w) % 16 as A row col, which moves D row 4 kq + w (the
+  // output this wave folds) into the lane's first result: d[0] = sumi of activation row
+  // 4 kq + w and weight row col.
+  const uint32_t arow = (col + wave) & 15;
+  const uint32_t orow = 4 * kq + wave;
+  float acc[MT];
 #pragma unroll
-      for (int v = 0; v < 4; ++v) {
-        const float dx = dxv[v];
-        if constexpr (T == Q4_0) {
-          const int32_t sumi = d[v] - 8 * xsv[v];
-          acc[v] += static_cast<float>(sumi) * dw * dx;
-        } else if constexpr (T == Q8_0) {
-          acc[v] += static_cast<float>(d[v]) * dw * dx;
-        } else {
-          const float mw = wmn[b * TN + wr];
-          acc[v] += static_cast<float>(d[v]) * dw * dx + mw * dx * static_cast<float>(xsv[v]);
-        }
+  for (uint32_t t = 0; t < MT; ++t) acc[t] = 0.0f;
+  auto sums = [&](uint32_t b, uint32_t t) {
+    const uint2 wq = *reinterpret_cast<const uint2*>(wa + col * P + b * 8 + 2 * kq);
+    const uint2 xq = *reinterpret_cast<const uint2*>(xa + (16 * t + arow) * P + b * 8 + 2 * kq);
+    const int64_t bw = static_cast<int64_t>((static_cast<uint64_t>(wq.y) << 32) | wq.x);
+    const int64_t ax = static_cast<int64_t>((static_cast<uint64_t>(xq.y) << 32) | xq.x);
+    i32x4 d = {0, 0, 0, 0};
+    d = __builtin_amdgcn_mfma_i32_16x16x32_i8(ax, bw, d, 0, 0, 0);
+    return d[0];
+  };
+  auto fold = [&](uint32_t b, uint32_t t, int32_t sumi) {
+    const uint32_t r = 16 * t + orow;
+    const float dw = wd[col * KC + b];
+    const float dx = xd[r * KC + b];
+    if constexpr (T == Q4_1) {
+      acc[t] += static_cast<float>(sumi) * dw * dx + wmn[col * KC + b] * dx * static_cast<float>(xs[r * KC + b]);
+    } else {
+      // Q4_0: sumi carries the -8 offset already (the weights entered as q - 8).
+      acc[t] += static_cast<float>(sumi) * dw * dx;
+    }
+  };
+  constexpr uint32_t kBatch = 8;  // MFMAs issued together before their sums are folded
+  static_assert(KC % kBatch == 0, "whole batches");
+
+  // Two chunks' loads in flight: chunk c + 2 goes into c's registers once they are expanded.
+  auto chunk = [&](uint32_t c, Raw& r) {
+    const uint32_t cb = min(KC, nb - c * KC);
+    expand(c, r);
+    __syncthreads();
+    if (c + 2 < n_chunks) load(c + 2, r);
+    if (cb == KC) {
+      for (uint32_t b0 = 0; b0 < KC; b0 += kBatch) {
+        int32_t d[kBatch][MT];
+#pragma unroll
+        for (uint32_t k = 0; k < kBatch; ++k)
+#pragma unroll
+          for (uint32_t t = 0; t < MT; ++t) d[k][t] = sums(b0 + k, t);
+#pragma unroll
+        for (uint32_t k = 0; k < kBatch; ++k)
+#pragma unroll
+          for (uint32_t t = 0; t < MT; ++t) fold(b0 + k, t, d[k][t]);
       }
+    } else {
+      for (uint32_t b = 0; b < cb; ++b)
+#pragma unroll
+        for (uint32_t t = 0; t < MT; ++t) fold(b, t, sums(b, t));
     }
     __syncthreads();
+  };
+  Raw ra, rb;
+  load(0, ra);
+  if (n_chunks > 1) load(1, rb);
+  for (uint32_t c = 0; c < n_chunks; c += 2) {
+    chunk(c, ra);
+    if (c + 1 < n_chunks) chunk(c + 1, rb);
   }
 
-  if (wr < nn) {
+  if (col < nn) {
 #pragma unroll
-    for (int v = 0; v < 4; ++v) {
-      const uint32_t r = wm * 16 + 4 * kq + v;
+    for (uint32_t t = 0; t < MT; ++t) {
+      const uint32_t r = 16 * t + orow;
       if (r < mm) {
-        float* y = seg.y + static_cast<size_t>(m0 + r) * seg.y_stride + n0 + wr;
-        *y = args.accumulate ? *y + acc[v] : acc[v];
+        float* y = seg.y + static_cast<size_t>(m0 + r) * seg.y_stride + n0 + col;
+        *y = args.accumulate ? *y + acc[t] : acc[t];
       }
     }
   }
 }
 
-template <int WN, int WM>
+template <int TM>
 int rows_launch(int type, MatvecArgs& a) {
-  constexpr uint32_t TN = 16 * WN, TM = 16 * WM;
   uint32_t wg = 0;
   for (int s = 0; s < a.n_seg; ++s) {
     a.seg[s].wg_begin = wg;
-    wg += static_cast<uint32_t>(ceil_div(a.seg[s].n_out, TN));
+    wg += static_cast<uint32_t>(ceil_div(a.seg[s].n_out, kRowsTN));
   }
   const dim3 grid(wg, static_cast<uint32_t>(ceil_div(a.m, TM)));
+  constexpr size_t lds = rows_lds<TM>();
+  static_assert(lds <= 65536, "within the default LDS grant");
   switch (type) {
-  case Q8_0: launch(mfma_rows_kernel<Q8_0, WN, WM>, grid, dim3(kThreads), rows_lds<Q8_0, WN, WM>(), a); break;
-  case Q4_0: launch(mfma_rows_kernel<Q4_0, WN, WM>, grid, dim3(kThreads), rows_lds<Q4_0, WN, WM>(), a); break;
-  case Q4_1: launch(mfma_rows_kernel<Q4_1, WN, WM>, grid, dim3(kThreads), rows_lds<Q4_1, WN, WM>(), a); break;
+  case Q8_0: launch(mfma_rows_kernel<Q8_0, TM>, grid, dim3(kThreads), lds, a); break;
+  case Q4_0: launch(mfma_rows_kernel<Q4_0, TM>, grid, dim3(kThreads), lds, a); break;
+  case Q4_1: launch(mfma_rows_kernel<Q4_1, TM>, grid, dim3(kThreads), lds, a); break;
   default: return fail(kUnsupported, "matmul rows: weight type %d", type);
   }
   return check_launch("mfma_rows");
@@ -373,9 +429,8 @@ bool matmul_q8_rows_fits(int type, const MatvecArgs& a) {
 
 int matmul_q8_rows_launch(int type, MatvecArgs& a) {
   if (!matmul_q8_rows_fits(type, a)) return fail(kUnsupported, "matmul rows: shape or alignment");
-  if (a.m <= 16) return rows_launch<4, 1>(type, a);
-  if (a.m <= 32) return rows_launch<2, 2>(type, a);
-  return rows_launch<1, 4>(type, a);
+  if (a.m <= 16) return rows_launch<16>(type, a);
+  return rows_launch<32>(type, a);
 }
 
 int matmul_q8_mfma_launch(int type, MatvecArgs& a) {
