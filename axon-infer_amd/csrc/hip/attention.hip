@@ -27,7 +27,7 @@ constexpr size_t kLdsScores = 48 * 1024;
 template <bool F16>
 __device__ __forceinline__ float kv_at(const void* base, size_t i) {
   if constexpr (F16) {
-    return half_bits_to_float(reinterpret_cast<const uint16_t*>(base)[i]);
+    return half_value(reinterpret_cast<const uint16_t*>(base)[i]);
   } else {
     return reinterpret_cast<const float*>(base)[i];
   }
@@ -58,9 +58,9 @@ __global__ __launch_bounds__(kThreads) void attention_kernel(AttnArgs a) {
   const uint32_t pitch = GLOBAL ? a.max_vis : n_vis;
 
   // 16-byte loads of K rows when every row of this span is 16-byte aligned.
-  const bool vec4 = !F16 && hd == 64 &&
-                    (reinterpret_cast<uintptr_t>(reinterpret_cast<const float*>(a.kv) + k_off) & 15u) == 0 &&
-                    (kv_row & 3u) == 0;
+  constexpr uint32_t es = F16 ? 2 : 4;
+  const bool vec4 = hd == 64 && ((reinterpret_cast<uintptr_t>(a.kv) + static_cast<uintptr_t>(k_off) * es) & 15u) == 0 &&
+                    ((kv_row * es) & 15u) == 0;
   const float* q = a.q + static_cast<size_t>(r) * a.q_stride + static_cast<size_t>(h_lo) * hd;
   for (uint32_t i = tid; i < nh * hd; i += kThreads) qs[i] = q[i];
   __syncthreads();
@@ -70,14 +70,28 @@ __global__ __launch_bounds__(kThreads) void attention_kernel(AttnArgs a) {
     const size_t krow = k_off + j * kv_row + static_cast<size_t>(g) * hd;
     if (vec4) {
       float kr[64];
-      const float4* kp = reinterpret_cast<const float4*>(reinterpret_cast<const float*>(a.kv) + krow);
+      if constexpr (F16) {
+        const uint4* kp = reinterpret_cast<const uint4*>(reinterpret_cast<const uint16_t*>(a.kv) + krow);
 #pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        const float4 t = kp[i];
-        kr[4 * i] = t.x;
-        kr[4 * i + 1] = t.y;
-        kr[4 * i + 2] = t.z;
-        kr[4 * i + 3] = t.w;
+        for (int i = 0; i < 8; ++i) {
+          const uint4 t = kp[i];
+          const uint32_t w4[4] = {t.x, t.y, t.z, t.w};
+#pragma unroll
+          for (int k = 0; k < 4; ++k) {
+            kr[8 * i + 2 * k] = half_value(w4[k] & 0xffffu);
+            kr[8 * i + 2 * k + 1] = half_value(w4[k] >> 16);
+          }
+        }
+      } else {
+        const float4* kp = reinterpret_cast<const float4*>(reinterpret_cast<const float*>(a.kv) + krow);
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+          const float4 t = kp[i];
+          kr[4 * i] = t.x;
+          kr[4 * i + 1] = t.y;
+          kr[4 * i + 2] = t.z;
+          kr[4 * i + 3] = t.w;
+        }
       }
       for (uint32_t h = 0; h < nh; ++h) {
         float acc = 0.0f;
@@ -337,10 +351,13 @@ __global__ __launch_bounds__(kThreads) void attn_mix_kernel(AttnArgs a) {
 // The float operations and their order are the fused kernel's, and the double sum of the
 // softmax follows the fused kernel's 256-thread tree (each lane carries the partial sums of
 // threads lane, lane + 64, lane + 128, lane + 192).
-constexpr uint32_t kKPitch = 68;  // floats per K row in LDS (64 + 4: conflict-free b128 reads)
+constexpr uint32_t kKPitch = 68;   // floats per K row in LDS (64 + 4: conflict-free b128 reads)
+constexpr uint32_t kKPitchH = 36;  // dwords per fp16 K row in LDS (32 + 4, the same banks)
 
+// F16: the cache holds fp16 bit patterns; each K value is widened exactly before its product.
+template <bool F16>
 __global__ __launch_bounds__(1024) void attn_scores64_kernel(AttnArgs a) {
-  extern __shared__ __attribute__((aligned(16))) float lds[];  // K [64][kKPitch], q [group][64]
+  extern __shared__ __attribute__((aligned(16))) float lds[];  // K [64][pitch], q [group][64]
   const uint32_t r = blockIdx.x;
   const uint32_t g = blockIdx.y;
   const uint32_t j0 = blockIdx.z * 64;
@@ -353,18 +370,22 @@ __global__ __launch_bounds__(1024) void attn_scores64_kernel(AttnArgs a) {
   const uint32_t rows = min(64u, n_vis - j0);
   const size_t kv_row = static_cast<size_t>(a.n_kv) * 64;
   const int64_t k_off = (a.k_off != nullptr ? a.k_off[r] : 0) + a.k_off_c;
+  constexpr uint32_t es = F16 ? 2 : 4;                // bytes per cache element
+  constexpr uint32_t pitch = F16 ? kKPitchH : kKPitch;  // dwords per K row in LDS
   float* kt = lds;
-  float* qs = lds + 64 * kKPitch;
+  float* qs = lds + 64 * pitch;
   // K rows j0 .. j0 + 63 of kv head g (rows past n_vis repeat the last one): one dword DMA per
-  // row, waves taking rows in turn.
-  const float* kbase = reinterpret_cast<const float*>(a.kv) + k_off + static_cast<size_t>(j0) * kv_row + g * 64;
+  // row (32 lanes of an fp16 row), waves taking rows in turn.
+  const uint8_t* kbase = static_cast<const uint8_t*>(a.kv) + (k_off + static_cast<size_t>(j0) * kv_row + g * 64) * es;
   const __amdgpu_buffer_rsrc_t rsrc = __builtin_amdgcn_make_buffer_rsrc(
-      const_cast<float*>(kbase), 0, static_cast<int>((static_cast<size_t>(rows - 1) * kv_row + 64) * 4),
+      const_cast<uint8_t*>(kbase), 0, static_cast<int>((static_cast<size_t>(rows - 1) * kv_row + 64) * es),
       static_cast<int>(kRawBufferWord3));
   for (uint32_t i = wave; i < 64; i += group) {
     const uint32_t row = min(i, rows - 1);
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, as_lds(kt + i * kKPitch), 4, 4 * lane,
-                                             static_cast<int>(row * kv_row * 4), 0, 0);
+    if (!F16 || lane < 32) {
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, as_lds(kt + i * pitch), 4, 4 * lane,
+                                               static_cast<int>(row * kv_row * es), 0, 0);
+    }
   }
   const float* q = a.q + static_cast<size_t>(r) * a.q_stride + static_cast<size_t>(g) * group * 64;
   for (uint32_t i = tid; i < group * 64; i += blockDim.x) qs[i] = q[i];
@@ -372,17 +393,35 @@ __global__ __launch_bounds__(1024) void attn_scores64_kernel(AttnArgs a) {
   __syncthreads();
   const uint32_t j = j0 + lane;
   if (j >= n_vis) return;
-  const float* kr = kt + lane * kKPitch;
+  const float* kr = kt + lane * pitch;
   const float* qh = qs + wave * 64;
   float acc = 0.0f;
+  if constexpr (F16) {
+    const uint32_t* kh = reinterpret_cast<const uint32_t*>(kr);
 #pragma unroll
-  for (int d = 0; d < 64; d += 4) {
-    const float4 k4 = *reinterpret_cast<const float4*>(kr + d);
-    const float4 q4 = *reinterpret_cast<const float4*>(qh + d);
-    acc += q4.x * k4.x;
-    acc += q4.y * k4.y;
-    acc += q4.z * k4.z;
-    acc += q4.w * k4.w;
+    for (int d = 0; d < 64; d += 8) {
+      const uint4 h = *reinterpret_cast<const uint4*>(kh + d / 2);
+      const float4 qa = *reinterpret_cast<const float4*>(qh + d);
+      const float4 qb = *reinterpret_cast<const float4*>(qh + d + 4);
+      acc += qa.x * half_value(h.x & 0xffffu);
+      acc += qa.y * half_value(h.x >> 16);
+      acc += qa.z * half_value(h.y & 0xffffu);
+      acc += qa.w * half_value(h.y >> 16);
+      acc += qb.x * half_value(h.z & 0xffffu);
+      acc += qb.y * half_value(h.z >> 16);
+      acc += qb.z * half_value(h.w & 0xffffu);
+      acc += qb.w * half_value(h.w >> 16);
+    }
+  } else {
+#pragma unroll
+    for (int d = 0; d < 64; d += 4) {
+      const float4 k4 = *reinterpret_cast<const float4*>(kr + d);
+      const float4 q4 = *reinterpret_cast<const float4*>(qh + d);
+      acc += q4.x * k4.x;
+      acc += q4.y * k4.y;
+      acc += q4.z * k4.z;
+      acc += q4.w * k4.w;
+    }
   }
   a.scratch[(static_cast<size_t>(r) * a.n_head + g * group + wave) * a.max_vis + j] = a.scale * acc;
 }
@@ -677,34 +716,38 @@ constexpr uint32_t kDTile = 32;                // positions per tile (4 KB)
 __host__ __device__ inline uint32_t mixd_pitch(uint32_t max_vis) { return ((max_vis + 63) & ~63u) + 4; }
 constexpr uint32_t kSPer = kMixMaxVis / 256;   // positions per lane per partial sum
 
-template <int G>
+// F16: the cache holds fp16 bit patterns, so a V half-row is 64 bytes and a tile two copies.
+template <int G, bool F16>
 struct MixD {
-  static constexpr uint32_t kCw = G < 4 ? G : 4;              // copying waves
-  static constexpr uint32_t kCmax = (4 + kCw - 1) / kCw;      // most copies per wave per tile
+  static constexpr uint32_t kCopies = F16 ? 2 : 4;            // 1 KB copies per tile
+  static constexpr uint32_t kTileBytes = kDTile * (F16 ? 64 : 128);
+  static constexpr uint32_t kCw = G < kCopies ? G : kCopies;  // copying waves
+  static constexpr uint32_t kCmax = (kCopies + kCw - 1) / kCw;  // most copies per wave per tile
   static constexpr uint32_t kBudget = 163840 - G * (kMixMaxVis + 4) * 4 - 512;  // LDS beside p
-  static constexpr uint32_t kR0 = (kBudget < 98304 ? kBudget : 98304) / (kDTile * 128);
+  static constexpr uint32_t kR0 = (kBudget < 98304 ? kBudget : 98304) / kTileBytes;
   // Tiles in flight, even (two halves). A wave holds at most kMixMaxVis / 128 score copies and
   // kRing * kCmax V copies outstanding, within the 63 that vmcnt counts (and the 31 that
   // wait_vm_upto waits on).
   static constexpr uint32_t kRing = (kR0 * kCmax > 27 ? 27 / kCmax : kR0) & ~1u;
 };
 
-template <int G>
+template <int G, bool F16>
 size_t mixd_lds(uint32_t max_vis) {
-  return static_cast<size_t>(MixD<G>::kRing) * kDTile * 128 + static_cast<size_t>(G) * mixd_pitch(max_vis) * 4 + 512;
+  return static_cast<size_t>(MixD<G, F16>::kRing) * MixD<G, F16>::kTileBytes +
+         static_cast<size_t>(G) * mixd_pitch(max_vis) * 4 + 512;
 }
 
 
-template <int G>
+template <int G, bool F16>
 __global__ __launch_bounds__(G * 128) void attn_mixd_kernel(AttnArgs a) {
-  using M = MixD<G>;
+  using M = MixD<G, F16>;
   constexpr uint32_t kR = M::kRing;
   constexpr uint32_t kCw = M::kCw;
   constexpr uint32_t kH = kR / 2;
   static_assert(kR >= 4 && kR * M::kCmax <= 27, "ring depth");
   extern __shared__ __attribute__((aligned(16))) float lds[];
-  float* ring = lds;                                   // [kR][kDTile][32]
-  float* pbase = lds + kR * kDTile * 32;               // [G][pitch]
+  float* ring = lds;                                   // [kR][kDTile][32] float or fp16 elements
+  float* pbase = reinterpret_cast<float*>(reinterpret_cast<uint8_t*>(lds) + kR * M::kTileBytes);  // [G][pitch]
   const uint32_t pitch = mixd_pitch(a.max_vis);
   float* red_m = pbase + G * pitch;                       // [G][2] maxima (64 bytes)
   double* red_s = reinterpret_cast<double*>(red_m + 16);  // [G][4] partial sums (256 bytes)
@@ -731,27 +774,30 @@ __global__ __launch_bounds__(G * 128) void attn_mixd_kernel(AttnArgs a) {
     lds_dma4(ssrc, 4 * (j0 + lane), p_lds + 4 * j0);
   }
 
-  const float* vbase = reinterpret_cast<const float*>(a.kv) + v_off + g * 64 + half * 32;
+  constexpr uint32_t es = F16 ? 2 : 4;        // bytes per cache element
+  constexpr uint32_t kCopies = M::kCopies;
+  constexpr uint32_t kPerCopy = kDTile / kCopies;  // positions per 1 KB copy: 8, or 16 in fp16
+  const uint8_t* vbase = static_cast<const uint8_t*>(a.kv) + (v_off + g * 64 + half * 32) * es;
   const RsrcWords rsrc =
-      raw_buffer_words(vbase, static_cast<uint32_t>((static_cast<size_t>(n_vis - 1) * kv_row + 32) * 4));
+      raw_buffer_words(vbase, static_cast<uint32_t>((static_cast<size_t>(n_vis - 1) * kv_row + 32) * es));
   const uint32_t ring_lds = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(as_lds(ring)));
   const uint32_t n_tiles = (n_vis + kDTile - 1) / kDTile;
-  // Copy k (0..3) of a tile moves its positions 8k .. 8k + 7 (lane / 8 picks the position,
-  // lane % 8 the 16 bytes); wave w < kCw issues k = w, w + kCw, ... A tile wholly below n_vis
-  // takes this lane's fixed offsets plus a uniform tile offset; the last tile clamps each
-  // position to the last one.
-  const uint32_t copies = w < kCw ? (4 - w + kCw - 1) / kCw : 0;  // this wave's copies per tile
-  const uint32_t row_bytes = static_cast<uint32_t>(kv_row * 4);
-  const uint32_t lane_row = lane / 8, lane_byte = (lane % 8) * 16;
+  // Copy k of a tile moves its positions kPerCopy k .. kPerCopy (k + 1) - 1 (lane / (64 /
+  // kPerCopy) picks the position, the rest of the lane its 16 bytes of the half-row); wave
+  // w < kCw issues k = w, w + kCw, ... A tile wholly below n_vis takes this lane's fixed offsets
+  // plus a uniform tile offset; the last tile clamps each position to the last one.
+  const uint32_t copies = w < kCw ? (kCopies - w + kCw - 1) / kCw : 0;  // this wave's copies per tile
+  const uint32_t row_bytes = static_cast<uint32_t>(kv_row * es);
+  const uint32_t lane_row = lane / (64 / kPerCopy), lane_byte = (lane % (64 / kPerCopy)) * 16;
   auto copy_tile = [&](uint32_t t) {
     if (t >= n_tiles) return;
-    const uint32_t dst = ring_lds + (t % kR) * kDTile * 128;
+    const uint32_t dst = ring_lds + (t % kR) * M::kTileBytes;
     const bool whole = (t + 1) * kDTile <= n_vis;
-    for (uint32_t k = w; k < 4 && w < kCw; k += kCw) {
+    for (uint32_t k = w; k < kCopies && w < kCw; k += kCw) {
       if (whole) {
-        lds_dma16_so(rsrc, (8 * k + lane_row) * row_bytes + lane_byte, t * kDTile * row_bytes, dst + k * 1024);
+        lds_dma16_so(rsrc, (kPerCopy * k + lane_row) * row_bytes + lane_byte, t * kDTile * row_bytes, dst + k * 1024);
       } else {
-        const uint32_t row = min(t * kDTile + 8 * k + lane_row, n_vis - 1);
+        const uint32_t row = min(t * kDTile + kPerCopy * k + lane_row, n_vis - 1);
         lds_dma16(rsrc, row * row_bytes + lane_byte, dst + k * 1024);
       }
     }
@@ -832,10 +878,16 @@ __global__ __launch_bounds__(G * 128) void attn_mixd_kernel(AttnArgs a) {
   float acc = 0.0f;
   float va[kDTile], pa[kDTile], vb[kDTile], pb[kDTile];
   auto load_tile = [&](uint32_t t, float (&v)[kDTile], float (&pp)[kDTile]) {
-    const float* vt = ring + (t % kR) * kDTile * 32 + d;
     const float* pt = ph + t * kDTile;
+    if constexpr (F16) {  // each value widened (exactly, but for NaN payloads)
+      const uint16_t* vt = reinterpret_cast<const uint16_t*>(ring) + (t % kR) * kDTile * 32 + d;
 #pragma unroll
-    for (uint32_t i = 0; i < kDTile; ++i) v[i] = vt[i * 32];
+      for (uint32_t i = 0; i < kDTile; ++i) v[i] = half_value(vt[i * 32]);
+    } else {
+      const float* vt = ring + (t % kR) * kDTile * 32 + d;
+#pragma unroll
+      for (uint32_t i = 0; i < kDTile; ++i) v[i] = vt[i * 32];
+    }
 #pragma unroll
     for (uint32_t i = 0; i < kDTile; i += 4) {
       const float4 q4 = *reinterpret_cast<const float4*>(pt + i);
@@ -897,7 +949,7 @@ __global__ __launch_bounds__(G * 128) void attn_mixd_kernel(AttnArgs a) {
 }
 
 // Dynamic LDS above 64 KB must be granted per kernel; 0 when the device cannot.
-template <int G>
+template <int G, bool F16>
 size_t mixd_lds_granted(uint32_t max_vis) {
   static int limit = -1;
   if (limit < 0) {
@@ -906,13 +958,36 @@ size_t mixd_lds_granted(uint32_t max_vis) {
              hipDeviceGetAttribute(&v, hipDeviceAttributeMaxSharedMemoryPerBlock, dev) == hipSuccess)
                 ? v
                 : 65536;
-    const int want = static_cast<int>(mixd_lds<G>(kMixMaxVis));
-    if (hipFuncSetAttribute(reinterpret_cast<const void*>(attn_mixd_kernel<G>),
+    const int want = static_cast<int>(mixd_lds<G, F16>(kMixMaxVis));
+    if (hipFuncSetAttribute(reinterpret_cast<const void*>(attn_mixd_kernel<G, F16>),
                             hipFuncAttributeMaxDynamicSharedMemorySize, std::min(want, limit)) != hipSuccess)
       limit = 65536;
   }
-  const size_t need = mixd_lds<G>(max_vis);
+  const size_t need = mixd_lds<G, F16>(max_vis);
   return need <= static_cast<size_t>(limit) ? need : 0;
+}
+
+// The mix kernel's granted LDS for a group size (3, 4, 7, 8), 0 when it has none or none fits.
+template <bool F16>
+size_t mixd_grant_for(uint32_t group, uint32_t max_vis) {
+  switch (group) {
+  case 3: return mixd_lds_granted<3, F16>(max_vis);
+  case 4: return mixd_lds_granted<4, F16>(max_vis);
+  case 7: return mixd_lds_granted<7, F16>(max_vis);
+  case 8: return mixd_lds_granted<8, F16>(max_vis);
+  default: return 0;
+  }
+}
+
+template <bool F16>
+void launch_mixd(uint32_t group, dim3 grid, size_t lds, const AttnArgs& a) {
+  switch (group) {
+  case 3: hipLaunchKernelGGL((attn_mixd_kernel<3, F16>), grid, dim3(384), lds, stream(), a); break;
+  case 4: hipLaunchKernelGGL((attn_mixd_kernel<4, F16>), grid, dim3(512), lds, stream(), a); break;
+  case 7: hipLaunchKernelGGL((attn_mixd_kernel<7, F16>), grid, dim3(896), lds, stream(), a); break;
+  case 8: hipLaunchKernelGGL((attn_mixd_kernel<8, F16>), grid, dim3(1024), lds, stream(), a); break;
+  default: break;
+  }
 }
 
 bool scores_fit_lds(const AttnArgs& a) {
@@ -943,32 +1018,35 @@ int attention_launch(const AttnArgs& a, uint32_t n_rows) {
     return fail(kInvalidArgument, "attention: heads [%u, %u) of %u", a.head_begin, a.head_end, a.n_head);
   if (a.head_begin == a.head_end) return kOk;
   const uint32_t group = a.n_head / a.n_kv;
-  if (a.scratch != nullptr && use_split(a, n_rows) && a.head_dim == 64 && !a.f16 && group <= 16 &&
-      a.max_vis <= kMixMaxVis) {
-    const dim3 sgrid(n_rows, a.n_kv, (a.max_vis + 63) / 64);
-    const size_t slds = (64 * kKPitch + static_cast<size_t>(group) * 64) * 4;
-    hipLaunchKernelGGL(attn_scores64_kernel, sgrid, dim3(group * 64), slds, stream(), a);
-    const size_t glds = mixg_lds(group, a.max_vis);
-    const dim3 ggrid(n_rows, a.n_kv);
-    const dim3 dgrid(n_rows, a.n_kv, 2);
-    size_t dlds = 0;
-    if (group == 4 && (dlds = mixd_lds_granted<4>(a.max_vis)) != 0) {
-      hipLaunchKernelGGL(attn_mixd_kernel<4>, dgrid, dim3(512), dlds, stream(), a);
-    } else if (group == 8 && (dlds = mixd_lds_granted<8>(a.max_vis)) != 0) {
-      hipLaunchKernelGGL(attn_mixd_kernel<8>, dgrid, dim3(1024), dlds, stream(), a);
-    } else if (group == 3 && (dlds = mixd_lds_granted<3>(a.max_vis)) != 0) {
-      hipLaunchKernelGGL(attn_mixd_kernel<3>, dgrid, dim3(384), dlds, stream(), a);
-    } else if (group == 7 && (dlds = mixd_lds_granted<7>(a.max_vis)) != 0) {
-      hipLaunchKernelGGL(attn_mixd_kernel<7>, dgrid, dim3(896), dlds, stream(), a);
-    } else if (glds <= 65536 && (group == 1 || group == 2 || group == 4 || group == 8)) {
-      if (group == 1) hipLaunchKernelGGL(attn_mixg_kernel<1>, ggrid, dim3(64), glds, stream(), a);
-      if (group == 2) hipLaunchKernelGGL(attn_mixg_kernel<2>, ggrid, dim3(128), glds, stream(), a);
-      if (group == 4) hipLaunchKernelGGL(attn_mixg_kernel<4>, ggrid, dim3(256), glds, stream(), a);
-      if (group == 8) hipLaunchKernelGGL(attn_mixg_kernel<8>, ggrid, dim3(512), glds, stream(), a);
-    } else {
-      hipLaunchKernelGGL(attn_mix64_kernel, dim3(n_rows, a.n_head), dim3(64), 0, stream(), a);
+  if (a.scratch != nullptr && use_split(a, n_rows) && a.head_dim == 64 && group <= 16 && a.max_vis <= kMixMaxVis) {
+    // The mix kernel for this group, if its LDS is granted; an fp16 cache without one takes
+    // the split kernels below.
+    const size_t dlds = a.f16 ? mixd_grant_for<true>(group, a.max_vis) : mixd_grant_for<false>(group, a.max_vis);
+    if (!a.f16 || dlds != 0) {
+      const dim3 sgrid(n_rows, a.n_kv, (a.max_vis + 63) / 64);
+      const dim3 dgrid(n_rows, a.n_kv, 2);
+      if (a.f16) {
+        const size_t slds = (64 * kKPitchH + static_cast<size_t>(group) * 64) * 4;
+        hipLaunchKernelGGL(attn_scores64_kernel<true>, sgrid, dim3(group * 64), slds, stream(), a);
+        launch_mixd<true>(group, dgrid, dlds, a);
+        return check_launch("attention (decode, fp16)");
+      }
+      const size_t slds = (64 * kKPitch + static_cast<size_t>(group) * 64) * 4;
+      hipLaunchKernelGGL(attn_scores64_kernel<false>, sgrid, dim3(group * 64), slds, stream(), a);
+      const size_t glds = mixg_lds(group, a.max_vis);
+      const dim3 ggrid(n_rows, a.n_kv);
+      if (dlds != 0) {
+        launch_mixd<false>(group, dgrid, dlds, a);
+      } else if (glds <= 65536 && (group == 1 || group == 2 || group == 4 || group == 8)) {
+        if (group == 1) hipLaunchKernelGGL(attn_mixg_kernel<1>, ggrid, dim3(64), glds, stream(), a);
+        if (group == 2) hipLaunchKernelGGL(attn_mixg_kernel<2>, ggrid, dim3(128), glds, stream(), a);
+        if (group == 4) hipLaunchKernelGGL(attn_mixg_kernel<4>, ggrid, dim3(256), glds, stream(), a);
+        if (group == 8) hipLaunchKernelGGL(attn_mixg_kernel<8>, ggrid, dim3(512), glds, stream(), a);
+      } else {
+        hipLaunchKernelGGL(attn_mix64_kernel, dim3(n_rows, a.n_head), dim3(64), 0, stream(), a);
+      }
+      return check_launch("attention (decode)");
     }
-    return check_launch("attention (decode)");
   }
   if (a.scratch != nullptr && use_split(a, n_rows)) {
     const dim3 sgrid(n_rows, a.n_kv, (a.max_vis + kThreads - 1) / kThreads);

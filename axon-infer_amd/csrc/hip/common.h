@@ -48,6 +48,13 @@ __device__ __forceinline__ float half_bits_to_float(uint32_t h) {
   return ((h >> 10) & 0x1fu) == 0x1fu ? __uint_as_float(special) : f;
 }
 
+// fp16 bits to float by the hardware conversion, for values read into arithmetic: exact for
+// every finite value (fp16 denormals are kept: the kernels' FP16/FP64 denormal mode) and for
+// infinities; a NaN converts to a NaN (its payload may differ from half_bits_to_float's).
+__device__ __forceinline__ float half_value(uint32_t h) {
+  return static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(h)));
+}
+
 // Round to nearest even, overflow to infinity, gradual underflow, NaN kept non-zero.
 __device__ __forceinline__ uint32_t float_to_half_bits(float f) {
   const uint32_t x = __float_as_uint(f);

@@ -358,18 +358,23 @@ def test_attention_over_one_position_returns_its_value(h):
 
 # ---- ragged rows entry (one launch over several sequences' caches) -----------------------------
 
-@pytest.mark.parametrize("n_head,n_kv,lens", [(32, 8, [1, 37, 600, 130]), (14, 2, [5, 1025]), (9, 3, [64] * 40)])
-def test_attention_rows_ragged_matches_oracle(o, h, n_head, n_kv, lens):
+@pytest.mark.parametrize("f16", [False, True])
+@pytest.mark.parametrize("n_head,n_kv,lens", [(32, 8, [1, 37, 600, 130]), (14, 2, [5, 1025]), (9, 3, [64] * 40),
+                                              (32, 4, [2000, 17, 33]), (32, 8, [2304])])
+def test_attention_rows_ragged_matches_oracle(o, h, n_head, n_kv, lens, f16):
     """axon_hip_attention_rows over a pool of caches, each row at its own length (decode-shaped
     batches take the two-kernel path; 40 rows x 3 kv heads take the fused one), against the
-    oracle's attention_kv_heads per sequence."""
+    oracle's attention_kv_heads (_f16 for a pool of fp16 bit patterns) per sequence."""
     import axon_hip as H
     hd = 64
-    rng = np.random.default_rng(sum(lens))
+    rng = np.random.default_rng(sum(lens) + int(f16))
     max_ctx = max(lens) + 3
     n = len(lens)
     row = n_kv * hd
     pool = rng.normal(0, 1, (n, 2, max_ctx, row)).astype(np.float32)     # per sequence: K rows, V rows
+    if f16:
+        pool[..., ::7] *= np.float32(1e-6)   # fp16 subnormals among the keys and values
+        pool = pool.astype(np.float16).view(np.uint16)
     q = rng.normal(0, 1, (n, n_head * hd)).astype(np.float32)
     slot = pool[0].size
     d_pool = H.DeviceBuffer.of(pool)
@@ -381,7 +386,7 @@ def test_attention_rows_ragged_matches_oracle(o, h, n_head, n_kv, lens):
     args = H.AttentionRowsArgs(q=d_q.ptr, out=d_out.ptr, q_stride=n_head * hd, out_stride=n_head * hd, kv=d_pool.ptr,
                                k_off=d_off.ptr, v_off=d_off.ptr, n_vis=d_vis.ptr, k_layer_off=0,
                                v_layer_off=max_ctx * row, n_past=0, n_head=n_head, n_kv=n_kv, head_dim=hd,
-                               scale=0.125, f16=0, scratch=0, max_vis=max(lens))
+                               scale=0.125, f16=int(f16), scratch=0, max_vis=max(lens))
     need = H.lib().axon_hip_attention_scratch_floats(C.byref(args), C.c_size_t(n))
     scratch = H.DeviceBuffer(max(need, 1) * 4)
     args.scratch = scratch.ptr if need else 0
@@ -389,5 +394,5 @@ def test_attention_rows_ragged_matches_oracle(o, h, n_head, n_kv, lens):
     got = d_out.download(np.float32).reshape(n, n_head, hd)
     for i, L in enumerate(lens):
         want = o.attention_kv_heads(q[i].reshape(1, n_head, hd), pool[i, 0, :L].copy(), pool[i, 1, :L].copy(), 1, L - 1,
-                                    n_head, n_kv, hd, 0.125, 0, n_head)[0]
+                                    n_head, n_kv, hd, 0.125, 0, n_head, f16=f16)[0]
         assert np.max(np.abs(got[i] - want)) <= 1e-6 * max(1.0, np.max(np.abs(want))), i
