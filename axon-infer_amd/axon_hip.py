@@ -224,6 +224,8 @@ def host() -> C.CDLL:
         L.axon_model_forward.argtypes = [C.c_void_p, C.c_void_p, C.c_size_t, C.c_void_p]
         L.axon_model_forward_prefill.argtypes = [C.c_void_p, C.c_int, C.c_void_p, C.c_size_t, C.c_void_p]
         L.axon_model_forward_batch.argtypes = [C.c_void_p, C.c_void_p, C.c_void_p, C.c_size_t, C.c_void_p]
+        L.axon_model_forward_mixed.argtypes = [C.c_void_p, C.c_int, C.c_void_p, C.c_size_t, C.c_void_p, C.c_void_p,
+                                               C.c_size_t, C.c_void_p]
         L.axon_model_greedy.argtypes = [C.c_void_p, C.c_void_p, C.c_void_p, C.c_float, C.c_int, C.c_void_p,
                                         C.c_size_t]
         L.axon_model_probe.argtypes = [C.c_void_p, C.c_int, C.c_int]
@@ -314,6 +316,22 @@ class Model:
         out = self._logits(len(t), logits)
         _mcheck(host().axon_model_forward_batch(self.h, cs.ctypes.data, t.ctypes.data, len(t),
                                                out.ctypes.data if out is not None else None), "forward_batch")
+        return out
+
+    def forward_mixed(self, prefill_cache, chunk, caches, tokens, logits: bool = True):
+        """One continuous-batching step as one pass (axon_model_forward_mixed): `chunk` into
+        prefill_cache (None with an empty chunk), tokens[i] into caches[i]. Returns the chunk's
+        last row of logits (if any) then one row per decode cache."""
+        ch = np.ascontiguousarray(chunk if chunk is not None else [], np.int32)
+        t = np.ascontiguousarray(tokens, np.int32)
+        cs = np.ascontiguousarray(caches, np.int32)
+        if len(cs) != len(t):
+            raise ValueError(f"forward_mixed: {len(cs)} caches for {len(t)} tokens")
+        out = self._logits(int(len(ch) > 0) + len(t), logits)
+        _mcheck(host().axon_model_forward_mixed(self.h, -1 if prefill_cache is None else prefill_cache,
+                                               ch.ctypes.data if len(ch) else None, len(ch),
+                                               cs.ctypes.data if len(cs) else None, t.ctypes.data if len(t) else None,
+                                               len(t), out.ctypes.data if out is not None else None), "forward_mixed")
         return out
 
     def greedy(self, n: int, recent=None, repeat_penalty: float = 1.0, repeat_last_n: int = 64) -> np.ndarray:

@@ -169,6 +169,28 @@ int axon_model_forward_batch(axon_model* model, const int* caches, const int32_t
   return copy_out(model->m->forward_batch(cs, std::span<const int32_t>(tokens, n)), logits);
 }
 
+int axon_model_forward_mixed(axon_model* model, int prefill_cache, const int32_t* prefill, size_t n_prefill,
+                             const int* caches, const int32_t* tokens, size_t n, float* logits) {
+  axon::model::KVCache* pc = nullptr;
+  if (n_prefill != 0) {
+    if (prefill == nullptr) return fail("forward_mixed: prefill tokens are NULL");
+    pc = find(model, prefill_cache);
+    if (pc == nullptr) return fail("forward_mixed: unknown cache " + std::to_string(prefill_cache));
+  }
+  if (n != 0 && (caches == nullptr || tokens == nullptr)) return fail("forward_mixed: caches or tokens are NULL");
+  std::vector<axon::model::KVCache*> cs(n);
+  for (size_t i = 0; i < n; ++i) {
+    cs[i] = find(model, caches[i]);
+    if (cs[i] == nullptr) return fail("forward_mixed: unknown cache " + std::to_string(caches[i]));
+  }
+  const std::span<const int32_t> chunk(prefill, n_prefill), toks(tokens, n);
+  if (logits == nullptr) {
+    auto r = model->m->forward_mixed_device(pc, chunk, cs, toks);
+    return r ? 0 : fail(r.error());
+  }
+  return copy_out(model->m->forward_mixed(pc, chunk, cs, toks), logits);
+}
+
 int axon_model_greedy(axon_model* model, const int32_t* const* recent, const size_t* recent_len, float repeat_penalty,
                       int repeat_last_n, int32_t* ids, size_t n) {
   if (ids == nullptr && n != 0) return fail("greedy: ids is NULL");

@@ -148,7 +148,8 @@ Expected<std::unique_ptr<LlamaModel>> LlamaModel::load(const std::string& path, 
   m->max_ctx_ = std::min<std::size_t>(options.max_ctx, c.n_ctx_train);
   m->max_seq_ = std::min(options.max_seq, m->max_ctx_);
   m->max_batch_ = std::max<std::size_t>(1, options.max_batch);
-  m->max_rows_ = std::max(m->max_seq_, m->max_batch_);
+  // A mixed pass carries a prompt chunk and a decode batch.
+  m->max_rows_ = m->max_seq_ + m->max_batch_;
   m->n_slots_ = options.max_caches != 0 ? options.max_caches : m->max_batch_ + 1;
   m->exact_ = options.exact_activations;
   m->cache_type_ = options.cache;
@@ -466,7 +467,7 @@ int LlamaModel::mm(const Tensor& w, const float* x, const void* xq, float* y, st
   return accumulate ? axon_hip_add(y, tmp_, n * n_out) : AXON_HIP_OK;
 }
 
-Expected<std::size_t> LlamaModel::run(std::span<const Row> rows, bool copy_logits) {
+Expected<std::size_t> LlamaModel::run(std::span<const Row> rows, bool copy_logits, std::size_t first_logit) {
   const std::size_t n = rows.size();
   const Config& c = cfg_;
   const std::size_t d = c.n_embd, dq = c.n_embd_q(), dkv = c.n_embd_kv(), ff = c.n_ff;
@@ -717,13 +718,18 @@ Expected<std::size_t> LlamaModel::run(std::span<const Row> rows, bool copy_logit
     }
     DEV(mm(L.w_down, gate_, xq_, x_, n, true));
   }
-  if (fused_ok(output_, 2, d, false)) {
+  // The final norm and the output matmul for the rows whose logits the pass returns.
+  float* const x_out = x_ + first_logit * d;
+  const std::size_t n_out = n - first_logit;
+  if (!exact_ && n_out <= 4 && q8_path(output_) &&
+      axon_hip_matvec_fused_supported(static_cast<int>(output_.type), 2, n_out, d, false) == 1) {
     axon_hip_matvec_fused_args fa = fused_args(output_);
+    fa.n_rows = n_out;
     fa.n_seg = 1;
     fa.w[0] = output_.dev;
     fa.n_out[0] = c.n_vocab;
     fa.in_mode = 2;
-    fa.x = x_;
+    fa.x = x_out;
     fa.x_stride = d;
     fa.norm_w = static_cast<const float*>(output_norm_.dev);
     fa.out_mode = 0;
@@ -731,21 +737,21 @@ Expected<std::size_t> LlamaModel::run(std::span<const Row> rows, bool copy_logit
     fa.y_stride[0] = c.n_vocab;
     probe_begin(output_);
     DEV(axon_hip_matvec_fused(&fa));
-    probe_end(output_, n, c.n_vocab, false);
+    probe_end(output_, n_out, c.n_vocab, false);
   } else {
     const bool out_q8 = q8_path(output_);
-    DEV(axon_hip_rmsnorm_rows(x_, static_cast<const float*>(output_norm_.dev), out_q8 ? nullptr : h_,
-                              out_q8 ? xq_ : nullptr, d, n, eps));
-    DEV(mm(output_, h_, xq_, logits_, n, false));
+    DEV(axon_hip_rmsnorm_rows(x_out, static_cast<const float*>(output_norm_.dev), out_q8 ? nullptr : h_,
+                              out_q8 ? xq_ : nullptr, d, n_out, eps));
+    DEV(mm(output_, h_, xq_, logits_, n_out, false));
   }
   if (copy_logits) {
-    logits_host_.resize(n * c.n_vocab);
+    logits_host_.resize(n_out * c.n_vocab);
     DEV(axon_hip_memcpy_d2h(logits_host_.data(), logits_, logits_host_.size() * 4));
   }
 #undef DEV
   (void)R;
-  last_rows_ = n;
-  return n;
+  last_rows_ = n_out;
+  return n_out;
 }
 
 Expected<std::size_t> LlamaModel::greedy(std::span<std::int32_t> ids,
@@ -902,6 +908,55 @@ Expected<std::size_t> LlamaModel::forward_batch_device(std::span<KVCache* const>
   if (!rows) return rows.error();
   auto r = run(*rows, false);
   if (!r) return r.error();
+  for (KVCache* cache : caches) cache->advance(1);
+  return *r;
+}
+
+Expected<std::vector<LlamaModel::Row>> LlamaModel::mixed_rows(KVCache* prefill, std::span<const std::int32_t> chunk,
+                                                               std::span<KVCache* const> caches,
+                                                               std::span<const std::int32_t> tokens) const {
+  if (chunk.empty() && tokens.empty()) return make_error(ErrorCode::InvalidArgument, "forward_mixed: no rows");
+  std::vector<Row> rows;
+  if (!chunk.empty()) {
+    if (prefill == nullptr || prefill->slot() < 0 || static_cast<std::size_t>(prefill->slot()) >= n_slots_ ||
+        prefill->max_ctx() != max_ctx_)
+      return make_error(ErrorCode::InvalidArgument, "forward_mixed: the prefill cache was built for a different model");
+    for (KVCache* c : caches) {
+      if (c == prefill || (c != nullptr && c->slot() == prefill->slot()))
+        return make_error(ErrorCode::InvalidArgument, "forward_mixed: the prefill cache is also in the decode batch");
+    }
+    auto p = prefill_rows(*prefill, chunk);
+    if (!p) return p.error();
+    rows = std::move(*p);
+  }
+  if (!tokens.empty() || !caches.empty()) {
+    auto b = batch_rows(caches, tokens);
+    if (!b) return b.error();
+    rows.insert(rows.end(), b->begin(), b->end());
+  }
+  return rows;
+}
+
+Expected<std::span<const float>> LlamaModel::forward_mixed(KVCache* prefill, std::span<const std::int32_t> chunk,
+                                                           std::span<KVCache* const> caches,
+                                                           std::span<const std::int32_t> tokens) {
+  auto rows = mixed_rows(prefill, chunk, caches, tokens);
+  if (!rows) return rows.error();
+  auto r = run(*rows, true, chunk.empty() ? 0 : chunk.size() - 1);
+  if (!r) return r.error();
+  if (!chunk.empty()) prefill->advance(chunk.size());
+  for (KVCache* cache : caches) cache->advance(1);
+  return std::span<const float>(logits_host_);
+}
+
+Expected<std::size_t> LlamaModel::forward_mixed_device(KVCache* prefill, std::span<const std::int32_t> chunk,
+                                                       std::span<KVCache* const> caches,
+                                                       std::span<const std::int32_t> tokens) {
+  auto rows = mixed_rows(prefill, chunk, caches, tokens);
+  if (!rows) return rows.error();
+  auto r = run(*rows, false, chunk.empty() ? 0 : chunk.size() - 1);
+  if (!r) return r.error();
+  if (!chunk.empty()) prefill->advance(chunk.size());
   for (KVCache* cache : caches) cache->advance(1);
   return *r;
 }

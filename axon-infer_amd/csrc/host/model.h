@@ -100,6 +100,16 @@ public:
   Expected<std::size_t> forward_device(std::span<const std::int32_t> tokens);
   Expected<std::size_t> forward_prefill_device(KVCache& cache, std::span<const std::int32_t> tokens);
   Expected<std::size_t> forward_batch_device(std::span<KVCache* const> caches, std::span<const std::int32_t> tokens);
+  // One continuous-batching step as one pass (batch.cpp:69-156 runs it as two: forward_prefill
+  // of one prompt chunk, then forward_batch of the sequences in decode): `prefill` takes
+  // `chunk` at its next positions (it may be null with an empty chunk) and caches[i] takes
+  // tokens[i]. Every row is computed as in those two passes, bit for bit; the logits are those
+  // that step observes: the chunk's last row (Sequence::prefill_chunk, sequence.cpp:118), then
+  // one row per decode cache. The chunk and the decode rows together fit max_seq + max_batch.
+  Expected<std::span<const float>> forward_mixed(KVCache* prefill, std::span<const std::int32_t> chunk,
+                                                 std::span<KVCache* const> caches, std::span<const std::int32_t> tokens);
+  Expected<std::size_t> forward_mixed_device(KVCache* prefill, std::span<const std::int32_t> chunk,
+                                             std::span<KVCache* const> caches, std::span<const std::int32_t> tokens);
   const float* logits_device() const { return logits_; }
   // Sampler::sample at temperature zero (src/sampling/sampler.cpp:67-102) over the last pass's
   // logits, on the device: the repetition penalty over each row's recent tokens (recent[r], the
@@ -145,7 +155,11 @@ private:
     std::int32_t pos;
     int slot;
   };
-  Expected<std::size_t> run(std::span<const Row> rows, bool copy_logits);
+  // Runs every row through the layers; the final norm and the output matmul run on rows
+  // [first_logit, rows.size()) only, whose logits are the pass's.
+  Expected<std::size_t> run(std::span<const Row> rows, bool copy_logits, std::size_t first_logit = 0);
+  Expected<std::vector<Row>> mixed_rows(KVCache* prefill, std::span<const std::int32_t> chunk,
+                                        std::span<KVCache* const> caches, std::span<const std::int32_t> tokens) const;
   Expected<std::span<const float>> forward_rows(std::span<const std::int32_t> tokens, bool copy_logits);
   Expected<std::vector<Row>> prefill_rows(const KVCache& cache, std::span<const std::int32_t> tokens) const;
   Expected<std::vector<Row>> batch_rows(std::span<KVCache* const> caches, std::span<const std::int32_t> tokens) const;

@@ -64,6 +64,17 @@ int axon_model_cache_read(axon_model* model, int cache, size_t layer, int values
 int axon_model_forward(axon_model* model, const int32_t* tokens, size_t n, float* logits);
 int axon_model_forward_prefill(axon_model* model, int cache, const int32_t* tokens, size_t n, float* logits);
 int axon_model_forward_batch(axon_model* model, const int* caches, const int32_t* tokens, size_t n, float* logits);
+/* One continuous-batching step as one pass. BatchEngine::step (src/engine/batch.cpp:69-156) runs
+ * two: forward_prefill of one prompt chunk, then forward_batch of the sequences in decode.
+ * prefill_cache takes prefill[0..n_prefill) at its next positions (n_prefill 0: no chunk, and
+ * prefill_cache is ignored); caches[i] takes tokens[i] (n may be 0). The chunk is at most
+ * max_seq tokens, n at most max_batch, and prefill_cache is not among caches. Every row equals
+ * what those two passes compute, bit for bit. logits: host [(n_prefill != 0) + n][n_vocab], the
+ * rows that step observes: the chunk's last row (Sequence::prefill_chunk, sequence.cpp:118),
+ * then one row per decode cache; the chunk's other rows get no logits. NULL leaves them in HBM
+ * for axon_model_greedy, which then takes (n_prefill != 0) + n ids. */
+int axon_model_forward_mixed(axon_model* model, int prefill_cache, const int32_t* prefill, size_t n_prefill,
+                             const int* caches, const int32_t* tokens, size_t n, float* logits);
 
 /* Sampler::sample at temperature zero on the device (src/sampling/sampler.cpp:67-102) over the
  * last pass's logits, which may have stayed in HBM (logits NULL): the repetition penalty over
