@@ -199,6 +199,44 @@ class ModelInfo(C.Structure):
                 ("kv_bytes_per_position", C.c_size_t), ("cache_type", C.c_int)]
 
 
+class SamplerConfig(C.Structure):
+    """axon_sampler_config: SamplerConfig (include/axon/sampler.h:10-17) without the seed; the
+    defaults are the reference's."""
+    _fields_ = [("temperature", C.c_float), ("top_k", C.c_int), ("top_p", C.c_float), ("min_p", C.c_float),
+                ("repeat_penalty", C.c_float), ("repeat_last_n", C.c_int)]
+
+    def __init__(self, temperature=0.8, top_k=40, top_p=0.95, min_p=0.05, repeat_penalty=1.1, repeat_last_n=64):
+        super().__init__(temperature, top_k, top_p, min_p, repeat_penalty, repeat_last_n)
+
+
+class Rng(C.Structure):
+    """axon_rng: the sampler's generator (src/sampling/rng.h), seeded as the reference seeds it."""
+    _fields_ = [("s", C.c_uint64 * 4)]
+
+    def __init__(self, seed: int = 0):
+        super().__init__()
+        host().axon_rng_seed(C.byref(self), C.c_uint64(seed))
+
+    def next(self) -> int:
+        return host().axon_rng_next(C.byref(self))
+
+    def uniform(self) -> float:
+        return host().axon_rng_uniform(C.byref(self))
+
+    def state(self):
+        return tuple(self.s)
+
+
+def sample_candidates(config: SamplerConfig, rng: Rng, logits, ids) -> int:
+    """The host stages of the sampler alone (axon_sample_candidates) over candidates in top-k order."""
+    lg = np.ascontiguousarray(logits, np.float32)
+    ix = np.ascontiguousarray(ids, np.int32)
+    out = C.c_int32(0)
+    _mcheck(host().axon_sample_candidates(C.byref(config), C.byref(rng), lg.ctypes.data, ix.ctypes.data, len(lg),
+                                          C.byref(out)), "sample_candidates")
+    return out.value
+
+
 _host = None
 
 
@@ -228,6 +266,15 @@ def host() -> C.CDLL:
                                                C.c_size_t, C.c_void_p]
         L.axon_model_greedy.argtypes = [C.c_void_p, C.c_void_p, C.c_void_p, C.c_float, C.c_int, C.c_void_p,
                                         C.c_size_t]
+        L.axon_rng_seed.argtypes = [C.c_void_p, C.c_uint64]
+        L.axon_rng_seed.restype = None
+        L.axon_rng_next.argtypes = [C.c_void_p]
+        L.axon_rng_next.restype = C.c_uint64
+        L.axon_rng_uniform.argtypes = [C.c_void_p]
+        L.axon_rng_uniform.restype = C.c_double
+        L.axon_model_sample.argtypes = [C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p,
+                                        C.c_size_t]
+        L.axon_sample_candidates.argtypes = [C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p, C.c_size_t, C.c_void_p]
         L.axon_model_probe.argtypes = [C.c_void_p, C.c_int, C.c_int]
         L.axon_model_probe_read.argtypes = [C.c_void_p, C.POINTER(C.c_double), C.POINTER(C.c_size_t),
                                             C.POINTER(C.c_double)]
@@ -346,6 +393,27 @@ class Model:
             lens = (C.c_size_t * n)(*[len(a) for a in arrs])
         _mcheck(host().axon_model_greedy(self.h, rec, lens, repeat_penalty, repeat_last_n, ids.ctypes.data, n),
                 "greedy")
+        return ids
+
+    def sample(self, configs, rngs, recent=None) -> np.ndarray:
+        """Sampler::sample over the last pass's rows (axon_model_sample): row i with configs[i]
+        and rngs[i] (advanced by one draw when its temperature is above zero)."""
+        n = len(configs)
+        if len(rngs) != n:
+            raise ValueError(f"sample: {len(rngs)} generators for {n} configs")
+        cfg = (SamplerConfig * n)(*configs)
+        rs = (Rng * n)()
+        for i, r in enumerate(rngs):
+            C.memmove(C.byref(rs[i]), C.byref(r), C.sizeof(Rng))
+        ids = np.empty(n, np.int32)
+        rec = lens = None
+        if recent is not None:
+            arrs = [np.ascontiguousarray(r, np.int32) for r in recent]
+            rec = (C.c_void_p * n)(*[a.ctypes.data if len(a) else None for a in arrs])
+            lens = (C.c_size_t * n)(*[len(a) for a in arrs])
+        _mcheck(host().axon_model_sample(self.h, cfg, rs, rec, lens, ids.ctypes.data, n), "sample")
+        for i, r in enumerate(rngs):
+            C.memmove(C.byref(r), C.byref(rs[i]), C.sizeof(Rng))
         return ids
 
     def probe(self, weight_type: int, enable: bool = True) -> None:

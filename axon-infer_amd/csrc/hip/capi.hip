@@ -587,6 +587,18 @@ int axon_hip_argmax_rows(const float* x, size_t n, size_t n_rows, size_t stride,
   return argmax_rows_launch(x, static_cast<uint32_t>(n), static_cast<uint32_t>(n_rows), stride, scratch, out);
 }
 
+static_assert(kMaxTopK == AXON_HIP_MAX_TOPK, "one top-k bound");
+
+int axon_hip_topk_rows(const float* x, size_t n, size_t n_rows, size_t stride, size_t k, float* out_logit,
+                       int32_t* out_id) {
+  AXON_READY();
+  if (!fits_u32(n) || !fits_u32(n_rows) || stride < n) return fail(kInvalidArgument, "topk: %zu x %zu, stride %zu", n_rows, n, stride);
+  if (k == 0 || k > kMaxTopK || k > n) return fail(kInvalidArgument, "topk: k %zu of %zu values (k in 1..%u)", k, n, kMaxTopK);
+  if (out_logit == nullptr || out_id == nullptr) return fail(kInvalidArgument, "topk: outputs are required");
+  return topk_rows_launch(x, static_cast<uint32_t>(n), static_cast<uint32_t>(n_rows), stride, static_cast<uint32_t>(k),
+                          out_logit, out_id);
+}
+
 int axon_hip_matmul_q8_fused(int type, const void* xq, size_t n_rows, size_t n_in, size_t n_seg,
                              const void* const* w, float* const* y, const size_t* n_out, const size_t* y_stride,
                              int accumulate) {

@@ -38,6 +38,11 @@ int add_launch(float* x, const float* y, size_t n);
 int repeat_penalty_launch(float* x, uint32_t n, uint32_t n_rows, size_t stride, const int32_t* recent,
                           const uint32_t* recent_len, size_t recent_stride, float penalty);
 size_t argmax_scratch_words(uint32_t n_rows);
+// The k largest values of each row (k <= kMaxTopK), descending, equal values by ascending index,
+// NaN skipped; out_logit/out_id [n_rows][k], id -1 past a row's non-NaN values.
+constexpr uint32_t kMaxTopK = 256;
+int topk_rows_launch(const float* x, uint32_t n, uint32_t n_rows, size_t stride, uint32_t k, float* out_logit,
+                     int32_t* out_id);
 int argmax_rows_launch(const float* x, uint32_t n, uint32_t n_rows, size_t stride, uint64_t* scratch, int32_t* out);
 int rope_rows_launch(const RopeRowsArgs& a, uint32_t n_rows);
 int embedding_launch(int type, const uint8_t* table, uint32_t n, const int32_t* ids, int64_t id0, uint32_t n_rows,

@@ -15,6 +15,17 @@
 // they do with `<`). NaN follows max_element's scan with `<`: a NaN never replaces the running
 // maximum and is skipped, except that a NaN in the first element is never replaced, so such a
 // row selects index 0.
+//
+// Top-k (the candidates of the stochastic stages, sampler.cpp:104-118): one workgroup per row
+// returns the row's k largest logits in descending order, equal logits by ascending id (the
+// reference's std::partial_sort leaves their order unspecified; ascending id is the oracle's
+// choice), NaN skipped. A candidate is the (value, index) key above, so every key is distinct.
+// Rounds: each thread keeps the four largest keys below a bound among its strided elements;
+// the 4096 kept keys are sorted in LDS (bitonic). Let M be the largest fourth key over the
+// threads that kept four. Every key above M is then among the kept ones (a thread's dropped keys
+// lie below its fourth), so the sorted keys above M are the row's next keys in order and are
+// taken. The thread that holds M kept three keys above it, so a round takes at least three,
+// and on a row of random logits the first round takes all k.
 #include "common.h"
 #include "elementwise.h"
 
@@ -97,7 +108,113 @@ __global__ __launch_bounds__(256) void repeat_penalty_kernel(float* __restrict__
   }
 }
 
+constexpr uint32_t kTopKThreads = 1024;
+constexpr uint32_t kTopKKeep = 4;
+constexpr uint32_t kTopKKeys = kTopKThreads * kTopKKeep;
+
+__global__ __launch_bounds__(kTopKThreads) void topk_rows_kernel(const float* __restrict__ x, uint32_t n, size_t stride,
+                                                                 uint32_t k, float* __restrict__ out_logit,
+                                                                 int32_t* __restrict__ out_id) {
+  __shared__ uint64_t keys[kTopKKeys];
+  __shared__ uint64_t red[kTopKThreads / 64];
+  __shared__ uint32_t taken;
+  const uint32_t r = blockIdx.x;
+  const uint32_t t = threadIdx.x;
+  const float* row = x + static_cast<size_t>(r) * stride;
+  float* ol = out_logit + static_cast<size_t>(r) * k;
+  int32_t* oi = out_id + static_cast<size_t>(r) * k;
+  uint32_t got = 0;
+  uint64_t bound = ~0ull;  // above every key
+  for (;;) {
+    uint64_t c0 = 0, c1 = 0, c2 = 0, c3 = 0;  // descending; 0 is below every key
+    for (uint32_t j = t; j < n; j += kTopKThreads) {
+      const float v = row[j];
+      if (v != v) continue;
+      const uint64_t key = argmax_key(v, j);
+      if (key >= bound || key <= c3) continue;
+      if (key > c2) {
+        c3 = c2;
+        if (key > c1) {
+          c2 = c1;
+          if (key > c0) {
+            c1 = c0;
+            c0 = key;
+          } else {
+            c1 = key;
+          }
+        } else {
+          c2 = key;
+        }
+      } else {
+        c3 = key;
+      }
+    }
+    const uint64_t m = max_key_wave(c3);
+    if ((t & 63) == 0) red[t >> 6] = m;
+    keys[kTopKKeep * t] = c0;
+    keys[kTopKKeep * t + 1] = c1;
+    keys[kTopKKeep * t + 2] = c2;
+    keys[kTopKKeep * t + 3] = c3;
+    if (t == 0) taken = 0;
+    __syncthreads();
+    // Bitonic sort, descending: 2048 compare-exchanges per stage, two per thread.
+    for (uint32_t size = 2; size <= kTopKKeys; size <<= 1) {
+      for (uint32_t half = size >> 1; half > 0; half >>= 1) {
+#pragma unroll
+        for (uint32_t p = 0; p < 2; ++p) {
+          const uint32_t q = t + p * kTopKThreads;  // pair index
+          const uint32_t i = 2 * q - (q & (half - 1));
+          const uint32_t j = i + half;
+          const uint64_t a = keys[i], b = keys[j];
+          const bool desc = (i & size) == 0;
+          if (desc ? a < b : a > b) {
+            keys[i] = b;
+            keys[j] = a;
+          }
+        }
+        __syncthreads();
+      }
+    }
+    uint64_t big_m = red[0];
+    for (uint32_t w = 1; w < kTopKThreads / 64; ++w) big_m = red[w] > big_m ? red[w] : big_m;
+    // g = the number of sorted keys above M (keys at or below M, zeros included, follow them).
+#pragma unroll
+    for (uint32_t p = 0; p < kTopKKeep; ++p) {
+      const uint32_t i = kTopKKeep * t + p;
+      if (keys[i] > big_m && (i + 1 == kTopKKeys || keys[i + 1] <= big_m)) taken = i + 1;
+    }
+    __syncthreads();
+    const uint32_t g = taken;
+    const uint32_t take = min(g, k - got);
+    for (uint32_t i = t; i < take; i += kTopKThreads) {
+      const uint64_t key = keys[i];
+      const uint32_t id = ~static_cast<uint32_t>(key & 0xffffffffu);
+      ol[got + i] = row[id];
+      oi[got + i] = static_cast<int32_t>(id);
+    }
+    got += take;
+    // Done at k keys, or when no thread kept four (every remaining key was taken).
+    if (got == k || big_m == 0) break;
+    bound = keys[take - 1];
+    __syncthreads();
+  }
+  for (uint32_t i = got + t; i < k; i += kTopKThreads) {  // fewer than k non-NaN values
+    ol[i] = 0.0f;
+    oi[i] = -1;
+  }
+}
+
 }  // namespace
+
+int topk_rows_launch(const float* x, uint32_t n, uint32_t n_rows, size_t stride, uint32_t k, float* out_logit,
+                     int32_t* out_id) {
+  if (n_rows == 0) return kOk;
+  if (n == 0 || k == 0 || k > kMaxTopK) return fail(kInvalidArgument, "topk: k %u of %u values (k in 1..%u)", k, n, kMaxTopK);
+  if (n_rows > 65535) return fail(kInvalidArgument, "topk: %u rows exceed one launch's 65535", n_rows);
+  hipLaunchKernelGGL(topk_rows_kernel, dim3(n_rows), dim3(kTopKThreads), 0, stream(), x, n, stride, k, out_logit,
+                     out_id);
+  return check_launch("topk");
+}
 
 int repeat_penalty_launch(float* x, uint32_t n, uint32_t n_rows, size_t stride, const int32_t* recent,
                           const uint32_t* recent_len, size_t recent_stride, float penalty) {

@@ -207,6 +207,49 @@ int axon_model_greedy(axon_model* model, const int32_t* const* recent, const siz
   return r ? 0 : fail(r.error());
 }
 
+static_assert(sizeof(axon_rng) == sizeof(axon::sampling::Rng), "axon_rng mirrors sampling::Rng");
+
+void axon_rng_seed(axon_rng* rng, uint64_t seed) { reinterpret_cast<axon::sampling::Rng*>(rng)->seed(seed); }
+uint64_t axon_rng_next(axon_rng* rng) { return reinterpret_cast<axon::sampling::Rng*>(rng)->next(); }
+double axon_rng_uniform(axon_rng* rng) { return reinterpret_cast<axon::sampling::Rng*>(rng)->uniform(); }
+
+namespace {
+axon::sampling::Config config_of(const axon_sampler_config& c) {
+  return axon::sampling::Config{c.temperature, c.top_k, c.top_p, c.min_p, c.repeat_penalty, c.repeat_last_n};
+}
+}  // namespace
+
+int axon_model_sample(axon_model* model, const axon_sampler_config* configs, axon_rng* rngs,
+                      const int32_t* const* recent, const size_t* recent_len, int32_t* ids, size_t n) {
+  if (n != 0 && (configs == nullptr || rngs == nullptr || ids == nullptr))
+    return fail("sample: configs, generators and ids are required");
+  std::vector<axon::sampling::Config> cs(n);
+  for (size_t i = 0; i < n; ++i) cs[i] = config_of(configs[i]);
+  std::vector<std::span<const int32_t>> windows;
+  if (recent != nullptr) {
+    if (recent_len == nullptr) return fail("sample: recent_len is NULL");
+    windows.resize(n);
+    for (size_t i = 0; i < n; ++i) {
+      if (recent[i] == nullptr && recent_len[i] != 0) return fail("sample: recent[" + std::to_string(i) + "] is NULL");
+      windows[i] = std::span<const int32_t>(recent[i], recent_len[i]);
+    }
+  }
+  auto r = model->m->sample(std::span<int32_t>(ids, n), cs,
+                            std::span<axon::sampling::Rng>(reinterpret_cast<axon::sampling::Rng*>(rngs), n), windows);
+  return r ? 0 : fail(r.error());
+}
+
+int axon_sample_candidates(const axon_sampler_config* config, axon_rng* rng, const float* logits, const int32_t* ids,
+                           size_t n, int32_t* out) {
+  if (config == nullptr || rng == nullptr || logits == nullptr || ids == nullptr || out == nullptr || n == 0)
+    return fail("sample_candidates: every argument is required and n >= 1");
+  if (!(config->temperature > 0.0F)) return fail("sample_candidates: the temperature must be above zero");
+  std::vector<double> probs(n);
+  *out = axon::sampling::draw(config_of(*config), *reinterpret_cast<axon::sampling::Rng*>(rng), logits, ids, n,
+                              probs.data());
+  return 0;
+}
+
 int axon_model_probe(axon_model* model, int type, int enable) {
   auto r = model->m->set_probe(type, enable != 0);
   return r ? 0 : fail(r.error());

@@ -276,8 +276,9 @@ Expected<std::unique_ptr<LlamaModel>> LlamaModel::load(const std::string& path, 
   const std::size_t info_bytes = align_up(12 * R, 8) + 8 * R;
   if (axon_hip_malloc(reinterpret_cast<void**>(&m->argmax_scratch_), axon_hip_argmax_scratch_words(R) * 8) !=
           AXON_HIP_OK ||
-      axon_hip_malloc(reinterpret_cast<void**>(&m->ids_), R * 4) != AXON_HIP_OK)
-    return m->device_error("argmax scratch");
+      axon_hip_malloc(reinterpret_cast<void**>(&m->ids_), R * 4) != AXON_HIP_OK ||
+      axon_hip_malloc(&m->cand_, R * AXON_HIP_MAX_TOPK * 8) != AXON_HIP_OK)
+    return m->device_error("sampling scratch");
   const std::size_t window_bytes = R * (kMaxPenaltyWindow + 1) * 4;
   if (axon_hip_malloc(&m->window_, window_bytes) != AXON_HIP_OK ||
       axon_hip_host_malloc(&m->window_host_, window_bytes) != AXON_HIP_OK)
@@ -315,7 +316,7 @@ LlamaModel::~LlamaModel() {
   for (void* p : {static_cast<void*>(x_), static_cast<void*>(h_), static_cast<void*>(q_), static_cast<void*>(k_),
                   static_cast<void*>(v_), static_cast<void*>(attn_), static_cast<void*>(gate_),
                   static_cast<void*>(up_), static_cast<void*>(tmp_), static_cast<void*>(logits_),
-                  static_cast<void*>(scores_), static_cast<void*>(argmax_scratch_), static_cast<void*>(ids_), window_,
+                  static_cast<void*>(scores_), static_cast<void*>(argmax_scratch_), static_cast<void*>(ids_), cand_, window_,
                   xq_, rowinfo_, kv_, static_cast<void*>(kv_free_),
                   static_cast<void*>(rope_table_), weights_}) {
     if (p != nullptr) axon_hip_free(p);
@@ -766,34 +767,115 @@ Expected<std::size_t> LlamaModel::greedy(std::span<std::int32_t> ids,
     return make_error(ErrorCode::InvalidArgument,
                       "greedy: " + std::to_string(recent.size()) + " recent windows for " + std::to_string(n) + " rows");
   last_rows_ = 0;
-  // sampler.cpp:73: the penalty runs when it is not 1 and the window is not empty.
-  std::size_t width = 0;
-  if (repeat_penalty != 1.0F && repeat_last_n > 0) {
-    for (const auto& r : recent) width = std::max(width, std::min(r.size(), static_cast<std::size_t>(repeat_last_n)));
-  }
-  if (width > kMaxPenaltyWindow)
-    return make_error(ErrorCode::InvalidArgument, "greedy: a penalty window of " + std::to_string(width) +
-                                                      " ids exceeds " + std::to_string(kMaxPenaltyWindow));
-  if (width != 0) {
-    // Row r's window is the last min(len, repeat_last_n) ids of its history, packed [n][width].
-    auto* win = static_cast<std::int32_t*>(window_host_);
-    auto* len = reinterpret_cast<std::uint32_t*>(win + n * width);
-    for (std::size_t r = 0; r < n; ++r) {
-      const std::size_t w = std::min(recent[r].size(), static_cast<std::size_t>(repeat_last_n));
-      std::copy(recent[r].end() - static_cast<std::ptrdiff_t>(w), recent[r].end(), win + r * width);
-      len[r] = static_cast<std::uint32_t>(w);
-    }
-    auto* dwin = static_cast<std::int32_t*>(window_);
-    auto* dlen = reinterpret_cast<std::uint32_t*>(dwin + n * width);
-    if (axon_hip_memcpy_h2d_async(window_, window_host_, n * (width + 1) * 4) != AXON_HIP_OK ||
-        axon_hip_repeat_penalty_rows(logits_, cfg_.n_vocab, n, cfg_.n_vocab, dwin, dlen, width, repeat_penalty) !=
-            AXON_HIP_OK)
-      return device_error("greedy: repetition penalty");
-  }
+  auto p = penalize(n, recent, repeat_penalty, repeat_last_n, {});
+  if (!p) return p.error();
   if (axon_hip_argmax_rows(logits_, cfg_.n_vocab, n, cfg_.n_vocab, argmax_scratch_, ids_) != AXON_HIP_OK)
     return device_error("greedy");
   // A synchronous copy on the library stream: the staging above is free again when it returns.
   if (axon_hip_memcpy_d2h(ids.data(), ids_, n * 4) != AXON_HIP_OK) return device_error("greedy");
+  return n;
+}
+
+Expected<bool> LlamaModel::penalize(std::size_t n, std::span<const std::span<const std::int32_t>> recent,
+                                    float penalty, int repeat_last_n, std::span<const std::uint8_t> select,
+                                    bool reuse) {
+  // sampler.cpp:73: the penalty runs when it is not 1 and the window is not empty.
+  std::size_t width = 0;
+  if (penalty != 1.0F && repeat_last_n > 0) {
+    for (std::size_t r = 0; r < recent.size(); ++r)
+      if (select.empty() || select[r] != 0)
+        width = std::max(width, std::min(recent[r].size(), static_cast<std::size_t>(repeat_last_n)));
+  }
+  if (width > kMaxPenaltyWindow)
+    return make_error(ErrorCode::InvalidArgument, "sampling: a penalty window of " + std::to_string(width) +
+                                                      " ids exceeds " + std::to_string(kMaxPenaltyWindow));
+  if (width == 0) return true;
+  // Row r's window is the last min(len, repeat_last_n) ids of its history, packed [n][width];
+  // rows outside the selection get an empty window.
+  auto* win = static_cast<std::int32_t*>(window_host_);
+  auto* len = reinterpret_cast<std::uint32_t*>(win + n * width);
+  for (std::size_t r = 0; r < n; ++r) {
+    const std::size_t w =
+        select.empty() || select[r] != 0 ? std::min(recent[r].size(), static_cast<std::size_t>(repeat_last_n)) : 0;
+    std::copy(recent[r].end() - static_cast<std::ptrdiff_t>(w), recent[r].end(), win + r * width);
+    len[r] = static_cast<std::uint32_t>(w);
+  }
+  auto* dwin = static_cast<std::int32_t*>(window_);
+  auto* dlen = reinterpret_cast<std::uint32_t*>(dwin + n * width);
+  // The copy from the pinned staging runs in stream order; a following call rewrites the
+  // staging, so it waits for the stream first.
+  if (axon_hip_memcpy_h2d_async(window_, window_host_, n * (width + 1) * 4) != AXON_HIP_OK ||
+      axon_hip_repeat_penalty_rows(logits_, cfg_.n_vocab, n, cfg_.n_vocab, dwin, dlen, width, penalty) != AXON_HIP_OK ||
+      (reuse && axon_hip_synchronize() != AXON_HIP_OK))
+    return device_error("sampling: repetition penalty");
+  return true;
+}
+
+Expected<std::size_t> LlamaModel::sample(std::span<std::int32_t> ids, std::span<const sampling::Config> configs,
+                                         std::span<sampling::Rng> rngs,
+                                         std::span<const std::span<const std::int32_t>> recent) {
+  const std::size_t n = last_rows_;
+  const std::size_t V = cfg_.n_vocab;
+  if (n == 0) return make_error(ErrorCode::InvalidArgument, "sample: no logits from a forward pass");
+  if (ids.size() != n || configs.size() != n || rngs.size() != n)
+    return make_error(ErrorCode::InvalidArgument, "sample: " + std::to_string(ids.size()) + " ids, " +
+                                                      std::to_string(configs.size()) + " configs and " +
+                                                      std::to_string(rngs.size()) + " generators for " +
+                                                      std::to_string(n) + " rows of logits");
+  if (!recent.empty() && recent.size() != n)
+    return make_error(ErrorCode::InvalidArgument,
+                      "sample: " + std::to_string(recent.size()) + " recent windows for " + std::to_string(n) + " rows");
+  std::size_t k_max = 0;
+  bool any_greedy = false;
+  for (std::size_t r = 0; r < n; ++r) {
+    if (configs[r].temperature <= 0.0F) {
+      any_greedy = true;
+      continue;
+    }
+    const std::size_t kept = sampling::kept_after_top_k(configs[r], V);
+    if (kept > AXON_HIP_MAX_TOPK)
+      return make_error(ErrorCode::Unsupported, "sample: row " + std::to_string(r) + " keeps " + std::to_string(kept) +
+                                                    " candidates after top-k; the device sampler keeps at most " +
+                                                    std::to_string(AXON_HIP_MAX_TOPK) + " (top_k 1.." +
+                                                    std::to_string(AXON_HIP_MAX_TOPK) + ")");
+    k_max = std::max(k_max, kept);
+  }
+  last_rows_ = 0;
+  // The penalty, once per distinct (penalty, window) setting among the rows.
+  if (!recent.empty()) {
+    std::vector<std::uint8_t> done(n, 0), select(n, 0);
+    for (std::size_t r = 0; r < n; ++r) {
+      if (done[r] != 0) continue;
+      for (std::size_t q = r; q < n; ++q) {
+        select[q] = configs[q].repeat_penalty == configs[r].repeat_penalty &&
+                    configs[q].repeat_last_n == configs[r].repeat_last_n;
+        done[q] |= select[q];
+      }
+      const bool more = std::find(done.begin(), done.end(), 0) != done.end();
+      auto p = penalize(n, recent, configs[r].repeat_penalty, configs[r].repeat_last_n, select, more);
+      if (!p) return p.error();
+      std::fill(select.begin(), select.end(), 0);
+    }
+  }
+  auto* cand_logits = static_cast<float*>(cand_);
+  auto* cand_ids = reinterpret_cast<std::int32_t*>(cand_logits + n * k_max);
+  if ((any_greedy && axon_hip_argmax_rows(logits_, V, n, V, argmax_scratch_, ids_) != AXON_HIP_OK) ||
+      (k_max != 0 && axon_hip_topk_rows(logits_, V, n, V, k_max, cand_logits, cand_ids) != AXON_HIP_OK))
+    return device_error("sample");
+  // Synchronous copies on the library stream.
+  if (any_greedy && axon_hip_memcpy_d2h(ids.data(), ids_, n * 4) != AXON_HIP_OK) return device_error("sample");
+  if (k_max == 0) return n;
+  cand_host_.resize(n * k_max * 8);
+  if (axon_hip_memcpy_d2h(cand_host_.data(), cand_, n * k_max * 8) != AXON_HIP_OK) return device_error("sample");
+  const auto* hl = reinterpret_cast<const float*>(cand_host_.data());
+  const auto* hi = reinterpret_cast<const std::int32_t*>(hl + n * k_max);
+  probs_.resize(k_max);
+  for (std::size_t r = 0; r < n; ++r) {
+    if (configs[r].temperature <= 0.0F) continue;
+    std::size_t kept = sampling::kept_after_top_k(configs[r], V);
+    while (kept > 1 && hi[r * k_max + kept - 1] < 0) --kept;  // NaN logits are never candidates
+    ids[r] = sampling::draw(configs[r], rngs[r], hl + r * k_max, hi + r * k_max, kept, probs_.data());
+  }
   return n;
 }
 

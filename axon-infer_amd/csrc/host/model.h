@@ -15,6 +15,7 @@
 #include "expected.h"
 #include "gguf.h"
 #include "kernels.h"
+#include "sampler.h"
 
 #include <cstddef>
 #include <cstdint>
@@ -119,6 +120,14 @@ public:
   static constexpr std::size_t kMaxPenaltyWindow = 4096;
   Expected<std::size_t> greedy(std::span<std::int32_t> ids, std::span<const std::span<const std::int32_t>> recent = {},
                                float repeat_penalty = 1.0F, int repeat_last_n = 64);
+  // Sampler::sample (sampler.cpp:67-183) for each row of the last pass, row r with configs[r] and
+  // its own generator rngs[r], as each Sequence holds its own Sampler. On the device: each row's
+  // repetition penalty, the greedy choice for rows at temperature zero, and the top-k candidates
+  // of the others (at most 256: top_k in 1..256, or a vocabulary of at most 256). On the host:
+  // the stages after top-k and one draw per stochastic row. Only the ids and the candidates
+  // cross to the host. Consumes the pass's logits, as greedy does.
+  Expected<std::size_t> sample(std::span<std::int32_t> ids, std::span<const sampling::Config> configs,
+                               std::span<sampling::Rng> rngs, std::span<const std::span<const std::int32_t>> recent = {});
 
   // A fresh cache in a free device slot, or an error when every slot is taken.
   Expected<std::unique_ptr<KVCache>> new_cache();
@@ -166,6 +175,11 @@ private:
   Error device_error(const char* what) const;
   int mm(const Tensor& w, const float* x, const void* xq, float* y, std::size_t n, bool accumulate);
   bool q8_path(const Tensor& w) const;
+  // The repetition penalty of one (penalty, window) setting on the rows with select[r] set (all
+  // rows when select is empty), on the device (sampler.cpp:73-97). `reuse`: another call follows,
+  // so wait until the staging has been copied.
+  Expected<bool> penalize(std::size_t n, std::span<const std::span<const std::int32_t>> recent, float penalty,
+                          int repeat_last_n, std::span<const std::uint8_t> select, bool reuse = false);
 
   std::unique_ptr<GgufFile> file_;
   Config cfg_;
@@ -192,6 +206,9 @@ private:
   std::size_t scores_floats_ = 0;
   std::uint64_t* argmax_scratch_ = nullptr;
   std::int32_t* ids_ = nullptr;
+  void* cand_ = nullptr;  // top-k candidates: [rows][k] logits, then [rows][k] ids
+  std::vector<std::byte> cand_host_;
+  std::vector<double> probs_;
   void* window_ = nullptr;       // device: recent ids [R][kMaxPenaltyWindow] | lengths [R]
   void* window_host_ = nullptr;  // pinned staging of the same
   std::size_t last_rows_ = 0;  // rows of the last pass's logits, 0 after a failed pass

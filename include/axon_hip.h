@@ -172,6 +172,14 @@ size_t axon_hip_argmax_scratch_words(size_t n_rows);
 int axon_hip_repeat_penalty_rows(float* x, size_t n, size_t n_rows, size_t stride, const int32_t* recent,
                                  const uint32_t* recent_len, size_t recent_stride, float penalty);
 int axon_hip_argmax_rows(const float* x, size_t n, size_t n_rows, size_t stride, uint64_t* scratch, int32_t* out);
+/* The top-k candidates of the stochastic sampler stages (src/sampling/sampler.cpp:104-118,
+ * std::ranges::partial_sort of the ids by logit, descending): row r's k largest values (rows
+ * stride floats apart) into out_logit[r * k + i] with their indices in out_id, descending, equal
+ * values by ascending index (the reference leaves their order unspecified). NaN is skipped; a
+ * row with fewer than k other values ends in ids -1. 1 <= k <= 256, k <= n. */
+#define AXON_HIP_MAX_TOPK 256
+int axon_hip_topk_rows(const float* x, size_t n, size_t n_rows, size_t stride, size_t k, float* out_logit,
+                       int32_t* out_id);
 /* Y_s[n_rows][n_out_s] (+)= X W_s^T for up to three weights of one type sharing one Q8_0
  * input (mm_fused, llama.cpp:425-472). w[s], y[s] device pointers in host arrays. Rows below
  * 16 run the v_dot4 matvec, 16 and more the int8 MFMA tiles. accumulate adds into y (the

@@ -86,6 +86,44 @@ int axon_model_forward_mixed(axon_model* model, int prefill_cache, const int32_t
 int axon_model_greedy(axon_model* model, const int32_t* const* recent, const size_t* recent_len, float repeat_penalty,
                       int repeat_last_n, int32_t* ids, size_t n);
 
+/* SamplerConfig (include/axon/sampler.h:10-17) without the seed, which seeds an axon_rng. */
+typedef struct {
+  float temperature; /* 0 or below: greedy */
+  int top_k;         /* 0: every id */
+  float top_p;       /* 1: off */
+  float min_p;       /* 0: off */
+  float repeat_penalty;
+  int repeat_last_n;
+} axon_sampler_config;
+
+/* The sampler's generator (src/sampling/rng.h:11-45): xoshiro256** seeded through SplitMix64.
+ * A seed of 0 is used as given (the reference's Sampler draws a clock seed for 0,
+ * sampler.cpp:37-48; that choice stays with the caller). */
+typedef struct {
+  uint64_t s[4];
+} axon_rng;
+void axon_rng_seed(axon_rng* rng, uint64_t seed);
+uint64_t axon_rng_next(axon_rng* rng);
+double axon_rng_uniform(axon_rng* rng);
+
+/* Sampler::sample (src/sampling/sampler.cpp:67-183) over the last pass's n rows, row i with
+ * configs[i] and generator rngs[i] (each sequence's own Sampler). On the device: each row's
+ * repetition penalty (recent as for axon_model_greedy), the greedy choice for rows at temperature
+ * zero, and the top-k candidates of the others, descending, equal logits by ascending id (the
+ * reference leaves their order unspecified). On the host: temperature, softmax in double, top-p,
+ * min-p and one draw from rngs[i] per stochastic row. Only the ids and at most 256 candidates
+ * per row cross to the host. A stochastic row must keep at most 256 candidates after top-k
+ * (top_k 1..256, or a vocabulary of at most 256), else Unsupported and nothing runs. The pass's
+ * logits are consumed. */
+int axon_model_sample(axon_model* model, const axon_sampler_config* configs, axon_rng* rngs,
+                      const int32_t* const* recent, const size_t* recent_len, int32_t* ids, size_t n);
+
+/* The host stages of axon_model_sample alone (sampler.cpp:120-183): temperature, softmax,
+ * top-p, min-p and the draw over n candidates in top-k order (logits descending). *out = the
+ * drawn id. */
+int axon_sample_candidates(const axon_sampler_config* config, axon_rng* rng, const float* logits, const int32_t* ids,
+                           size_t n, int32_t* out);
+
 /* Kernel-time probe (measurement only): while enabled, the kernel of every matmul on weights of
  * ggml type `type` records its dispatch's start and end on HIP events (axon_hip_probe_next_launch);
  * probe_read returns the summed kernel milliseconds, the launch count and the launches'

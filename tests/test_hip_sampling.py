@@ -1,11 +1,14 @@
-"""The device greedy step (sampling.hip: axon_hip_repeat_penalty_rows, axon_hip_argmax_rows, and
-the model's axon_model_greedy) against the oracle's sampler at temperature zero, which
-tests/test_oracle_sampling.py pins to the reference's Sampler draw for draw.
+"""The device sampler (sampling.hip: axon_hip_repeat_penalty_rows, axon_hip_argmax_rows,
+axon_hip_topk_rows, and the model's axon_model_greedy and axon_model_sample) against the oracle's
+sampler, which tests/test_oracle_sampling.py pins to the reference's Sampler draw for draw.
 
-Greedy selection is index work, so the bar is bit-exact: the same id for every row, and the
-penalised logits bit-identical to the oracle's. Rows cover the full Llama-3 vocabulary (128256),
-widths around the kernel's 64-way split (1, 63, 64, 65, 4097), ties placed across split
-boundaries, NaN (first element and elsewhere), signed zeros, infinities and strided rows."""
+Selection is index work, so the bar is bit-exact: the same id for every row, the penalised
+logits bit-identical to the oracle's, and for the stochastic stages the same draws and generator
+states. Greedy rows cover the full Llama-3 vocabulary (128256), widths around the kernel's 64-way
+split (1, 63, 64, 65, 4097), ties placed across split boundaries, NaN (first element and
+elsewhere), signed zeros, infinities and strided rows. Top-k rows cover the Qwen2.5 and Llama-3
+vocabularies, k of 1, 40 and 256, ties, NaN, signed zeros, and rows laid out so that one thread's
+stride holds the largest values (the kernel's later rounds)."""
 import ctypes as C
 from dataclasses import replace
 
@@ -221,3 +224,129 @@ def test_model_greedy_after_every_pass_kind(H, c1_model):
     b.forward_prefill(cb, toks, logits=False)
     assert b.greedy(len(toks)).tolist() == want
     assert a.cache_pos(ca) == b.cache_pos(cb) == len(toks)
+
+
+# ---- top-k candidates and the stochastic sampler ----------------------------------------------
+
+def topk_reference(x, k):
+    """The kernel's contract: the k largest non-NaN values, descending, equal values by
+    ascending index (-0 equal to +0), ids -1 past the non-NaN values."""
+    n = len(x)
+    ok = ~np.isnan(x)
+    idx = np.nonzero(ok)[0]
+    v = x[idx] + np.float32(0.0)  # -0 -> +0
+    order = idx[np.lexsort((idx, -v))][:k]
+    ids = np.full(k, -1, np.int32)
+    ids[:len(order)] = order
+    vals = np.zeros(k, np.float32)
+    vals[:len(order)] = x[order]
+    return vals, ids
+
+
+def topk_rows(kind, n, rng):
+    x = rng.standard_normal(n).astype(np.float32) * np.float32(3.0)
+    if kind == "ties":
+        x = np.round(x * 2) / 2          # a handful of distinct values
+    elif kind == "nan":
+        x[rng.integers(0, n, n // 5)] = NAN
+    elif kind == "zeros":
+        x = -np.abs(x) - 1
+        x[rng.integers(0, n, 30)] = np.float32(-0.0)
+        x[rng.integers(0, n, 30)] = np.float32(0.0)
+    elif kind == "equal":
+        x[:] = np.float32(0.25)
+    elif kind == "one-stride":          # every large value in one thread's stride of 1024
+        x[5::1024] = np.float32(100.0) + np.arange(len(x[5::1024]), dtype=np.float32)
+    elif kind == "ascending":
+        x = np.sort(x)
+    elif kind == "descending":
+        x = np.sort(x)[::-1].copy()
+    return x.astype(np.float32)
+
+
+@pytest.mark.parametrize("n", [151936, 128256, 4097, 300, 40])
+@pytest.mark.parametrize("k", [1, 40, 256])
+def test_topk_rows_match_sorted_order(H, n, k):
+    if k > n:
+        pytest.skip("k above the row length is refused")
+    kinds = ["normal", "ties", "nan", "zeros", "equal", "one-stride", "ascending", "descending"]
+    rng = np.random.default_rng(n + k)
+    x = np.stack([topk_rows(kind, n, rng) for kind in kinds])
+    stride = n + 3
+    xs = np.zeros((len(kinds), stride), np.float32)
+    xs[:, :n] = x
+    dx = H.DeviceBuffer.of(xs)
+    ol = H.DeviceBuffer(4 * len(kinds) * k)
+    oi = H.DeviceBuffer(4 * len(kinds) * k)
+    H.call("topk_rows", dx, n, len(kinds), stride, k, ol, oi)
+    got_v = ol.download(np.float32, len(kinds) * k).reshape(len(kinds), k)
+    got_i = oi.download(np.int32, len(kinds) * k).reshape(len(kinds), k)
+    for r, kind in enumerate(kinds):
+        want_v, want_i = topk_reference(x[r], k)
+        assert np.array_equal(got_i[r], want_i), (kind, np.nonzero(got_i[r] != want_i)[0][:5])
+        assert np.array_equal(got_v[r].view(np.uint32), want_v.view(np.uint32)), kind
+
+
+def test_topk_rows_bounds(H):
+    dx = H.DeviceBuffer.of(np.zeros(300, np.float32))
+    out = H.DeviceBuffer(4 * 300)
+    with pytest.raises(H.HipError, match="k"):
+        H.call("topk_rows", dx, 300, 1, 300, 257, out, out)
+    with pytest.raises(H.HipError, match="k"):
+        H.call("topk_rows", dx, 30, 1, 30, 31, out, out)
+    with pytest.raises(H.HipError, match="stride"):
+        H.call("topk_rows", dx, 300, 1, 200, 4, out, out)
+
+
+ROW_CONFIGS = [
+    dict(temperature=0.8, top_k=40, top_p=0.95, min_p=0.05, repeat_penalty=1.1, repeat_last_n=64),
+    dict(temperature=0.8, top_k=40, top_p=0.9, min_p=0.05, repeat_penalty=1.0, repeat_last_n=64),
+    dict(temperature=0.0, top_k=40, top_p=0.95, min_p=0.05, repeat_penalty=1.3, repeat_last_n=16),
+    dict(temperature=1.0, top_k=1, top_p=0.95, min_p=0.05, repeat_penalty=1.1, repeat_last_n=64),
+    dict(temperature=1.7, top_k=256, top_p=1.0, min_p=0.0, repeat_penalty=1.5, repeat_last_n=8),
+]
+
+
+def test_model_sample_matches_oracle_sampler(H, c1_model):
+    """Five sequences decoded together for 24 steps, each row with its own sampler settings and
+    generator (greedy with a penalty among them): every drawn id and every generator state
+    equal the oracle sampler's on the host logits of the same pass."""
+    n_seq = len(ROW_CONFIGS)
+    m = hip_model(c1_model, max_seq=32, max_ctx=128, max_batch=n_seq, max_caches=n_seq)
+    rng = np.random.default_rng(21)
+    prompts = [rng.integers(0, 2048, 6 + 3 * i).astype(np.int32) for i in range(n_seq)]
+    caches = [m.new_cache() for _ in range(n_seq)]
+    hist = [list(p) for p in prompts]
+    cfgs = [H.SamplerConfig(**c) for c in ROW_CONFIGS]
+    gens = [H.Rng(1000 + i) for i in range(n_seq)]
+    orc = [OracleSampler(2048, seed=1000 + i, **c) for i, c in enumerate(ROW_CONFIGS)]
+    for i in range(n_seq):
+        m.forward_prefill(caches[i], prompts[i][:-1], logits=False)
+    toks = [int(p[-1]) for p in prompts]
+    for step in range(24):
+        logits = m.forward_batch(caches, toks)
+        got = m.sample(cfgs, gens, hist)
+        want = [orc[i].sample(logits[i], np.array(hist[i], np.int32)) for i in range(n_seq)]
+        assert got.tolist() == want, (step, got.tolist(), want)
+        for i in range(n_seq):
+            assert gens[i].state() == tuple(orc[i].rng.s), (step, i)
+            hist[i].append(int(got[i]))
+        toks = [int(t) for t in got]
+
+
+def test_model_sample_bounds(H, c1_model):
+    m = hip_model(c1_model, max_seq=32, max_ctx=64, max_batch=2, max_caches=2)
+    c = m.new_cache()
+    with pytest.raises(H.HipError, match="no logits"):
+        m.sample([H.SamplerConfig()], [H.Rng(1)])
+    m.forward_prefill(c, [1, 2, 3], logits=False)
+    with pytest.raises(H.HipError, match="3 rows"):
+        m.sample([H.SamplerConfig()], [H.Rng(1)])
+    g = H.Rng(5)
+    before = g.state()
+    with pytest.raises(H.HipError, match="at most 256"):
+        m.sample([H.SamplerConfig(top_k=0)] * 3, [g, H.Rng(6), H.Rng(7)])
+    assert g.state() == before  # nothing ran
+    # The pass's logits are still there after a refused call.
+    ids = m.sample([H.SamplerConfig(temperature=0.0)] * 3, [H.Rng(1)] * 3)
+    assert len(ids) == 3
