@@ -31,6 +31,13 @@ The line also carries:
   f16_cache    decode-b1 and ragged-32 again with the KV cache held as fp16 (LoadOptions::cache
                = F16): half the cache bytes per position (kv_bytes_per_position).
 
+  c5_mixed     config 5: the Qwen2.5-0.5B-shaped model, 64 sequences with prompts U[32, 1024]
+               admitted together, each step one 512-token prompt chunk plus one token of every
+               sequence in decode, seeded top-k 40 / top-p 0.9 / T 0.8 sampling (candidates on the
+               device, the draw on the host), 128 tokens each. one_pass runs each step as one
+               forward (axon_model_forward_mixed), two_pass as the reference's two; both must give
+               the same token streams. tokens_per_s = sampled tokens over the whole run.
+
   traffic      HBM bytes per launch of that kernel, from two rocprofv3 counter passes over
                `bench.py --traffic-probe` (FETCH_SIZE, then WRITE_SIZE, KiB per dispatch), each
                scaled by what the same counter reads for a device-to-device copy of 256 MiB in the
@@ -68,9 +75,11 @@ def log(msg: str) -> None:
 
 
 def prefill_greedy(model, cache, tokens):
-    """Prefill with the logits left in HBM; the last row's greedy id, chosen on the device."""
-    model.forward_prefill(cache, tokens, logits=False)
-    return int(model.greedy(len(tokens))[-1])
+    """Prefill with the logits left in HBM; the last row's greedy id, chosen on the device. The
+    pass computes logits for the last row only, the one the reference's Sequence observes
+    (src/engine/sequence.cpp:118)."""
+    model.forward_mixed(cache, tokens, [], [], logits=False)
+    return int(model.greedy(1)[0])
 
 
 def greedy_decode(model, cache, tok, steps):
@@ -176,6 +185,120 @@ def bench_ragged(H, model, n_vocab, seed, n_seq=32, decode_steps=128, cohort=4, 
             "mean_batch": float(np.mean(batch_sizes)), "max_batch": int(max(batch_sizes)),
             "prefill_tokens": int(ctx.sum()), "prefill_s": prefill_s, "decode_s": decode_s,
             "contexts": {"min": int(ctx.min()), "mean": float(ctx.mean()), "max": int(ctx.max())}}
+
+
+C5_SAMPLER = dict(temperature=0.8, top_k=40, top_p=0.9, min_p=0.05, repeat_penalty=1.1, repeat_last_n=64)
+
+
+def run_engine(H, model, prompts, decode_tokens, seed, one_pass):
+    """BatchEngine::step (src/engine/batch.cpp:69-156) over sequences admitted together: each step
+    feeds the next max_seq-token chunk of the oldest sequence still in prefill and one token of
+    every sequence in decode, then samples (Sampler::sample with config 5's settings, each
+    sequence with its own seeded generator; SamplerConfig's min_p 0.05 and repeat penalty 1.1
+    over the last 64 ids are kept). The chunk that completes a prompt draws the sequence's first
+    token from its last row (sequence.cpp:101-123); an earlier chunk draws nothing. one_pass:
+    the chunk and the decode rows in one pass (axon_model_forward_mixed); else as the reference,
+    the chunk's pass (its last row's logits only) then forward_batch. Logits stay in HBM."""
+    n = len(prompts)
+    max_seq = model.info.max_seq
+    caches = [model.new_cache() for _ in range(n)]
+    cfg = H.SamplerConfig(**C5_SAMPLER)
+    quiet = H.SamplerConfig(temperature=0.0, repeat_penalty=1.0)  # an unfinished chunk: no draw
+    gens = [H.Rng(seed * 1000 + i + 1) for i in range(n)]
+    fed = [0] * n
+    out = [[] for _ in range(n)]
+    steps = 0
+    H.synchronize()
+    t0 = time.perf_counter()
+    while True:
+        pre = [i for i in range(n) if fed[i] < len(prompts[i])]
+        # Sequence::accept_pending (sequence.cpp:129-142): a sequence feeds its pending token until
+        # it has generated decode_tokens, so the last pass samples one token that is dropped.
+        dec = [i for i in range(n) if fed[i] == len(prompts[i]) and 0 < len(out[i]) <= decode_tokens]
+        if not pre and not dec:
+            break
+        pi = pre[0] if pre else None
+        chunk = prompts[pi][fed[pi]:fed[pi] + max_seq] if pi is not None else []
+        done_prompt = pi is not None and fed[pi] + len(chunk) == len(prompts[pi])
+        # The penalty reads the last repeat_last_n ids of each history (sampler.cpp:75-76).
+        last_n = C5_SAMPLER["repeat_last_n"]
+
+        def tail(i, upto):
+            t = out[i][-last_n:]
+            if len(t) < last_n:
+                t = [int(v) for v in prompts[i][max(0, upto - (last_n - len(t))):upto]] + t
+            return t
+
+        hist = {i: tail(i, fed[i]) for i in dec}
+        toks = [out[i][-1] for i in dec]
+        dcfg, dgen, drec = [cfg] * len(dec), [gens[i] for i in dec], [hist[i] for i in dec]
+        if pi is not None:
+            pcfg = cfg if done_prompt else quiet
+            prec = tail(pi, fed[pi] + len(chunk))
+        if one_pass:
+            model.forward_mixed(caches[pi] if pi is not None else None, chunk, [caches[i] for i in dec], toks,
+                                logits=False)
+            if pi is not None:
+                ids = model.sample([pcfg] + dcfg, [gens[pi]] + dgen, [prec] + drec)
+            else:
+                ids = model.sample(dcfg, dgen, drec)
+        else:
+            ids = []
+            if pi is not None:
+                model.forward_mixed(caches[pi], chunk, [], [], logits=False)
+                ids += list(model.sample([pcfg], [gens[pi]], [prec]))
+            if dec:
+                model.forward_batch([caches[i] for i in dec], toks, logits=False)
+                ids += list(model.sample(dcfg, dgen, drec))
+        r = 0
+        if pi is not None:
+            fed[pi] += len(chunk)
+            if done_prompt:
+                out[pi].append(int(ids[0]))
+            r = 1
+        for j, i in enumerate(dec):
+            out[i].append(int(ids[r + j]))
+        steps += 1
+    H.synchronize()
+    elapsed = time.perf_counter() - t0
+    for c in caches:
+        model.free_cache(c)
+    return [o[:decode_tokens] for o in out], steps, elapsed
+
+
+def bench_c5(H, seed, n_seq=64, decode_tokens=128):
+    """Config 5 at full size: the Qwen2.5-0.5B-shaped model (Q4_0, q/k/v bias, NeoX RoPE, Q8_0
+    output), 64 sequences with prompts drawn U[32, 1024] from the seed, 128 sampled tokens each,
+    prompt chunks mixed with decode in the same steps. Both engines run the same schedule and
+    must produce the same token streams."""
+    import synth
+    spec = synth.CONFIGS["c5"]
+    path = synth.cached_model(spec)
+    model = H.Model(path, max_seq=512, max_ctx=1024 + decode_tokens + 64, max_batch=n_seq, max_caches=n_seq)
+    rng = np.random.default_rng(seed + 11)
+    lens = rng.integers(32, 1025, n_seq)
+    prompts = [rng.integers(0, spec.n_vocab, int(k)).astype(np.int32) for k in lens]
+    # Warm-up: a short schedule of four sequences.
+    run_engine(H, model, [p[:40] for p in prompts[:4]], 4, seed, True)
+    res = {}
+    streams = []
+    for name, one in (("one_pass", True), ("two_pass", False)):
+        out, steps, elapsed = run_engine(H, model, prompts, decode_tokens, seed, one)
+        gen = sum(len(o) for o in out)
+        res[name] = {"tokens_per_s": round(gen / elapsed, 1),
+                     "total_tokens_per_s": round((gen + int(lens.sum())) / elapsed, 1),
+                     "seconds": round(elapsed, 3), "steps": steps}
+        streams.append(out)
+        log(f"c5 {name}: {gen} tokens in {elapsed:.2f}s over {steps} steps ({gen / elapsed:.0f} tok/s)")
+    model.close()
+    res["streams_identical"] = streams[0] == streams[1]
+    res["generated_tokens"] = n_seq * decode_tokens
+    res["prompt_tokens"] = int(lens.sum())
+    res["speedup_one_pass"] = round(res["two_pass"]["seconds"] / res["one_pass"]["seconds"], 3)
+    res["workload"] = ("config 5: Qwen2.5-0.5B-shaped (24 layers, hidden 896, 14/2 heads, FFN 4864, vocab 151936, "
+                       "Q4_0 + q/k/v bias, NeoX, Q8_0 output), 64 sequences, prompts U[32, 1024], chunks of 512 "
+                       "mixed with decode, top-k 40 / top-p 0.9 / T 0.8 / min-p 0.05 / penalty 1.1, 128 tokens each")
+    return res
 
 
 def traffic_probe(H, model, n_vocab, steps, prompt_len, seed):
@@ -303,6 +426,7 @@ def main() -> int:
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-ragged", action="store_true", help="skip the 32-sequence workload")
     ap.add_argument("--no-f16", action="store_true", help="skip the fp16-cache runs")
+    ap.add_argument("--no-c5", action="store_true", help="skip the config-5 mixed prefill/decode workload")
     ap.add_argument("--cpu-budget", type=float, default=12.0, help="seconds per CPU baseline sample")
     ap.add_argument("--traffic-probe", action="store_true",
                     help="run the workload of the FETCH_SIZE / WRITE_SIZE counter passes and exit")
@@ -404,6 +528,8 @@ def main() -> int:
                                "prefill_s": round(rg16["prefill_s"], 3)}
         m16.close()
         result["f16_cache"] = f16
+    if not args.no_c5:
+        result["c5_mixed"] = bench_c5(H, args.seed)
     if not args.no_cpu:
         b1c, rgc = cpu_baseline(path, info.n_vocab, args.seed, args.cpu_budget)
         result["cpu_baseline"] = b1c
