@@ -538,6 +538,38 @@ int axon_hip_matmul_q6_k_rows(const void* w, const float* x, float* y, size_t n_
 
 // ---- coarse entries ---------------------------------------------------------------------
 
+size_t axon_hip_q6k_planar_bytes(size_t n_out, size_t n_in) {
+  if (!fits_u32(n_out) || n_in % kQKK != 0) return 0;
+  return q6k_planar_column_bytes(static_cast<uint32_t>(n_out)) * (n_in / kQKK);
+}
+
+int axon_hip_q6k_repack(const void* w, size_t n_out, size_t n_in, void* planar) {
+  AXON_READY();
+  if (n_in % kQKK != 0 || !fits_u32(n_out) || !fits_u32(n_in / kQKK))
+    return fail(kInvalidArgument, "q6k_repack: %zu x %zu (n_in a multiple of 256)", n_out, n_in);
+  if (w == nullptr || planar == nullptr) return fail(kInvalidArgument, "q6k_repack: null pointer");
+  return q6k_repack_launch(static_cast<const uint8_t*>(w), static_cast<uint8_t*>(planar), static_cast<uint32_t>(n_out),
+                           static_cast<uint32_t>(n_in / kQKK));
+}
+
+int axon_hip_matmul_q6_k_planar(const void* planar, const float* x, float* y, size_t n_rows, size_t n_out,
+                                size_t n_in, size_t y_stride) {
+  AXON_READY();
+  if (n_in % kQKK != 0) return fail(kInvalidArgument, "matmul_q6_k_planar: n_in %zu is not a multiple of 256", n_in);
+  if (!fits_u32(n_rows) || !fits_u32(n_out) || !fits_u32(n_in) || !fits_u32(y_stride))
+    return fail(kInvalidArgument, "matmul_q6_k_planar: sizes too large");
+  if (n_rows > 1 && y_stride < n_out)
+    return fail(kInvalidArgument, "matmul_q6_k_planar: y_stride %zu < n_out %zu", y_stride, n_out);
+  MatvecArgs a{};
+  a.seg[0] = MatvecSeg{static_cast<const uint8_t*>(planar), y, static_cast<uint32_t>(n_out),
+                       static_cast<uint32_t>(y_stride), 0};
+  a.n_seg = 1;
+  a.xq = reinterpret_cast<const uint8_t*>(x);
+  a.nb = static_cast<uint32_t>(n_in / kQKK);
+  a.m = static_cast<uint32_t>(n_rows);
+  return matvec_q6k_planar_launch(a, static_cast<uint32_t>(n_in));
+}
+
 int axon_hip_rmsnorm_rows(const float* x, const float* weight, float* y, void* yq, size_t n, size_t n_rows,
                           float eps) {
   AXON_READY();

@@ -67,6 +67,11 @@ int matvec_q8_launch(int type, MatvecArgs& a);
 uint32_t matvec_q8_max_rows(int type, uint32_t nb);
 // Q6_K weights against float activations, any m (launched in groups that fit LDS).
 int matvec_q6k_launch(MatvecArgs& a, uint32_t n_in);
+// The planar Q6_K layout (matvec_q6k.hip): bytes per super-block column, the one-time repack
+// from native blocks, and the matvec over it (seg[0].w the planar copy).
+size_t q6k_planar_column_bytes(uint32_t n_out);
+int q6k_repack_launch(const uint8_t* src, uint8_t* dst, uint32_t n_out, uint32_t nsb);
+int matvec_q6k_planar_launch(MatvecArgs& a, uint32_t n_in);
 // int8 MFMA tiles for 16 or more Q8_0 activation rows.
 int matmul_q8_mfma_launch(int type, MatvecArgs& a);
 // int8 MFMA for 1..kRowsMaxM activation rows (batched decode): every segment in one grid, one

@@ -250,7 +250,170 @@ __global__ __launch_bounds__(kStreamRows) void q6k_stream_kernel(MatvecArgs args
   }
 }
 
+// ---- The planar layout (one-time repack at upload) --------------------------------------
+// Super-block column c of an [n_out][nsb] matrix becomes a region of q6k_planar_column_bytes:
+// 13 slices [n_out][16 bytes], slice s holding bytes 16s..16s+15 of each row's super-block
+// (ql 0..127, qh 128..191, scales 192..207), then the d plane [n_out] of halves, padded to 16
+// bytes. A lane's loads of its row are aligned 16-byte loads, and lane i of a wave reads the
+// 16 bytes after lane i-1's: one load instruction moves 1 KB of one slice, contiguous.
+
+__global__ __launch_bounds__(256) void q6k_repack_kernel(const uint8_t* __restrict__ src, uint8_t* __restrict__ dst,
+                                                         uint32_t n_out, uint32_t nsb, size_t col_bytes) {
+  const size_t i = static_cast<size_t>(blockIdx.x) * 256 + threadIdx.x;
+  if (i >= static_cast<size_t>(n_out) * nsb) return;
+  const uint32_t row = static_cast<uint32_t>(i % n_out);
+  const uint32_t c = static_cast<uint32_t>(i / n_out);
+  const uint16_t* sb = reinterpret_cast<const uint16_t*>(src + (static_cast<size_t>(row) * nsb + c) * kBytesQ6_K);
+  uint8_t* col = dst + static_cast<size_t>(c) * col_bytes;
+#pragma unroll
+  for (int s = 0; s < 13; ++s) {
+    uint32_t v[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) v[k] = sb[8 * s + 2 * k] | (static_cast<uint32_t>(sb[8 * s + 2 * k + 1]) << 16);
+    *reinterpret_cast<uint4*>(col + static_cast<size_t>(s) * 16 * n_out + 16 * static_cast<size_t>(row)) =
+        make_uint4(v[0], v[1], v[2], v[3]);
+  }
+  reinterpret_cast<uint16_t*>(col + static_cast<size_t>(208) * n_out)[row] = sb[104];
+}
+
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+struct PlanarBlock {
+  u32x4 q[13];
+  uint32_t d;
+};
+
+__device__ __forceinline__ void planar_fetch(const uint8_t* col, uint32_t n_out, uint32_t row, PlanarBlock& b) {
+#pragma unroll
+  for (int s = 0; s < 13; ++s)
+    b.q[s] = __builtin_nontemporal_load(
+        reinterpret_cast<const u32x4*>(col + static_cast<size_t>(s) * 16 * n_out) + row);
+  b.d = reinterpret_cast<const uint16_t*>(col + static_cast<size_t>(208) * n_out)[row];
+}
+
+// The row's super-block in element order, as q6k_window: value (d*scale)*(q-32), then
+// acc += value * x, element after element.
+template <int MM>
+__device__ __forceinline__ void planar_superblock(const PlanarBlock& b, const float* x, uint32_t n_in,
+                                                  float (&acc)[MM]) {
+  auto dw = [&](int o) {
+    return b.q[o / 16][(o / 4) & 3];
+  };
+  const float d = half_value(b.d);
+  uint32_t sc[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) sc[i] = dw(192 + 4 * i);
+#pragma unroll
+  for (int n = 0; n < 2; ++n) {
+#pragma unroll
+    for (int qi = 0; qi < 4; ++qi) {
+#pragma unroll
+      for (int half = 0; half < 2; ++half) {
+        const int si = n * 8 + qi * 2 + half;
+        const float scale = static_cast<float>(static_cast<int8_t>((sc[si >> 2] >> (8 * (si & 3))) & 0xffu));
+        const float ds = d * scale;       // exact
+        const float neg32 = -32.0f * ds;  // exact
+#pragma unroll
+        for (int l4 = 0; l4 < 4; ++l4) {
+          const int l = 16 * half + 4 * l4;
+          const uint32_t lw = dw(64 * n + 32 * (qi & 1) + l);
+          const uint32_t hw = dw(128 + 32 * n + l);
+          const uint32_t q = ((lw >> (4 * (qi >> 1))) & 0x0f0f0f0fu) | (((hw >> (2 * qi)) & 0x03030303u) << 4);
+          const uint32_t e0 = 128 * n + 32 * qi + l;
+#pragma unroll
+          for (int m = 0; m < MM; ++m) {
+            const float4 x4 = *reinterpret_cast<const float4*>(x + m * n_in + e0);
+            const float xv[4] = {x4.x, x4.y, x4.z, x4.w};
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              const float v = fmaf(ds, static_cast<float>((q >> (8 * e)) & 0xffu), neg32);  // (d*scale)*(q-32)
+              acc[m] += v * xv[e];
+            }
+          }
+        }
+      }
+    }
+  }
+}
+
+// One lane per output row, 256 rows per workgroup; the activations of all MM rows in LDS; the
+// row's super-blocks double-buffered in registers, two per trip so the buffers swap roles
+// without copies, every fetch unconditional (clamped to the last column).
+template <int MM>
+__global__ __launch_bounds__(kThreads) void q6k_planar_kernel(MatvecArgs args, uint32_t n_in, size_t col_bytes) {
+  extern __shared__ __attribute__((aligned(16))) float xs[];  // [MM][n_in]
+  const uint32_t tid = threadIdx.x;
+  const uint32_t nsb = args.nb;
+  const MatvecSeg seg = args.seg[0];
+  const float4* x4 = reinterpret_cast<const float4*>(args.xq);
+  for (uint32_t i = tid; i < MM * n_in / 4; i += kThreads) reinterpret_cast<float4*>(xs)[i] = x4[i];
+  __syncthreads();
+  const uint32_t row = blockIdx.x * kThreads + tid;
+  if (row >= seg.n_out) return;
+  float acc[MM];
+#pragma unroll
+  for (int m = 0; m < MM; ++m) acc[m] = 0.0f;
+  const uint32_t last = nsb - 1;
+  auto col_at = [&](uint32_t c) { return seg.w + static_cast<size_t>(min(c, last)) * col_bytes; };
+  PlanarBlock a, b;
+  planar_fetch(col_at(0), seg.n_out, row, a);
+  for (uint32_t c = 0; c < nsb; c += 2) {
+    planar_fetch(col_at(c + 1), seg.n_out, row, b);
+    planar_superblock<MM>(a, xs + c * kQKK, n_in, acc);
+    planar_fetch(col_at(c + 2), seg.n_out, row, a);
+    if (c + 1 < nsb) planar_superblock<MM>(b, xs + (c + 1) * kQKK, n_in, acc);
+  }
+#pragma unroll
+  for (int m = 0; m < MM; ++m) seg.y[static_cast<size_t>(m) * seg.y_stride + row] = acc[m];
+}
+
 }  // namespace
+
+size_t q6k_planar_column_bytes(uint32_t n_out) {
+  return static_cast<size_t>(208) * n_out + ((static_cast<size_t>(2) * n_out + 15) & ~static_cast<size_t>(15));
+}
+
+int q6k_repack_launch(const uint8_t* src, uint8_t* dst, uint32_t n_out, uint32_t nsb) {
+  if (n_out == 0 || nsb == 0) return kOk;
+  if ((reinterpret_cast<uintptr_t>(src) & 1u) != 0 || (reinterpret_cast<uintptr_t>(dst) & 15u) != 0)
+    return fail(kInvalidArgument, "q6k_repack: native rows must be 2-byte and the planar copy 16-byte aligned");
+  const size_t total = static_cast<size_t>(n_out) * nsb;
+  hipLaunchKernelGGL(q6k_repack_kernel, dim3(static_cast<uint32_t>(ceil_div(total, 256))), dim3(256), 0, stream(), src,
+                     dst, n_out, nsb, q6k_planar_column_bytes(n_out));
+  return check_launch("q6k_repack");
+}
+
+int matvec_q6k_planar_launch(MatvecArgs& a, uint32_t n_in) {
+  const uint32_t n_out = a.seg[0].n_out;
+  if (a.m == 0 || n_out == 0) return kOk;
+  if (n_in % kQKK != 0) return fail(kInvalidArgument, "matmul_q6_k_planar: n_in %u is not a multiple of 256", n_in);
+  if ((reinterpret_cast<uintptr_t>(a.seg[0].w) & 15u) != 0 || (reinterpret_cast<uintptr_t>(a.xq) & 15u) != 0)
+    return fail(kInvalidArgument, "matmul_q6_k_planar: the planar weights and the activations must be 16-byte aligned");
+  const size_t col_bytes = q6k_planar_column_bytes(n_out);
+  const MatvecArgs base = a;
+  const float* x = reinterpret_cast<const float*>(a.xq);
+  const dim3 grid(static_cast<uint32_t>(ceil_div(n_out, kThreads)));
+  for (uint32_t done = 0; done < base.m;) {
+    uint32_t mm = std::min<uint32_t>(4, base.m - done);
+    while (mm > 1 && static_cast<size_t>(mm) * n_in * 4 > 65536) --mm;
+    const size_t lds = static_cast<size_t>(mm) * n_in * 4;
+    if (lds > 65536) return fail(kUnsupported, "matmul_q6_k_planar: n_in %u too large for LDS", n_in);
+    MatvecArgs g = base;
+    g.m = mm;
+    g.xq = reinterpret_cast<const uint8_t*>(x + static_cast<size_t>(done) * n_in);
+    g.seg[0].y = base.seg[0].y + static_cast<size_t>(done) * base.seg[0].y_stride;
+    switch (mm) {
+    case 4: launch(q6k_planar_kernel<4>, grid, dim3(kThreads), lds, g, n_in, col_bytes); break;
+    case 3: launch(q6k_planar_kernel<3>, grid, dim3(kThreads), lds, g, n_in, col_bytes); break;
+    case 2: launch(q6k_planar_kernel<2>, grid, dim3(kThreads), lds, g, n_in, col_bytes); break;
+    default: launch(q6k_planar_kernel<1>, grid, dim3(kThreads), lds, g, n_in, col_bytes); break;
+    }
+    const int rc = check_launch("q6k_planar");
+    if (rc != kOk) return rc;
+    done += mm;
+  }
+  return kOk;
+}
 
 int matvec_q6k_launch(MatvecArgs& a, uint32_t n_in) {
   const uint32_t n_out = a.seg[0].n_out;

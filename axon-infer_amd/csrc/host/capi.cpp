@@ -62,6 +62,7 @@ int axon_model_load(const char* path, const axon_model_options* options, axon_mo
     if (options->cache_type != 0 && options->cache_type != 1)
       return fail("cache_type: expected 0 (F32) or 1 (F16), found " + std::to_string(options->cache_type));
     o.cache = options->cache_type == 1 ? axon::model::CacheType::F16 : axon::model::CacheType::F32;
+    o.repack = options->no_repack == 0;
     if (options->kernels != nullptr && !axon::kernels::parse_kernel_set(options->kernels, o.kernels))
       return fail(std::string("kernels: expected auto, scalar, neon or hip, found '") + options->kernels + "'");
   }

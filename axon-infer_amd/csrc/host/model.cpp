@@ -233,6 +233,19 @@ Expected<std::unique_ptr<LlamaModel>> LlamaModel::load(const std::string& path, 
   }
   if (c.tie_embeddings) m->output_ = m->token_embd_;
   m->device_bytes_ = total;
+  // The one-time repack of the Q6_K output matrix (the f2 row of the build plan): planes of
+  // aligned 16-byte slices, checked against the native blocks by dequantization in the tests.
+  if (options.repack && m->output_.type == DType::Q6_K) {
+    const std::size_t pb = axon_hip_q6k_planar_bytes(m->output_.ne1, m->output_.ne0);
+    if (pb != 0) {
+      if (axon_hip_malloc(&m->planar_, pb) != AXON_HIP_OK ||
+          axon_hip_q6k_repack(m->output_.dev, m->output_.ne1, m->output_.ne0, m->planar_) != AXON_HIP_OK ||
+          axon_hip_synchronize() != AXON_HIP_OK)
+        return m->device_error("Q6_K repack");
+      m->output_.planar = m->planar_;
+      m->device_bytes_ += pb;
+    }
+  }
 
   // cos/sin table [pos][rotary_dim/2], evaluated in double with the host libm exactly as
   // src/kernels/ref/rope.cpp:19-26 does, then rounded to float.
@@ -318,7 +331,7 @@ LlamaModel::~LlamaModel() {
                   static_cast<void*>(up_), static_cast<void*>(tmp_), static_cast<void*>(logits_),
                   static_cast<void*>(scores_), static_cast<void*>(argmax_scratch_), static_cast<void*>(ids_), cand_, window_,
                   xq_, rowinfo_, kv_, static_cast<void*>(kv_free_),
-                  static_cast<void*>(rope_table_), weights_}) {
+                  static_cast<void*>(rope_table_), weights_, planar_}) {
     if (p != nullptr) axon_hip_free(p);
   }
   if (rowinfo_host_ != nullptr) axon_hip_host_free(rowinfo_host_);
@@ -459,6 +472,11 @@ int LlamaModel::mm(const Tensor& w, const float* x, const void* xq, float* y, st
     break;
   }
   case DType::Q6_K: {
+    if (w.planar != nullptr) {
+      const int rc = axon_hip_matmul_q6_k_planar(w.planar, x, out, n, n_out, n_in, n_out);
+      if (rc != AXON_HIP_OK) return rc;
+      break;
+    }
     const auto* p = static_cast<const BlockQ6_K*>(w.dev);
     one ? k.matmul_q6_k(p, x, out, n_out, n_in) : k.matmul_q6_k_rows(p, x, out, n, n_out, n_in, n_out);
     break;

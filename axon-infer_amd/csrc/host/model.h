@@ -38,6 +38,9 @@ struct LoadOptions {
   bool exact_activations = false;
   kernels::KernelSet kernels = kernels::KernelSet::Hip;
   CacheType cache = CacheType::F32;  // llama.h:40-42
+  // Repack Q6_K matmul weights (the output matrix) at upload into 16-byte-aligned planes; the
+  // native blocks stay for the embedding lookup and the table's entries.
+  bool repack = true;
 };
 
 struct Config {
@@ -58,6 +61,7 @@ struct Tensor {
   std::size_t row_bytes = 0, total_bytes = 0;
   const std::byte* host = nullptr;
   void* dev = nullptr;
+  void* planar = nullptr;  // Q6_K: the repacked copy the matmuls stream (axon_hip_q6k_repack)
 };
 
 struct Layer {
@@ -194,6 +198,7 @@ private:
 
   // Device memory.
   void* weights_ = nullptr;
+  void* planar_ = nullptr;  // the repacked Q6_K output matrix
   float* rope_table_ = nullptr;
   void* kv_ = nullptr;        // n_slots_ cache slots of slot_elems_ elements (float or fp16)
   float* kv_free_ = nullptr;  // the cache-free forward's keys and values: float, max_seq positions

@@ -495,7 +495,7 @@ def main() -> int:
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
                      "launches": launches, "bytes_per_launch": round(nbytes / max(launches, 1)),
                      "avg_us": round(1e3 * ms / max(launches, 1), 3)},
-        "roofline_q6_k": {"kernel": "matvec_q6k_kernel<1> (tied output, 128256 x 2048)",
+        "roofline_q6_k": {"kernel": "q6k_planar_kernel<1> (tied output, 128256 x 2048, repacked at upload)",
                           "achieved": round(q6_gbs, 1), "frac": round(q6_gbs / HBM_PEAK_GBS, 4),
                           "avg_us": round(1e3 * q6_ms / max(q6_n, 1), 3)},
         "prefill_tokens_per_s": round(b1["prefill_tokens_per_s"], 1),

@@ -150,6 +150,19 @@ int axon_hip_matmul_q6_k_rows(const void* w, const float* x, float* y, size_t n_
 
 /* ---- Coarse entries of the device-resident forward pass --------------------------------- */
 
+/* The one-time repack of a Q6_K matrix at upload (the GGUF block layout, src/core/dtype.h
+ * BlockQ6_K, turned into 16-byte-aligned planes; no counterpart in the reference, which reads
+ * the blocks in place). Super-block column c of the [n_out][n_in/256] matrix becomes 13 slices
+ * [n_out][16 bytes] (slice s: bytes 16s..16s+15 of each row's block: ql, qh, scales), then the
+ * d plane [n_out] of halves padded to 16 bytes. planar_bytes: the copy's size (0 for an n_in
+ * that is not a multiple of 256). repack: w (2-byte aligned) into planar (16-byte aligned). */
+size_t axon_hip_q6k_planar_bytes(size_t n_out, size_t n_in);
+int axon_hip_q6k_repack(const void* w, size_t n_out, size_t n_in, void* planar);
+/* matmul_q6_k_rows (kernels.h:125-128) over the planar copy: the same outputs, bit for bit.
+ * x 16-byte aligned. */
+int axon_hip_matmul_q6_k_planar(const void* planar, const float* x, float* y, size_t n_rows, size_t n_out,
+                                size_t n_in, size_t y_stride);
+
 /* rmsnorm over rows (src/model/llama.cpp:128-134), writing y, its Q8_0 blocks (the next
  * matmul's input, llama.cpp:399-417), or both (either may be NULL). */
 int axon_hip_rmsnorm_rows(const float* x, const float* weight, float* y, void* yq, size_t n, size_t n_rows,

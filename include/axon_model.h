@@ -32,6 +32,9 @@ typedef struct {
   /* LoadOptions::cache (src/model/llama.h:40-42, CacheType src/model/config.h:16): 0 F32, 1 F16
    * (keys and values rounded once into an fp16 cache; the cache-free forward stays float). */
   int cache_type;
+  /* 1: keep the Q6_K output matrix in its GGUF blocks only. 0 (default): also repack it at upload
+   * into 16-byte-aligned planes (axon_hip_q6k_repack) that its matmuls stream; same logits. */
+  int no_repack;
 } axon_model_options;
 
 typedef struct {

@@ -1,0 +1,155 @@
+"""The one-time repack of Q6_K weights at upload (axon_hip_q6k_repack) and the matmul over the
+repacked planes (axon_hip_matmul_q6_k_planar): the step before the path, turning the GGUF blocks
+(BlockQ6_K, src/core/dtype.h; dequantize_block_q6_k, src/core/dtype.cpp:313-336) into 16-byte
+aligned planes for the device.
+
+* The planes are checked against the native block bytes by dequantization: a NumPy dequantizer
+  that reads the documented planar layout directly (13 slices [rows][16 bytes] per super-block
+  column, then the d plane) gives the oracle's dequantization of the native blocks, float for
+  float; the oracle's dequantizer is pinned to the reference's by its fixture.
+* The planar matmul equals the oracle's matmul_q6_k bit for bit (one row and several, strided
+  outputs), and the native stream kernel on the Llama-3 output shape.
+* A model's logits are the same with and without the repack."""
+from dataclasses import replace
+
+import numpy as np
+import pytest
+
+from helpers import Q6_K
+from tables import CTable, HipTable, dequantize, random_floats, random_weights
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def H():
+    HipTable()
+    import axon_hip
+    import ctypes as C
+    axon_hip.lib().axon_hip_q6k_planar_bytes.restype = C.c_size_t
+    return axon_hip
+
+
+@pytest.fixture(scope="module")
+def o():
+    return CTable("oracle")
+
+
+def q6k_weights(n_out, n_in, seed):
+    w = random_weights("q6_k", n_out, n_in, seed)
+    rng = np.random.default_rng(seed + 1)
+    w["d"] = rng.uniform(1e-4, 4e-3, len(w)).astype(np.float16).view(np.uint16)  # a scale per block
+    return w
+
+
+def repack(H, w, n_out, n_in, native_offset=0):
+    import ctypes as C
+    nbytes = H.lib().axon_hip_q6k_planar_bytes(C.c_size_t(n_out), C.c_size_t(n_in))
+    src = H.DeviceBuffer(w.nbytes + native_offset)
+    src.upload(w.view(np.uint8), native_offset)
+    dst = H.DeviceBuffer(nbytes)
+    H.call("q6k_repack", src.at(native_offset), n_out, n_in, dst)
+    return dst, nbytes
+
+
+def dequantize_planar(planar: np.ndarray, n_out: int, n_in: int) -> np.ndarray:
+    """The planar layout read back as weights: per column, slices 0-7 are ql, 8-11 qh, 12 the
+    int8 scales, then the d plane; values d * scale * (q - 32) in float."""
+    nsb = n_in // 256
+    col = 208 * n_out + ((2 * n_out + 15) // 16) * 16
+    out = np.zeros((n_out, n_in), np.float32)
+    for c in range(nsb):
+        reg = planar[c * col:(c + 1) * col]
+        sl = reg[:208 * n_out].reshape(13, n_out, 16)
+        ql = sl[0:8].transpose(1, 0, 2).reshape(n_out, 128)
+        qh = sl[8:12].transpose(1, 0, 2).reshape(n_out, 64)
+        sc = sl[12].view(np.int8).astype(np.float32)
+        d = reg[208 * n_out:208 * n_out + 2 * n_out].view(np.float16).astype(np.float32)
+        y = out[:, 256 * c:256 * (c + 1)]
+        for n in range(2):
+            lq, hq, s = ql[:, 64 * n:64 * n + 64], qh[:, 32 * n:32 * n + 32], sc[:, 8 * n:8 * n + 8]
+            l = np.arange(32)
+            iss = l // 16
+            parts = [((lq[:, l] & 15) | ((hq[:, l] & 3) << 4), 0), ((lq[:, l + 32] & 15) | (((hq[:, l] >> 2) & 3) << 4), 2),
+                     ((lq[:, l] >> 4) | (((hq[:, l] >> 4) & 3) << 4), 4), ((lq[:, l + 32] >> 4) | (((hq[:, l] >> 6) & 3) << 4), 6)]
+            for k, (q, so) in enumerate(parts):
+                ds = d[:, None] * s[:, iss + so]
+                y[:, 128 * n + 32 * k + l] = ds * (q.astype(np.int32) - 32).astype(np.float32)
+    return out
+
+
+@pytest.mark.parametrize("n_out, n_in", [(8, 256), (13, 512), (1000, 2048), (77, 4096)])
+def test_repack_dequantizes_as_the_native_blocks(H, n_out, n_in):
+    w = q6k_weights(n_out, n_in, n_out + n_in)
+    for off in (0, 2):  # native rows at a 2-byte (not 4-byte) boundary too
+        dst, nbytes = repack(H, w, n_out, n_in, off)
+        planar = dst.download(np.uint8, nbytes)
+        got = dequantize_planar(planar, n_out, n_in)
+        want = dequantize("q6_k", w, n_out, n_in)
+        assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+
+
+@pytest.mark.parametrize("n_out, n_in", [(13, 256), (1000, 2048), (4096, 4096), (300, 8192)])
+@pytest.mark.parametrize("n_rows", [1, 3, 4, 6, 9])
+def test_planar_matmul_bit_exact(H, o, n_out, n_in, n_rows):
+    w = q6k_weights(n_out, n_in, 3 * n_out + n_rows)
+    x = random_floats(n_rows * n_in, n_in + n_rows)
+    dst, _ = repack(H, w, n_out, n_in)
+    stride = n_out + 1 if n_rows > 1 else n_out
+    dx = H.DeviceBuffer.of(x)
+    dy = H.DeviceBuffer.of(np.full(n_rows * stride, np.float32(-7.25), np.float32))
+    H.call("matmul_q6_k_planar", dst, dx, dy, n_rows, n_out, n_in, stride)
+    got = dy.download(np.float32, n_rows * stride)
+    want = o.matmul("q6_k", w, x, n_out, n_in, n_rows=n_rows, y_stride=stride)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+
+
+def test_planar_matmul_equals_the_stream_kernel_on_the_output_shape(H):
+    n_out, n_in = 128256, 2048
+    w = q6k_weights(n_out, n_in, 5)
+    dst, _ = repack(H, w, n_out, n_in)
+    dw = H.DeviceBuffer.of(w)
+    for n_rows in (1, 4, 5):
+        x = random_floats(n_rows * n_in, 40 + n_rows)
+        dx = H.DeviceBuffer.of(x)
+        a = H.DeviceBuffer(4 * n_rows * n_out)
+        b = H.DeviceBuffer(4 * n_rows * n_out)
+        H.call("matmul_q6_k_planar", dst, dx, a, n_rows, n_out, n_in, n_out)
+        H.call("matmul_q6_k_rows", dw, dx, b, n_rows, n_out, n_in, n_out)
+        assert np.array_equal(a.download(np.uint32, n_rows * n_out), b.download(np.uint32, n_rows * n_out))
+
+
+def test_planar_bounds(H):
+    import ctypes as C
+    assert H.lib().axon_hip_q6k_planar_bytes(C.c_size_t(10), C.c_size_t(300)) == 0
+    assert H.lib().axon_hip_q6k_planar_bytes(C.c_size_t(8), C.c_size_t(512)) == 2 * 8 * 210
+    assert H.lib().axon_hip_q6k_planar_bytes(C.c_size_t(9), C.c_size_t(256)) == 208 * 9 + 32
+    buf = H.DeviceBuffer(4096)
+    with pytest.raises(H.HipError, match="multiple of 256"):
+        H.call("q6k_repack", buf, 4, 300, buf)
+    with pytest.raises(H.HipError, match="aligned"):
+        H.call("q6k_repack", buf.at(1), 1, 256, buf)
+    with pytest.raises(H.HipError, match="aligned"):
+        H.call("matmul_q6_k_planar", buf.at(8), buf, buf, 1, 1, 256, 1)
+
+
+def test_model_logits_unchanged_by_the_repack(H, tmp_path_factory):
+    """The config-4 shape (tied Q6_K output) at 2 layers and a 2048-token vocabulary: the same
+    logits bit for bit with and without the repacked output matrix, for a prefill and a batch."""
+    import synth
+    spec = replace(synth.CONFIGS["c4"], name="t-c4-repack-2l", n_layer=2, n_vocab=2048, seed=17)
+    path = synth.cached_model(spec, tmp_path_factory.mktemp("models"))
+    toks = np.random.default_rng(3).integers(0, 2048, 21).astype(np.int32)
+    out = []
+    for repack_on in (True, False):
+        m = H.Model(path, max_seq=32, max_ctx=64, max_batch=3, max_caches=4, repack=repack_on)
+        c = m.new_cache()
+        a = m.forward_prefill(c, toks[:13])
+        cs = [c, m.new_cache(), m.new_cache()]
+        m.forward_prefill(cs[1], toks[13:17])
+        m.forward_prefill(cs[2], toks[17:18])
+        b = m.forward_batch(cs, toks[18:21])
+        out.append((a, b, m.info.device_bytes))
+        m.close()
+    assert np.array_equal(out[0][0], out[1][0]) and np.array_equal(out[0][1], out[1][1])
+    assert out[0][2] - out[1][2] == 2048 * 2048 // 256 * 210
