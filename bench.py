@@ -331,7 +331,7 @@ def traffic_summary(fetch_csv, write_csv):
     """Per-dispatch FETCH_SIZE and WRITE_SIZE (KiB) of the Q4_0 decode matvec, each scaled by
     the counter's reading for the calibration copy (COPY_BYTES read and written)."""
     def per_kernel(path, counter):
-        copy, mv = [], []
+        copy, mv, q6 = [], [], []
         for name, cname, value in _counter_rows(path):
             if cname != counter:
                 continue
@@ -339,11 +339,13 @@ def traffic_summary(fetch_csv, write_csv):
                 copy.append(value)
             elif any(k in name.replace(" ", "") for k in MATVEC_KERNELS):
                 mv.append(value)
+            elif "q6k_planar_kernel<1>" in name.replace(" ", ""):
+                q6.append(value)
         if not copy or not mv:
             raise SystemExit(f"{path}: no {counter} rows for the copy ({len(copy)}) or {'/'.join(MATVEC_KERNELS)} ({len(mv)})")
-        return max(copy), mv
-    fcopy, fmv = per_kernel(fetch_csv, "FETCH_SIZE")
-    wcopy, wmv = per_kernel(write_csv, "WRITE_SIZE")
+        return max(copy), mv, q6
+    fcopy, fmv, fq6 = per_kernel(fetch_csv, "FETCH_SIZE")
+    wcopy, wmv, wq6 = per_kernel(write_csv, "WRITE_SIZE")
     f_scale = COPY_BYTES / (fcopy * 1024.0)
     w_scale = COPY_BYTES / (wcopy * 1024.0)
     fetch = float(np.mean(fmv)) * 1024.0 * f_scale
@@ -354,6 +356,10 @@ def traffic_summary(fetch_csv, write_csv):
            "copy_bytes": COPY_BYTES, "copy_fetch_kib": fcopy, "copy_write_kib": wcopy,
            "fetch_scale": round(f_scale, 4), "write_scale": round(w_scale, 4),
            "counters": [str(fetch_csv), str(write_csv)]}
+    if fq6 and wq6:  # the Q6_K output matvec over the planar copy, for comparison
+        out["q6k_planar_kernel<1>"] = {"dispatches": len(fq6),
+                                       "traffic_bytes_per_launch": round(float(np.mean(fq6)) * 1024.0 * f_scale +
+                                                                         float(np.mean(wq6)) * 1024.0 * w_scale)}
     TRAFFIC_FILE.write_text(json.dumps(out, indent=1) + "\n")
     print(json.dumps(out))
     return 0
