@@ -65,8 +65,10 @@ int ready() {
 bool fits_u32(size_t v) { return v <= 0xffffffffull; }
 
 // The Q8_0-activation path: groups of up to four rows on the dot4 matvec below 5 rows, the
-// few-rows MFMA kernel (every segment in one launch) from 5 to 64 rows, 64 x 64 MFMA tiles
-// beyond. All of them give the same bits for a row.
+// few-rows MFMA kernel (every segment in one launch) from 5 to 64 rows, the tile MFMA kernel
+// (every segment in one launch) beyond; rows whose bases or lengths do not suit their dword
+// loads take the staged 64 x 64 MFMA tiles or the dot4 groups. All of them give the same bits
+// for a row.
 int q8_matmul(int type, const void* xq, size_t n_rows, size_t n_in, size_t n_seg, const void* const* w,
               float* const* y, const size_t* n_out, const size_t* y_stride, int accumulate) {
   if (n_in % kQK != 0) return fail(kInvalidArgument, "quantized matmul: n_in %zu is not a multiple of 32", n_in);
@@ -80,7 +82,7 @@ int q8_matmul(int type, const void* xq, size_t n_rows, size_t n_in, size_t n_seg
   if (n_rows == 0) return kOk;
   const uint32_t nb = static_cast<uint32_t>(n_in / kQK);
   const size_t xrow = static_cast<size_t>(nb) * kBytesQ8_0;
-  if (n_rows >= 5 && n_rows <= kRowsMaxM) {
+  if (n_rows >= 5) {
     MatvecArgs a{};
     for (size_t s = 0; s < n_seg; ++s) {
       a.seg[s] = MatvecSeg{static_cast<const uint8_t*>(w[s]), y[s], static_cast<uint32_t>(n_out[s]),
@@ -91,7 +93,8 @@ int q8_matmul(int type, const void* xq, size_t n_rows, size_t n_in, size_t n_seg
     a.nb = nb;
     a.m = static_cast<uint32_t>(n_rows);
     a.accumulate = accumulate;
-    if (matmul_q8_rows_fits(type, a)) return matmul_q8_rows_launch(type, a);
+    if (n_rows <= kRowsMaxM && matmul_q8_rows_fits(type, a)) return matmul_q8_rows_launch(type, a);
+    if (n_rows > kRowsMaxM && matmul_q8_rows_fits(type, a, true)) return matmul_q8_tile_launch(type, a);
   }
   if (n_rows >= 16) {
     for (size_t s = 0; s < n_seg; ++s) {

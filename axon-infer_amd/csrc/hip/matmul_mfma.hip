@@ -392,6 +392,268 @@ __global__ __launch_bounds__(kThreads) void mfma_rows_kernel(MatvecArgs args) {
   }
 }
 
+// ---- Many activation rows (prefill, mixed passes): 65 rows and more ------------------------
+// A workgroup owns TN weight rows x 64 activation rows; wave w owns activation rows
+// 16w..16w+15 against all TN weight rows, so each MFMA runs once and the wave that ran it folds
+// its four results: per block a lane folds TN/16 x 4 outputs, with one float4 of activation
+// scales and TN/16 weight scales from LDS. The K chunks (kTileChunk blocks) load into registers
+// while the previous chunk computes and expand into aligned int8 in LDS as in mfma_rows_kernel;
+// the scales sit block-major ([block][row], padded) so a lane's four activation scales are one
+// 16-byte read. Every segment of the call is one grid. The per-output order is the scalar
+// table's: block after block, acc += float(sumi) * d_w * d_x (+ m_w * d_x * float(sumx), Q4_1).
+constexpr uint32_t kTileChunk = 16;
+constexpr uint32_t kTilePitch = kTileChunk * 8 + 4;  // dwords per expanded row
+constexpr uint32_t kTileRows = 64;
+
+template <uint32_t TN>
+__host__ __device__ constexpr uint32_t tile_wp() { return TN + 4; }  // scale pitch, weights
+__host__ __device__ constexpr uint32_t tile_xp() { return kTileRows + 4; }  // scale pitch, activations
+
+template <int T, uint32_t TN>
+__host__ __device__ constexpr size_t tile_lds() {
+  const size_t scales = static_cast<size_t>(kTileChunk) * (tile_wp<TN>() + tile_xp()) * (T == Q4_1 ? 2 : 1);
+  return (static_cast<size_t>(TN + kTileRows) * kTilePitch + scales) * 4;
+}
+
+template <int T, uint32_t TN>
+__global__ __launch_bounds__(kThreads) void mfma_tile_kernel(MatvecArgs args) {
+  constexpr int bs = block_bytes<T>();
+  constexpr uint32_t TM = kTileRows, KC = kTileChunk, P = kTilePitch;
+  constexpr uint32_t WP = tile_wp<TN>(), XP = tile_xp();
+  constexpr uint32_t NT = TN / 16;                      // weight sub-tiles per wave
+  constexpr uint32_t WI = TN * KC / kThreads;           // weight items per thread per chunk
+  constexpr uint32_t XI = TM * KC / kThreads;           // activation items per thread per chunk
+  constexpr uint32_t WD = item_dwords<T>(), XD = item_dwords<Q8_0>();
+  static_assert(TN * KC % kThreads == 0 && TM * KC % kThreads == 0, "whole items per thread");
+
+  extern __shared__ __attribute__((aligned(16))) uint32_t lds_tile[];
+  uint32_t* wa = lds_tile;                               // [TN][P]
+  uint32_t* xa = wa + TN * P;                            // [TM][P]
+  float* wd = reinterpret_cast<float*>(xa + TM * P);     // [KC][WP]
+  float* xd = wd + KC * WP;                              // [KC][XP]
+  float* wmn = xd + KC * XP;                             // [KC][WP] (Q4_1)
+  int32_t* xs = reinterpret_cast<int32_t*>(wmn + KC * WP);  // [KC][XP] (Q4_1)
+
+  const uint32_t tid = threadIdx.x;
+  const uint32_t lane = tid & 63;
+  const uint32_t wave = tid >> 6;
+  int s = 0;
+  if (args.n_seg > 1 && blockIdx.x >= args.seg[1].wg_begin) s = 1;
+  if (args.n_seg > 2 && blockIdx.x >= args.seg[2].wg_begin) s = 2;
+  const MatvecSeg seg = args.seg[s];
+  const uint32_t n0 = (blockIdx.x - seg.wg_begin) * TN;
+  const uint32_t m0 = blockIdx.y * TM;
+  const uint32_t nn = min(TN, seg.n_out - n0);
+  const uint32_t mm = min(TM, args.m - m0);
+  const uint32_t nb = args.nb;
+  const uint32_t n_chunks = (nb + KC - 1) / KC;
+  const uint32_t w_pitch = nb * bs, x_pitch = nb * kBytesQ8_0;
+  const __amdgpu_buffer_rsrc_t wsrc = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<uint8_t*>(seg.w) + static_cast<size_t>(n0) * w_pitch, 0, static_cast<int>(nn * w_pitch),
+      static_cast<int>(kRawBufferWord3));
+  const __amdgpu_buffer_rsrc_t xsrc = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<uint8_t*>(args.xq) + static_cast<size_t>(m0) * x_pitch, 0, static_cast<int>(mm * x_pitch),
+      static_cast<int>(kRawBufferWord3));
+
+  struct Raw {
+    uint32_t w[WI][WD];
+    uint32_t x[XI][XD];
+  };
+  // Item i of a chunk: block i % KC of row i / KC (consecutive threads, consecutive blocks).
+  auto load = [&](uint32_t c, Raw& r) {
+    const uint32_t b0 = c * KC;
+#pragma unroll
+    for (uint32_t k = 0; k < WI; ++k) {
+      const uint32_t i = tid + k * kThreads;
+      const uint32_t row = i / KC, b = i - row * KC;
+      const uint32_t off = row * w_pitch + (b0 + b) * bs;
+#pragma unroll
+      for (uint32_t d = 0; d < WD; ++d)
+        r.w[k][d] = __builtin_amdgcn_raw_buffer_load_b32(wsrc, (off & ~3u) + 4 * d, 0, 0);
+    }
+#pragma unroll
+    for (uint32_t k = 0; k < XI; ++k) {
+      const uint32_t i = tid + k * kThreads;
+      const uint32_t row = i / KC, b = i - row * KC;
+      const uint32_t off = row * x_pitch + (b0 + b) * kBytesQ8_0;
+#pragma unroll
+      for (uint32_t d = 0; d < XD; ++d)
+        r.x[k][d] = __builtin_amdgcn_raw_buffer_load_b32(xsrc, (off & ~3u) + 4 * d, 0, 0);
+    }
+  };
+  auto expand = [&](uint32_t c, const Raw& r) {
+    const uint32_t b0 = c * KC;
+#pragma unroll
+    for (uint32_t k = 0; k < WI; ++k) {
+      const uint32_t i = tid + k * kThreads;
+      const uint32_t row = i / KC, b = i - row * KC;
+      const uint32_t sh = (((b0 + b) * bs) & 3u) * 8;
+      uint32_t v[WD];
+#pragma unroll
+      for (uint32_t d = 0; d < WD; ++d) v[d] = __builtin_amdgcn_alignbit(d + 1 < WD ? r.w[k][d + 1] : 0u, r.w[k][d], sh);
+      uint32_t q[8];
+      if constexpr (T == Q8_0) {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) q[j] = __builtin_amdgcn_alignbit(v[j + 1], v[j], 16);
+      } else {
+        constexpr uint32_t first = T == Q4_0 ? 0 : 1;
+        constexpr uint32_t bsh = T == Q4_0 ? 16 : 0;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const uint32_t n4 = bsh ? __builtin_amdgcn_alignbit(v[first + j + 1], v[first + j], bsh) : v[first + j];
+          q[j] = n4 & 0x0f0f0f0fu;
+          q[j + 4] = (n4 >> 4) & 0x0f0f0f0fu;
+          if constexpr (T == Q4_0) {  // q - 8 per byte (no carry crosses bytes)
+            q[j] = (q[j] + 0x78787878u) ^ 0x80808080u;
+            q[j + 4] = (q[j + 4] + 0x78787878u) ^ 0x80808080u;
+          }
+        }
+      }
+      uint4* dst = reinterpret_cast<uint4*>(wa + row * P + b * 8);
+      dst[0] = make_uint4(q[0], q[1], q[2], q[3]);
+      dst[1] = make_uint4(q[4], q[5], q[6], q[7]);
+      wd[b * WP + row] = half_bits_to_float(v[0] & 0xffffu);
+      if constexpr (T == Q4_1) wmn[b * WP + row] = half_bits_to_float(v[0] >> 16);
+    }
+#pragma unroll
+    for (uint32_t k = 0; k < XI; ++k) {
+      const uint32_t i = tid + k * kThreads;
+      const uint32_t row = i / KC, b = i - row * KC;
+      const uint32_t sh = (((b0 + b) * kBytesQ8_0) & 3u) * 8;
+      uint32_t v[XD];
+#pragma unroll
+      for (uint32_t d = 0; d < XD; ++d) v[d] = __builtin_amdgcn_alignbit(d + 1 < XD ? r.x[k][d + 1] : 0u, r.x[k][d], sh);
+      uint32_t q[8];
+      int32_t sum = 0;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        q[j] = __builtin_amdgcn_alignbit(v[j + 1], v[j], 16);
+        if constexpr (T == Q4_1) sum = __builtin_amdgcn_sdot4(static_cast<int32_t>(q[j]), 0x01010101, sum, false);
+      }
+      uint4* dst = reinterpret_cast<uint4*>(xa + row * P + b * 8);
+      dst[0] = make_uint4(q[0], q[1], q[2], q[3]);
+      dst[1] = make_uint4(q[4], q[5], q[6], q[7]);
+      xd[b * XP + row] = half_bits_to_float(v[0] & 0xffffu);
+      if constexpr (T == Q4_1) xs[b * XP + row] = sum;
+    }
+  };
+
+  const uint32_t col = lane & 15;  // weight row within a 16-row sub-tile; A row within the wave's 16
+  const uint32_t kq = lane >> 4;   // which 8 of a block's 32 elements this lane feeds
+  const uint32_t arow = 16 * wave + col;        // the A operand row (activation row in the tile)
+  const uint32_t orow = 16 * wave + 4 * kq;     // the lane's output rows: orow .. orow + 3
+  float acc[NT][4];
+#pragma unroll
+  for (uint32_t j = 0; j < NT; ++j)
+#pragma unroll
+    for (int v = 0; v < 4; ++v) acc[j][v] = 0.0f;
+
+  constexpr uint32_t kBatch = 4;  // blocks whose MFMAs are issued before their folds
+  static_assert(KC % kBatch == 0, "whole batches");
+  auto block_sums = [&](uint32_t b, i32x4 (&d)[NT]) {
+    const uint2 xq = *reinterpret_cast<const uint2*>(xa + arow * P + b * 8 + 2 * kq);
+    const int64_t ax = static_cast<int64_t>((static_cast<uint64_t>(xq.y) << 32) | xq.x);
+#pragma unroll
+    for (uint32_t j = 0; j < NT; ++j) {
+      const uint2 wq = *reinterpret_cast<const uint2*>(wa + (16 * j + col) * P + b * 8 + 2 * kq);
+      const int64_t bw = static_cast<int64_t>((static_cast<uint64_t>(wq.y) << 32) | wq.x);
+      i32x4 z = {0, 0, 0, 0};
+      d[j] = __builtin_amdgcn_mfma_i32_16x16x32_i8(ax, bw, z, 0, 0, 0);
+    }
+  };
+  auto block_fold = [&](uint32_t b, const i32x4 (&d)[NT]) {
+    const float4 dx = *reinterpret_cast<const float4*>(xd + b * XP + orow);
+    const float dxv[4] = {dx.x, dx.y, dx.z, dx.w};
+    int4 sx = make_int4(0, 0, 0, 0);
+    if constexpr (T == Q4_1) sx = *reinterpret_cast<const int4*>(xs + b * XP + orow);
+    const int32_t sxv[4] = {sx.x, sx.y, sx.z, sx.w};
+#pragma unroll
+    for (uint32_t j = 0; j < NT; ++j) {
+      const float dw = wd[b * WP + 16 * j + col];
+      float mw = 0.0f;
+      if constexpr (T == Q4_1) mw = wmn[b * WP + 16 * j + col];
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        if constexpr (T == Q4_1) {
+          acc[j][v] += static_cast<float>(d[j][v]) * dw * dxv[v] + mw * dxv[v] * static_cast<float>(sxv[v]);
+        } else {
+          acc[j][v] += static_cast<float>(d[j][v]) * dw * dxv[v];
+        }
+      }
+    }
+  };
+
+  Raw r;
+  load(0, r);
+  for (uint32_t c = 0; c < n_chunks; ++c) {
+    const uint32_t cb = min(KC, nb - c * KC);
+    expand(c, r);
+    __syncthreads();
+    if (c + 1 < n_chunks) load(c + 1, r);
+    if (cb == KC) {
+      for (uint32_t b0 = 0; b0 < KC; b0 += kBatch) {
+        i32x4 d[kBatch][NT];
+#pragma unroll
+        for (uint32_t k = 0; k < kBatch; ++k) block_sums(b0 + k, d[k]);
+#pragma unroll
+        for (uint32_t k = 0; k < kBatch; ++k) block_fold(b0 + k, d[k]);
+      }
+    } else {
+      for (uint32_t b = 0; b < cb; ++b) {
+        i32x4 d[NT];
+        block_sums(b, d);
+        block_fold(b, d);
+      }
+    }
+    __syncthreads();
+  }
+
+#pragma unroll
+  for (uint32_t j = 0; j < NT; ++j) {
+    if (16 * j + col < nn) {
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        const uint32_t rr = orow + v;
+        if (rr < mm) {
+          float* y = seg.y + static_cast<size_t>(m0 + rr) * seg.y_stride + n0 + 16 * j + col;
+          *y = args.accumulate ? *y + acc[j][v] : acc[j][v];
+        }
+      }
+    }
+  }
+}
+
+template <uint32_t TN>
+int tile_launch(int type, MatvecArgs& a) {
+  uint32_t wg = 0;
+  for (int s = 0; s < a.n_seg; ++s) {
+    a.seg[s].wg_begin = wg;
+    wg += static_cast<uint32_t>(ceil_div(a.seg[s].n_out, TN));
+  }
+  const dim3 grid(wg, static_cast<uint32_t>(ceil_div(a.m, kTileRows)));
+  // Dynamic LDS above 64 KB is granted per kernel, once.
+  static const bool granted = [] {
+    bool ok = true;
+    auto grant = [&](auto kernel, size_t lds) {
+      if (lds > 65536)
+        ok = ok && hipFuncSetAttribute(reinterpret_cast<const void*>(kernel), hipFuncAttributeMaxDynamicSharedMemorySize,
+                                       static_cast<int>(lds)) == hipSuccess;
+    };
+    grant(mfma_tile_kernel<Q8_0, TN>, tile_lds<Q8_0, TN>());
+    grant(mfma_tile_kernel<Q4_0, TN>, tile_lds<Q4_0, TN>());
+    grant(mfma_tile_kernel<Q4_1, TN>, tile_lds<Q4_1, TN>());
+    return ok;
+  }();
+  if (!granted) return fail(kUnsupported, "matmul tile: the LDS grant was refused");
+  switch (type) {
+  case Q8_0: launch(mfma_tile_kernel<Q8_0, TN>, grid, dim3(kThreads), tile_lds<Q8_0, TN>(), a); break;
+  case Q4_0: launch(mfma_tile_kernel<Q4_0, TN>, grid, dim3(kThreads), tile_lds<Q4_0, TN>(), a); break;
+  case Q4_1: launch(mfma_tile_kernel<Q4_1, TN>, grid, dim3(kThreads), tile_lds<Q4_1, TN>(), a); break;
+  default: return fail(kUnsupported, "matmul tile: weight type %d", type);
+  }
+  return check_launch("mfma_tile");
+}
+
 template <int TM>
 int rows_launch(int type, MatvecArgs& a) {
   uint32_t wg = 0;
@@ -413,8 +675,8 @@ int rows_launch(int type, MatvecArgs& a) {
 
 }  // namespace
 
-bool matmul_q8_rows_fits(int type, const MatvecArgs& a) {
-  if (a.m < 1 || a.m > kRowsMaxM || a.nb == 0) return false;
+bool matmul_q8_rows_fits(int type, const MatvecArgs& a, bool many_rows) {
+  if (a.m < 1 || (!many_rows && a.m > kRowsMaxM) || a.nb == 0) return false;
   if (type != Q8_0 && type != Q4_0 && type != Q4_1) return false;
   const uint32_t bs = type == Q8_0 ? kBytesQ8_0 : type == Q4_0 ? kBytesQ4_0 : kBytesQ4_1;
   // Dword loads: every weight row and activation row starts on a 4-byte boundary, and the
@@ -424,7 +686,18 @@ bool matmul_q8_rows_fits(int type, const MatvecArgs& a) {
     bases |= reinterpret_cast<uintptr_t>(a.seg[s].w);
     if (static_cast<uint64_t>(a.nb) * bs * 64 >= (uint64_t(1) << 31)) return false;
   }
+  if (static_cast<uint64_t>(a.nb) * kBytesQ8_0 * 64 >= (uint64_t(1) << 31)) return false;
   return (bases & 3u) == 0 && (a.nb * bs) % 4 == 0 && (a.nb * kBytesQ8_0) % 4 == 0;
+}
+
+int matmul_q8_tile_launch(int type, MatvecArgs& a) {
+  if (!matmul_q8_rows_fits(type, a, true)) return fail(kUnsupported, "matmul tile: shape or alignment");
+  // 64-row weight tiles when they give the chip a few workgroups per CU, else 32-row tiles.
+  uint32_t wg64 = 0;
+  for (int s = 0; s < a.n_seg; ++s) wg64 += static_cast<uint32_t>(ceil_div(a.seg[s].n_out, 64));
+  const uint64_t tiles64 = static_cast<uint64_t>(wg64) * ceil_div(a.m, kTileRows);
+  if (tiles64 >= 768) return tile_launch<64>(type, a);
+  return tile_launch<32>(type, a);
 }
 
 int matmul_q8_rows_launch(int type, MatvecArgs& a) {

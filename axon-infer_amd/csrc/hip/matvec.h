@@ -77,7 +77,11 @@ int matmul_q8_mfma_launch(int type, MatvecArgs& a);
 // int8 MFMA for 1..kRowsMaxM activation rows (batched decode): every segment in one grid, one
 // 16 x 16 tile per wave; the same outputs, bit for bit, as the other Q8_0-activation paths.
 constexpr uint32_t kRowsMaxM = 64;
-bool matmul_q8_rows_fits(int type, const MatvecArgs& a);
+// many_rows: the prefill tile kernel's bounds (any row count) instead of 1..kRowsMaxM.
+bool matmul_q8_rows_fits(int type, const MatvecArgs& a, bool many_rows = false);
 int matmul_q8_rows_launch(int type, MatvecArgs& a);
+// int8 MFMA for 65 and more activation rows (prefill, mixed passes): TN x 64 tiles, every
+// segment in one grid, the same per-output order.
+int matmul_q8_tile_launch(int type, MatvecArgs& a);
 
 }  // namespace axon_hip
