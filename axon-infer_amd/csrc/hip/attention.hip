@@ -22,7 +22,14 @@ namespace axon_hip {
 namespace {
 
 constexpr int kThreads = 256;
-constexpr size_t kLdsScores = 48 * 1024;
+// The fused kernel's LDS: q [group][hd], the scores [group][pitch] when they fit, and a value
+// tile [hd][kVPitch] (kVTile positions, transposed).
+constexpr uint32_t kVTile = 64;
+constexpr uint32_t kVPitch = kVTile + 4;
+constexpr uint32_t kVMaxItems = kVTile * 128 / 4 / kThreads;  // 4-float items per thread, hd <= 128
+
+__host__ __device__ inline uint32_t round4(uint32_t v) { return (v + 3) & ~3u; }
+__host__ __device__ inline size_t vtile_bytes(uint32_t hd) { return static_cast<size_t>(hd) * kVPitch * 4; }
 
 template <bool F16>
 __device__ __forceinline__ float kv_at(const void* base, size_t i) {
@@ -55,7 +62,7 @@ __global__ __launch_bounds__(kThreads) void attention_kernel(AttnArgs a) {
   __shared__ double red_d[kThreads / 64];
   __shared__ float red_f[kThreads / 64];
   float* sc = GLOBAL ? a.scratch + (static_cast<size_t>(r) * gridDim.y + g) * group * a.max_vis : lds + group * hd;
-  const uint32_t pitch = GLOBAL ? a.max_vis : n_vis;
+  const uint32_t pitch = GLOBAL ? a.max_vis : round4(n_vis);
 
   // 16-byte loads of K rows when every row of this span is 16-byte aligned.
   constexpr uint32_t es = F16 ? 2 : 4;
@@ -139,7 +146,92 @@ __global__ __launch_bounds__(kThreads) void attention_kernel(AttnArgs a) {
 
   // Value mix: one (head, d) per lane, positions in ascending order.
   float* out = a.out + static_cast<size_t>(r) * a.out_stride + static_cast<size_t>(h_lo) * hd;
-  for (uint32_t t = tid; t < nh * hd; t += kThreads) {
+  const uint32_t pairs = nh * hd;
+  constexpr uint32_t es2 = F16 ? 8 : 16;  // bytes of one 4-element load
+  const bool tiled = hd % 4 == 0 && hd <= 128 && pairs <= 4 * kThreads &&
+                     ((reinterpret_cast<uintptr_t>(a.kv) + static_cast<uintptr_t>(v_off) * es) % es2) == 0 &&
+                     (kv_row * es) % es2 == 0;
+  if (tiled) {
+    // V tiles of kVTile positions, loaded by the whole workgroup (the next tile's loads in
+    // flight while the current one is walked) and stored transposed, [d][position], so a lane
+    // reads four positions of its dim, and four of its head's probabilities, per 16-byte read.
+    float* vt = lds + group * hd + (GLOBAL ? 0 : group * pitch);
+    const uint32_t quads = hd / 4;
+    const uint32_t items = kVTile * quads;
+    const size_t vcol = v_off + static_cast<size_t>(g) * hd;
+    float4 reg[kVMaxItems];
+    auto load_tile = [&](uint32_t j0) {
+#pragma unroll
+      for (uint32_t k = 0; k < kVMaxItems; ++k) {
+        const uint32_t it = tid + k * kThreads;
+        float4 v = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        const uint32_t jj = it / quads, dq = it - jj * quads;
+        if (it < items && j0 + jj < n_vis) {
+          const size_t e = vcol + static_cast<size_t>(j0 + jj) * kv_row + 4 * dq;
+          if constexpr (F16) {
+            const uint2 h = *reinterpret_cast<const uint2*>(reinterpret_cast<const uint16_t*>(a.kv) + e);
+            v = make_float4(half_value(h.x & 0xffffu), half_value(h.x >> 16), half_value(h.y & 0xffffu),
+                            half_value(h.y >> 16));
+          } else {
+            v = *reinterpret_cast<const float4*>(reinterpret_cast<const float*>(a.kv) + e);
+          }
+        }
+        reg[k] = v;
+      }
+    };
+    const bool p4 = pitch % 4 == 0;
+    float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    load_tile(0);
+    for (uint32_t j0 = 0; j0 < n_vis; j0 += kVTile) {
+      __syncthreads();  // the previous tile has been read
+#pragma unroll
+      for (uint32_t k = 0; k < kVMaxItems; ++k) {
+        const uint32_t it = tid + k * kThreads;
+        if (it < items) {
+          const uint32_t jj = it / quads, dq = it - jj * quads;
+          float* col = vt + 4 * dq * kVPitch + jj;
+          col[0] = reg[k].x;
+          col[kVPitch] = reg[k].y;
+          col[2 * kVPitch] = reg[k].z;
+          col[3 * kVPitch] = reg[k].w;
+        }
+      }
+      __syncthreads();
+      if (j0 + kVTile < n_vis) load_tile(j0 + kVTile);
+      const uint32_t cnt = min(kVTile, n_vis - j0);
+#pragma unroll
+      for (uint32_t q = 0; q < 4; ++q) {
+        const uint32_t t = tid + q * kThreads;
+        if (t < pairs) {
+          const uint32_t h = t / hd;
+          const uint32_t d = t - h * hd;
+          const float* pp = sc + h * pitch + j0;
+          const float* vv = vt + d * kVPitch;
+          float sum = acc[q];
+          uint32_t j = 0;
+          if (p4) {
+            for (; j + 4 <= cnt; j += 4) {
+              const float4 p4v = *reinterpret_cast<const float4*>(pp + j);
+              const float4 v4 = *reinterpret_cast<const float4*>(vv + j);
+              sum += p4v.x * v4.x;
+              sum += p4v.y * v4.y;
+              sum += p4v.z * v4.z;
+              sum += p4v.w * v4.w;
+            }
+          }
+          for (; j < cnt; ++j) sum += pp[j] * vv[j];
+          acc[q] = sum;
+        }
+      }
+    }
+#pragma unroll
+    for (uint32_t q = 0; q < 4; ++q) {
+      const uint32_t t = tid + q * kThreads;
+      if (t < pairs) out[t] = acc[q];
+    }
+    return;
+  }
+  for (uint32_t t = tid; t < pairs; t += kThreads) {
     const uint32_t h = t / hd;
     const uint32_t d = t - h * hd;
     const float* p = sc + h * pitch;
@@ -992,7 +1084,7 @@ void launch_mixd(uint32_t group, dim3 grid, size_t lds, const AttnArgs& a) {
 
 bool scores_fit_lds(const AttnArgs& a) {
   const uint32_t group = a.n_head / a.n_kv;
-  return static_cast<size_t>(group) * (a.head_dim + a.max_vis) * 4 <= kLdsScores;
+  return static_cast<size_t>(group) * (a.head_dim + round4(a.max_vis)) * 4 + vtile_bytes(a.head_dim) <= 65536;
 }
 
 }  // namespace
@@ -1077,8 +1169,10 @@ int attention_launch(const AttnArgs& a, uint32_t n_rows) {
   const dim3 grid(n_rows, a.n_kv);
   const bool lds_ok = scores_fit_lds(a);
   if (!lds_ok && a.scratch == nullptr) return fail(kInvalidArgument, "attention: %u positions need a score scratch", a.max_vis);
-  const size_t lds = lds_ok ? static_cast<size_t>(group) * (a.head_dim + a.max_vis) * 4
-                            : static_cast<size_t>(group) * a.head_dim * 4;
+  const size_t tile = a.head_dim <= 128 ? vtile_bytes(a.head_dim) : 0;
+  const size_t lds = (lds_ok ? static_cast<size_t>(group) * (a.head_dim + round4(a.max_vis)) * 4
+                             : static_cast<size_t>(group) * a.head_dim * 4) + tile;
+  if (lds > 65536) return fail(kUnsupported, "attention: %zu bytes of LDS", lds);
   if (a.f16) {
     if (lds_ok) hipLaunchKernelGGL((attention_kernel<true, false>), grid, dim3(kThreads), lds, stream(), a);
     else hipLaunchKernelGGL((attention_kernel<true, true>), grid, dim3(kThreads), lds, stream(), a);
