@@ -324,6 +324,19 @@ def traffic_probe(H, model, n_vocab, steps, prompt_len, seed):
     model.free_cache(cache)
 
 
+def prefill_probe(H, model, n_vocab, seed, passes=4, prompt_len=512):
+    """The workload of the prefill profiles: `passes` 512-token prefill passes (logits of the
+    last row only), each on a new cache."""
+    rng = np.random.default_rng(seed + 5)
+    for i in range(passes):
+        c = model.new_cache()
+        t0 = time.perf_counter()
+        model.forward_mixed(c, rng.integers(0, n_vocab, prompt_len).astype(np.int32), [], [], logits=False)
+        H.synchronize()
+        log(f"prefill {i}: {prompt_len / (time.perf_counter() - t0):.0f} tok/s")
+        model.free_cache(c)
+
+
 def _counter_rows(path):
     """(kernel name, counter name, value) of every dispatch in a rocprofv3 counter CSV."""
     import csv
@@ -439,6 +452,8 @@ def main() -> int:
     ap.add_argument("--no-ragged", action="store_true", help="skip the 32-sequence workload")
     ap.add_argument("--no-f16", action="store_true", help="skip the fp16-cache runs")
     ap.add_argument("--no-c5", action="store_true", help="skip the config-5 mixed prefill/decode workload")
+    ap.add_argument("--prefill-probe", action="store_true",
+                    help="only run four 512-token prefill passes (the workload of the prefill profiles)")
     ap.add_argument("--cpu-budget", type=float, default=12.0, help="seconds per CPU baseline sample")
     ap.add_argument("--traffic-probe", action="store_true",
                     help="run the workload of the FETCH_SIZE / WRITE_SIZE counter passes and exit")
@@ -469,6 +484,11 @@ def main() -> int:
         traffic_probe(H, model, info.n_vocab, min(args.steps, 16), args.prompt, args.seed)
         model.close()
         log("traffic probe done")
+        return 0
+    if args.prefill_probe:
+        prefill_probe(H, model, info.n_vocab, args.seed)
+        model.close()
+        log("prefill probe done")
         return 0
 
     b1 = bench_decode_b1(H, model, info.n_vocab, args.steps, args.warmup, args.prompt, args.seed)
