@@ -66,7 +66,8 @@ bool fits_u32(size_t v) { return v <= 0xffffffffull; }
 
 // The Q8_0-activation path: groups of up to four rows on the dot4 matvec below 5 rows, the
 // few-rows MFMA kernel (every segment in one launch) from 5 to 64 rows, the tile MFMA kernel
-// (every segment in one launch) beyond; rows whose bases or lengths do not suit their dword
+// (every segment in one launch, 64-row tiles) beyond, and from 33 rows on matrices wide enough
+// to fill the chip with its tiles (the output matrix: its weights are read once, not twice); rows whose bases or lengths do not suit their dword
 // loads take the staged 64 x 64 MFMA tiles or the dot4 groups. All of them give the same bits
 // for a row.
 int q8_matmul(int type, const void* xq, size_t n_rows, size_t n_in, size_t n_seg, const void* const* w,
@@ -93,8 +94,11 @@ int q8_matmul(int type, const void* xq, size_t n_rows, size_t n_in, size_t n_seg
     a.nb = nb;
     a.m = static_cast<uint32_t>(n_rows);
     a.accumulate = accumulate;
-    if (n_rows <= kRowsMaxM && matmul_q8_rows_fits(type, a)) return matmul_q8_rows_launch(type, a);
-    if (n_rows > kRowsMaxM && matmul_q8_rows_fits(type, a, true)) return matmul_q8_tile_launch(type, a);
+    if (n_rows > kRowsMaxM || matmul_q8_tile_fills(a)) {
+      if (matmul_q8_rows_fits(type, a, true)) return matmul_q8_tile_launch(type, a);
+    } else if (matmul_q8_rows_fits(type, a)) {
+      return matmul_q8_rows_launch(type, a);
+    }
   }
   if (n_rows >= 16) {
     for (size_t s = 0; s < n_seg; ++s) {

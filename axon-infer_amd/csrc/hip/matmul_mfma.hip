@@ -690,6 +690,13 @@ bool matmul_q8_rows_fits(int type, const MatvecArgs& a, bool many_rows) {
   return (bases & 3u) == 0 && (a.nb * bs) % 4 == 0 && (a.nb * kBytesQ8_0) % 4 == 0;
 }
 
+bool matmul_q8_tile_fills(const MatvecArgs& a) {
+  if (a.m < 33 || a.m > kRowsMaxM) return false;
+  uint32_t wg64 = 0;
+  for (int s = 0; s < a.n_seg; ++s) wg64 += static_cast<uint32_t>(ceil_div(a.seg[s].n_out, 64));
+  return wg64 >= 512;
+}
+
 int matmul_q8_tile_launch(int type, MatvecArgs& a) {
   if (!matmul_q8_rows_fits(type, a, true)) return fail(kUnsupported, "matmul tile: shape or alignment");
   // 64-row weight tiles when they give the chip a few workgroups per CU, else 32-row tiles.

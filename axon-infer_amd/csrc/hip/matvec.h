@@ -83,5 +83,8 @@ int matmul_q8_rows_launch(int type, MatvecArgs& a);
 // int8 MFMA for 65 and more activation rows (prefill, mixed passes): TN x 64 tiles, every
 // segment in one grid, the same per-output order.
 int matmul_q8_tile_launch(int type, MatvecArgs& a);
+// 33..64 rows on matrices of at least 512 tiles of 64 weight rows: the tile kernel reads the
+// weights once where the few-rows kernel's 32-row tiles read them twice.
+bool matmul_q8_tile_fills(const MatvecArgs& a);
 
 }  // namespace axon_hip

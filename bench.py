@@ -452,6 +452,8 @@ def main() -> int:
     ap.add_argument("--no-ragged", action="store_true", help="skip the 32-sequence workload")
     ap.add_argument("--no-f16", action="store_true", help="skip the fp16-cache runs")
     ap.add_argument("--no-c5", action="store_true", help="skip the config-5 mixed prefill/decode workload")
+    ap.add_argument("--c5-only", action="store_true",
+                    help="only run the config-5 workload and print its figures (the workload of its profile)")
     ap.add_argument("--prefill-probe", action="store_true",
                     help="only run four 512-token prefill passes (the workload of the prefill profiles)")
     ap.add_argument("--cpu-budget", type=float, default=12.0, help="seconds per CPU baseline sample")
@@ -470,6 +472,10 @@ def main() -> int:
     import axon_hip as H
     import synth
 
+    if args.c5_only:
+        H.init(0)
+        print(json.dumps(bench_c5(H, args.seed)), flush=True)
+        return 0
     spec = synth.LLAMA32_1B
     log(f"model: {spec.name} (writing the seeded GGUF on first use)")
     t0 = time.perf_counter()

@@ -159,10 +159,12 @@ def test_q8_fused_segments_few_rows_bit_exact(o, n_rows, n_in):
 
 @pytest.mark.parametrize("n_rows, n_in, n_out", [(65, 896, [300, 7, 64]), (77, 2048, [300, 7, 64]),
                                                   (200, 896, [1152, 896, 40]), (576, 896, [4096, 1024, 1024]),
-                                                  (130, 4864, [896, 33, 64])])
+                                                  (130, 4864, [896, 33, 64]), (40, 896, [32768, 7, 64]),
+                                                  (64, 256, [32800])])
 def test_q8_fused_segments_many_rows_bit_exact(o, n_rows, n_in, n_out):
-    """The tile MFMA path (65 rows and more, prefill and mixed passes): three segments in one
-    grid with 32- and 64-row weight tiles (the last shape fills the chip with 64-row tiles),
+    """The tile MFMA path (65 rows and more, prefill and mixed passes; 33 to 64 rows on matrices
+    of 512 or more 64-row tiles, the last two shapes): segments in one grid with 32- and 64-row
+    weight tiles,
     partial activation and weight tiles, a last K chunk shorter than 16 blocks, y_stride past
     n_out with the sentinels between rows untouched, and accumulate (y += W x) — each output
     equal to the oracle's row by row."""
