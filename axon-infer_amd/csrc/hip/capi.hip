@@ -628,6 +628,24 @@ int axon_hip_argmax_rows(const float* x, size_t n, size_t n_rows, size_t stride,
 
 static_assert(kMaxTopK == AXON_HIP_MAX_TOPK, "one top-k bound");
 
+int axon_hip_matmul_q8_swiglu(int type, const void* xq, size_t n_rows, size_t n_in, const void* w_gate,
+                              const void* w_up, size_t n_ff, float* out, void* outq) {
+  AXON_READY();
+  if (n_in % kQK != 0 || n_ff % kQK != 0 || !fits_u32(n_rows) || !fits_u32(n_in) || !fits_u32(n_ff))
+    return fail(kInvalidArgument, "matmul_q8_swiglu: %zu x %zu -> %zu", n_rows, n_in, n_ff);
+  if (xq == nullptr || w_gate == nullptr || w_up == nullptr || outq == nullptr)
+    return fail(kInvalidArgument, "matmul_q8_swiglu: null pointer");
+  MatvecArgs a{};
+  a.seg[0] = MatvecSeg{static_cast<const uint8_t*>(w_gate), out, static_cast<uint32_t>(n_ff), static_cast<uint32_t>(n_ff), 0};
+  a.seg[1] = MatvecSeg{static_cast<const uint8_t*>(w_up), nullptr, static_cast<uint32_t>(n_ff), static_cast<uint32_t>(n_ff), 0};
+  a.n_seg = 2;
+  a.xq = static_cast<const uint8_t*>(xq);
+  a.nb = static_cast<uint32_t>(n_in / kQK);
+  a.m = static_cast<uint32_t>(n_rows);
+  a.outq = static_cast<uint8_t*>(outq);
+  return matmul_q8_swiglu_launch(type, a);
+}
+
 int axon_hip_topk_rows(const float* x, size_t n, size_t n_rows, size_t stride, size_t k, float* out_logit,
                        int32_t* out_id) {
   AXON_READY();

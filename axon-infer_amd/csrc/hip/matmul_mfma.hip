@@ -415,7 +415,7 @@ __host__ __device__ constexpr size_t tile_lds() {
   return (static_cast<size_t>(TN + kTileRows) * kTilePitch + scales) * 4;
 }
 
-template <int T, uint32_t TN>
+template <int T, uint32_t TN, bool SWIGLU = false>
 __global__ __launch_bounds__(kThreads) void mfma_tile_kernel(MatvecArgs args) {
   constexpr int bs = block_bytes<T>();
   constexpr uint32_t TM = kTileRows, KC = kTileChunk, P = kTilePitch;
@@ -437,20 +437,26 @@ __global__ __launch_bounds__(kThreads) void mfma_tile_kernel(MatvecArgs args) {
   const uint32_t tid = threadIdx.x;
   const uint32_t lane = tid & 63;
   const uint32_t wave = tid >> 6;
+  static_assert(!SWIGLU || TN == 64, "the SwiGLU tile pairs 32 gate rows with 32 up rows");
   int s = 0;
-  if (args.n_seg > 1 && blockIdx.x >= args.seg[1].wg_begin) s = 1;
-  if (args.n_seg > 2 && blockIdx.x >= args.seg[2].wg_begin) s = 2;
+  if (!SWIGLU && args.n_seg > 1 && blockIdx.x >= args.seg[1].wg_begin) s = 1;
+  if (!SWIGLU && args.n_seg > 2 && blockIdx.x >= args.seg[2].wg_begin) s = 2;
   const MatvecSeg seg = args.seg[s];
-  const uint32_t n0 = (blockIdx.x - seg.wg_begin) * TN;
+  // SwiGLU: tile rows 0..31 are gate rows n0.., rows 32..63 the up rows of the same outputs.
+  const uint32_t n0 = SWIGLU ? blockIdx.x * 32 : (blockIdx.x - seg.wg_begin) * TN;
   const uint32_t m0 = blockIdx.y * TM;
-  const uint32_t nn = min(TN, seg.n_out - n0);
+  const uint32_t nn = SWIGLU ? 64 : min(TN, seg.n_out - n0);
   const uint32_t mm = min(TM, args.m - m0);
   const uint32_t nb = args.nb;
   const uint32_t n_chunks = (nb + KC - 1) / KC;
   const uint32_t w_pitch = nb * bs, x_pitch = nb * kBytesQ8_0;
+  const uint32_t w_rows = SWIGLU ? 32 : nn;  // rows behind each weight resource
   const __amdgpu_buffer_rsrc_t wsrc = __builtin_amdgcn_make_buffer_rsrc(
-      const_cast<uint8_t*>(seg.w) + static_cast<size_t>(n0) * w_pitch, 0, static_cast<int>(nn * w_pitch),
+      const_cast<uint8_t*>(seg.w) + static_cast<size_t>(n0) * w_pitch, 0, static_cast<int>(w_rows * w_pitch),
       static_cast<int>(kRawBufferWord3));
+  const __amdgpu_buffer_rsrc_t usrc = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<uint8_t*>(SWIGLU ? args.seg[1].w : seg.w) + static_cast<size_t>(n0) * w_pitch, 0,
+      static_cast<int>(w_rows * w_pitch), static_cast<int>(kRawBufferWord3));
   const __amdgpu_buffer_rsrc_t xsrc = __builtin_amdgcn_make_buffer_rsrc(
       const_cast<uint8_t*>(args.xq) + static_cast<size_t>(m0) * x_pitch, 0, static_cast<int>(mm * x_pitch),
       static_cast<int>(kRawBufferWord3));
@@ -466,10 +472,13 @@ __global__ __launch_bounds__(kThreads) void mfma_tile_kernel(MatvecArgs args) {
     for (uint32_t k = 0; k < WI; ++k) {
       const uint32_t i = tid + k * kThreads;
       const uint32_t row = i / KC, b = i - row * KC;
-      const uint32_t off = row * w_pitch + (b0 + b) * bs;
+      // SwiGLU: items k < WI / 2 are rows 0..31 (gate), the rest rows 32..63 (up); the choice
+      // of resource is uniform per k.
+      const bool upper = SWIGLU && k >= WI / 2;
+      const uint32_t off = (SWIGLU ? row & 31u : row) * w_pitch + (b0 + b) * bs;
 #pragma unroll
       for (uint32_t d = 0; d < WD; ++d)
-        r.w[k][d] = __builtin_amdgcn_raw_buffer_load_b32(wsrc, (off & ~3u) + 4 * d, 0, 0);
+        r.w[k][d] = __builtin_amdgcn_raw_buffer_load_b32(upper ? usrc : wsrc, (off & ~3u) + 4 * d, 0, 0);
     }
 #pragma unroll
     for (uint32_t k = 0; k < XI; ++k) {
@@ -608,6 +617,36 @@ __global__ __launch_bounds__(kThreads) void mfma_tile_kernel(MatvecArgs args) {
     __syncthreads();
   }
 
+  if constexpr (SWIGLU) {
+    // Output n0 + col (sub-tiles 0 and 2) and n0 + 16 + col (1 and 3): silu(gate) * up as
+    // silu_mul_kernel forms it, then each row's 32 outputs as one Q8_0 block, quantized as
+    // quantize_block_lanes does (the 16 lanes of a kq group hold the block).
+    const size_t row_blocks = seg.n_out / kQK;
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      const uint32_t rr = orow + v;
+      const float g0 = acc[0][v], g1 = acc[1][v];
+      const float y0 = g0 / (1.0f + exp_rounded(-g0)) * acc[2][v];
+      const float y1 = g1 / (1.0f + exp_rounded(-g1)) * acc[3][v];
+      float amax = fmaxf(fabsf(y0), fabsf(y1));
+#pragma unroll
+      for (int off = 8; off > 0; off >>= 1) amax = fmaxf(amax, __shfl_xor(amax, off, 64));
+      if (rr < mm) {
+        if (seg.y != nullptr) {
+          float* y = seg.y + static_cast<size_t>(m0 + rr) * seg.y_stride + n0 + col;
+          y[0] = y0;
+          y[16] = y1;
+        }
+        const float dq = amax / 127.0f;
+        const float id = dq != 0.0f ? 1.0f / dq : 0.0f;
+        uint8_t* blk = args.outq + (static_cast<size_t>(m0 + rr) * row_blocks + n0 / kQK) * kBytesQ8_0;
+        blk[2 + col] = static_cast<uint8_t>(static_cast<int32_t>(roundf(y0 * id)) & 0xff);
+        blk[2 + 16 + col] = static_cast<uint8_t>(static_cast<int32_t>(roundf(y1 * id)) & 0xff);
+        if (col == 0) *reinterpret_cast<uint16_t*>(blk) = static_cast<uint16_t>(float_to_half_bits(dq));
+      }
+    }
+    return;
+  }
 #pragma unroll
   for (uint32_t j = 0; j < NT; ++j) {
     if (16 * j + col < nn) {
@@ -695,6 +734,35 @@ bool matmul_q8_tile_fills(const MatvecArgs& a) {
   uint32_t wg64 = 0;
   for (int s = 0; s < a.n_seg; ++s) wg64 += static_cast<uint32_t>(ceil_div(a.seg[s].n_out, 64));
   return wg64 >= 512;
+}
+
+int matmul_q8_swiglu_launch(int type, MatvecArgs& a) {
+  MatvecArgs probe = a;
+  probe.n_seg = 2;
+  if (a.n_seg != 2 || a.outq == nullptr || a.m <= kRowsMaxM || a.seg[0].n_out != a.seg[1].n_out ||
+      a.seg[0].n_out % kQK != 0 || !matmul_q8_rows_fits(type, probe, true))
+    return fail(kUnsupported, "matmul swiglu: shape or alignment");
+  const dim3 grid(static_cast<uint32_t>(a.seg[0].n_out / 32), static_cast<uint32_t>(ceil_div(a.m, kTileRows)));
+  static const bool granted = [] {
+    bool ok = true;
+    auto grant = [&](auto kernel, size_t lds) {
+      if (lds > 65536)
+        ok = ok && hipFuncSetAttribute(reinterpret_cast<const void*>(kernel), hipFuncAttributeMaxDynamicSharedMemorySize,
+                                       static_cast<int>(lds)) == hipSuccess;
+    };
+    grant(mfma_tile_kernel<Q8_0, 64, true>, tile_lds<Q8_0, 64>());
+    grant(mfma_tile_kernel<Q4_0, 64, true>, tile_lds<Q4_0, 64>());
+    grant(mfma_tile_kernel<Q4_1, 64, true>, tile_lds<Q4_1, 64>());
+    return ok;
+  }();
+  if (!granted) return fail(kUnsupported, "matmul swiglu: the LDS grant was refused");
+  switch (type) {
+  case Q8_0: launch(mfma_tile_kernel<Q8_0, 64, true>, grid, dim3(kThreads), tile_lds<Q8_0, 64>(), a); break;
+  case Q4_0: launch(mfma_tile_kernel<Q4_0, 64, true>, grid, dim3(kThreads), tile_lds<Q4_0, 64>(), a); break;
+  case Q4_1: launch(mfma_tile_kernel<Q4_1, 64, true>, grid, dim3(kThreads), tile_lds<Q4_1, 64>(), a); break;
+  default: return fail(kUnsupported, "matmul swiglu: weight type %d", type);
+  }
+  return check_launch("mfma_tile (swiglu)");
 }
 
 int matmul_q8_tile_launch(int type, MatvecArgs& a) {

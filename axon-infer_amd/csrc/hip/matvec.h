@@ -24,6 +24,7 @@ struct MatvecArgs {
   uint32_t lds_scratch;
   int n_seg;
   int accumulate;     // y += W x instead of y = W x
+  uint8_t* outq;      // the SwiGLU tile path: Q8_0 blocks of each output row
 };
 
 // The fused decode matvec (matvec_fused.hip): input prologue and output epilogue modes.
@@ -86,5 +87,8 @@ int matmul_q8_tile_launch(int type, MatvecArgs& a);
 // 33..64 rows on matrices of at least 512 tiles of 64 weight rows: the tile kernel reads the
 // weights once where the few-rows kernel's 32-row tiles read them twice.
 bool matmul_q8_tile_fills(const MatvecArgs& a);
+// gate|up over 65+ rows with the SwiGLU product and its Q8_0 blocks in the epilogue: seg[0]
+// gate (y: the float product, or null), seg[1] up, outq the blocks; n_out a multiple of 32.
+int matmul_q8_swiglu_launch(int type, MatvecArgs& a);
 
 }  // namespace axon_hip

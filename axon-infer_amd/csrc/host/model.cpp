@@ -719,23 +719,41 @@ Expected<std::size_t> LlamaModel::run(std::span<const Row> rows, bool copy_logit
     const bool ff_f = !q8_path(L.w_gate) || !q8_path(L.w_up);
     DEV(axon_hip_rmsnorm_rows(x_, static_cast<const float*>(L.ffn_norm.dev), ff_f ? h_ : nullptr,
                               ff_q8 ? xq_ : nullptr, d, n, eps));
-    if (gu_q8) {
-      const void* ws[2] = {L.w_gate.dev, L.w_up.dev};
-      float* ys[2] = {gate_, up_};
-      const std::size_t no[2] = {ff, ff};
+    // Many rows: gate|up, SiLU and down's Q8_0 input in one tile launch, the blocks into tmp_
+    // (xq_ is still being read as its input).
+    const void* down_xq = xq_;
+    bool swiglu = false;
+    if (gu_q8 && q8_path(L.w_down) && n > 64 && ff % 32 == 0) {
       probe_begin(L.w_gate);
-      DEV(axon_hip_matmul_q8_fused(static_cast<int>(L.w_gate.type), xq_, n, d, 2, ws, ys, no, no, 0));
+      const int rc = axon_hip_matmul_q8_swiglu(static_cast<int>(L.w_gate.type), xq_, n, d, L.w_gate.dev, L.w_up.dev,
+                                               ff, nullptr, tmp_);
       probe_end(L.w_gate, n, 2 * ff, false);
-    } else {
-      DEV(mm(L.w_gate, h_, xq_, gate_, n, false));
-      DEV(mm(L.w_up, h_, xq_, up_, n, false));
+      if (rc == AXON_HIP_OK) {
+        swiglu = true;
+        down_xq = tmp_;
+      } else if (rc != AXON_HIP_E_UNSUPPORTED) {
+        return device_error("matmul_q8_swiglu");
+      }
     }
-    if (q8_path(L.w_down)) {
-      DEV(axon_hip_silu_mul_rows(gate_, up_, nullptr, xq_, ff, n));
-    } else {
-      DEV(axon_hip_silu_mul_rows(gate_, up_, gate_, nullptr, ff, n));
+    if (!swiglu) {
+      if (gu_q8) {
+        const void* ws[2] = {L.w_gate.dev, L.w_up.dev};
+        float* ys[2] = {gate_, up_};
+        const std::size_t no[2] = {ff, ff};
+        probe_begin(L.w_gate);
+        DEV(axon_hip_matmul_q8_fused(static_cast<int>(L.w_gate.type), xq_, n, d, 2, ws, ys, no, no, 0));
+        probe_end(L.w_gate, n, 2 * ff, false);
+      } else {
+        DEV(mm(L.w_gate, h_, xq_, gate_, n, false));
+        DEV(mm(L.w_up, h_, xq_, up_, n, false));
+      }
+      if (q8_path(L.w_down)) {
+        DEV(axon_hip_silu_mul_rows(gate_, up_, nullptr, xq_, ff, n));
+      } else {
+        DEV(axon_hip_silu_mul_rows(gate_, up_, gate_, nullptr, ff, n));
+      }
     }
-    DEV(mm(L.w_down, gate_, xq_, x_, n, true));
+    DEV(mm(L.w_down, gate_, down_xq, x_, n, true));
   }
   // The final norm and the output matmul for the rows whose logits the pass returns.
   float* const x_out = x_ + first_logit * d;

@@ -190,6 +190,15 @@ int axon_hip_argmax_rows(const float* x, size_t n, size_t n_rows, size_t stride,
  * stride floats apart) into out_logit[r * k + i] with their indices in out_id, descending, equal
  * values by ascending index (the reference leaves their order unspecified). NaN is skipped; a
  * row with fewer than k other values ends in ids -1. 1 <= k <= 256, k <= n. */
+/* gate|up with the SwiGLU product and its Q8_0 quantization in one launch, for 65 or more
+ * rows (llama.cpp:600-620: out = silu(x W_gate^T) * (x W_up^T), then quantize_row_q8_0 of each
+ * row for w_down): the same bits as matmul_q8_fused of the two weights, silu_mul_rows and
+ * quantize_rows. out: float [n_rows][n_ff] or NULL; outq: [n_rows][n_ff / 32] Q8_0 blocks, which
+ * must not alias xq. n_ff a multiple of 32. AXON_HIP_E_UNSUPPORTED (nothing launched) for fewer
+ * rows or bases the tile kernel cannot load. */
+int axon_hip_matmul_q8_swiglu(int type, const void* xq, size_t n_rows, size_t n_in, const void* w_gate,
+                              const void* w_up, size_t n_ff, float* out, void* outq);
+
 #define AXON_HIP_MAX_TOPK 256
 int axon_hip_topk_rows(const float* x, size_t n, size_t n_rows, size_t stride, size_t k, float* out_logit,
                        int32_t* out_id);

@@ -195,6 +195,50 @@ def test_q8_fused_segments_many_rows_bit_exact(o, n_rows, n_in, n_out):
                 assert np.array_equal(got[:, n_out[j]:], base[j].reshape(n_rows, stride[j])[:, n_out[j]:])
 
 
+@pytest.mark.parametrize("n_rows, n_in, n_ff", [(65, 896, 4864), (130, 2048, 1024), (512, 256, 96)])
+def test_q8_swiglu_tile_bit_exact(o, n_rows, n_in, n_ff):
+    """gate|up with the SwiGLU product and down's Q8_0 input in the tile kernel's epilogue
+    (axon_hip_matmul_q8_swiglu): the float product and the Q8_0 blocks equal, bit for bit,
+    the unfused device path (matmul_q8_fused of both weights, then silu_mul_rows), whose parts
+    are pinned to the oracle elsewhere; and the product is within 2 ulp of the oracle's
+    matmuls and silu_mul (the exponential's last bit)."""
+    import axon_hip as H
+    xs = random_floats(n_rows * n_in, n_rows + n_ff, 3.0)
+    xq = np.concatenate([o.quantize_row_q8_0(xs[i * n_in:(i + 1) * n_in]) for i in range(n_rows)])
+    dx = H.DeviceBuffer.of(xq)
+    for kind in QUANT_TYPES:
+        wg = random_weights(kind, n_ff, n_in, 11 + n_rows)
+        wu = random_weights(kind, n_ff, n_in, 12 + n_rows)
+        g = o.matmul(f"{kind}_q8", wg, xq, n_ff, n_in, n_rows=n_rows, y_stride=n_ff).reshape(n_rows, n_ff)
+        u = o.matmul(f"{kind}_q8", wu, xq, n_ff, n_in, n_rows=n_rows, y_stride=n_ff).reshape(n_rows, n_ff)
+        prod = np.stack([o.silu_mul(g[r], u[r]) for r in range(n_rows)])
+        want_q = np.concatenate([o.quantize_row_q8_0(prod[r]) for r in range(n_rows)])
+        dwg, dwu = H.DeviceBuffer.of(wg), H.DeviceBuffer.of(wu)
+        out = H.DeviceBuffer.of(np.full(n_rows * n_ff, np.float32(-3.5), np.float32))
+        outq = H.DeviceBuffer(want_q.nbytes)
+        H.check(H.lib().axon_hip_matmul_q8_swiglu(
+            C.c_int(TYPE_ID[kind]), C.c_void_p(dx.ptr), C.c_size_t(n_rows), C.c_size_t(n_in), C.c_void_p(dwg.ptr),
+            C.c_void_p(dwu.ptr), C.c_size_t(n_ff), C.c_void_p(out.ptr), C.c_void_p(outq.ptr)), "matmul_q8_swiglu")
+        got = out.download(np.float32).reshape(n_rows, n_ff)
+        got_q = outq.download(np.uint8, want_q.nbytes)
+        # The unfused device path.
+        dg, du = H.DeviceBuffer(4 * n_rows * n_ff), H.DeviceBuffer(4 * n_rows * n_ff)
+        H.check(H.lib().axon_hip_matmul_q8_fused(
+            C.c_int(TYPE_ID[kind]), C.c_void_p(dx.ptr), C.c_size_t(n_rows), C.c_size_t(n_in), C.c_size_t(2),
+            (C.c_void_p * 2)(dwg.ptr, dwu.ptr), (C.c_void_p * 2)(dg.ptr, du.ptr), (C.c_size_t * 2)(n_ff, n_ff),
+            (C.c_size_t * 2)(n_ff, n_ff), C.c_int(0)), "matmul_q8_fused")
+        ref_out, ref_q = H.DeviceBuffer(4 * n_rows * n_ff), H.DeviceBuffer(want_q.nbytes)
+        H.call("silu_mul_rows", dg, du, ref_out, ref_q, n_ff, n_rows)
+        assert np.array_equal(got.view(np.uint32), ref_out.download(np.uint32, n_rows * n_ff).reshape(n_rows, n_ff)), kind
+        assert got_q.tobytes() == ref_q.download(np.uint8, want_q.nbytes).tobytes(), kind
+        assert np.allclose(got, prod, rtol=2.5e-7, atol=0), kind
+    # Below the tile kernel's rows: refused, nothing launched.
+    with pytest.raises(H.HipError, match="swiglu"):
+        H.check(H.lib().axon_hip_matmul_q8_swiglu(C.c_int(2), C.c_void_p(dx.ptr), C.c_size_t(64), C.c_size_t(n_in),
+                                                  C.c_void_p(dx.ptr), C.c_void_p(dx.ptr), C.c_size_t(n_ff), None,
+                                                  C.c_void_p(dx.ptr)), "matmul_q8_swiglu")
+
+
 @pytest.mark.parametrize("name,dt", [("q8_0", Q8_0), ("q4_0", Q4_0), ("q4_1", Q4_1)])
 def test_q8_matmul_fixtures(h, name, dt):
     # The reference's float64 integer-dot fixtures (test_kernels_quant.cpp:50-84, 101-134).
