@@ -48,7 +48,8 @@ int init_device(int device) {
   e = hipStreamCreateWithFlags(&g_stream, hipStreamNonBlocking);
   if (e != hipSuccess) return hip_fail(e, "hipStreamCreateWithFlags");
   g_device = device;
-  return kOk;
+  // The fixed scratch of the allocation-free entry, looked up once with this device current.
+  return argmax_noalloc_setup();
 }
 
 int ready() {
@@ -626,7 +627,15 @@ int axon_hip_argmax_rows(const float* x, size_t n, size_t n_rows, size_t stride,
   return argmax_rows_launch(x, static_cast<uint32_t>(n), static_cast<uint32_t>(n_rows), stride, scratch, out);
 }
 
+int axon_hip_argmax_rows_noalloc(const float* x, size_t n, size_t n_rows, size_t stride, int32_t* out) {
+  AXON_READY();
+  if (!fits_u32(n) || !fits_u32(n_rows) || stride < n) return fail(kInvalidArgument, "argmax: %zu x %zu, stride %zu", n_rows, n, stride);
+  if (out == nullptr) return fail(kInvalidArgument, "argmax: the output is required");
+  return argmax_rows_noalloc_launch(x, static_cast<uint32_t>(n), static_cast<uint32_t>(n_rows), stride, out);
+}
+
 static_assert(kMaxTopK == AXON_HIP_MAX_TOPK, "one top-k bound");
+static_assert(kArgmaxNoAllocRows == AXON_HIP_ARGMAX_NOALLOC_MAX_ROWS, "one no-allocation row bound");
 
 int axon_hip_matmul_q8_swiglu(int type, const void* xq, size_t n_rows, size_t n_in, const void* w_gate,
                               const void* w_up, size_t n_ff, float* out, void* outq) {

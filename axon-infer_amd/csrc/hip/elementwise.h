@@ -44,6 +44,11 @@ constexpr uint32_t kMaxTopK = 256;
 int topk_rows_launch(const float* x, uint32_t n, uint32_t n_rows, size_t stride, uint32_t k, float* out_logit,
                      int32_t* out_id);
 int argmax_rows_launch(const float* x, uint32_t n, uint32_t n_rows, size_t stride, uint64_t* scratch, int32_t* out);
+// argmax_rows over a fixed per-device array instead of a workspace (at most kArgmaxNoAllocRows rows);
+// argmax_noalloc_setup finds the array's address on the current device (once per device).
+constexpr uint32_t kArgmaxNoAllocRows = 512;
+int argmax_noalloc_setup();
+int argmax_rows_noalloc_launch(const float* x, uint32_t n, uint32_t n_rows, size_t stride, int32_t* out);
 int rope_rows_launch(const RopeRowsArgs& a, uint32_t n_rows);
 int embedding_launch(int type, const uint8_t* table, uint32_t n, const int32_t* ids, int64_t id0, uint32_t n_rows,
                      float* out);

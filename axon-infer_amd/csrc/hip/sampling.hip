@@ -29,6 +29,8 @@
 #include "common.h"
 #include "elementwise.h"
 
+#include <mutex>
+
 namespace axon_hip {
 
 namespace {
@@ -233,6 +235,47 @@ int argmax_rows_launch(const float* x, uint32_t n, uint32_t n_rows, size_t strid
   hipLaunchKernelGGL(argmax_partial_kernel, dim3(kParts, n_rows), dim3(kThreads), 0, stream(), x, n, stride, scratch);
   hipLaunchKernelGGL(argmax_final_kernel, dim3(n_rows), dim3(64), 0, stream(), x, stride, scratch, out);
   return check_launch("argmax");
+}
+
+// ---- The allocation-free greedy choice -------------------------------------------------------
+// The partial keys of argmax_rows_launch in a fixed device array instead of a caller workspace,
+// for callers that cannot allocate. Each GPU holds its own copy for the life of the process;
+// host code never passes the array's name to a kernel (in host code it is only a stand-in for
+// the symbol): it passes the address hipGetSymbolAddress returned for the current device. Every
+// slot a call reads is written earlier in the same call, so nothing needs clearing; two calls
+// that overlap on one GPU share the array and race.
+static __device__ __align__(256) uint64_t scratch[kArgmaxNoAllocRows * kParts];
+
+namespace {
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mutex;
+uint64_t* g_scratch_ptr[kMaxDevices] = {};
+}  // namespace
+
+int argmax_noalloc_setup() {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return fail(kHipError, "argmax (no allocation): hipGetDevice: %s", hipGetErrorString(e));
+  if (dev < 0 || dev >= kMaxDevices) return fail(kInvalidArgument, "argmax (no allocation): device %d", dev);
+  std::lock_guard<std::mutex> lock(g_scratch_mutex);
+  if (g_scratch_ptr[dev] != nullptr) return kOk;
+  void* p = nullptr;
+  e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+  if (e != hipSuccess || p == nullptr)
+    return fail(kHipError, "argmax (no allocation): hipGetSymbolAddress: %s", hipGetErrorString(e));
+  g_scratch_ptr[dev] = static_cast<uint64_t*>(p);
+  return kOk;
+}
+
+int argmax_rows_noalloc_launch(const float* x, uint32_t n, uint32_t n_rows, size_t stride, int32_t* out) {
+  if (n_rows > kArgmaxNoAllocRows)
+    return fail(kInvalidArgument, "argmax (no allocation): %u rows exceed the fixed scratch's %u", n_rows,
+                kArgmaxNoAllocRows);
+  const int rc = argmax_noalloc_setup();  // a lookup after the first call on this device
+  if (rc != kOk) return rc;
+  int dev = 0;
+  (void)hipGetDevice(&dev);
+  return argmax_rows_launch(x, n, n_rows, stride, g_scratch_ptr[dev], out);
 }
 
 }  // namespace axon_hip

@@ -185,6 +185,15 @@ size_t axon_hip_argmax_scratch_words(size_t n_rows);
 int axon_hip_repeat_penalty_rows(float* x, size_t n, size_t n_rows, size_t stride, const int32_t* recent,
                                  const uint32_t* recent_len, size_t recent_stride, float penalty);
 int axon_hip_argmax_rows(const float* x, size_t n, size_t n_rows, size_t stride, uint64_t* scratch, int32_t* out);
+/* argmax_rows without a workspace and without allocating: no counterpart in the reference. For
+ * callers that cannot allocate device memory (code under HIP graph capture, serving loops,
+ * harnesses that forbid hipMalloc). The partial keys live in a fixed device array of
+ * AXON_HIP_ARGMAX_NOALLOC_MAX_ROWS * 64 words (256 KiB) that each GPU holds until the process
+ * ends; more rows are refused with AXON_HIP_E_INVALID. Every call on one GPU shares that array,
+ * so calls that overlap on one GPU (other streams, concurrent graph replays) race. Same ids as
+ * axon_hip_argmax_rows. */
+#define AXON_HIP_ARGMAX_NOALLOC_MAX_ROWS 512
+int axon_hip_argmax_rows_noalloc(const float* x, size_t n, size_t n_rows, size_t stride, int32_t* out);
 /* The top-k candidates of the stochastic sampler stages (src/sampling/sampler.cpp:104-118,
  * std::ranges::partial_sort of the ids by logit, descending): row r's k largest values (rows
  * stride floats apart) into out_logit[r * k + i] with their indices in out_id, descending, equal
