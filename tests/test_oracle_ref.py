@@ -191,3 +191,37 @@ def test_f32_model_matches_numpy_fixture():
         tokens = golden(f"model/{base}.tokens.axt")
         want = golden(f"model/{base}.logits.axt")
         assert np.max(np.abs(om.forward(tokens) - want)) < 1e-4
+
+
+@pytest.mark.parametrize("cfg", ["c1", "c3", "c4", "c5"])
+@pytest.mark.parametrize("f16", [False, True], ids=["f32cache", "f16cache"])
+def test_oracle_model_bit_exact_with_reference_on_config_shapes(cfg, f16, tmp_path_factory):
+    """The BASELINE model shapes at full width, two layers and a 4096-token vocabulary, through
+    the oracle and the reference's own LlamaModel (scalar table): the cache-free pass, a prefill
+    chunk then single cached steps, and a ragged forward_batch, bit for bit, with either cache
+    type. This covers the paths the 2-layer fixtures do not: Q8_0 everywhere with 9/3 heads (C1);
+    Q4_0 with a Q4_1 ffn_down, a Q4_0 embedding, an untied Q6_K output and a GQA group of 8 (C3);
+    llama3 rope factors and a tied Q6_K embedding/output (C4); qwen2 Q/K/V bias, the NeoX layout
+    and a Q8_0 output (C5)."""
+    import synth
+    from dataclasses import replace
+    spec = replace(synth.CONFIGS[cfg], name=f"pin-{cfg}-2l", n_layer=2, n_vocab=4096, seed=21)
+    path = synth.cached_model(spec, tmp_path_factory.getbasetemp() / "pin-models")
+    toks = np.random.default_rng(7).integers(0, spec.n_vocab, 20).astype(np.int32)
+    om = OracleModel(path)
+    rm = RefModel(path, max_seq=32, max_ctx=64, max_batch=4, n_threads=4, f16=f16)
+    full = om.forward(toks)
+    assert np.array_equal(full, rm.forward(toks))
+    oc = om.new_cache(64, f16=f16)
+    rc = rm.new_cache()
+    assert np.array_equal(om.forward(toks[:12], oc), rm.forward_prefill(rc, toks[:12]))
+    for i in range(12, 16):
+        assert np.array_equal(om.forward(toks[i:i + 1], oc), rm.forward_prefill(rc, toks[i:i + 1])), i
+    lens = (2, 7, 13)
+    caches_o = [om.new_cache(64, f16=f16) for _ in lens]
+    caches_r = [rm.new_cache() for _ in lens]
+    for j, n in enumerate(lens):
+        om.forward(toks[:n], caches_o[j])
+        rm.forward_prefill(caches_r[j], toks[:n])
+    nxt = np.array([toks[n] for n in lens], np.int32)
+    assert np.array_equal(om.forward_batch(nxt, caches_o), rm.forward_batch(caches_r, nxt))
