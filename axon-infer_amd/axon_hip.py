@@ -259,6 +259,7 @@ def host() -> C.CDLL:
         L.axon_model_cache_pos.argtypes = [C.c_void_p, C.c_int, C.POINTER(C.c_size_t)]
         L.axon_model_cache_truncate.argtypes = [C.c_void_p, C.c_int, C.c_size_t]
         L.axon_model_cache_read.argtypes = [C.c_void_p, C.c_int, C.c_size_t, C.c_int, C.c_size_t, C.c_void_p]
+        L.axon_model_cache_fill.argtypes = [C.c_void_p, C.c_int, C.c_void_p, C.c_size_t]
         L.axon_model_forward.argtypes = [C.c_void_p, C.c_void_p, C.c_size_t, C.c_void_p]
         L.axon_model_forward_prefill.argtypes = [C.c_void_p, C.c_int, C.c_void_p, C.c_size_t, C.c_void_p]
         L.axon_model_forward_batch.argtypes = [C.c_void_p, C.c_void_p, C.c_void_p, C.c_size_t, C.c_void_p]
@@ -339,6 +340,15 @@ class Model:
         out = np.zeros((n, self.info.n_head_kv * self.info.head_dim), np.float32)
         _mcheck(host().axon_model_cache_read(self.h, cache, layer, int(values), n, out.ctypes.data), "cache_read")
         return out
+
+    def cache_fill(self, cache: int, rows) -> None:
+        """Positions [pos, pos + n) of every layer's K and V from rows [n_layer][2][n][n_kv * head_dim]
+        (float32), as if prefilled (axon_model_cache_fill)."""
+        r = np.ascontiguousarray(rows, np.float32)
+        row = self.info.n_head_kv * self.info.head_dim
+        if r.ndim != 4 or r.shape[0] != self.info.n_layer or r.shape[1] != 2 or r.shape[3] != row:
+            raise ValueError(f"cache_fill: rows of shape {r.shape}, expected [n_layer][2][n][{row}]")
+        _mcheck(host().axon_model_cache_fill(self.h, cache, r.ctypes.data, r.shape[2]), "cache_fill")
 
     def _logits(self, n: int, want: bool):
         return np.zeros((n, self.n_vocab), np.float32) if want else None

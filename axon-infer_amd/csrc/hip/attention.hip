@@ -129,7 +129,7 @@ __global__ __launch_bounds__(kThreads) void attention_kernel(AttnArgs a) {
     for (int w = 1; w < kThreads / 64; ++w) m = fmaxf(m, red_f[w]);
     double sum = 0.0;
     for (uint32_t j = tid; j < n_vis; j += kThreads) {
-      const float e = exp_rounded(s[j] - m);
+      const float e = exp_libm(s[j] - m);
       s[j] = e;
       sum += static_cast<double>(e);
     }
@@ -357,7 +357,7 @@ __global__ __launch_bounds__(kThreads) void attn_mix_kernel(AttnArgs a) {
     for (int w = 1; w < kThreads / 64; ++w) m = fmaxf(m, red_f[w]);
     double sum = 0.0;
     for (uint32_t j = tid; j < n_vis; j += kThreads) {
-      const float e = exp_rounded(row[j] - m);
+      const float e = exp_libm(row[j] - m);
       row[j] = e;
       sum += static_cast<double>(e);
     }
@@ -575,7 +575,7 @@ __global__ __launch_bounds__(64) void attn_mix64_kernel(AttnArgs a) {
 #pragma unroll
   for (int w = 0; w < 4; ++w) {
     for (uint32_t j = lane + 64 * w; j < n_vis; j += 256) {
-      const float e = exp_rounded(p[j] - m);
+      const float e = exp_libm(p[j] - m);
       p[j] = e;
       part[w] += static_cast<double>(e);
     }
@@ -718,7 +718,7 @@ __global__ __launch_bounds__(G * 64) void attn_mixg_kernel(AttnArgs a) {
 #pragma unroll
   for (int q = 0; q < 4; ++q) {
     for (uint32_t j = lane + 64 * q; j < n_vis; j += 256) {
-      const float e = exp_rounded(p[j] - m);
+      const float e = exp_libm(p[j] - m);
       p[j] = e;
       part[q] += static_cast<double>(e);
     }
@@ -932,7 +932,7 @@ __global__ __launch_bounds__(G * 128) void attn_mixd_kernel(AttnArgs a) {
 #pragma unroll
     for (uint32_t i = 0; i < 2; ++i) {
       if (64 * (2 * ss + i) + 256 * k < n_vis) {
-        x[2 * k + i] = exp_rounded(x[2 * k + i] - m);
+        x[2 * k + i] = exp_libm(x[2 * k + i] - m);
         part[i] += static_cast<double>(x[2 * k + i]);
       }
     }

@@ -88,10 +88,48 @@ __device__ __forceinline__ uint32_t float_to_half_bits(float f) {
 
 __device__ __forceinline__ float bf16_bits_to_float(uint32_t h) { return __uint_as_float(h << 16); }
 
-// exp of a binary32 argument, evaluated in binary64 and rounded once: the correctly rounded
-// binary32 exponential except for arguments within ~2^-29 ulp of a rounding midpoint.
-__device__ __forceinline__ float exp_rounded(float x) {
-  return static_cast<float>(exp(static_cast<double>(x)));
+// The binary32 exponential of the host C library the scalar table runs on (std::exp(float) in
+// the reference's softmax and SiLU, src/kernels/ref/softmax.cpp:18, silu.cpp:11): glibc 2.35's
+// expf, the published ARM optimized-routines method (Szabolcs Nagy, 2017). It is not correctly
+// rounded (it differs from the once-rounded binary64 exp on about 1 in 10^4 arguments near 0), so
+// bit parity needs its steps, restated here: with N = 32, k = round(x N / ln 2) and
+// r = x N / ln 2 - k (one fused multiply-add), exp(x) = 2^(k/N) (1 + C2 r + C1 r^2 + C0 r^3) in
+// binary64, rounded once to binary32. 2^(k/N) is kExp2Tab[k mod N] with k/N added to its exponent
+// field; entry i is 2^(i/N) rounded to binary64, less i << 47 (so that adding k << 47 carries
+// the whole of k/N into the exponent). Checked against the host's expf on every binary32
+// argument of the main range (x in (-103.97, 88.72), 2.24e9 values): identical. Outside it
+// expf is 0 (underflow), +inf (overflow) or NaN (x + x).
+__device__ const uint64_t kExp2Tab[32] = {
+  0x3ff0000000000000ull, 0x3fefd9b0d3158574ull, 0x3fefb5586cf9890full, 0x3fef9301d0125b51ull,
+  0x3fef72b83c7d517bull, 0x3fef54873168b9aaull, 0x3fef387a6e756238ull, 0x3fef1e9df51fdee1ull,
+  0x3fef06fe0a31b715ull, 0x3feef1a7373aa9cbull, 0x3feedea64c123422ull, 0x3feece086061892dull,
+  0x3feebfdad5362a27ull, 0x3feeb42b569d4f82ull, 0x3feeab07dd485429ull, 0x3feea47eb03a5585ull,
+  0x3feea09e667f3bcdull, 0x3fee9f75e8ec5f74ull, 0x3feea11473eb0187ull, 0x3feea589994cce13ull,
+  0x3feeace5422aa0dbull, 0x3feeb737b0cdc5e5ull, 0x3feec49182a3f090ull, 0x3feed503b23e255dull,
+  0x3feee89f995ad3adull, 0x3feeff76f2fb5e47ull, 0x3fef199bdd85529cull, 0x3fef3720dcef9069ull,
+  0x3fef5818dcfba487ull, 0x3fef7c97337b9b5full, 0x3fefa4afa2a490daull, 0x3fefd0765b6e4540ull,
+};
+
+__device__ __forceinline__ float exp_libm(float x) {
+  constexpr double kInvLn2N = 0x1.71547652b82fep+0 * 32;  // N / ln 2
+  constexpr double kShift = 0x1.8p+52;                    // adds and strips to round to an integer
+  constexpr double kC0 = 0x1.c6af84b912394p-5 / 32 / 32 / 32;
+  constexpr double kC1 = 0x1.ebfce50fac4f3p-3 / 32 / 32;
+  constexpr double kC2 = 0x1.62e42ff0c52d6p-1 / 32;
+  if (x != x) return x + x;
+  if (x > 0x1.62e42ep6f) return __builtin_inff();
+  if (x < -0x1.9fe368p6f) return 0.0f;
+  const double xd = static_cast<double>(x);
+  double kd = kInvLn2N * xd + kShift;
+  const uint64_t ki = static_cast<uint64_t>(__double_as_longlong(kd));
+  kd -= kShift;
+  const double r = fma(kInvLn2N, xd, -kd);
+  const double s = __longlong_as_double(static_cast<long long>(kExp2Tab[ki & 31u] + (ki << 47)));
+  const double p = kC0 * r + kC1;
+  const double r2 = r * r;
+  double y = kC2 * r + 1.0;
+  y = p * r2 + y;
+  return static_cast<float>(y * s);
 }
 
 // ------------------------------------------------------------------------------------------

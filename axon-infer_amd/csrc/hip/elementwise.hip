@@ -119,7 +119,7 @@ __global__ __launch_bounds__(256) void silu_mul_kernel(const float* __restrict__
     for (size_t i = static_cast<size_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < total;
          i += static_cast<size_t>(gridDim.x) * blockDim.x) {
       const float g = gate[i];
-      out[i] = g / (1.0f + exp_rounded(-g)) * up[i];
+      out[i] = g / (1.0f + exp_libm(-g)) * up[i];
     }
     return;
   }
@@ -130,7 +130,7 @@ __global__ __launch_bounds__(256) void silu_mul_kernel(const float* __restrict__
        blk += static_cast<size_t>(gridDim.x) * (blockDim.x / 32)) {
     const size_t i = blk * kQK + lane;
     const float g = gate[i];
-    const float v = g / (1.0f + exp_rounded(-g)) * up[i];
+    const float v = g / (1.0f + exp_libm(-g)) * up[i];
     if (out != nullptr) out[i] = v;
     quantize_block_lanes(v, lane, outq + blk * kBytesQ8_0);
   }
@@ -146,7 +146,7 @@ __global__ __launch_bounds__(256) void softmax_kernel(float* x, uint32_t n) {
   m = block_max(m, redf);
   double s = 0.0;
   for (uint32_t i = threadIdx.x; i < n; i += blockDim.x) {
-    const float e = exp_rounded(x[i] - m);
+    const float e = exp_libm(x[i] - m);
     x[i] = e;
     s += static_cast<double>(e);
   }

@@ -626,8 +626,8 @@ __global__ __launch_bounds__(kThreads) void mfma_tile_kernel(MatvecArgs args) {
     for (int v = 0; v < 4; ++v) {
       const uint32_t rr = orow + v;
       const float g0 = acc[0][v], g1 = acc[1][v];
-      const float y0 = g0 / (1.0f + exp_rounded(-g0)) * acc[2][v];
-      const float y1 = g1 / (1.0f + exp_rounded(-g1)) * acc[3][v];
+      const float y0 = g0 / (1.0f + exp_libm(-g0)) * acc[2][v];
+      const float y1 = g1 / (1.0f + exp_libm(-g1)) * acc[3][v];
       float amax = fmaxf(fabsf(y0), fabsf(y1));
 #pragma unroll
       for (int off = 8; off > 0; off >>= 1) amax = fmaxf(amax, __shfl_xor(amax, off, 64));

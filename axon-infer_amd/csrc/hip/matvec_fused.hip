@@ -231,7 +231,7 @@ __device__ __forceinline__ void fused_body(const FusedArgs& args, const WgRows& 
       const uint32_t r = tid - m * nr;
       const float gt = outv[m * 2 * R + r];
       const float u = outv[m * 2 * R + g.pitch_rows + r];
-      const float h = gt / (1.0f + exp_rounded(-gt)) * u;
+      const float h = gt / (1.0f + exp_libm(-gt)) * u;
       args.y[0][static_cast<size_t>(m) * args.y_stride[0] + r0 + r] = h;
       // Q8_0 blocks of h (the launcher gives each workgroup whole blocks: 32 rows, so the 32
       // outputs of one block sit in 32 aligned lanes, r = lane % 32).

@@ -139,6 +139,13 @@ int axon_model_cache_read(axon_model* model, int cache, size_t layer, int values
   return 0;
 }
 
+int axon_model_cache_fill(axon_model* model, int cache, const float* rows, size_t n) {
+  axon::model::KVCache* c = find(model, cache);
+  if (c == nullptr) return fail("cache_fill: unknown cache " + std::to_string(cache));
+  auto r = model->m->fill_cache(*c, rows, n);
+  return r ? 0 : fail(r.error());
+}
+
 int axon_model_forward(axon_model* model, const int32_t* tokens, size_t n, float* logits) {
   if (logits == nullptr) {
     auto r = model->m->forward_device(std::span<const int32_t>(tokens, n));

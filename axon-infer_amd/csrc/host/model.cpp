@@ -32,6 +32,30 @@ float half_to_float(std::uint16_t h) {
   return out;
 }
 
+// float to fp16 bits, rounding to nearest even; overflow to infinity, NaN stays NaN (the
+// payload's top ten bits, at least 1), as src/core/dtype.cpp fp32_to_fp16 specifies.
+std::uint16_t float_to_half(float f) {
+  std::uint32_t b;
+  std::memcpy(&b, &f, 4);
+  const auto sign = static_cast<std::uint16_t>((b >> 16) & 0x8000u);
+  const std::uint32_t a = b & 0x7fffffffu;
+  if (a >= 0x7f800000u) {
+    const std::uint32_t payload = (a >> 13) & 0x3ffu;
+    return static_cast<std::uint16_t>(sign | 0x7c00u | (a == 0x7f800000u ? 0u : (payload != 0 ? payload : 1u)));
+  }
+  if (a >= 0x477ff000u) return static_cast<std::uint16_t>(sign | 0x7c00u);  // at or past 65520: infinity
+  if (a >= 0x38800000u) {  // a normal half: rebias the exponent, round the 13 dropped bits
+    std::uint32_t m = a - 0x38000000u;
+    m += 0xfffu + ((m >> 13) & 1u);
+    return static_cast<std::uint16_t>(sign | (m >> 13));
+  }
+  // A subnormal half (or zero): the value in units of 2^-24, rounded to nearest even (scaling by
+  // a power of two is exact).
+  float mag;
+  std::memcpy(&mag, &a, 4);
+  return static_cast<std::uint16_t>(sign | static_cast<std::uint16_t>(std::nearbyint(mag * 16777216.0f)));
+}
+
 bool matmul_type(DType t) {
   switch (t) {
   case DType::F32: case DType::F16: case DType::BF16: case DType::Q8_0: case DType::Q4_0: case DType::Q4_1:
@@ -416,6 +440,36 @@ Expected<std::vector<float>> LlamaModel::read_cache(const KVCache& cache, std::s
     return device_error("read_cache");
   for (std::size_t i = 0; i < bits.size(); ++i) out[i] = half_to_float(bits[i]);
   return out;
+}
+
+Expected<bool> LlamaModel::fill_cache(KVCache& cache, const float* rows, std::size_t n) {
+  if (cache.slot() < 0 || static_cast<std::size_t>(cache.slot()) >= n_slots_)
+    return make_error(ErrorCode::InvalidArgument, "fill_cache: the cache was built for a different model");
+  if (cache.pos() + n > max_ctx_)
+    return make_error(ErrorCode::InvalidArgument, "context overflow: " + std::to_string(cache.pos()) + " cached + " +
+                                                      std::to_string(n) + " filled positions exceed " +
+                                                      std::to_string(max_ctx_));
+  if (n == 0) return true;
+  if (rows == nullptr) return make_error(ErrorCode::InvalidArgument, "fill_cache: no rows");
+  const std::size_t dkv = cfg_.n_embd_kv();
+  const std::size_t span = n * dkv;
+  std::vector<std::uint16_t> half(cache_type_ == CacheType::F16 ? span : 0);
+  for (std::size_t l = 0; l < cfg_.n_layer; ++l) {
+    for (std::size_t kv = 0; kv < 2; ++kv) {
+      const float* src = rows + (2 * l + kv) * span;
+      const std::size_t at = cache.slot() * slot_elems_ + (2 * l + kv) * max_ctx_ * dkv + cache.pos() * dkv;
+      int rc;
+      if (cache_type_ == CacheType::F32) {
+        rc = axon_hip_memcpy_h2d(static_cast<float*>(kv_) + at, src, span * 4);
+      } else {
+        for (std::size_t i = 0; i < span; ++i) half[i] = float_to_half(src[i]);
+        rc = axon_hip_memcpy_h2d(static_cast<std::uint16_t*>(kv_) + at, half.data(), span * 2);
+      }
+      if (rc != AXON_HIP_OK) return device_error("fill_cache");
+    }
+  }
+  cache.advance(n);
+  return true;
 }
 
 bool LlamaModel::q8_path(const Tensor& w) const {

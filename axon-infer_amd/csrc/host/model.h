@@ -138,6 +138,12 @@ public:
   void release_cache(const KVCache& cache);
   // Copies rows [0, n) of layer l's K or V of a cache to the host as floats (tests).
   Expected<std::vector<float>> read_cache(const KVCache& cache, std::size_t layer, bool values, std::size_t n);
+  // Writes positions [pos, pos + n) of every layer's K and V from host rows laid out
+  // [n_layer][2][n][n_head_kv * head_dim] (K then V per layer) and advances the cache, as if
+  // those positions had been prefilled; an fp16 cache takes each float rounded to nearest even
+  // once, as its own writes do (kv_cache.h:34-43). For restoring a saved context, and for tests
+  // that start the device and a reference from the same cache contents.
+  Expected<bool> fill_cache(KVCache& cache, const float* rows, std::size_t n);
 
   // Kernel-time probe: while enabled, every matmul launch on weights of `type` (one ggml type
   // id) is bracketed by HIP events on the library stream. read_probe sums the bracketed device

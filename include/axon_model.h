@@ -61,6 +61,13 @@ int axon_model_cache_truncate(axon_model* model, int cache, size_t pos);
 /* Rows [0, n) of layer l's keys (values = 0) or values (1) of a cache, to the host as floats
  * (fp16 elements widened exactly). */
 int axon_model_cache_read(axon_model* model, int cache, size_t layer, int values, size_t n, float* out);
+/* Writes positions [pos, pos + n) of every layer's keys and values from host floats laid out
+ * [n_layer][2][n][n_head_kv * head_dim] (K then V per layer) and advances the cache, as if they
+ * had been prefilled; an fp16 cache rounds each value to nearest even once. No counterpart entry
+ * in the reference, whose KVCache exposes the same rows as host pointers (kv_cache.h:22-40): this is
+ * how a caller restores a saved context into device memory, and how tests start the device and
+ * the reference from the same cache contents. */
+int axon_model_cache_fill(axon_model* model, int cache, const float* rows, size_t n);
 
 /* The passes. logits: host [n][n_vocab], or NULL to leave them in HBM for axon_model_greedy (or
  * for timing the pass alone). */

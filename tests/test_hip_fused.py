@@ -162,10 +162,8 @@ def test_norm_silu_matches_unfused(H, o, kind, n_rows, n_in, ff):
     og = oracle_rows(o, kind, wg, normed, ff, n_in)
     ou = oracle_rows(o, kind, wu, normed, ff, n_in)
     assert np.array_equal(gate.download(np.float32).reshape(n_rows, ff), og)
-    # exp differs from the oracle's expf by at most 1 ulp; the division and the product after it
-    # can carry that to 2 ulp of the result.
     want = np.stack([o.silu_mul(og[i], ou[i]) for i in range(n_rows)])
-    assert ulp_diff(got, want) <= 2
+    assert np.array_equal(got, want)
 
 
 @pytest.mark.parametrize("kind", KINDS)
