@@ -61,7 +61,10 @@ __global__ __launch_bounds__(kThreads) void attention_kernel(AttnArgs a) {
   float* qs = lds;                                   // [nh][hd]
   __shared__ double red_d[kThreads / 64];
   __shared__ float red_f[kThreads / 64];
-  float* sc = GLOBAL ? a.scratch + (static_cast<size_t>(r) * gridDim.y + g) * group * a.max_vis : lds + group * hd;
+  // The global scratch holds [row][head - head_begin][max_vis]: the heads of this launch only.
+  float* sc = GLOBAL ? a.scratch + (static_cast<size_t>(r) * (a.head_end - a.head_begin) + (h_lo - a.head_begin)) *
+                                       a.max_vis
+                     : lds + group * hd;
   const uint32_t pitch = GLOBAL ? a.max_vis : round4(n_vis);
 
   // 16-byte loads of K rows when every row of this span is 16-byte aligned.
@@ -1169,6 +1172,19 @@ int attention_launch(const AttnArgs& a, uint32_t n_rows) {
   const dim3 grid(n_rows, a.n_kv);
   const bool lds_ok = scores_fit_lds(a);
   if (!lds_ok && a.scratch == nullptr) return fail(kInvalidArgument, "attention: %u positions need a score scratch", a.max_vis);
+  if (!lds_ok && !a.split && a.head_end - a.head_begin > 1) {
+    // A table call (src/kernels/kernels.h:67-75) brings scratch for one head's scores,
+    // n_q * (n_past + n_q) floats: its heads run one launch each, in stream order, each
+    // reusing that scratch.
+    for (uint32_t h = a.head_begin; h < a.head_end; ++h) {
+      AttnArgs b = a;
+      b.head_begin = h;
+      b.head_end = h + 1;
+      const int rc = attention_launch(b, n_rows);
+      if (rc != kOk) return rc;
+    }
+    return kOk;
+  }
   const size_t tile = a.head_dim <= 128 ? vtile_bytes(a.head_dim) : 0;
   const size_t lds = (lds_ok ? static_cast<size_t>(group) * (a.head_dim + round4(a.max_vis)) * 4
                              : static_cast<size_t>(group) * a.head_dim * 4) + tile;

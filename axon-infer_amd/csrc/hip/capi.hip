@@ -319,7 +319,14 @@ int axon_hip_memcpy_h2d_async(void* dst, const void* src, size_t bytes) {
 int axon_hip_memset(void* dst, int value, size_t bytes) {
   AXON_READY();
   if (bytes == 0) return kOk;
-  hipError_t e = hipMemsetAsync(dst, value, bytes, g_stream);
+  // A memset node in a captured graph is not replayed reliably on this platform, and the
+  // synchronize below is illegal under capture: refuse while axon_hip_graph_begin is open.
+  hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+  hipError_t e = hipStreamIsCapturing(g_stream, &cap);
+  if (e != hipSuccess) return hip_fail(e, "memset: hipStreamIsCapturing");
+  if (cap != hipStreamCaptureStatusNone)
+    return fail(kInvalidArgument, "memset: refused while a graph capture is open on the library stream");
+  e = hipMemsetAsync(dst, value, bytes, g_stream);
   if (e == hipSuccess) e = hipStreamSynchronize(g_stream);
   return e == hipSuccess ? kOk : hip_fail(e, "memset");
 }

@@ -5,6 +5,7 @@
 #include <sys/stat.h>
 #include <unistd.h>
 
+#include <cstdint>
 #include <cstring>
 #include <utility>
 
@@ -168,6 +169,15 @@ Expected<GgufFile> GgufFile::open(const std::string& path) {
     t.n_dims = r.get<std::uint32_t>();
     if (!r.ok || t.n_dims == 0 || t.n_dims > 4) return corrupt(path, "tensor " + t.name + ": bad dimension count");
     for (std::uint32_t d = 0; d < t.n_dims; ++d) t.ne[d] = r.get<std::uint64_t>();
+    if (!r.ok) return corrupt(path, "truncated tensor info");
+    // Every extent non-zero and the element count representable, so that the byte size
+    // computed below cannot wrap around to something that passes the bounds check.
+    std::uint64_t elements = 1;
+    for (std::uint32_t d = 0; d < t.n_dims; ++d) {
+      if (t.ne[d] == 0) return corrupt(path, "tensor " + t.name + ": an extent of zero");
+      if (t.ne[d] > UINT64_MAX / elements) return corrupt(path, "tensor " + t.name + ": element count overflows 64 bits");
+      elements *= t.ne[d];
+    }
     t.type = static_cast<DType>(r.get<std::uint32_t>());
     const auto offset = r.get<std::uint64_t>();
     if (!r.ok) return corrupt(path, "truncated tensor info");
@@ -178,13 +188,14 @@ Expected<GgufFile> GgufFile::open(const std::string& path) {
   const std::size_t data = (r.off + align - 1) / align * align;
   if (data > size) return corrupt(path, "data section past the end of the file");
   for (auto& [t, offset] : infos) {
+    if (t.ne[0] > (SIZE_MAX >> 3)) return corrupt(path, "tensor " + t.name + ": row length overflows");
     const std::size_t row = row_bytes_of(t.type, t.ne[0]);
     if (row == 0) {
       // Types outside the table's set are kept as size 0; binding rejects them by name.
       t.nbytes = 0;
     } else {
-      std::uint64_t rows = 1;
-      for (std::uint32_t d = 1; d < t.n_dims; ++d) rows *= t.ne[d];
+      const std::uint64_t rows = (t.n_dims > 1 ? t.ne[1] : 1) * (t.n_dims > 2 ? t.ne[2] : 1) * (t.n_dims > 3 ? t.ne[3] : 1);
+      if (rows > SIZE_MAX / row) return corrupt(path, "tensor " + t.name + ": byte size overflows");
       t.nbytes = row * rows;
     }
     if (offset > size - data || t.nbytes > size - data - offset) return corrupt(path, "tensor " + t.name + " out of bounds");

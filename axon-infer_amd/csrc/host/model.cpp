@@ -92,47 +92,63 @@ Expected<Tensor> bind_tensor(const GgufFile& f, const std::string& name, Kind ki
   return out;
 }
 
+// The model's shape from the file's metadata. The keys, their defaults and the detection of
+// tied embeddings, Q/K/V bias and llama3 rope factors are the GGUF contract the reference reads
+// (src/model/config.cpp:27-123); the validation is this library's.
 Expected<Config> config_of(const GgufFile& f) {
   Config c;
   c.arch = f.string_or("general.architecture", "");
-  if (c.arch == "llama") {
-    c.rope_style = kernels::RopeStyle::Normal;
-  } else if (c.arch == "qwen2") {
-    c.rope_style = kernels::RopeStyle::NeoX;
-  } else {
-    return make_error(ErrorCode::Unsupported, "general.architecture: expected llama or qwen2, found '" + c.arch + "'");
-  }
-  const auto key = [&](const char* s) { return c.arch + "." + s; };
-  const char* required[] = {"block_count", "embedding_length", "attention.head_count", "feed_forward_length",
-                            "context_length"};
-  std::uint32_t* fields[] = {&c.n_layer, &c.n_embd, &c.n_head, &c.n_ff, &c.n_ctx_train};
-  for (int i = 0; i < 5; ++i) {
-    const GgufValue* v = f.meta(key(required[i]));
+  if (c.arch != "llama" && c.arch != "qwen2")
+    return make_error(ErrorCode::Unsupported, "model architecture '" + c.arch + "' is not supported (llama, qwen2)");
+  c.rope_style = c.arch == "qwen2" ? kernels::RopeStyle::NeoX : kernels::RopeStyle::Normal;
+  const std::string ns = c.arch + ".";
+
+  // Required extents first, then the ones that default to a value derived from them.
+  struct Extent {
+    const char* name;
+    std::uint32_t* field;
+  };
+  for (const Extent& e : {Extent{"block_count", &c.n_layer}, Extent{"embedding_length", &c.n_embd},
+                          Extent{"attention.head_count", &c.n_head}, Extent{"feed_forward_length", &c.n_ff},
+                          Extent{"context_length", &c.n_ctx_train}}) {
+    const GgufValue* v = f.meta(ns + e.name);
     if (v == nullptr || v->kind != GgufValue::Kind::UInt || v->u > 0xffffffffull)
-      return make_error(ErrorCode::InvalidArgument, key(required[i]) + ": missing or not a 32-bit unsigned value");
-    *fields[i] = static_cast<std::uint32_t>(v->u);
+      return make_error(ErrorCode::InvalidArgument, ns + e.name + " is absent or not an unsigned 32-bit value");
+    *e.field = static_cast<std::uint32_t>(v->u);
   }
-  c.n_head_kv = static_cast<std::uint32_t>(f.uint_or(key("attention.head_count_kv"), c.n_head));
-  if (c.n_layer == 0 || c.n_embd == 0 || c.n_head == 0 || c.n_ff == 0)
-    return make_error(ErrorCode::InvalidArgument, c.arch + ": layer, embedding, head and feed-forward counts must be non-zero");
+  if (c.n_layer * std::uint64_t{c.n_embd} * c.n_head * c.n_ff == 0)
+    return make_error(ErrorCode::InvalidArgument,
+                      "model shape has an empty extent: " + std::to_string(c.n_layer) + " layers, width " +
+                          std::to_string(c.n_embd) + ", " + std::to_string(c.n_head) + " heads, feed-forward " +
+                          std::to_string(c.n_ff));
+  c.n_head_kv = static_cast<std::uint32_t>(f.uint_or(ns + "attention.head_count_kv", c.n_head));
+  c.head_dim = static_cast<std::uint32_t>(f.uint_or(ns + "attention.key_length", c.n_embd / c.n_head));
+  c.rotary_dim = static_cast<std::uint32_t>(f.uint_or(ns + "rope.dimension_count", c.head_dim));
+  c.rope_theta = static_cast<float>(f.float_or(ns + "rope.freq_base", 10000.0));
+  c.rms_eps = static_cast<float>(f.float_or(ns + "attention.layer_norm_rms_epsilon", 1e-5));
   if (c.n_head_kv == 0 || c.n_head % c.n_head_kv != 0)
-    return make_error(ErrorCode::InvalidArgument, key("attention.head_count_kv") + ": does not divide head_count");
-  c.head_dim = static_cast<std::uint32_t>(f.uint_or(key("attention.key_length"), c.n_embd / c.n_head));
-  if (c.head_dim == 0 || c.head_dim % 2 != 0) return make_error(ErrorCode::InvalidArgument, c.arch + ": expected an even head size");
-  c.rotary_dim = static_cast<std::uint32_t>(f.uint_or(key("rope.dimension_count"), c.head_dim));
+    return make_error(ErrorCode::InvalidArgument, std::to_string(c.n_head_kv) + " key/value heads cannot serve " +
+                                                      std::to_string(c.n_head) + " query heads in equal groups");
+  if (c.head_dim == 0 || c.head_dim % 2 != 0)
+    return make_error(ErrorCode::InvalidArgument, "head size " + std::to_string(c.head_dim) + " is not a positive even number");
   if (c.rotary_dim == 0 || c.rotary_dim % 2 != 0 || c.rotary_dim > c.head_dim)
-    return make_error(ErrorCode::InvalidArgument, key("rope.dimension_count") + ": expected an even value up to the head size");
-  c.rope_theta = static_cast<float>(f.float_or(key("rope.freq_base"), 10000.0));
-  c.rms_eps = static_cast<float>(f.float_or(key("attention.layer_norm_rms_epsilon"), 1e-5));
+    return make_error(ErrorCode::InvalidArgument, "rotary width " + std::to_string(c.rotary_dim) +
+                                                      " must be positive, even and within the head size " +
+                                                      std::to_string(c.head_dim));
+
+  // The vocabulary is the embedding's row count; the declared sizes must agree with it.
   const GgufTensor* embd = f.tensor("token_embd.weight");
-  if (embd == nullptr) return make_error(ErrorCode::InvalidArgument, "token_embd.weight: missing");
+  if (embd == nullptr) return make_error(ErrorCode::InvalidArgument, "the token embedding (token_embd.weight) is absent");
   if (embd->n_dims != 2 || embd->ne[0] != c.n_embd)
-    return make_error(ErrorCode::InvalidArgument, "token_embd.weight: expected shape " + std::to_string(c.n_embd) + "xN");
+    return make_error(ErrorCode::InvalidArgument, "token_embd.weight rows are " + std::to_string(embd->ne[0]) +
+                                                      " wide, not the model width " + std::to_string(c.n_embd));
   c.n_vocab = static_cast<std::uint32_t>(embd->ne[1]);
-  if (const GgufValue* vs = f.meta(key("vocab_size")); vs != nullptr && vs->u != c.n_vocab)
-    return make_error(ErrorCode::InvalidArgument, key("vocab_size") + ": differs from the embedding rows");
+  const std::string vocab_rows = std::to_string(c.n_vocab) + " embedding rows";
+  if (const GgufValue* vs = f.meta(ns + "vocab_size"); vs != nullptr && vs->u != c.n_vocab)
+    return make_error(ErrorCode::InvalidArgument, ns + "vocab_size says " + std::to_string(vs->u) + " for " + vocab_rows);
   if (const GgufValue* toks = f.meta("tokenizer.ggml.tokens"); toks != nullptr && toks->array_size != c.n_vocab)
-    return make_error(ErrorCode::InvalidArgument, "tokenizer.ggml.tokens: expected one entry per embedding row");
+    return make_error(ErrorCode::InvalidArgument,
+                      "the tokenizer lists " + std::to_string(toks->array_size) + " tokens for " + vocab_rows);
   c.tie_embeddings = f.tensor("output.weight") == nullptr;
   c.attn_bias = f.tensor("blk.0.attn_q.bias") != nullptr;
   c.llama3 = f.tensor("rope_freqs.weight") != nullptr;
@@ -344,6 +360,14 @@ Expected<std::unique_ptr<LlamaModel>> LlamaModel::load(const std::string& path, 
       axon_hip_malloc(reinterpret_cast<void**>(&m->scores_), m->scores_floats_ * 4) != AXON_HIP_OK)
     return m->device_error("attention scratch");
   m->slot_used_.assign(m->n_slots_, false);
+  // Host staging that every pass reuses: the row list, the logits of max_rows rows, and the
+  // sampler's per-row flags, so that a pass allocates no host memory.
+  m->rows_.resize(R);
+  m->logits_host_.reserve(R * c.n_vocab);
+  m->sample_done_.reserve(R);
+  m->sample_select_.reserve(R);
+  m->cand_host_.reserve(R * AXON_HIP_MAX_TOPK * 8);
+  m->probs_.reserve(AXON_HIP_MAX_TOPK);
   m->file_ = std::make_unique<GgufFile>(std::move(*file));
   return m;
 }
@@ -385,12 +409,17 @@ void LlamaModel::probe_begin(const Tensor& w) {
   axon_hip_probe_next_launch(probe_events_[2 * probe_used_], probe_events_[2 * probe_used_ + 1]);
 }
 
-void LlamaModel::probe_end(const Tensor& w, std::size_t n_rows, std::size_t n_out_total, bool accumulate) {
+void LlamaModel::probe_cancel() { axon_hip_probe_next_launch(nullptr, nullptr); }
+
+void LlamaModel::probe_end(const Tensor& w, std::size_t n_rows, std::size_t n_out_total, bool accumulate,
+                           double out_bytes_override) {
   if (static_cast<int>(w.type) != probe_type_ || 2 * probe_used_ + 2 > probe_events_.size()) return;
   axon_hip_probe_next_launch(nullptr, nullptr);
   const double in_bytes = q8_path(w) ? static_cast<double>(n_rows) * (w.ne0 / 32) * sizeof(BlockQ8_0)
                                      : static_cast<double>(n_rows) * w.ne0 * 4.0;
-  const double out_bytes = static_cast<double>(n_rows) * n_out_total * 4.0 * (accumulate ? 2 : 1);
+  const double out_bytes = out_bytes_override >= 0
+                               ? out_bytes_override
+                               : static_cast<double>(n_rows) * n_out_total * 4.0 * (accumulate ? 2 : 1);
   probe_bytes_.push_back(static_cast<double>(w.row_bytes) * n_out_total + in_bytes + out_bytes);
   ++probe_used_;
 }
@@ -781,7 +810,12 @@ Expected<std::size_t> LlamaModel::run(std::span<const Row> rows, bool copy_logit
       probe_begin(L.w_gate);
       const int rc = axon_hip_matmul_q8_swiglu(static_cast<int>(L.w_gate.type), xq_, n, d, L.w_gate.dev, L.w_up.dev,
                                                ff, nullptr, tmp_);
-      probe_end(L.w_gate, n, 2 * ff, false);
+      if (rc == AXON_HIP_OK) {
+        // Its output is down's Q8_0 blocks, not 2 * ff floats per row.
+        probe_end(L.w_gate, n, 2 * ff, false, static_cast<double>(n) * (ff / 32) * sizeof(BlockQ8_0));
+      } else {
+        probe_cancel();  // refused: nothing was launched, so no event pair was recorded
+      }
       if (rc == AXON_HIP_OK) {
         swiglu = true;
         down_xq = tmp_;
@@ -933,7 +967,10 @@ Expected<std::size_t> LlamaModel::sample(std::span<std::int32_t> ids, std::span<
   last_rows_ = 0;
   // The penalty, once per distinct (penalty, window) setting among the rows.
   if (!recent.empty()) {
-    std::vector<std::uint8_t> done(n, 0), select(n, 0);
+    std::vector<std::uint8_t>& done = sample_done_;
+    std::vector<std::uint8_t>& select = sample_select_;
+    done.assign(n, 0);
+    select.assign(n, 0);
     for (std::size_t r = 0; r < n; ++r) {
       if (done[r] != 0) continue;
       for (std::size_t q = r; q < n; ++q) {
@@ -983,19 +1020,18 @@ Expected<std::span<const float>> LlamaModel::forward_rows(std::span<const std::i
   if (tokens.empty()) return make_error(ErrorCode::InvalidArgument, "forward: empty token sequence");
   if (tokens.size() > max_seq_)
     return make_error(ErrorCode::InvalidArgument, "forward: " + std::to_string(tokens.size()) + " tokens exceed max_seq");
-  std::vector<Row> rows(tokens.size());
   for (std::size_t i = 0; i < tokens.size(); ++i) {
     if (tokens[i] < 0 || static_cast<std::uint32_t>(tokens[i]) >= cfg_.n_vocab)
       return make_error(ErrorCode::InvalidArgument, "forward: token id " + std::to_string(tokens[i]) + " outside the vocabulary");
-    rows[i] = Row{tokens[i], static_cast<std::int32_t>(i), static_cast<int>(n_slots_)};
+    rows_[i] = Row{tokens[i], static_cast<std::int32_t>(i), static_cast<int>(n_slots_)};
   }
-  auto r = run(rows, copy_logits);
+  auto r = run(std::span<const Row>(rows_.data(), tokens.size()), copy_logits);
   if (!r) return r.error();
   return std::span<const float>(logits_host_);
 }
 
-Expected<std::vector<LlamaModel::Row>> LlamaModel::prefill_rows(const KVCache& cache,
-                                                                 std::span<const std::int32_t> tokens) const {
+Expected<std::size_t> LlamaModel::prefill_rows(const KVCache& cache, std::span<const std::int32_t> tokens,
+                                               std::size_t at) {
   if (tokens.empty()) return make_error(ErrorCode::InvalidArgument, "forward: empty token sequence");
   if (tokens.size() > max_seq_)
     return make_error(ErrorCode::InvalidArgument, "forward: " + std::to_string(tokens.size()) + " tokens exceed max_seq");
@@ -1003,28 +1039,27 @@ Expected<std::vector<LlamaModel::Row>> LlamaModel::prefill_rows(const KVCache& c
     return make_error(ErrorCode::InvalidArgument, "context overflow: " + std::to_string(cache.pos()) + " cached + " +
                                                       std::to_string(tokens.size()) + " new tokens exceed " +
                                                       std::to_string(cache.max_ctx()));
-  std::vector<Row> rows(tokens.size());
   for (std::size_t i = 0; i < tokens.size(); ++i) {
     if (tokens[i] < 0 || static_cast<std::uint32_t>(tokens[i]) >= cfg_.n_vocab)
       return make_error(ErrorCode::InvalidArgument, "forward: token id " + std::to_string(tokens[i]) + " outside the vocabulary");
-    rows[i] = Row{tokens[i], static_cast<std::int32_t>(cache.pos() + i), cache.slot()};
+    rows_[at + i] = Row{tokens[i], static_cast<std::int32_t>(cache.pos() + i), cache.slot()};
   }
-  return rows;
+  return tokens.size();
 }
 
 Expected<std::span<const float>> LlamaModel::forward_prefill(KVCache& cache, std::span<const std::int32_t> tokens) {
-  auto rows = prefill_rows(cache, tokens);
+  auto rows = prefill_rows(cache, tokens, 0);
   if (!rows) return rows.error();
-  auto r = run(*rows, true);
+  auto r = run(std::span<const Row>(rows_.data(), *rows), true);
   if (!r) return r.error();
   cache.advance(tokens.size());
   return std::span<const float>(logits_host_);
 }
 
 Expected<std::size_t> LlamaModel::forward_prefill_device(KVCache& cache, std::span<const std::int32_t> tokens) {
-  auto rows = prefill_rows(cache, tokens);
+  auto rows = prefill_rows(cache, tokens, 0);
   if (!rows) return rows.error();
-  auto r = run(*rows, false);
+  auto r = run(std::span<const Row>(rows_.data(), *rows), false);
   if (!r) return r.error();
   cache.advance(tokens.size());
   return *r;
@@ -1034,8 +1069,8 @@ Expected<std::span<const float>> LlamaModel::forward_one(KVCache& cache, std::in
   return forward_prefill(cache, std::span<const std::int32_t>(&token, 1));
 }
 
-Expected<std::vector<LlamaModel::Row>> LlamaModel::batch_rows(std::span<KVCache* const> caches,
-                                                               std::span<const std::int32_t> tokens) const {
+Expected<std::size_t> LlamaModel::batch_rows(std::span<KVCache* const> caches, std::span<const std::int32_t> tokens,
+                                             std::size_t at) {
   // The checks of llama.cpp:269-302.
   if (caches.empty() || caches.size() != tokens.size())
     return make_error(ErrorCode::InvalidArgument, "forward_batch: " + std::to_string(caches.size()) + " caches for " +
@@ -1043,7 +1078,6 @@ Expected<std::vector<LlamaModel::Row>> LlamaModel::batch_rows(std::span<KVCache*
   if (caches.size() > max_batch_)
     return make_error(ErrorCode::InvalidArgument, "forward_batch: " + std::to_string(caches.size()) +
                                                       " sequences exceed max_batch " + std::to_string(max_batch_));
-  std::vector<Row> rows(tokens.size());
   for (std::size_t i = 0; i < caches.size(); ++i) {
     const KVCache* cache = caches[i];
     if (cache == nullptr || cache->slot() < 0 || static_cast<std::size_t>(cache->slot()) >= n_slots_ ||
@@ -1059,16 +1093,16 @@ Expected<std::vector<LlamaModel::Row>> LlamaModel::batch_rows(std::span<KVCache*
     }
     if (tokens[i] < 0 || static_cast<std::uint32_t>(tokens[i]) >= cfg_.n_vocab)
       return make_error(ErrorCode::InvalidArgument, "forward: token id " + std::to_string(tokens[i]) + " outside the vocabulary");
-    rows[i] = Row{tokens[i], static_cast<std::int32_t>(cache->pos()), cache->slot()};
+    rows_[at + i] = Row{tokens[i], static_cast<std::int32_t>(cache->pos()), cache->slot()};
   }
-  return rows;
+  return tokens.size();
 }
 
 Expected<std::span<const float>> LlamaModel::forward_batch(std::span<KVCache* const> caches,
                                                            std::span<const std::int32_t> tokens) {
-  auto rows = batch_rows(caches, tokens);
+  auto rows = batch_rows(caches, tokens, 0);
   if (!rows) return rows.error();
-  auto r = run(*rows, true);
+  auto r = run(std::span<const Row>(rows_.data(), *rows), true);
   if (!r) return r.error();
   for (KVCache* cache : caches) cache->advance(1);
   return std::span<const float>(logits_host_);
@@ -1076,19 +1110,18 @@ Expected<std::span<const float>> LlamaModel::forward_batch(std::span<KVCache* co
 
 Expected<std::size_t> LlamaModel::forward_batch_device(std::span<KVCache* const> caches,
                                                        std::span<const std::int32_t> tokens) {
-  auto rows = batch_rows(caches, tokens);
+  auto rows = batch_rows(caches, tokens, 0);
   if (!rows) return rows.error();
-  auto r = run(*rows, false);
+  auto r = run(std::span<const Row>(rows_.data(), *rows), false);
   if (!r) return r.error();
   for (KVCache* cache : caches) cache->advance(1);
   return *r;
 }
 
-Expected<std::vector<LlamaModel::Row>> LlamaModel::mixed_rows(KVCache* prefill, std::span<const std::int32_t> chunk,
-                                                               std::span<KVCache* const> caches,
-                                                               std::span<const std::int32_t> tokens) const {
+Expected<std::size_t> LlamaModel::mixed_rows(KVCache* prefill, std::span<const std::int32_t> chunk,
+                                             std::span<KVCache* const> caches, std::span<const std::int32_t> tokens) {
   if (chunk.empty() && tokens.empty()) return make_error(ErrorCode::InvalidArgument, "forward_mixed: no rows");
-  std::vector<Row> rows;
+  std::size_t n = 0;
   if (!chunk.empty()) {
     if (prefill == nullptr || prefill->slot() < 0 || static_cast<std::size_t>(prefill->slot()) >= n_slots_ ||
         prefill->max_ctx() != max_ctx_)
@@ -1097,16 +1130,16 @@ Expected<std::vector<LlamaModel::Row>> LlamaModel::mixed_rows(KVCache* prefill, 
       if (c == prefill || (c != nullptr && c->slot() == prefill->slot()))
         return make_error(ErrorCode::InvalidArgument, "forward_mixed: the prefill cache is also in the decode batch");
     }
-    auto p = prefill_rows(*prefill, chunk);
+    auto p = prefill_rows(*prefill, chunk, 0);
     if (!p) return p.error();
-    rows = std::move(*p);
+    n = *p;
   }
   if (!tokens.empty() || !caches.empty()) {
-    auto b = batch_rows(caches, tokens);
+    auto b = batch_rows(caches, tokens, n);  // after the chunk: at most max_seq + max_batch rows
     if (!b) return b.error();
-    rows.insert(rows.end(), b->begin(), b->end());
+    n += *b;
   }
-  return rows;
+  return n;
 }
 
 Expected<std::span<const float>> LlamaModel::forward_mixed(KVCache* prefill, std::span<const std::int32_t> chunk,
@@ -1114,7 +1147,7 @@ Expected<std::span<const float>> LlamaModel::forward_mixed(KVCache* prefill, std
                                                            std::span<const std::int32_t> tokens) {
   auto rows = mixed_rows(prefill, chunk, caches, tokens);
   if (!rows) return rows.error();
-  auto r = run(*rows, true, chunk.empty() ? 0 : chunk.size() - 1);
+  auto r = run(std::span<const Row>(rows_.data(), *rows), true, chunk.empty() ? 0 : chunk.size() - 1);
   if (!r) return r.error();
   if (!chunk.empty()) prefill->advance(chunk.size());
   for (KVCache* cache : caches) cache->advance(1);
@@ -1126,7 +1159,7 @@ Expected<std::size_t> LlamaModel::forward_mixed_device(KVCache* prefill, std::sp
                                                        std::span<const std::int32_t> tokens) {
   auto rows = mixed_rows(prefill, chunk, caches, tokens);
   if (!rows) return rows.error();
-  auto r = run(*rows, false, chunk.empty() ? 0 : chunk.size() - 1);
+  auto r = run(std::span<const Row>(rows_.data(), *rows), false, chunk.empty() ? 0 : chunk.size() - 1);
   if (!r) return r.error();
   if (!chunk.empty()) prefill->advance(chunk.size());
   for (KVCache* cache : caches) cache->advance(1);

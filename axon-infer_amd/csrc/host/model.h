@@ -177,11 +177,15 @@ private:
   // Runs every row through the layers; the final norm and the output matmul run on rows
   // [first_logit, rows.size()) only, whose logits are the pass's.
   Expected<std::size_t> run(std::span<const Row> rows, bool copy_logits, std::size_t first_logit = 0);
-  Expected<std::vector<Row>> mixed_rows(KVCache* prefill, std::span<const std::int32_t> chunk,
-                                        std::span<KVCache* const> caches, std::span<const std::int32_t> tokens) const;
+  // The row builders check their arguments as llama.cpp:269-302, 322-351 do and write rows_
+  // from index `at`, returning the row count (rows_ holds max_rows entries from load on).
+  Expected<std::size_t> mixed_rows(KVCache* prefill, std::span<const std::int32_t> chunk,
+                                   std::span<KVCache* const> caches, std::span<const std::int32_t> tokens);
   Expected<std::span<const float>> forward_rows(std::span<const std::int32_t> tokens, bool copy_logits);
-  Expected<std::vector<Row>> prefill_rows(const KVCache& cache, std::span<const std::int32_t> tokens) const;
-  Expected<std::vector<Row>> batch_rows(std::span<KVCache* const> caches, std::span<const std::int32_t> tokens) const;
+  Expected<std::size_t> prefill_rows(const KVCache& cache, std::span<const std::int32_t> tokens, std::size_t at);
+  Expected<std::size_t> batch_rows(std::span<KVCache* const> caches, std::span<const std::int32_t> tokens,
+                                   std::size_t at);
+  std::vector<Row> rows_;
   Error device_error(const char* what) const;
   int mm(const Tensor& w, const float* x, const void* xq, float* y, std::size_t n, bool accumulate);
   bool q8_path(const Tensor& w) const;
@@ -224,13 +228,17 @@ private:
   void* window_host_ = nullptr;  // pinned staging of the same
   std::size_t last_rows_ = 0;  // rows of the last pass's logits, 0 after a failed pass
   std::vector<float> logits_host_;
+  std::vector<std::uint8_t> sample_done_, sample_select_;
   // Probe state (set_probe / read_probe).
   int probe_type_ = -1;
   std::vector<void*> probe_events_;
   std::size_t probe_used_ = 0;
   std::vector<double> probe_bytes_;
   void probe_begin(const Tensor& w);
-  void probe_end(const Tensor& w, std::size_t n_rows, std::size_t n_out_total, bool accumulate);
+  // out_bytes_override >= 0 replaces the float output bytes (a launch that writes Q8_0 blocks).
+  void probe_end(const Tensor& w, std::size_t n_rows, std::size_t n_out_total, bool accumulate,
+                 double out_bytes_override = -1.0);
+  void probe_cancel();
   std::vector<bool> slot_used_;
 };
 

@@ -103,9 +103,10 @@ int axon_hip_softmax(float* x, size_t n);
 int axon_hip_silu_mul(const float* gate, const float* up, float* out, size_t n);
 /* kernels.h:57-59 */
 int axon_hip_embedding_row(int type, const void* table, size_t n, int64_t index, float* out);
-/* kernels.h:60-66. scores: the reference's per-call scratch; this table keeps scores in LDS
- * and only reads the pointer for contexts too long for LDS, where it must hold
- * n_q * n_head * (n_past + n_q) floats. */
+/* kernels.h:60-66. scores: the reference's per-call scratch of n_q * (n_past + n_q) floats
+ * (kernels.h:67-75), for attention and each of the entries below. This table keeps scores in LDS
+ * and only uses the pointer for contexts too long for LDS; it then runs the call's heads one
+ * after another, each within that scratch. */
 int axon_hip_attention(const float* q, const float* k, const float* v, float* out, float* scores, size_t seq,
                        size_t n_head, size_t n_head_kv, size_t head_dim, float scale);
 /* kernels.h:67-75 */
@@ -199,6 +200,9 @@ int axon_hip_argmax_rows_noalloc(const float* x, size_t n, size_t n_rows, size_t
  * stride floats apart) into out_logit[r * k + i] with their indices in out_id, descending, equal
  * values by ascending index (the reference leaves their order unspecified). NaN is skipped; a
  * row with fewer than k other values ends in ids -1. 1 <= k <= 256, k <= n. */
+#define AXON_HIP_MAX_TOPK 256
+int axon_hip_topk_rows(const float* x, size_t n, size_t n_rows, size_t stride, size_t k, float* out_logit,
+                       int32_t* out_id);
 /* gate|up with the SwiGLU product and its Q8_0 quantization in one launch, for 65 or more
  * rows (llama.cpp:600-620: out = silu(x W_gate^T) * (x W_up^T), then quantize_row_q8_0 of each
  * row for w_down): the same bits as matmul_q8_fused of the two weights, silu_mul_rows and
@@ -208,9 +212,6 @@ int axon_hip_argmax_rows_noalloc(const float* x, size_t n, size_t n_rows, size_t
 int axon_hip_matmul_q8_swiglu(int type, const void* xq, size_t n_rows, size_t n_in, const void* w_gate,
                               const void* w_up, size_t n_ff, float* out, void* outq);
 
-#define AXON_HIP_MAX_TOPK 256
-int axon_hip_topk_rows(const float* x, size_t n, size_t n_rows, size_t stride, size_t k, float* out_logit,
-                       int32_t* out_id);
 /* Y_s[n_rows][n_out_s] (+)= X W_s^T for up to three weights of one type sharing one Q8_0
  * input (mm_fused, llama.cpp:425-472). w[s], y[s] device pointers in host arrays. Rows below
  * 16 run the v_dot4 matvec, 16 and more the int8 MFMA tiles. accumulate adds into y (the

@@ -193,7 +193,7 @@ class HipTable:
     def attention_kv_heads(self, q, k, v, n_q, n_past, n_head, n_head_kv, head_dim, scale, hb, he, f16=False):
         dq, dk, dv = self._dev(q), self._dev(k), self._dev(v)
         out = self._dev(np.zeros((n_q, n_head, head_dim), dtype=np.float32))
-        scores = self.H.DeviceBuffer(max(1, n_q * n_head * (n_past + n_q)) * 4)
+        scores = self.H.DeviceBuffer(max(1, n_q * (n_past + n_q)) * 4)  # the reference's contract, kernels.h:67-75
         self.H.call("attention_kv_heads_f16" if f16 else "attention_kv_heads", dq, dk, dv, out, scores, n_q, n_past,
                     n_head, n_head_kv, head_dim, float(scale), hb, he)
         return out.download(np.float32).reshape(n_q, n_head, head_dim)

@@ -13,7 +13,7 @@ import ctypes as C
 import numpy as np
 import pytest
 
-from helpers import (BLOCK, GOLDEN, Q4_0, Q4_1, Q6_K, Q8_0, golden, golden_blocks)
+from helpers import (BLOCK, GOLDEN, Q4_0, Q4_1, Q6_K, Q8_0, call, golden, golden_blocks)
 from tables import CTable, HipTable, QUANT_TYPES, dequantize, random_floats, random_weights, relative_error
 
 pytestmark = pytest.mark.gpu
@@ -451,6 +451,64 @@ def test_attention_over_one_position_returns_its_value(h):
     v = rng.normal(0, 1, (1, 2, 64)).astype(np.float32)
     got = h.attention_kv_heads(q, k, v, 1, 0, 4, 2, 64, 0.125, 0, 4)
     assert np.array_equal(got[0, 0], v[0, 0]) and np.array_equal(got[0, 3], v[0, 1])
+
+
+@pytest.mark.parametrize("f16", [False, True])
+def test_attention_heads_stay_within_the_reference_scratch(o, f16):
+    """The reference's scratch contract (kernels.h:67-75): a call over heads [h, h + 1), or over
+    every head, with scores of n_q * (n_past + n_q) floats only, at a context whose scores spill
+    out of LDS (3000 positions, a GQA group of 8, as LlamaModel calls it per head,
+    llama.cpp:540-556). The floats after the scratch are a guard that must stay untouched, heads
+    outside the range keep their sentinel outputs, and every head equals the oracle."""
+    import axon_hip as H
+    n_q, n_past, n_head, n_kv, hd = 2, 3000, 32, 4, 64
+    total = n_past + n_q
+    rng = np.random.default_rng(31 + int(f16))
+    q = rng.normal(0, 1, (n_q, n_head, hd)).astype(np.float32)
+    k = rng.normal(0, 1, (total, n_kv, hd)).astype(np.float32)
+    v = rng.normal(0, 1, (total, n_kv, hd)).astype(np.float32)
+    if f16:
+        k, v = k.astype(np.float16).view(np.uint16), v.astype(np.float16).view(np.uint16)
+    want = o.attention_kv_heads(q, k, v, n_q, n_past, n_head, n_kv, hd, 0.125, 0, n_head, f16=f16)
+    guard = np.full(4096, np.float32(-7.25), np.float32)
+    dq, dk, dv = H.DeviceBuffer.of(q), H.DeviceBuffer.of(k), H.DeviceBuffer.of(v)
+    scores = H.DeviceBuffer(4 * (n_q * total + guard.size))
+    scores.upload(guard, offset=4 * n_q * total)
+    entry = "attention_kv_heads_f16" if f16 else "attention_kv_heads"
+    for hb, he in ((5, 6), (16, 17), (31, 32), (0, n_head)):
+        sentinel = np.full((n_q, n_head, hd), np.float32(9.5), np.float32)
+        out = H.DeviceBuffer.of(sentinel)
+        H.call(entry, dq, dk, dv, out, scores, n_q, n_past, n_head, n_kv, hd, 0.125, hb, he)
+        got = out.download(np.float32).reshape(n_q, n_head, hd)
+        assert np.array_equal(got[:, hb:he], want[:, hb:he]), (hb, he)
+        assert np.array_equal(np.delete(got, np.s_[hb:he], axis=1), np.delete(sentinel, np.s_[hb:he], axis=1))
+        assert np.array_equal(scores.download(np.float32, guard.size, 4 * n_q * total), guard), (hb, he)
+
+
+@pytest.mark.parametrize("seq,n_past,n_head,n_kv", [(7, 0, 8, 2), (1, 900, 14, 2), (3, 2500, 32, 8), (2, 3000, 16, 2)])
+def test_attention_and_attention_kv_entries(o, seq, n_past, n_head, n_kv):
+    """The table's attention (a whole sequence, no cache: kernels.h:60-66) and attention_kv (every
+    head, kernels.h:67-75) entries against the oracle's, bit for bit, within the reference's
+    scratch size."""
+    import axon_hip as H
+    hd = 64
+    total = n_past + seq
+    rng = np.random.default_rng(seq + n_past)
+    q = rng.normal(0, 1, (seq, n_head, hd)).astype(np.float32)
+    k = rng.normal(0, 1, (total, n_kv, hd)).astype(np.float32)
+    v = rng.normal(0, 1, (total, n_kv, hd)).astype(np.float32)
+    dq, dk, dv = H.DeviceBuffer.of(q), H.DeviceBuffer.of(k), H.DeviceBuffer.of(v)
+    scores = H.DeviceBuffer(4 * seq * total)
+    out = H.DeviceBuffer(q.nbytes)
+    want = np.zeros_like(q)
+    osc = np.zeros(seq * total, np.float32)
+    if n_past == 0:
+        H.call("attention", dq, dk, dv, out, scores, seq, n_head, n_kv, hd, 0.125)
+        call(o.lib, "ora_attention", q, k, v, want, osc, seq, n_head, n_kv, hd, 0.125)
+    else:
+        H.call("attention_kv", dq, dk, dv, out, scores, seq, n_past, n_head, n_kv, hd, 0.125)
+        call(o.lib, "ora_attention_kv", q, k, v, want, osc, seq, n_past, n_head, n_kv, hd, 0.125)
+    assert np.array_equal(out.download(np.float32).reshape(q.shape), want)
 
 
 # ---- ragged rows entry (one launch over several sequences' caches) -----------------------------

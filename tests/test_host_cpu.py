@@ -128,3 +128,34 @@ def test_ctypes_structs_match_the_header_layout(tmp_path, cname, pyname):
     got = [int(v) for v in subprocess.run([str(exe)], check=True, capture_output=True, text=True).stdout.split()]
     assert got[0] == C.sizeof(py)
     assert got[1:] == [getattr(py, f).offset for f in fields]
+
+
+def _gguf_one_tensor(path, dims, type_id):
+    """A GGUF v3 file holding general.architecture and one tensor info with the given extents,
+    followed by 64 bytes of data."""
+    import struct
+    s = lambda t: struct.pack("<Q", len(t)) + t  # noqa: E731
+    key, val = b"general.architecture", b"llama"
+    head = struct.pack("<IIQQ", 0x46554747, 3, 1, 1) + s(key) + struct.pack("<I", 8) + s(val)
+    info = s(b"blk.0.attn_q.weight") + struct.pack("<I", len(dims)) + struct.pack(f"<{len(dims)}Q", *dims)
+    info += struct.pack("<IQ", type_id, 0)
+    blob = head + info
+    blob += b"\0" * ((-len(blob)) % 32) + b"\0" * 64
+    Path(path).write_bytes(blob)
+
+
+@pytest.mark.parametrize("dims,type_id,message", [
+    ([32, 550 * 10 ** 15], 8, "byte size overflows"),    # 2^64 > elements, but 34-byte blocks wrap
+    ([2 ** 40, 2 ** 30], 0, "element count overflows"),  # 2^70 elements
+    ([32, 0], 8, "extent of zero"),
+    ([2 ** 62, 1], 0, "row length overflows"),           # 4 * 2^62 bytes per row wraps to 0
+])
+def test_gguf_rejects_extents_whose_size_wraps(tmp_path, dims, type_id, message):
+    """The GGUF reader refuses tensor extents whose byte size would wrap around and slip past
+    the bounds check (the reference's checks, src/core/gguf.cpp:595-633): zero extents, element
+    counts past 64 bits, rows times row bytes past size_t."""
+    import axon_hip as H
+    path = tmp_path / "wrapped.gguf"
+    _gguf_one_tensor(path, dims, type_id)
+    with pytest.raises(H.HipError, match=message):
+        H.Model(path, max_seq=8, max_ctx=16)
