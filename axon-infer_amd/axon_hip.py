@@ -188,7 +188,7 @@ def ptr_of(b) -> int:
 class ModelOptions(C.Structure):
     _fields_ = [("max_seq", C.c_size_t), ("max_ctx", C.c_size_t), ("max_batch", C.c_size_t),
                 ("max_caches", C.c_size_t), ("exact_activations", C.c_int), ("kernels", C.c_char_p),
-                ("cache_type", C.c_int), ("no_repack", C.c_int)]
+                ("cache_type", C.c_int), ("no_repack", C.c_int), ("no_persistent", C.c_int)]
 
 
 class ModelInfo(C.Structure):
@@ -196,7 +196,7 @@ class ModelInfo(C.Structure):
                 ("n_ff", C.c_uint32), ("n_vocab", C.c_uint32), ("head_dim", C.c_uint32), ("rotary_dim", C.c_uint32),
                 ("max_seq", C.c_size_t), ("max_ctx", C.c_size_t), ("max_batch", C.c_size_t),
                 ("weight_bytes_per_token", C.c_size_t), ("device_bytes", C.c_size_t),
-                ("kv_bytes_per_position", C.c_size_t), ("cache_type", C.c_int)]
+                ("kv_bytes_per_position", C.c_size_t), ("cache_type", C.c_int), ("persistent_decode", C.c_int)]
 
 
 class SamplerConfig(C.Structure):
@@ -295,11 +295,11 @@ class Model:
     CACHE_TYPES = {"f32": 0, "f16": 1}  # CacheType (src/model/config.h:16)
 
     def __init__(self, path, max_seq=512, max_ctx=4096, max_batch=1, max_caches=0, exact=False, kernels="hip",
-                 cache="f32", repack=True):
+                 cache="f32", repack=True, persistent=True):
         if cache not in self.CACHE_TYPES:
             raise ValueError(f"cache type {cache!r}: f32 or f16")
         o = ModelOptions(max_seq, max_ctx, max_batch, max_caches, int(exact), kernels.encode(),
-                         self.CACHE_TYPES[cache], int(not repack))
+                         self.CACHE_TYPES[cache], int(not repack), int(not persistent))
         h = C.c_void_p(0)
         _mcheck(host().axon_model_load(str(path).encode(), C.byref(o), C.byref(h)), f"load {path}")
         self.h = h

@@ -2,6 +2,7 @@
 // thin adapter per entry that validates sizes on the host, then launches the kernels of this
 // library on the library stream. No entry falls back to the CPU.
 #include "common.h"
+#include "decode_step.h"
 #include "elementwise.h"
 #include "matmul_float.h"
 #include "matvec.h"
@@ -776,6 +777,67 @@ int axon_hip_matvec_fused(const axon_hip_matvec_fused_args* p) {
   if (a.outq != nullptr && (a.out_mode != kOutSilu || a.n_out[0] % kQK != 0))
     return fail(kInvalidArgument, "matvec_fused: Q8_0 output needs the SiLU epilogue and outputs in whole blocks");
   return matvec_fused_launch(p->type, a);
+}
+
+namespace {
+axon_hip::StepShape step_shape_of(const axon_hip_decode_shape* sh) {
+  axon_hip::StepShape s{};
+  s.n_layer = sh->n_layer;
+  s.d = sh->n_embd;
+  s.dq = sh->n_head * 64;
+  s.dkv = sh->n_head_kv * 64;
+  s.ff = sh->n_ff;
+  s.n_head = sh->n_head;
+  s.n_kv = sh->n_head_kv;
+  s.rot_half = sh->rotary_dim / 2;
+  s.t_qkv = sh->type_qkv;
+  s.t_o = sh->type_o;
+  s.t_gu = sh->type_gate_up;
+  s.t_down = sh->type_down;
+  s.max_ctx = sh->max_ctx;
+  return s;
+}
+constexpr uint32_t kStepSpinLimit = 1u << 20;  // polls of one barrier (about a second) before giving up
+static_assert(sizeof(axon_hip_decode_layer) == sizeof(axon_hip::StepLayer), "one layer record layout");
+}  // namespace
+
+size_t axon_hip_decode_layers_workspace_bytes(const axon_hip_decode_shape* shape) {
+  return shape == nullptr ? 0 : step_workspace_bytes(step_shape_of(shape));
+}
+
+const char* axon_hip_decode_layers_unsupported(const axon_hip_decode_shape* shape) {
+  if (shape == nullptr) return "no shape";
+  if (ready() != kOk) return "no device";
+  if (shape->rotary_dim == 0 || shape->rotary_dim % 2 != 0 || shape->rotary_dim > 64) return "a rotary width outside the head";
+  return step_unsupported(step_shape_of(shape));
+}
+
+int axon_hip_decode_layers(const axon_hip_decode_shape* shape, const axon_hip_decode_layers_args* a) {
+  AXON_READY();
+  if (shape == nullptr || a == nullptr || a->layers == nullptr || a->x == nullptr || a->cache == nullptr ||
+      a->work == nullptr || a->epoch == nullptr || a->status == nullptr || a->rope_table == nullptr)
+    return fail(kInvalidArgument, "decode_layers: missing argument");
+  if (*reinterpret_cast<volatile uint32_t*>(a->status) != 0)
+    return fail(kHipError, "decode_layers: an earlier call gave up at a device-wide barrier (status %u); "
+                           "zero the workspace and reset epoch and status", *a->status);
+  StepCall c{};
+  c.layers = reinterpret_cast<const StepLayer*>(a->layers);
+  c.eps = a->eps;
+  c.scale = a->scale;
+  c.rope_table = a->rope_table;
+  c.x = a->x;
+  c.cache = a->cache;
+  c.cache_off = a->cache_off;
+  c.pos = a->pos;
+  c.work = a->work;
+  c.epoch = *a->epoch;
+  c.status = a->status;
+  c.spin_limit = kStepSpinLimit;
+  const StepShape s = step_shape_of(shape);
+  const int rc = step_launch(s, c);
+  if (rc != kOk) return rc;
+  *a->epoch += step_phases(s);
+  return check_launch("decode_layers");
 }
 
 int axon_hip_embedding_rows(int type, const void* table, size_t n, const int32_t* ids, size_t n_rows, float* out) {

@@ -63,6 +63,7 @@ int axon_model_load(const char* path, const axon_model_options* options, axon_mo
       return fail("cache_type: expected 0 (F32) or 1 (F16), found " + std::to_string(options->cache_type));
     o.cache = options->cache_type == 1 ? axon::model::CacheType::F16 : axon::model::CacheType::F32;
     o.repack = options->no_repack == 0;
+    o.persistent_decode = options->no_persistent == 0;
     if (options->kernels != nullptr && !axon::kernels::parse_kernel_set(options->kernels, o.kernels))
       return fail(std::string("kernels: expected auto, scalar, neon or hip, found '") + options->kernels + "'");
   }
@@ -91,6 +92,7 @@ int axon_model_get_info(const axon_model* model, axon_model_info* out) {
   out->device_bytes = model->m->device_bytes();
   out->kv_bytes_per_position = static_cast<size_t>(c.n_layer) * 2 * c.n_embd_kv() * model->m->kv_element_bytes();
   out->cache_type = model->m->cache_type() == axon::model::CacheType::F16 ? 1 : 0;
+  out->persistent_decode = model->m->persistent_decode() ? 1 : 0;
   return 0;
 }
 

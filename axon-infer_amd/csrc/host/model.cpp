@@ -360,6 +360,12 @@ Expected<std::unique_ptr<LlamaModel>> LlamaModel::load(const std::string& path, 
       axon_hip_malloc(reinterpret_cast<void**>(&m->scores_), m->scores_floats_ * 4) != AXON_HIP_OK)
     return m->device_error("attention scratch");
   m->slot_used_.assign(m->n_slots_, false);
+  if (options.persistent_decode) {
+    auto st = m->setup_persistent_decode();
+    if (!st) return st.error();
+  } else {
+    m->step_reason_ = "turned off by LoadOptions::persistent_decode";
+  }
   // Host staging that every pass reuses: the row list, the logits of max_rows rows, and the
   // sampler's per-row flags, so that a pass allocates no host memory.
   m->rows_.resize(R);
@@ -383,6 +389,9 @@ LlamaModel::~LlamaModel() {
     if (p != nullptr) axon_hip_free(p);
   }
   if (rowinfo_host_ != nullptr) axon_hip_host_free(rowinfo_host_);
+  if (step_layers_ != nullptr) axon_hip_free(step_layers_);
+  if (step_work_ != nullptr) axon_hip_free(step_work_);
+  if (step_status_ != nullptr) axon_hip_host_free(step_status_);
   if (window_host_ != nullptr) axon_hip_host_free(window_host_);
   for (void* e : probe_events_) axon_hip_event_destroy(e);
 }
@@ -501,6 +510,103 @@ Expected<bool> LlamaModel::fill_cache(KVCache& cache, const float* rows, std::si
   return true;
 }
 
+Expected<bool> LlamaModel::setup_persistent_decode() {
+  const Config& c = cfg_;
+  auto reason = [&](const char* why) {
+    step_reason_ = why;
+    return true;
+  };
+  if (exact_) return reason("exact activations (float matmul inputs)");
+  if (cache_type_ != CacheType::F32) return reason("an fp16 KV cache");
+  if (c.rope_style != kernels::RopeStyle::Normal) return reason("NeoX rotary layout");
+  if (c.head_dim != 64) return reason("a head size other than 64");
+  for (const Layer& L : layers_) {
+    if (!q8_path(L.wq) || !q8_path(L.wo) || !q8_path(L.w_gate) || !q8_path(L.w_down))
+      return reason("a layer matrix outside Q8_0 / Q4_0 / Q4_1");
+    if (L.wq.type != L.wk.type || L.wk.type != L.wv.type || L.w_gate.type != L.w_up.type ||
+        L.wq.type != layers_[0].wq.type || L.wo.type != layers_[0].wo.type || L.w_gate.type != layers_[0].w_gate.type ||
+        L.w_down.type != layers_[0].w_down.type)
+      return reason("matrix types that differ within a role or across layers");
+  }
+  axon_hip_decode_shape& sh = step_shape_;
+  sh.n_layer = c.n_layer;
+  sh.n_embd = c.n_embd;
+  sh.n_head = c.n_head;
+  sh.n_head_kv = c.n_head_kv;
+  sh.n_ff = c.n_ff;
+  sh.rotary_dim = c.rotary_dim;
+  sh.type_qkv = static_cast<int>(layers_[0].wq.type);
+  sh.type_o = static_cast<int>(layers_[0].wo.type);
+  sh.type_gate_up = static_cast<int>(layers_[0].w_gate.type);
+  sh.type_down = static_cast<int>(layers_[0].w_down.type);
+  sh.max_ctx = static_cast<std::uint32_t>(max_ctx_);
+  if (const char* why = axon_hip_decode_layers_unsupported(&sh); why != nullptr)
+    return reason(why);
+  const std::size_t dkv = c.n_embd_kv();
+  std::vector<axon_hip_decode_layer> recs(c.n_layer);
+  for (std::size_t l = 0; l < c.n_layer; ++l) {
+    const Layer& L = layers_[l];
+    axon_hip_decode_layer& r = recs[l];
+    r.wq = L.wq.dev;
+    r.wk = L.wk.dev;
+    r.wv = L.wv.dev;
+    r.wo = L.wo.dev;
+    r.w_gate = L.w_gate.dev;
+    r.w_up = L.w_up.dev;
+    r.w_down = L.w_down.dev;
+    r.attn_norm = static_cast<const float*>(L.attn_norm.dev);
+    r.ffn_norm = static_cast<const float*>(L.ffn_norm.dev);
+    if (L.bias) {
+      r.bq = static_cast<const float*>(L.bq.dev);
+      r.bk = static_cast<const float*>(L.bk.dev);
+      r.bv = static_cast<const float*>(L.bv.dev);
+    }
+    r.k_layer_off = static_cast<std::int64_t>(2 * l) * static_cast<std::int64_t>(max_ctx_ * dkv);
+    r.v_layer_off = r.k_layer_off + static_cast<std::int64_t>(max_ctx_ * dkv);
+  }
+  step_work_bytes_ = axon_hip_decode_layers_workspace_bytes(&sh);
+  if (axon_hip_malloc(&step_layers_, recs.size() * sizeof(axon_hip_decode_layer)) != AXON_HIP_OK ||
+      axon_hip_memcpy_h2d(step_layers_, recs.data(), recs.size() * sizeof(axon_hip_decode_layer)) != AXON_HIP_OK ||
+      axon_hip_malloc(&step_work_, step_work_bytes_) != AXON_HIP_OK ||
+      axon_hip_memset(step_work_, 0, step_work_bytes_) != AXON_HIP_OK ||
+      axon_hip_host_malloc(reinterpret_cast<void**>(&step_status_), sizeof(std::uint32_t)) != AXON_HIP_OK)
+    return device_error("persistent decode setup");
+  *step_status_ = 0;
+  step_epoch_ = 0;
+  device_bytes_ += recs.size() * sizeof(axon_hip_decode_layer) + step_work_bytes_;
+  step_ok_ = true;
+  step_reason_.clear();
+  return true;
+}
+
+// After a synchronization: a persistent-kernel pass that gave up waiting for another workgroup's
+// output voids that pass; the workspace is reset so later passes run, and the error names what
+// happened.
+Expected<bool> LlamaModel::check_persistent_status() {
+  if (step_status_ == nullptr || *reinterpret_cast<volatile std::uint32_t*>(step_status_) == 0) return true;
+  const std::uint32_t st = *step_status_;
+  if (axon_hip_memset(step_work_, 0, step_work_bytes_) != AXON_HIP_OK) return device_error("persistent decode reset");
+  step_epoch_ = 0;
+  *step_status_ = 0;
+  return make_error(ErrorCode::Device, "a one-row pass's persistent kernel gave up waiting for another workgroup (status " +
+                                           std::to_string(st) + "); that pass's results are void");
+}
+
+// Algorithmic HBM bytes of one persistent decode step over n_vis positions: every layer's
+// weights and norm vectors, the K and V rows read (the new one included) and written, the
+// activation row in and out.
+double LlamaModel::step_bytes(std::size_t n_vis) const {
+  const Config& c = cfg_;
+  const double dkv = static_cast<double>(c.n_embd_kv()), d = static_cast<double>(c.n_embd);
+  double b = 0;
+  for (const Layer& L : layers_) {
+    for (const Tensor* w : {&L.wq, &L.wk, &L.wv, &L.wo, &L.w_gate, &L.w_up, &L.w_down})
+      b += static_cast<double>(w->row_bytes) * w->ne1;
+    b += 2 * d * 4 + 2 * dkv * 4 * (static_cast<double>(n_vis) + 1);
+  }
+  return b + 2 * d * 4;
+}
+
 bool LlamaModel::q8_path(const Tensor& w) const {
   return !exact_ && (w.type == DType::Q8_0 || w.type == DType::Q4_0 || w.type == DType::Q4_1);
 }
@@ -589,6 +695,7 @@ Expected<std::size_t> LlamaModel::run(std::span<const Row> rows, bool copy_logit
   const std::size_t layer_ctx = free_pass ? max_seq_ : max_ctx_;
   // The previous call's row table may still be in flight when its logits stayed on the device.
   if (axon_hip_synchronize() != AXON_HIP_OK) return device_error("synchronize");
+  if (auto st = check_persistent_status(); !st) return st.error();
   std::uint32_t max_vis = 0;
   for (std::size_t i = 0; i < n; ++i) {
     ids[i] = rows[i].token;
@@ -626,7 +733,33 @@ Expected<std::size_t> LlamaModel::run(std::span<const Row> rows, bool copy_logit
     fa.eps = eps;
     return fa;
   };
-  for (std::size_t l = 0; l < c.n_layer; ++l) {
+  // One row of a cached pass: every layer in one persistent kernel.
+  const bool persistent = step_ok_ && n == 1 && !free_pass;
+  if (persistent) {
+    axon_hip_decode_layers_args sa{};
+    sa.layers = static_cast<const axon_hip_decode_layer*>(step_layers_);
+    sa.eps = eps;
+    sa.scale = scale;
+    sa.rope_table = rope_table_;
+    sa.x = x_;
+    sa.cache = static_cast<float*>(kv_);
+    sa.cache_off = coff[0];
+    sa.pos = pos[0];
+    sa.work = step_work_;
+    sa.epoch = &step_epoch_;
+    sa.status = step_status_;
+    // The probe counts the whole kernel as one launch of the layers' q|k|v type.
+    const bool probed = probe_type_ == step_shape_.type_qkv && 2 * probe_used_ + 2 <= probe_events_.size();
+    if (probed) axon_hip_probe_next_launch(probe_events_[2 * probe_used_], probe_events_[2 * probe_used_ + 1]);
+    const int rc = axon_hip_decode_layers(&step_shape_, &sa);
+    if (probed) axon_hip_probe_next_launch(nullptr, nullptr);
+    if (rc != AXON_HIP_OK) return device_error("decode_layers");
+    if (probed) {
+      probe_bytes_.push_back(step_bytes(static_cast<std::size_t>(pos[0]) + 1));
+      ++probe_used_;
+    }
+  }
+  for (std::size_t l = 0; l < (persistent ? 0 : c.n_layer); ++l) {
     const Layer& L = layers_[l];
     const std::int64_t k_layer = static_cast<std::int64_t>(2 * l) * layer_ctx * dkv;
     const std::int64_t v_layer = k_layer + static_cast<std::int64_t>(layer_ctx * dkv);
@@ -872,6 +1005,7 @@ Expected<std::size_t> LlamaModel::run(std::span<const Row> rows, bool copy_logit
   if (copy_logits) {
     logits_host_.resize(n_out * c.n_vocab);
     DEV(axon_hip_memcpy_d2h(logits_host_.data(), logits_, logits_host_.size() * 4));
+    if (auto st = check_persistent_status(); !st) return st.error();
   }
 #undef DEV
   (void)R;
@@ -897,6 +1031,7 @@ Expected<std::size_t> LlamaModel::greedy(std::span<std::int32_t> ids,
     return device_error("greedy");
   // A synchronous copy on the library stream: the staging above is free again when it returns.
   if (axon_hip_memcpy_d2h(ids.data(), ids_, n * 4) != AXON_HIP_OK) return device_error("greedy");
+  if (auto st = check_persistent_status(); !st) return st.error();
   return n;
 }
 
@@ -991,6 +1126,7 @@ Expected<std::size_t> LlamaModel::sample(std::span<std::int32_t> ids, std::span<
     return device_error("sample");
   // Synchronous copies on the library stream.
   if (any_greedy && axon_hip_memcpy_d2h(ids.data(), ids_, n * 4) != AXON_HIP_OK) return device_error("sample");
+  if (auto st = check_persistent_status(); !st) return st.error();
   if (k_max == 0) return n;
   cand_host_.resize(n * k_max * 8);
   if (axon_hip_memcpy_d2h(cand_host_.data(), cand_, n * k_max * 8) != AXON_HIP_OK) return device_error("sample");

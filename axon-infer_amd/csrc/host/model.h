@@ -12,6 +12,7 @@
 // quantize, fused q|k|v and gate|up matvecs, rope + bias + KV write, one ragged attention
 // launch per layer, residual adds fused into the wo and down matvecs.
 
+#include "axon_hip.h"
 #include "expected.h"
 #include "gguf.h"
 #include "kernels.h"
@@ -41,6 +42,9 @@ struct LoadOptions {
   // Repack Q6_K matmul weights (the output matrix) at upload into 16-byte-aligned planes; the
   // native blocks stay for the embedding lookup and the table's entries.
   bool repack = true;
+  // Run every layer of a one-row cached pass as one persistent kernel (axon_hip_decode_layers)
+  // when the model's shape allows it; otherwise, and with false, one launch per step of a layer.
+  bool persistent_decode = true;
 };
 
 struct Config {
@@ -165,6 +169,9 @@ public:
   std::size_t max_seq() const { return max_seq_; }
   std::size_t max_batch() const { return max_batch_; }
   CacheType cache_type() const { return cache_type_; }
+  // Whether one-row cached passes run as the persistent kernel, and if not, why.
+  bool persistent_decode() const { return step_ok_; }
+  const std::string& persistent_decode_reason() const { return step_reason_; }
   std::size_t kv_element_bytes() const { return cache_type_ == CacheType::F16 ? 2 : 4; }
 
 private:
@@ -188,6 +195,7 @@ private:
   std::vector<Row> rows_;
   Error device_error(const char* what) const;
   int mm(const Tensor& w, const float* x, const void* xq, float* y, std::size_t n, bool accumulate);
+  double step_bytes(std::size_t n_vis) const;
   bool q8_path(const Tensor& w) const;
   // The repetition penalty of one (penalty, window) setting on the rows with select[r] set (all
   // rows when select is empty), on the device (sampler.cpp:73-97). `reuse`: another call follows,
@@ -240,6 +248,18 @@ private:
                  double out_bytes_override = -1.0);
   void probe_cancel();
   std::vector<bool> slot_used_;
+  // The persistent decode kernel (axon_hip_decode_layers): its shape, the device array of layer
+  // records, its workspace and phase count, and the status word in pinned host memory.
+  Expected<bool> setup_persistent_decode();
+  Expected<bool> check_persistent_status();
+  bool step_ok_ = false;
+  std::string step_reason_;
+  axon_hip_decode_shape step_shape_{};
+  void* step_layers_ = nullptr;
+  void* step_work_ = nullptr;
+  std::size_t step_work_bytes_ = 0;
+  std::uint64_t step_epoch_ = 0;
+  std::uint32_t* step_status_ = nullptr;
 };
 
 }  // namespace axon::model

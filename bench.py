@@ -67,6 +67,9 @@ COPY_BYTES = 256 << 20
 # The Q4_0 decode matvec's two kernels (Q4_0 is ggml type 2): matvec_dma_kernel for q|k|v, wo
 # and down, matvec_norm1_kernel (the row RMSNorm'd while the weights arrive) for gate|up.
 MATVEC_KERNELS = ("matvec_dma_kernel<2>", "matvec_norm1_kernel<2>")
+# The persistent decode-step kernel: every layer of a one-row pass in one cooperative launch.
+STEP_KERNEL = ("decode_step_kernel: all 16 layers of one decode step (norms, q|k|v+rope+cache, attention, "
+               "wo+add, gate|up+silu, down+add) in one persistent launch")
 METRIC = "decode tokens/s + HBM GB/s (% peak), Q4_0 1B model, batch 1 and 32 ragged"
 
 
@@ -579,7 +582,8 @@ def main() -> int:
     model = H.Model(path, max_seq=512, max_ctx=2048 + 128 + 64, max_batch=32, max_caches=34)
     info = model.info
     log(f"loaded on the {model.table_name} table: {info.device_bytes / 1e9:.2f} GB in HBM, "
-        f"{info.weight_bytes_per_token / 1e6:.2f} MB of weights per token")
+        f"{info.weight_bytes_per_token / 1e6:.2f} MB of weights per token; one-row passes as "
+        f"{'one persistent kernel' if info.persistent_decode else 'per-layer launches'}")
     if args.traffic_probe:
         traffic_probe(H, model, info.n_vocab, min(args.steps, 16), args.prompt, args.seed)
         model.close()
@@ -595,6 +599,8 @@ def main() -> int:
     log(f"decode-b1: {b1['tokens_per_s']:.1f} tok/s ({b1['ms_per_step']:.3f} ms/step)")
 
     ms, launches, nbytes = probe_pass(H, model, info.n_vocab, min(args.steps, 32), args.prompt, args.seed, synth.Q4_0)
+    if launches == 0:
+        raise SystemExit("bench.py: the Q4_0 probe recorded no launch")
     achieved = nbytes / (ms * 1e-3) / 1e9
     q6_ms, q6_n, q6_b = probe_pass(H, model, info.n_vocab, min(args.steps, 32), args.prompt, args.seed, synth.Q6_K)
     q6_gbs = q6_b / (q6_ms * 1e-3) / 1e9
@@ -621,8 +627,9 @@ def main() -> int:
                    "model": spec.name, "global_batch": 1, "seq_len": args.prompt, "parallelism": "none"},
         "hbm_gbs_per_step": round(step_bytes / (b1["ms_per_step"] * 1e-3) / 1e9, 1),
         "hbm_frac_per_step": round(step_bytes / (b1["ms_per_step"] * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
-        "roofline": {"bound": "hbm", "kernel": "decode matvec <Q4_0>: matvec_dma_kernel (q|k|v+rope, wo+add, down+add) "
-                                                     "and matvec_norm1_kernel (gate|up+silu)",
+        "roofline": {"bound": "hbm", "kernel": STEP_KERNEL if info.persistent_decode else
+                     "decode matvec <Q4_0>: matvec_dma_kernel (q|k|v+rope, wo+add, down+add) "
+                     "and matvec_norm1_kernel (gate|up+silu)",
                      "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
                      "launches": launches, "bytes_per_launch": round(nbytes / max(launches, 1)),
@@ -630,6 +637,8 @@ def main() -> int:
         "roofline_q6_k": {"kernel": "q6k_planar_kernel<1> (tied output, 128256 x 2048, repacked at upload)",
                           "achieved": round(q6_gbs, 1), "frac": round(q6_gbs / HBM_PEAK_GBS, 4),
                           "avg_us": round(1e3 * q6_ms / max(q6_n, 1), 3)},
+        "decode_path": ("one persistent kernel per step" if info.persistent_decode else
+                        "per-layer launches"),
         "prefill_tokens_per_s": round(b1["prefill_tokens_per_s"], 1),
         "decode_b1_host_argmax": b1["host_argmax"],
         "cpu_baseline": None,

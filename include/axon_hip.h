@@ -309,6 +309,58 @@ int axon_hip_matvec_fused(const axon_hip_matvec_fused_args* args);
 /* 1 when axon_hip_matvec_fused takes this shape (rows, row length, input mode, SiLU pairing). */
 int axon_hip_matvec_fused_supported(int type, int in_mode, size_t n_rows, size_t n_in, int silu);
 
+/* Every layer of one decode row as a single persistent kernel (llama.cpp:487-623 for a batch of
+ * one): per layer, attn_norm, q|k|v, bias, RoPE (Normal style) and the KV write at pos, the
+ * attention of every head over positions [0, pos], wo with the residual add, ffn_norm, gate|up,
+ * SiLU * up, down with the residual add. The same bits as those steps launched one by one
+ * (matvec_fused and attention_rows). One workgroup per CU; a phase's outputs carry the phase's
+ * number and their readers poll for it; the caller's stream then continues with the output
+ * norm and matrix. F32 cache, head
+ * size 64, n_embd a multiple of 32 up to 2048, Q8_0 / Q4_0 / Q4_1 layer matrices (one type per
+ * matrix role); axon_hip_decode_layers_unsupported names what else it needs. */
+typedef struct {
+  const void* wq;
+  const void* wk;
+  const void* wv;
+  const void* wo;
+  const void* w_gate;
+  const void* w_up;
+  const void* w_down;
+  const float* attn_norm;
+  const float* ffn_norm;
+  const float* bq; /* Q/K/V biases, all or none */
+  const float* bk;
+  const float* bv;
+  int64_t k_layer_off, v_layer_off; /* cache elements from a sequence's slot to this layer's K / V rows */
+} axon_hip_decode_layer;
+
+typedef struct {
+  uint32_t n_layer, n_embd, n_head, n_head_kv, n_ff, rotary_dim;
+  int type_qkv, type_o, type_gate_up, type_down;
+  uint32_t max_ctx; /* positions of a cache slot: calls take pos < max_ctx */
+} axon_hip_decode_shape;
+
+typedef struct {
+  const axon_hip_decode_layer* layers; /* device array of n_layer records */
+  float eps, scale;                    /* RMSNorm epsilon; 1 / sqrt(head size) */
+  const float* rope_table;             /* device (cos, sin) [pos][rotary_dim / 2], built on the host */
+  float* x;                            /* device [n_embd]: the row's residual stream, in and out */
+  float* cache;                        /* device KV pool (float elements) */
+  int64_t cache_off;                   /* the row's slot, in elements */
+  int32_t pos;                         /* the row's position */
+  void* work;                          /* device workspace, zeroed once before its first call */
+  uint64_t* epoch;                     /* host: phases run on this workspace, updated by the call */
+  uint32_t* status;                    /* pinned host word, 0 at the start: nonzero once a call gave up */
+} axon_hip_decode_layers_args;
+
+size_t axon_hip_decode_layers_workspace_bytes(const axon_hip_decode_shape* shape);
+/* NULL when this device runs the shape, else the reason. */
+const char* axon_hip_decode_layers_unsupported(const axon_hip_decode_shape* shape);
+/* Refuses (AXON_HIP_E_HIP) while *status is nonzero: a previous call gave up waiting for
+ * another workgroup's output after about a second of polling, its results are void, and the
+ * workspace must be zeroed again and *epoch, *status reset before the next call. */
+int axon_hip_decode_layers(const axon_hip_decode_shape* shape, const axon_hip_decode_layers_args* args);
+
 /* embedding_row for a device array of token ids (llama.cpp:482-485). */
 int axon_hip_embedding_rows(int type, const void* table, size_t n, const int32_t* ids, size_t n_rows, float* out);
 

@@ -35,6 +35,10 @@ typedef struct {
   /* 1: keep the Q6_K output matrix in its GGUF blocks only. 0 (default): also repack it at upload
    * into 16-byte-aligned planes (axon_hip_q6k_repack) that its matmuls stream; same logits. */
   int no_repack;
+  /* 1: one-row cached passes launch each step of a layer on its own. 0 (default): they run every
+   * layer as one persistent kernel (axon_hip_decode_layers) where the model's shape allows it;
+   * same logits either way. */
+  int no_persistent;
 } axon_model_options;
 
 typedef struct {
@@ -44,6 +48,7 @@ typedef struct {
   size_t device_bytes;
   size_t kv_bytes_per_position;  /* both K and V, all layers, one sequence */
   int cache_type;                /* 0 F32, 1 F16 */
+  int persistent_decode;         /* one-row cached passes run as one persistent kernel */
 } axon_model_info;
 
 const char* axon_model_last_error(void);

@@ -267,3 +267,26 @@ def test_c5_sampled_stream_matches_the_reference_sampler():
         hm.forward_prefill(hc, [hid], logits=False)
         rl = rm.prefill(rc, [hid])[0]
     hm.close()
+
+
+@pytest.mark.parametrize("cfg", ["c1", "c3", "c4"])
+def test_persistent_decode_equals_launch_by_launch(cfg):
+    """The one-kernel decode step (axon_hip_decode_layers) against the same model launching each
+    step of a layer on its own: the persistent path is taken (info.persistent_decode), and 48
+    greedy steps after a 40-token prompt give bit-identical logits."""
+    path = model_path(cfg)
+    a = hip(path, max_seq=64, max_ctx=160)
+    b = hip(path, max_seq=64, max_ctx=160, persistent=False)
+    assert a.info.persistent_decode == 1 and b.info.persistent_decode == 0
+    prompt = np.random.default_rng(77).integers(0, a.n_vocab, 40).astype(np.int32)
+    ca, cb = a.new_cache(), b.new_cache()
+    la, lb = a.forward_prefill(ca, prompt)[-1], b.forward_prefill(cb, prompt)[-1]
+    for s in range(48):
+        t = int(np.argmax(la))
+        la, lb = a.forward_prefill(ca, [t])[0], b.forward_prefill(cb, [t])[0]
+        assert np.array_equal(la, lb), f"{cfg} step {s}: max diff {np.max(np.abs(la - lb))}"
+    for layer in (0, a.info.n_layer - 1):
+        for v in (False, True):
+            assert np.array_equal(a.cache_rows(ca, layer, v, 88), b.cache_rows(cb, layer, v, 88))
+    a.close()
+    b.close()
