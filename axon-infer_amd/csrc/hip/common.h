@@ -110,7 +110,8 @@ __device__ const uint64_t kExp2Tab[32] = {
   0x3fef5818dcfba487ull, 0x3fef7c97337b9b5full, 0x3fefa4afa2a490daull, 0x3fefd0765b6e4540ull,
 };
 
-__device__ __forceinline__ float exp_libm(float x) {
+// exp_libm with the table read from `tab` (kExp2Tab, or a copy of it in LDS).
+__device__ __forceinline__ float exp_libm_from(float x, const uint64_t* tab) {
   constexpr double kInvLn2N = 0x1.71547652b82fep+0 * 32;  // N / ln 2
   constexpr double kShift = 0x1.8p+52;                    // adds and strips to round to an integer
   constexpr double kC0 = 0x1.c6af84b912394p-5 / 32 / 32 / 32;
@@ -124,13 +125,15 @@ __device__ __forceinline__ float exp_libm(float x) {
   const uint64_t ki = static_cast<uint64_t>(__double_as_longlong(kd));
   kd -= kShift;
   const double r = fma(kInvLn2N, xd, -kd);
-  const double s = __longlong_as_double(static_cast<long long>(kExp2Tab[ki & 31u] + (ki << 47)));
+  const double s = __longlong_as_double(static_cast<long long>(tab[ki & 31u] + (ki << 47)));
   const double p = kC0 * r + kC1;
   const double r2 = r * r;
   double y = kC2 * r + 1.0;
   y = p * r2 + y;
   return static_cast<float>(y * s);
 }
+
+__device__ __forceinline__ float exp_libm(float x) { return exp_libm_from(x, kExp2Tab); }
 
 // ------------------------------------------------------------------------------------------
 // Byte streams in LDS. GGUF blocks are 18, 20, 34 or 210 bytes, so a block starts on a 2-byte

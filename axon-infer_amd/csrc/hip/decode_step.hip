@@ -32,6 +32,8 @@
 #include "decode_step.h"
 
 #include <algorithm>
+#include <cstdlib>
+#include <cstring>
 #include <mutex>
 
 namespace axon_hip {
@@ -174,13 +176,13 @@ __device__ uint32_t region_copies(const StepK& k, const StepLayer& L, int region
 // blocks, terms[r][b] with row pitch tp: the decomposition of the fused decode matvec.
 template <int T>
 __device__ __forceinline__ void terms_of(const uint8_t* tile, uint32_t rb, uint32_t nr, uint32_t nb,
-                                         const ActBlock* act, float* terms, uint32_t tp, uint32_t t) {
+                                         const ActBlock* act, float* terms, uint32_t tp, uint32_t t, uint32_t workers) {
   constexpr uint32_t bs = wbytes<T>();
-  const uint32_t groups = nb <= kCompute ? kCompute / nb : 1;
-  const uint32_t col0 = nb <= kCompute ? t % nb : t;
-  const uint32_t rg = nb <= kCompute ? t / nb : 0;
+  const uint32_t groups = nb <= workers ? workers / nb : 1;
+  const uint32_t col0 = nb <= workers ? t % nb : t;
+  const uint32_t rg = nb <= workers ? t / nb : 0;
   if (rg >= groups) return;
-  for (uint32_t b = col0; b < nb; b += kCompute) {
+  for (uint32_t b = col0; b < nb; b += workers) {
     const ActBlock a = act[b];
     uint32_t r = rg;
     // Four rows at a time, so the LDS reads of all four are in flight together.
@@ -199,12 +201,25 @@ __device__ __forceinline__ void terms_of(const uint8_t* tile, uint32_t rb, uint3
 }
 
 __device__ __forceinline__ void terms_any(int type, const uint8_t* tile, uint32_t rb, uint32_t nr, uint32_t nb,
-                                          const ActBlock* act, float* terms, uint32_t tp, uint32_t t) {
+                                          const ActBlock* act, float* terms, uint32_t tp, uint32_t t, uint32_t workers) {
   switch (type) {
-  case Q8_0: terms_of<Q8_0>(tile, rb, nr, nb, act, terms, tp, t); break;
-  case Q4_0: terms_of<Q4_0>(tile, rb, nr, nb, act, terms, tp, t); break;
-  default: terms_of<Q4_1>(tile, rb, nr, nb, act, terms, tp, t); break;
+  case Q8_0: terms_of<Q8_0>(tile, rb, nr, nb, act, terms, tp, t, workers); break;
+  case Q4_0: terms_of<Q4_0>(tile, rb, nr, nb, act, terms, tp, t, workers); break;
+  default: terms_of<Q4_1>(tile, rb, nr, nb, act, terms, tp, t, workers); break;
   }
+}
+
+// A block-terms job in LDS, published by the compute waves so the copying waves take half of
+// it: the weight type, the LDS byte offsets of the weight tile, the activation blocks and the
+// terms, and the shape.
+struct TermsJob {
+  int type;
+  uint32_t tile, act, terms, rb, nr, nb, tp;
+};
+
+__device__ __forceinline__ void run_job(const TermsJob& j, uint8_t* smem, uint32_t worker) {
+  terms_any(j.type, smem + j.tile, j.rb, j.nr, j.nb, reinterpret_cast<const ActBlock*>(smem + j.act),
+            reinterpret_cast<float*>(smem + j.terms), j.tp, worker, kStepThreads);
 }
 
 // A tagged word: the phase's tag in the high half, 32 payload bits in the low half.
@@ -308,14 +323,17 @@ struct StepLds {
   double red[4];
   float redf[4];
   uint32_t abort, done;
+  uint32_t job_seq;  // bumped when a new terms job is published
+  TermsJob job;
+  uint64_t exp_tab[32];  // kExp2Tab, for exp_libm_from
 };
 
 // The copying waves (4-7): the layer's weight slices into LDS, one region after the phase that
 // used it, waits before the phase that needs it; between them, one barrier for each of the
 // compute waves' until the phase-done flag. Its own loop, sharing no code after the split, so
 // no wait the compiler places for the compute waves' loads runs here.
-__device__ __forceinline__ void copier_main(const StepK& k, StepLds& sh, const StepLayer* layers, uint32_t lds_base,
-                                            uint32_t w, uint32_t dw, uint32_t lane) {
+__device__ __forceinline__ void copier_main(const StepK& k, StepLds& sh, uint8_t* smem, const StepLayer* layers,
+                                            uint32_t lds_base, uint32_t w, uint32_t dw, uint32_t lane) {
   const StepShape& s = k.s;
   uint32_t nq = region_copies(k, layers[0], kQkv, w, lds_base, dw, lane, true);
   uint32_t no = region_copies(k, layers[0], kWo, w, lds_base, dw, lane, true);
@@ -327,9 +345,15 @@ __device__ __forceinline__ void copier_main(const StepK& k, StepLds& sh, const S
     bar();
     return sh.abort == 0;
   };
+  uint32_t jobs_done = 0;
   auto follow = [&]() {
     for (;;) {
       bar();
+      if (sh.job_seq != jobs_done) {  // this wave's half of the terms; the next barrier ends it
+        jobs_done = sh.job_seq;
+        run_job(sh.job, smem, threadIdx.x);
+        continue;
+      }
       if (sh.done != 0) break;
     }
     bar();
@@ -380,10 +404,12 @@ __global__ __launch_bounds__(kStepThreads) void decode_step_kernel(StepK k) {
   if (tid == 0) {
     sh.abort = 0;
     sh.done = 0;
+    sh.job_seq = 0;
   }
+  if (tid < 32) sh.exp_tab[tid] = kExp2Tab[tid];
   bar();
   if (tid >= kCompute) {
-    copier_main(k, sh, layers, lds_base, w, (tid - kCompute) >> 6, lane);
+    copier_main(k, sh, smem, layers, lds_base, w, (tid - kCompute) >> 6, lane);
     return;
   }
 
@@ -404,6 +430,19 @@ __global__ __launch_bounds__(kStepThreads) void decode_step_kernel(StepK k) {
     bar();
     bar();
     if (tid == 0) sh.done = 0;
+  };
+  // Block terms over all eight waves: the job is published before the barrier that precedes
+  // it, and the barrier after it ends the copying waves' half.
+  auto terms = [&](int type, uint32_t tile, uint32_t rb, uint32_t nr, uint32_t nb, const ActBlock* act, float* out,
+                   uint32_t tp) {
+    if (tid == 0) {
+      sh.job = TermsJob{type, tile, static_cast<uint32_t>(reinterpret_cast<const uint8_t*>(act) - smem),
+                        static_cast<uint32_t>(reinterpret_cast<uint8_t*>(out) - smem), rb, nr, nb, tp};
+      ++sh.job_seq;
+    }
+    bar();
+    run_job(sh.job, smem, tid);
+    bar();
   };
   auto give_up = [&]() {
     sh.abort = 1;
@@ -447,16 +486,14 @@ __global__ __launch_bounds__(kStepThreads) void decode_step_kernel(StepK k) {
       if (nr > 0) {
         ActBlock* act = reinterpret_cast<ActBlock*>(scratch);
         const uint32_t nb = s.d / kQK;
-        float* terms = reinterpret_cast<float*>(scratch + nb * sizeof(ActBlock));
+        float* tv = reinterpret_cast<float*>(scratch + nb * sizeof(ActBlock));
         const uint32_t tp = term_pitch(nb);
-        float* outv = terms + k.r_qkv * tp + 64;
+        float* outv = tv + k.r_qkv * tp + 64;
         // x: the launch's input, or the previous layer's down phase.
         if (!norm_quantize(k, L.attn_norm, l == 0 ? nullptr : k.xt, tag_a - 1, act, red, t)) give_up();
         asm volatile("" ::"v"(touch));  // the reads are complete: x came after them
-        bar();
-        terms_any(s.t_qkv, smem + k.lds_qkv, k.rb_d, nr, nb, act, terms, tp, t);
-        bar();
-        if (t < nr) outv[t] = ordered_sum(terms + t * tp, nb);
+        terms(s.t_qkv, k.lds_qkv, k.rb_d, nr, nb, act, tv, tp);
+        if (t < nr) outv[t] = ordered_sum(tv + t * tp, nb);
         bar();
         if (t < nr / 2) {
           const uint32_t o = r0 + 2 * t;
@@ -577,7 +614,7 @@ __global__ __launch_bounds__(kStepThreads) void decode_step_kernel(StepK k) {
           m = fmaxf(fmaxf(sh.redf[0], sh.redf[1]), fmaxf(sh.redf[2], sh.redf[3]));
           double part = 0.0;
           for (uint32_t j = t; j < n_vis; j += kCompute) {
-            const float e = exp_libm(sc[j] - m);
+            const float e = exp_libm_from(sc[j] - m, sh.exp_tab);
             sc[j] = e;
             part += static_cast<double>(e);
           }
@@ -649,9 +686,9 @@ __global__ __launch_bounds__(kStepThreads) void decode_step_kernel(StepK k) {
     if (nrx > 0) {
       const uint32_t nb = s.dq / kQK;
       ActBlock* act = reinterpret_cast<ActBlock*>(scratch);
-      float* terms = reinterpret_cast<float*>(scratch + nb * sizeof(ActBlock));
+      float* tv = reinterpret_cast<float*>(scratch + nb * sizeof(ActBlock));
       const uint32_t tp = term_pitch(nb);
-      float* outv = terms + k.r_o * tp + 64;
+      float* outv = tv + k.r_o * tp + 64;
       if (t * 8 < s.dq) {  // the heads' outputs as Q8_0 blocks, 8 values per thread
         uint32_t u[8];
         if (!take<8>(k.attnt + t * 8, tag_b, u, k.spin_limit)) give_up();
@@ -660,10 +697,8 @@ __global__ __launch_bounds__(kStepThreads) void decode_step_kernel(StepK k) {
         for (int i = 0; i < 8; ++i) v[i] = __uint_as_float(u[i]);
         quantize8_to_act(v, t & 3u, act[t / 4]);
       }
-      bar();
-      terms_any(s.t_o, smem + k.lds_o, k.rb_o, nrx, nb, act, terms, tp, t);
-      bar();
-      if (t < nrx) outv[t] = ordered_sum(terms + t * tp, nb);
+      terms(s.t_o, k.lds_o, k.rb_o, nrx, nb, act, tv, tp);
+      if (t < nrx) outv[t] = ordered_sum(tv + t * tp, nb);
       bar();
       if (t < nrx) {
         xr = xr + outv[t];
@@ -677,19 +712,17 @@ __global__ __launch_bounds__(kStepThreads) void decode_step_kernel(StepK k) {
     if (w * kGuRows < s.ff) {
       const uint32_t nb = s.d / kQK;
       ActBlock* act = reinterpret_cast<ActBlock*>(scratch);
-      float* terms = reinterpret_cast<float*>(scratch + nb * sizeof(ActBlock));
+      float* tv = reinterpret_cast<float*>(scratch + nb * sizeof(ActBlock));
       const uint32_t tp = term_pitch(nb);
-      float* outv = terms + 2 * kGuRows * tp + 64;
+      float* outv = tv + 2 * kGuRows * tp + 64;
       if (!norm_quantize(k, L.ffn_norm, k.xt, tag_c, act, red, t)) give_up();
-      bar();
-      terms_any(s.t_gu, smem + k.lds_gu, k.rb_d, 2 * kGuRows, nb, act, terms, tp, t);
-      bar();
-      if (t < 2 * kGuRows) outv[t] = ordered_sum(terms + t * tp, nb);
+      terms(s.t_gu, k.lds_gu, k.rb_d, 2 * kGuRows, nb, act, tv, tp);
+      if (t < 2 * kGuRows) outv[t] = ordered_sum(tv + t * tp, nb);
       bar();
       if (t < kGuRows) {
         const float gt = outv[t];
         const float u = outv[kGuRows + t];
-        const float hv = gt / (1.0f + exp_libm(-gt)) * u;
+        const float hv = gt / (1.0f + exp_libm_from(-gt, sh.exp_tab)) * u;
         put_act_block(hv, t, k.ht + static_cast<size_t>(w) * 10, tag_d);
       }
     }
@@ -700,9 +733,9 @@ __global__ __launch_bounds__(kStepThreads) void decode_step_kernel(StepK k) {
     if (nrx > 0) {
       const uint32_t nb = s.ff / kQK;
       ActBlock* act = reinterpret_cast<ActBlock*>(scratch);
-      float* terms = reinterpret_cast<float*>(scratch + nb * sizeof(ActBlock));
+      float* tv = reinterpret_cast<float*>(scratch + nb * sizeof(ActBlock));
       const uint32_t tp = term_pitch(nb);
-      float* outv = terms + k.r_d * tp + 64;
+      float* outv = tv + k.r_d * tp + 64;
       if (t < nb) {
         uint32_t u[10];
         if (!take<10>(k.ht + static_cast<size_t>(t) * 10, tag_d, u, k.spin_limit)) give_up();
@@ -712,10 +745,8 @@ __global__ __launch_bounds__(kStepThreads) void decode_step_kernel(StepK k) {
         a.d = __uint_as_float(u[8]);
         a.sum = static_cast<int32_t>(u[9]);
       }
-      bar();
-      terms_any(s.t_down, smem + k.lds_dn, k.rb_down, nrx, nb, act, terms, tp, t);
-      bar();
-      if (t < nrx) outv[t] = ordered_sum(terms + t * tp, nb);
+      terms(s.t_down, k.lds_dn, k.rb_down, nrx, nb, act, tv, tp);
+      if (t < nrx) outv[t] = ordered_sum(tv + t * tp, nb);
       bar();
       if (t < nrx) {
         xr = xr + outv[t];
@@ -918,9 +949,20 @@ int step_launch(const StepShape& s, const StepCall& c) {
   take_probe(&start, &stop);
   if (start != nullptr && hipEventRecord(start, stream()) != hipSuccess)
     return fail(kHipError, "decode step: probe start event");
-  const hipError_t e = hipLaunchCooperativeKernel(reinterpret_cast<const void*>(decode_step_kernel), dim3(cus),
-                                                  dim3(kStepThreads), args, static_cast<unsigned>(lds), stream());
-  if (e != hipSuccess) return fail(kHipError, "decode step: cooperative launch: %s", hipGetErrorString(e));
+  // AXON_HIP_STEP_LAUNCH=plain: an ordinary launch of the same grid (one workgroup per CU, the
+  // most a CU holds at this LDS size), for profiling tools that cannot follow a cooperative
+  // launch. Residency is then not guaranteed, but every wait is bounded: a workgroup that never
+  // became resident makes the call give up (status word), not hang.
+  static const bool plain = [] {
+    const char* v = std::getenv("AXON_HIP_STEP_LAUNCH");
+    return v != nullptr && std::strcmp(v, "plain") == 0;
+  }();
+  const hipError_t e =
+      plain ? hipLaunchKernel(reinterpret_cast<const void*>(decode_step_kernel), dim3(cus), dim3(kStepThreads), args,
+                              static_cast<unsigned>(lds), stream())
+            : hipLaunchCooperativeKernel(reinterpret_cast<const void*>(decode_step_kernel), dim3(cus),
+                                         dim3(kStepThreads), args, static_cast<unsigned>(lds), stream());
+  if (e != hipSuccess) return fail(kHipError, "decode step: launch: %s", hipGetErrorString(e));
   if (stop != nullptr && hipEventRecord(stop, stream()) != hipSuccess)
     return fail(kHipError, "decode step: probe stop event");
   return kOk;

@@ -18,13 +18,13 @@ Two workloads, both greedy:
                forward_batch time (device greedy choice and the ids to the host included).
 
 The line also carries:
-  roofline     the Q4_0 decode matvec (matvec_dma_kernel<Q4_0> for q|k|v, wo and down,
-               matvec_norm1_kernel<Q4_0> for gate|up, of every layer; the dominant kernels by
-               time), from a probe pass of the same
-               decode-b1 steps in which each such launch records its own dispatch start and end on
-               HIP events (hipExtLaunchKernel, on the library stream): achieved = algorithmic bytes
-               (weight rows + activations + outputs) / summed kernel time. The Q6_K output matvec
-               is probed the same way (roofline_q6_k).
+  roofline     the dominant kernel: the persistent decode-step kernel (all layers of a one-row
+               pass in one launch), or, where one-row passes run layer by layer, the Q4_0 decode
+               matvec (matvec_dma_kernel<Q4_0> for q|k|v, wo and down, matvec_norm1_kernel<Q4_0>
+               for gate|up), from a probe pass of the same decode-b1 steps in which each such
+               launch is bracketed by HIP events on the library stream: achieved = algorithmic
+               bytes (weights, norm vectors, the K and V rows read and written, activations) /
+               summed kernel time. The Q6_K output matvec is probed the same way (roofline_q6_k).
   cpu_baseline the reference's own LlamaModel on its scalar table (oracle/_ref, compiled from the
                reference sources) on the same GGUF, threads = the host's cores, on a bounded sample.
 
@@ -42,7 +42,7 @@ The line also carries:
                `bench.py --traffic-probe` (FETCH_SIZE, then WRITE_SIZE, KiB per dispatch), each
                scaled by what the same counter reads for a device-to-device copy of 256 MiB in the
                same process; `bench.py --traffic-summary FETCH_CSV WRITE_CSV` reduces the two
-               counter files to profiles/traffic_matvec_q4_0.json, which this line reports.
+               counter files to profiles/traffic_decode_step.json, which this line reports.
 
 Prints one JSON line. --gpus above 1 exits: this build measures one GPU.
 """
@@ -62,11 +62,13 @@ sys.path.insert(0, str(ROOT / "axon-infer_amd"))
 sys.path.insert(0, str(ROOT / "tests"))
 
 HBM_PEAK_GBS = 8000.0
-TRAFFIC_FILE = ROOT / "profiles" / "traffic_matvec_q4_0.json"
+TRAFFIC_FILE = ROOT / "profiles" / "traffic_decode_step.json"
 COPY_BYTES = 256 << 20
 # The Q4_0 decode matvec's two kernels (Q4_0 is ggml type 2): matvec_dma_kernel for q|k|v, wo
 # and down, matvec_norm1_kernel (the row RMSNorm'd while the weights arrive) for gate|up.
 MATVEC_KERNELS = ("matvec_dma_kernel<2>", "matvec_norm1_kernel<2>")
+# The persistent decode-step kernel, the dominant kernel when one-row passes run as one launch.
+STEP_KERNEL_NAME = "decode_step_kernel"
 # The persistent decode-step kernel: every layer of a one-row pass in one cooperative launch.
 STEP_KERNEL = ("decode_step_kernel: all 16 layers of one decode step (norms, q|k|v+rope+cache, attention, "
                "wo+add, gate|up+silu, down+add) in one persistent launch")
@@ -350,29 +352,35 @@ def _counter_rows(path):
 
 
 def traffic_summary(fetch_csv, write_csv):
-    """Per-dispatch FETCH_SIZE and WRITE_SIZE (KiB) of the Q4_0 decode matvec, each scaled by
-    the counter's reading for the calibration copy (COPY_BYTES read and written)."""
+    """Per-dispatch FETCH_SIZE and WRITE_SIZE (KiB) of the dominant decode kernel (the
+    persistent decode-step kernel, or the Q4_0 decode matvec where one-row passes run layer by
+    layer), each scaled by the counter's reading for the calibration copy (COPY_BYTES read and
+    written)."""
     def per_kernel(path, counter):
-        copy, mv, q6 = [], [], []
+        copy, step, mv, q6 = [], [], [], []
         for name, cname, value in _counter_rows(path):
             if cname != counter:
                 continue
+            n = name.replace(" ", "")
             if "copyBuffer" in name:
                 copy.append(value)
-            elif any(k in name.replace(" ", "") for k in MATVEC_KERNELS):
+            elif STEP_KERNEL_NAME in n:
+                step.append(value)
+            elif any(k in n for k in MATVEC_KERNELS):
                 mv.append(value)
-            elif "q6k_planar_kernel<1>" in name.replace(" ", ""):
+            elif "q6k_planar_kernel<1>" in n:
                 q6.append(value)
-        if not copy or not mv:
-            raise SystemExit(f"{path}: no {counter} rows for the copy ({len(copy)}) or {'/'.join(MATVEC_KERNELS)} ({len(mv)})")
-        return max(copy), mv, q6
-    fcopy, fmv, fq6 = per_kernel(fetch_csv, "FETCH_SIZE")
-    wcopy, wmv, wq6 = per_kernel(write_csv, "WRITE_SIZE")
+        main = step or mv
+        if not copy or not main:
+            raise SystemExit(f"{path}: no {counter} rows for the copy ({len(copy)}) or the decode kernel ({len(main)})")
+        return max(copy), main, q6, bool(step)
+    fcopy, fmv, fq6, is_step = per_kernel(fetch_csv, "FETCH_SIZE")
+    wcopy, wmv, wq6, _ = per_kernel(write_csv, "WRITE_SIZE")
     f_scale = COPY_BYTES / (fcopy * 1024.0)
     w_scale = COPY_BYTES / (wcopy * 1024.0)
     fetch = float(np.mean(fmv)) * 1024.0 * f_scale
     write = float(np.mean(wmv)) * 1024.0 * w_scale
-    out = {"kernel": " + ".join(MATVEC_KERNELS), "dispatches": len(fmv),
+    out = {"kernel": STEP_KERNEL_NAME if is_step else " + ".join(MATVEC_KERNELS), "dispatches": len(fmv),
            "fetch_bytes_per_launch": round(fetch), "write_bytes_per_launch": round(write),
            "traffic_bytes_per_launch": round(fetch + write),
            "copy_bytes": COPY_BYTES, "copy_fetch_kib": fcopy, "copy_write_kib": wcopy,
