@@ -185,6 +185,10 @@ def ptr_of(b) -> int:
 # ---------------------------------------------------------------------------------------------
 # The device-resident forward pass (libaxon_host.so, include/axon_model.h)
 
+# axon_model_probe's type for the attention launches (AXON_MODEL_PROBE_ATTENTION).
+PROBE_ATTENTION = -2
+
+
 class ModelOptions(C.Structure):
     _fields_ = [("max_seq", C.c_size_t), ("max_ctx", C.c_size_t), ("max_batch", C.c_size_t),
                 ("max_caches", C.c_size_t), ("exact_activations", C.c_int), ("kernels", C.c_char_p),

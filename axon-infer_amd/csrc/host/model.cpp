@@ -866,7 +866,20 @@ Expected<std::size_t> LlamaModel::run(std::span<const Row> rows, bool copy_logit
     aa.max_vis = max_vis;
     // wo's Q8_0 input, quantized in the attention epilogue.
     aa.outq = q8_path(L.wo) ? xq_ : nullptr;
+    // The attention probe brackets the layer's attention launches with events on the stream.
+    const bool attn_probed = probe_type_ == kProbeAttention && 2 * probe_used_ + 2 <= probe_events_.size();
+    if (attn_probed && axon_hip_event_record(probe_events_[2 * probe_used_]) != AXON_HIP_OK)
+      return device_error("attention probe");
     DEV(axon_hip_attention_rows(&aa, n));
+    if (attn_probed) {
+      if (axon_hip_event_record(probe_events_[2 * probe_used_ + 1]) != AXON_HIP_OK) return device_error("attention probe");
+      // Algorithmic bytes: each row's K and V rows over its visible positions, q in, the output.
+      double kv_rows = 0;
+      for (std::size_t i = 0; i < n; ++i) kv_rows += nvis[i];
+      const double elem = kv_f16 ? 2.0 : 4.0;
+      probe_bytes_.push_back(kv_rows * 2.0 * static_cast<double>(dkv) * elem + 2.0 * static_cast<double>(n * dq) * 4.0);
+      ++probe_used_;
+    }
 
     if (wo_fused) {
       axon_hip_matvec_fused_args fa = fused_args(L.wo);

@@ -166,6 +166,10 @@ def bench_ragged(H, model, n_vocab, seed, n_seq=32, decode_steps=128, cohort=4, 
     decoded = 0
     step = 0
     batch_sizes = []
+    # Algorithmic HBM bytes of the decode steps: the weights once per step, and each row's K and
+    # V rows over its visible positions.
+    info = model.info
+    kv_bytes = 0.0
     while any(d < decode_steps for d in done):
         t0 = time.perf_counter()
         for i in range(n_seq):
@@ -180,6 +184,7 @@ def bench_ragged(H, model, n_vocab, seed, n_seq=32, decode_steps=128, cohort=4, 
         prefill_s += time.perf_counter() - t0
         active = [i for i in range(n_seq) if caches[i] is not None and done[i] < decode_steps]
         if active:
+            kv_bytes += sum(int(ctx[i]) + done[i] + 1 for i in active) * info.kv_bytes_per_position
             t0 = time.perf_counter()
             model.forward_batch([caches[i] for i in active], [next_tok[i] for i in active], logits=False)
             toks = model.greedy(len(active))
@@ -192,10 +197,47 @@ def bench_ragged(H, model, n_vocab, seed, n_seq=32, decode_steps=128, cohort=4, 
             decoded += len(active)
             batch_sizes.append(len(active))
         step += 1
+    step_bytes = len(batch_sizes) * info.weight_bytes_per_token + kv_bytes
     return {"tokens_per_s": decoded / decode_s, "decoded_tokens": decoded, "steps": step,
+            "hbm_gbs": step_bytes / decode_s / 1e9, "hbm_frac": step_bytes / decode_s / 1e9 / HBM_PEAK_GBS,
             "mean_batch": float(np.mean(batch_sizes)), "max_batch": int(max(batch_sizes)),
             "prefill_tokens": int(ctx.sum()), "prefill_s": prefill_s, "decode_s": decode_s,
             "contexts": {"min": int(ctx.min()), "mean": float(ctx.mean()), "max": int(ctx.max())}}
+
+
+def probe_attention_ragged(H, model, n_vocab, seed, n_seq=32, steps=8):
+    """The batched decode attention alone: 32 caches prefilled to the ragged workload's contexts,
+    then `steps` forward_batch steps of all 32 rows with each layer's attention launches
+    bracketed by events (AXON_MODEL_PROBE_ATTENTION): achieved = the rows' K and V bytes over
+    their visible positions (+ q and the output) / the attention time."""
+    rng = np.random.default_rng(seed + 7)
+    ctx = rng.integers(64, 2049, n_seq)
+    max_seq = model.info.max_seq
+    caches, toks = [], []
+    for i in range(n_seq):
+        c = model.new_cache()
+        p = rng.integers(0, n_vocab, int(ctx[i])).astype(np.int32)
+        for s0 in range(0, len(p), max_seq):
+            tok = prefill_greedy(model, c, p[s0:s0 + max_seq])
+        caches.append(c)
+        toks.append(tok)
+    model.forward_batch(caches, toks, logits=False)  # untimed first batch
+    toks = [int(t) for t in model.greedy(n_seq)]
+    H.synchronize()
+    model.probe(H.PROBE_ATTENTION, True)
+    model.probe_read()
+    for _ in range(steps):
+        model.forward_batch(caches, toks, logits=False)
+        toks = [int(t) for t in model.greedy(n_seq)]
+    ms, launches, nbytes = model.probe_read()
+    model.probe(H.PROBE_ATTENTION, False)
+    for c in caches:
+        model.free_cache(c)
+    gbs = nbytes / (ms * 1e-3) / 1e9
+    return {"kernel": "attn_scores64_kernel + attn_mixd_kernel (one attention_rows call per layer)",
+            "rows": n_seq, "contexts_mean": float(ctx.mean()), "layer_calls": launches,
+            "us_per_layer": round(1e3 * ms / max(launches, 1), 2), "bytes_per_layer": round(nbytes / max(launches, 1)),
+            "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4)}
 
 
 C5_SAMPLER = dict(temperature=0.8, top_k=40, top_p=0.9, min_p=0.05, repeat_penalty=1.1, repeat_last_n=64)
@@ -489,22 +531,29 @@ def host_cores() -> int:
         return os.cpu_count() or 1
 
 
-def cpu_baseline(path, n_vocab, seed, budget_s):
+def cpu_baseline(path, n_vocab, seed, budget_s, ctx0):
     """The reference's LlamaModel (scalar table) on the host cores: batch-1 decode and one
     32-sequence batched step over caches filled to the ragged contexts."""
     from helpers import have_ref
     if not have_ref():
         return None, None
     from helpers import RefModel, ref
-    import ctypes as C
     cores = host_cores()
     rng = np.random.default_rng(seed)
-    prompt = rng.integers(0, n_vocab, 8).astype(np.int32)
     log(f"cpu baseline: reference scalar table, {cores} threads, loading")
     r = RefModel(path, max_seq=32, max_ctx=2176, max_batch=32, n_threads=cores)
+    from helpers import GGUF, ModelConfig
+    import ctypes as C
+    cfg = ModelConfig(GGUF(path))
+    lib = ref()
+    # decode-b1 at the GPU leg's context: the cache filled with ctx0 positions of seeded random
+    # K/V rows (the GPU leg's prompt plus its warm-up steps), then greedy steps from there.
     c = r.new_cache()
-    logits = r.forward_prefill(c, prompt)
-    tok = int(np.argmax(logits[-1]))
+    row = cfg.n_head_kv * cfg.head_dim
+    kv = (0.5 * rng.standard_normal(cfg.n_layer * 2 * ctx0 * row)).astype(np.float32)
+    lib.ref_cache_fill(C.c_void_p(r.h), c, C.c_void_p(kv.ctypes.data), C.c_size_t(ctx0))
+    del kv
+    tok = int(rng.integers(0, n_vocab))
     steps, t0 = 0, time.perf_counter()
     while steps < 3 or (time.perf_counter() - t0 < budget_s and steps < 64):
         logits = r.forward_prefill(c, [tok])
@@ -512,14 +561,12 @@ def cpu_baseline(path, n_vocab, seed, budget_s):
         steps += 1
     dt = time.perf_counter() - t0
     b1 = {"value": steps / dt, "unit": "tokens/s", "cores": cores, "kind": "reference",
-          "sample": f"{steps} greedy decode steps after an 8-token prompt (contexts 9..{8 + steps}), "
-                    f"reference LlamaModel on its scalar table, {cores} threads"}
+          "sample": f"{steps} greedy decode steps at contexts {ctx0 + 1}..{ctx0 + steps} (the GPU leg's), over a "
+                    f"cache filled with {ctx0} seeded random positions; reference LlamaModel on its scalar "
+                    f"table, {cores} threads"}
     log(f"cpu baseline b1: {b1['value']:.3f} tok/s")
     # Ragged: 32 caches filled (zeros) to the ragged contexts, then batched decode steps.
     ctx = np.random.default_rng(seed + 7).integers(64, 2049, 32)
-    from helpers import GGUF, ModelConfig
-    cfg = ModelConfig(GGUF(path))
-    lib = ref()
     zeros = np.zeros(cfg.n_layer * 2 * int(ctx.max()) * cfg.n_head_kv * cfg.head_dim, np.float32)
     ids = []
     for n in ctx:
@@ -660,7 +707,9 @@ def main() -> int:
     if not args.no_ragged:
         rg = bench_ragged(H, model, info.n_vocab, args.seed)
         log(f"ragged-32: {rg['tokens_per_s']:.1f} tok/s over {rg['steps']} steps (mean batch {rg['mean_batch']:.1f})")
-        result["ragged32"] = {k: (round(v, 3) if isinstance(v, float) else v) for k, v in rg.items()}
+        result["ragged32"] = {k: (round(v, 4) if isinstance(v, float) else v) for k, v in rg.items()}
+        result["ragged32"]["attention_roofline"] = probe_attention_ragged(H, model, info.n_vocab, args.seed)
+        log(f"ragged-32 attention: {result['ragged32']['attention_roofline']}")
     model.close()
     if not args.no_f16:
         # The same workloads over an fp16 KV cache (LoadOptions::cache = F16): half the cache
@@ -682,7 +731,7 @@ def main() -> int:
     if not args.no_sweep:
         result["c2_sweep"] = bench_sweep(H, args.seed)
     if not args.no_cpu:
-        b1c, rgc = cpu_baseline(path, info.n_vocab, args.seed, args.cpu_budget)
+        b1c, rgc = cpu_baseline(path, info.n_vocab, args.seed, args.cpu_budget, args.prompt + args.warmup)
         result["cpu_baseline"] = b1c
         if b1c is not None:
             result["vs_cpu"] = round(result["value"] / b1c["value"], 1)

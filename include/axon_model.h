@@ -141,8 +141,10 @@ int axon_sample_candidates(const axon_sampler_config* config, axon_rng* rng, con
 
 /* Kernel-time probe (measurement only): while enabled, the kernel of every matmul on weights of
  * ggml type `type` records its dispatch's start and end on HIP events (axon_hip_probe_next_launch);
- * probe_read returns the summed kernel milliseconds, the launch count and the launches'
- * algorithmic bytes, and resets. */
+ * with type AXON_MODEL_PROBE_ATTENTION, each layer's attention launches are bracketed by events
+ * instead (their bytes: the rows' visible K and V rows, q and the output). probe_read returns the
+ * summed kernel milliseconds, the launch count and the launches' algorithmic bytes, and resets. */
+#define AXON_MODEL_PROBE_ATTENTION (-2)
 int axon_model_probe(axon_model* model, int type, int enable);
 int axon_model_probe_read(axon_model* model, double* ms, size_t* launches, double* bytes);
 
