@@ -43,9 +43,12 @@ enum Status : int {
 // The hardware conversion is exact for every finite half (subnormals included: half denormals
 // are on); infinities and NaNs take the bit-level form so NaN payloads pass through unchanged.
 __device__ __forceinline__ float half_bits_to_float(uint32_t h) {
-  const float f = static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(h)));
+  const uint32_t f = __float_as_uint(static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(h))));
   const uint32_t special = ((h & 0x8000u) << 16) | 0x7f800000u | ((h & 0x3ffu) << 13);
-  return ((h >> 10) & 0x1fu) == 0x1fu ? __uint_as_float(special) : f;
+  // A select by mask, so the conversion stays one basic block (a branch here splits every loop
+  // that widens a block scale and stops the scheduler from overlapping its LDS reads).
+  const uint32_t m = 0u - static_cast<uint32_t>(((h >> 10) & 0x1fu) == 0x1fu);
+  return __uint_as_float((f & ~m) | (special & m));
 }
 
 // fp16 bits to float by the hardware conversion, for values read into arithmetic: exact for

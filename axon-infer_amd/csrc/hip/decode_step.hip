@@ -434,7 +434,7 @@ __global__ __launch_bounds__(kStepThreads) void decode_step_kernel(StepK k) {
   // Block terms over all eight waves: the job is published before the barrier that precedes
   // it, and the barrier after it ends the copying waves' half.
   auto terms = [&](int type, uint32_t tile, uint32_t rb, uint32_t nr, uint32_t nb, const ActBlock* act, float* out,
-                   uint32_t tp) {
+                   uint32_t tp) __attribute__((always_inline)) {
     if (tid == 0) {
       sh.job = TermsJob{type, tile, static_cast<uint32_t>(reinterpret_cast<const uint8_t*>(act) - smem),
                         static_cast<uint32_t>(reinterpret_cast<uint8_t*>(out) - smem), rb, nr, nb, tp};
