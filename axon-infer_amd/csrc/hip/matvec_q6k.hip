@@ -336,19 +336,27 @@ __device__ __forceinline__ void planar_superblock(const PlanarBlock& b, const fl
   }
 }
 
-// One lane per output row, 256 rows per workgroup; the activations of all MM rows in LDS; the
-// row's super-blocks double-buffered in registers, two per trip so the buffers swap roles
-// without copies, every fetch unconditional (clamped to the last column).
-template <int MM>
-__global__ __launch_bounds__(kThreads) void q6k_planar_kernel(MatvecArgs args, uint32_t n_in, size_t col_bytes) {
+// One lane per output row, TH rows per workgroup (TH = 64 spreads a short matrix over more
+// CUs); workgroup (blockIdx.x, blockIdx.y) takes activation rows [MM * blockIdx.x, +MM) against
+// output rows [TH * blockIdx.y, +TH), so the workgroups that share a weight slice are launched
+// one after another. The chunk's activation rows sit in LDS (rows past m_total are zeros and
+// their outputs are not stored); the row's super-blocks are double-buffered in registers, two
+// per trip so the buffers swap roles without copies, every fetch unconditional (clamped to the
+// last column).
+template <int MM, int TH>
+__global__ __launch_bounds__(TH) void q6k_planar_kernel(MatvecArgs args, uint32_t n_in, size_t col_bytes,
+                                                        uint32_t m_total) {
   extern __shared__ __attribute__((aligned(16))) float xs[];  // [MM][n_in]
   const uint32_t tid = threadIdx.x;
   const uint32_t nsb = args.nb;
   const MatvecSeg seg = args.seg[0];
-  const float4* x4 = reinterpret_cast<const float4*>(args.xq);
-  for (uint32_t i = tid; i < MM * n_in / 4; i += kThreads) reinterpret_cast<float4*>(xs)[i] = x4[i];
+  const uint32_t m0 = blockIdx.x * MM;
+  const uint32_t mm = min(static_cast<uint32_t>(MM), m_total - m0);
+  const float4* x4 = reinterpret_cast<const float4*>(args.xq) + static_cast<size_t>(m0) * n_in / 4;
+  for (uint32_t i = tid; i < MM * n_in / 4; i += TH)
+    reinterpret_cast<float4*>(xs)[i] = i < mm * n_in / 4 ? x4[i] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
   __syncthreads();
-  const uint32_t row = blockIdx.x * kThreads + tid;
+  const uint32_t row = blockIdx.y * TH + tid;
   if (row >= seg.n_out) return;
   float acc[MM];
 #pragma unroll
@@ -364,7 +372,8 @@ __global__ __launch_bounds__(kThreads) void q6k_planar_kernel(MatvecArgs args, u
     if (c + 1 < nsb) planar_superblock<MM>(b, xs + (c + 1) * kQKK, n_in, acc);
   }
 #pragma unroll
-  for (int m = 0; m < MM; ++m) seg.y[static_cast<size_t>(m) * seg.y_stride + row] = acc[m];
+  for (int m = 0; m < MM; ++m)
+    if (m < static_cast<int>(mm)) seg.y[static_cast<size_t>(m0 + m) * seg.y_stride + row] = acc[m];
 }
 
 }  // namespace
@@ -390,29 +399,40 @@ int matvec_q6k_planar_launch(MatvecArgs& a, uint32_t n_in) {
   if ((reinterpret_cast<uintptr_t>(a.seg[0].w) & 15u) != 0 || (reinterpret_cast<uintptr_t>(a.xq) & 15u) != 0)
     return fail(kInvalidArgument, "matmul_q6_k_planar: the planar weights and the activations must be 16-byte aligned");
   const size_t col_bytes = q6k_planar_column_bytes(n_out);
-  const MatvecArgs base = a;
-  const float* x = reinterpret_cast<const float*>(a.xq);
-  const dim3 grid(static_cast<uint32_t>(ceil_div(n_out, kThreads)));
-  for (uint32_t done = 0; done < base.m;) {
-    uint32_t mm = std::min<uint32_t>(4, base.m - done);
-    while (mm > 1 && static_cast<size_t>(mm) * n_in * 4 > 65536) --mm;
-    const size_t lds = static_cast<size_t>(mm) * n_in * 4;
-    if (lds > 65536) return fail(kUnsupported, "matmul_q6_k_planar: n_in %u too large for LDS", n_in);
-    MatvecArgs g = base;
-    g.m = mm;
-    g.xq = reinterpret_cast<const uint8_t*>(x + static_cast<size_t>(done) * n_in);
-    g.seg[0].y = base.seg[0].y + static_cast<size_t>(done) * base.seg[0].y_stride;
-    switch (mm) {
-    case 4: launch(q6k_planar_kernel<4>, grid, dim3(kThreads), lds, g, n_in, col_bytes); break;
-    case 3: launch(q6k_planar_kernel<3>, grid, dim3(kThreads), lds, g, n_in, col_bytes); break;
-    case 2: launch(q6k_planar_kernel<2>, grid, dim3(kThreads), lds, g, n_in, col_bytes); break;
-    default: launch(q6k_planar_kernel<1>, grid, dim3(kThreads), lds, g, n_in, col_bytes); break;
-    }
-    const int rc = check_launch("q6k_planar");
-    if (rc != kOk) return rc;
-    done += mm;
+  // Activation rows per workgroup: up to 8 (each lane then runs 8 chains, and every weight
+  // slice is read once per 8 rows), as many as 64 KB of LDS holds, but fewer while that leaves
+  // under 1024 waves of 64 rows: a lane's chains run one element after another, so a short
+  // matrix needs the rows spread over more waves more than it needs fewer weight reads. One
+  // launch covers every row.
+  uint32_t mm = 1;
+  while (mm < 8 && mm < a.m && static_cast<size_t>(2 * mm) * n_in * 4 <= 65536) mm *= 2;
+  while (mm > 1 && ceil_div(a.m, mm) * ceil_div(n_out, 64) < 1024) mm /= 2;
+  const size_t lds = static_cast<size_t>(mm) * n_in * 4;
+  if (lds > 65536) return fail(kUnsupported, "matmul_q6_k_planar: n_in %u too large for LDS", n_in);
+  const uint32_t chunks = static_cast<uint32_t>(ceil_div(a.m, mm));
+  // 256 rows per workgroup when that still gives a workgroup per CU, else 64.
+  const bool wide = ceil_div(n_out, 256) * chunks >= 256;
+  const uint32_t th = wide ? 256 : 64;
+  const uint32_t blocks = static_cast<uint32_t>(ceil_div(n_out, th));
+  if (blocks > 65535) return fail(kUnsupported, "matmul_q6_k_planar: %u output rows", n_out);
+  const dim3 grid(chunks, blocks);
+  const uint32_t m_total = a.m;
+#define AXON_Q6P(MM_)                                                                                       \
+  case MM_:                                                                                                 \
+    if (wide) launch(q6k_planar_kernel<MM_, 256>, grid, dim3(256), lds, a, n_in, col_bytes, m_total);      \
+    else launch(q6k_planar_kernel<MM_, 64>, grid, dim3(64), lds, a, n_in, col_bytes, m_total);              \
+    break;
+  switch (mm) {
+    AXON_Q6P(8)
+    AXON_Q6P(4)
+    AXON_Q6P(2)
+    default:
+      if (wide) launch(q6k_planar_kernel<1, 256>, grid, dim3(256), lds, a, n_in, col_bytes, m_total);
+      else launch(q6k_planar_kernel<1, 64>, grid, dim3(64), lds, a, n_in, col_bytes, m_total);
+      break;
   }
-  return kOk;
+#undef AXON_Q6P
+  return check_launch("q6k_planar");
 }
 
 int matvec_q6k_launch(MatvecArgs& a, uint32_t n_in) {

@@ -410,7 +410,7 @@ def traffic_summary(fetch_csv, write_csv):
                 step.append(value)
             elif any(k in n for k in MATVEC_KERNELS):
                 mv.append(value)
-            elif "q6k_planar_kernel<1>" in n:
+            elif "q6k_planar_kernel<1>" in n or "q6k_planar_kernel<1,256>" in n:
                 q6.append(value)
         main = step or mv
         if not copy or not main:
@@ -689,7 +689,7 @@ def main() -> int:
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
                      "launches": launches, "bytes_per_launch": round(nbytes / max(launches, 1)),
                      "avg_us": round(1e3 * ms / max(launches, 1), 3)},
-        "roofline_q6_k": {"kernel": "q6k_planar_kernel<1> (tied output, 128256 x 2048, repacked at upload)",
+        "roofline_q6_k": {"kernel": "q6k_planar_kernel<1, 256> (tied output, 128256 x 2048, repacked at upload)",
                           "achieved": round(q6_gbs, 1), "frac": round(q6_gbs / HBM_PEAK_GBS, 4),
                           "avg_us": round(1e3 * q6_ms / max(q6_n, 1), 3)},
         "decode_path": ("one persistent kernel per step" if info.persistent_decode else
