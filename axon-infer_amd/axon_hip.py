@@ -269,6 +269,7 @@ def host() -> C.CDLL:
         L.axon_model_forward_batch.argtypes = [C.c_void_p, C.c_void_p, C.c_void_p, C.c_size_t, C.c_void_p]
         L.axon_model_forward_mixed.argtypes = [C.c_void_p, C.c_int, C.c_void_p, C.c_size_t, C.c_void_p, C.c_void_p,
                                                C.c_size_t, C.c_void_p]
+        L.axon_model_generate_greedy.argtypes = [C.c_void_p, C.c_int, C.c_int32, C.c_size_t, C.c_void_p]
         L.axon_model_greedy.argtypes = [C.c_void_p, C.c_void_p, C.c_void_p, C.c_float, C.c_int, C.c_void_p,
                                         C.c_size_t]
         L.axon_rng_seed.argtypes = [C.c_void_p, C.c_uint64]
@@ -393,6 +394,13 @@ class Model:
                                                ch.ctypes.data if len(ch) else None, len(ch),
                                                cs.ctypes.data if len(cs) else None, t.ctypes.data if len(t) else None,
                                                len(t), out.ctypes.data if out is not None else None), "forward_mixed")
+        return out
+
+    def generate_greedy(self, cache: int, token: int, n: int) -> np.ndarray:
+        """n greedy steps after `token` with the ids kept on the device between steps
+        (axon_model_generate_greedy); the n chosen ids."""
+        out = np.zeros(n, np.int32)
+        _mcheck(host().axon_model_generate_greedy(self.h, cache, int(token), n, out.ctypes.data), "generate_greedy")
         return out
 
     def greedy(self, n: int, recent=None, repeat_penalty: float = 1.0, repeat_last_n: int = 64) -> np.ndarray:

@@ -166,6 +166,14 @@ int axon_model_forward_prefill(axon_model* model, int cache, const int32_t* toke
   return copy_out(model->m->forward_prefill(*c, std::span<const int32_t>(tokens, n)), logits);
 }
 
+int axon_model_generate_greedy(axon_model* model, int cache, int32_t token, size_t n, int32_t* out) {
+  axon::model::KVCache* c = find(model, cache);
+  if (c == nullptr) return fail("generate: unknown cache " + std::to_string(cache));
+  if (out == nullptr && n > 0) return fail("generate: out is NULL");
+  auto r = model->m->generate_greedy(*c, token, std::span<int32_t>(out, n));
+  return r ? 0 : fail(r.error());
+}
+
 int axon_model_forward_batch(axon_model* model, const int* caches, const int32_t* tokens, size_t n, float* logits) {
   std::vector<axon::model::KVCache*> cs(n);
   for (size_t i = 0; i < n; ++i) {

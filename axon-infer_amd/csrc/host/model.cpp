@@ -330,6 +330,7 @@ Expected<std::unique_ptr<LlamaModel>> LlamaModel::load(const std::string& path, 
   if (axon_hip_malloc(reinterpret_cast<void**>(&m->argmax_scratch_), axon_hip_argmax_scratch_words(R) * 8) !=
           AXON_HIP_OK ||
       axon_hip_malloc(reinterpret_cast<void**>(&m->ids_), R * 4) != AXON_HIP_OK ||
+      axon_hip_malloc(reinterpret_cast<void**>(&m->gen_ids_), (m->max_ctx_ + 1) * 4) != AXON_HIP_OK ||
       axon_hip_malloc(&m->cand_, R * AXON_HIP_MAX_TOPK * 8) != AXON_HIP_OK)
     return m->device_error("sampling scratch");
   const std::size_t window_bytes = R * (kMaxPenaltyWindow + 1) * 4;
@@ -383,7 +384,8 @@ LlamaModel::~LlamaModel() {
   for (void* p : {static_cast<void*>(x_), static_cast<void*>(h_), static_cast<void*>(q_), static_cast<void*>(k_),
                   static_cast<void*>(v_), static_cast<void*>(attn_), static_cast<void*>(gate_),
                   static_cast<void*>(up_), static_cast<void*>(tmp_), static_cast<void*>(logits_),
-                  static_cast<void*>(scores_), static_cast<void*>(argmax_scratch_), static_cast<void*>(ids_), cand_, window_,
+                  static_cast<void*>(scores_), static_cast<void*>(argmax_scratch_), static_cast<void*>(ids_),
+                  static_cast<void*>(gen_ids_), cand_, window_,
                   xq_, rowinfo_, kv_, static_cast<void*>(kv_free_),
                   static_cast<void*>(rope_table_), weights_, planar_}) {
     if (p != nullptr) axon_hip_free(p);
@@ -1045,6 +1047,90 @@ Expected<std::size_t> LlamaModel::greedy(std::span<std::int32_t> ids,
   // A synchronous copy on the library stream: the staging above is free again when it returns.
   if (axon_hip_memcpy_d2h(ids.data(), ids_, n * 4) != AXON_HIP_OK) return device_error("greedy");
   if (auto st = check_persistent_status(); !st) return st.error();
+  return n;
+}
+
+Expected<std::size_t> LlamaModel::generate_greedy(KVCache& cache, std::int32_t token, std::span<std::int32_t> out) {
+  const std::size_t n = out.size();
+  const Config& c = cfg_;
+  if (n == 0) return std::size_t{0};
+  if (cache.slot() < 0 || static_cast<std::size_t>(cache.slot()) >= n_slots_ || cache.max_ctx() != max_ctx_)
+    return make_error(ErrorCode::InvalidArgument, "generate: the cache was built for a different model");
+  if (token < 0 || static_cast<std::uint32_t>(token) >= c.n_vocab)
+    return make_error(ErrorCode::InvalidArgument, "forward: token id " + std::to_string(token) + " outside the vocabulary");
+  if (cache.pos() + n > max_ctx_)
+    return make_error(ErrorCode::InvalidArgument, "context overflow: " + std::to_string(n) + " steps from position " +
+                                                      std::to_string(cache.pos()) + " exceed " + std::to_string(max_ctx_));
+  if (!step_ok_) {
+    // Without the persistent kernel, the host loop of forward_one and greedy.
+    std::int32_t tok = token;
+    for (std::size_t i = 0; i < n; ++i) {
+      auto r = forward_prefill_device(cache, std::span<const std::int32_t>(&tok, 1));
+      if (!r) return r.error();
+      auto g = greedy(std::span<std::int32_t>(&tok, 1));
+      if (!g) return g.error();
+      out[i] = tok;
+    }
+    return n;
+  }
+  if (axon_hip_synchronize() != AXON_HIP_OK) return device_error("synchronize");
+  if (auto st = check_persistent_status(); !st) return st.error();
+  last_rows_ = 0;
+  if (axon_hip_memcpy_h2d(gen_ids_, &token, 4) != AXON_HIP_OK) return device_error("generate");
+  const std::size_t d = c.n_embd;
+  const std::int64_t coff = static_cast<std::int64_t>(cache.slot()) * static_cast<std::int64_t>(slot_elems_);
+  const float scale = 1.0f / std::sqrt(static_cast<float>(c.head_dim));
+  const bool out_fused = !exact_ && q8_path(output_) &&
+                         axon_hip_matvec_fused_supported(static_cast<int>(output_.type), 2, 1, d, false) == 1;
+  for (std::size_t i = 0; i < n; ++i) {
+    // Step i: the embedding of gen_ids_[i] (the previous step's choice), every layer in one
+    // launch, the output norm and matrix, the greedy choice into gen_ids_[i + 1].
+    if (axon_hip_embedding_rows(static_cast<int>(token_embd_.type), token_embd_.dev, d, gen_ids_ + i, 1, x_) !=
+        AXON_HIP_OK)
+      return device_error("generate: embedding");
+    axon_hip_decode_layers_args sa{};
+    sa.layers = static_cast<const axon_hip_decode_layer*>(step_layers_);
+    sa.eps = c.rms_eps;
+    sa.scale = scale;
+    sa.rope_table = rope_table_;
+    sa.x = x_;
+    sa.cache = static_cast<float*>(kv_);
+    sa.cache_off = coff;
+    sa.pos = static_cast<std::int32_t>(cache.pos() + i);
+    sa.work = step_work_;
+    sa.epoch = &step_epoch_;
+    sa.status = step_status_;
+    if (axon_hip_decode_layers(&step_shape_, &sa) != AXON_HIP_OK) return device_error("generate: decode_layers");
+    if (out_fused) {
+      axon_hip_matvec_fused_args fa{};
+      fa.type = static_cast<int>(output_.type);
+      fa.n_rows = 1;
+      fa.n_in = d;
+      fa.eps = c.rms_eps;
+      fa.n_seg = 1;
+      fa.w[0] = output_.dev;
+      fa.n_out[0] = c.n_vocab;
+      fa.in_mode = 2;
+      fa.x = x_;
+      fa.x_stride = d;
+      fa.norm_w = static_cast<const float*>(output_norm_.dev);
+      fa.out_mode = 0;
+      fa.y[0] = logits_;
+      fa.y_stride[0] = c.n_vocab;
+      if (axon_hip_matvec_fused(&fa) != AXON_HIP_OK) return device_error("generate: output");
+    } else {
+      const bool out_q8 = q8_path(output_);
+      if (axon_hip_rmsnorm_rows(x_, static_cast<const float*>(output_norm_.dev), out_q8 ? nullptr : h_,
+                                out_q8 ? xq_ : nullptr, d, 1, c.rms_eps) != AXON_HIP_OK ||
+          mm(output_, h_, xq_, logits_, 1, false) != AXON_HIP_OK)
+        return device_error("generate: output");
+    }
+    if (axon_hip_argmax_rows(logits_, c.n_vocab, 1, c.n_vocab, argmax_scratch_, gen_ids_ + i + 1) != AXON_HIP_OK)
+      return device_error("generate: greedy");
+  }
+  if (axon_hip_memcpy_d2h(out.data(), gen_ids_ + 1, n * 4) != AXON_HIP_OK) return device_error("generate");
+  if (auto st = check_persistent_status(); !st) return st.error();
+  cache.advance(n);
   return n;
 }
 

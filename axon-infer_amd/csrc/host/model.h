@@ -128,6 +128,14 @@ public:
   static constexpr std::size_t kMaxPenaltyWindow = 4096;
   Expected<std::size_t> greedy(std::span<std::int32_t> ids, std::span<const std::span<const std::int32_t>> recent = {},
                                float repeat_penalty = 1.0F, int repeat_last_n = 64);
+  // Engine::generate's loop (src/engine/engine.cpp:50-58) at temperature zero without a
+  // repetition penalty, for out.size() tokens after `token`: each step's token is the greedy
+  // choice of the previous step's logits (forward_one, then Sampler::sample). On the device the
+  // chosen id stays in HBM, where the next step's embedding reads it, so the steps run back to
+  // back without a host round trip; the ids come to the host once, at the end. The caller
+  // applies stop tokens to `out` afterwards: every id up to the first stop token is the one the
+  // host loop would produce, and the cache holds out.size() more positions.
+  Expected<std::size_t> generate_greedy(KVCache& cache, std::int32_t token, std::span<std::int32_t> out);
   // Sampler::sample (sampler.cpp:67-183) for each row of the last pass, row r with configs[r] and
   // its own generator rngs[r], as each Sequence holds its own Sampler. On the device: each row's
   // repetition penalty, the greedy choice for rows at temperature zero, and the top-k candidates
@@ -229,6 +237,7 @@ private:
   std::size_t scores_floats_ = 0;
   std::uint64_t* argmax_scratch_ = nullptr;
   std::int32_t* ids_ = nullptr;
+  std::int32_t* gen_ids_ = nullptr;  // generate_greedy's ids: [max_ctx + 1]
   void* cand_ = nullptr;  // top-k candidates: [rows][k] logits, then [rows][k] ids
   std::vector<std::byte> cand_host_;
   std::vector<double> probs_;

@@ -94,6 +94,12 @@ def greedy_decode(model, cache, tok, steps):
     return tok
 
 
+def device_loop_decode(model, cache, tok, steps):
+    """The same greedy steps with the chosen id kept on the device between steps
+    (axon_model_generate_greedy): no host round trip per token."""
+    return int(model.generate_greedy(cache, tok, steps)[-1])
+
+
 def host_argmax_decode(model, cache, tok, steps):
     for _ in range(steps):
         logits = model.forward_prefill(cache, [tok])
@@ -121,6 +127,14 @@ def bench_decode_b1(H, model, n_vocab, steps, warmup, prompt_len, seed):
     H.synchronize()
     elapsed = time.perf_counter() - t0
     ctx_end = model.cache_pos(cache)
+    # The same steps with the id kept on the device between steps, over the next steps of the
+    # same sequence (its warm-up first).
+    tok = device_loop_decode(model, cache, tok, warmup)
+    H.synchronize()
+    t0 = time.perf_counter()
+    tok = device_loop_decode(model, cache, tok, steps)
+    H.synchronize()
+    loop_s = time.perf_counter() - t0
     # The same step with the logits row copied to the host and argmax'd there (the reference's
     # placement of the sampler), over the next steps of the same sequence.
     host_steps = min(steps, 64)
@@ -132,7 +146,9 @@ def bench_decode_b1(H, model, n_vocab, steps, warmup, prompt_len, seed):
     return {"tokens_per_s": steps / elapsed, "ms_per_step": 1e3 * elapsed / steps, "prefill_tokens_per_s":
             prompt_len / prefill_s, "context": [prompt_len + warmup, ctx_end],
             "host_argmax": {"tokens_per_s": round(host_steps / host_s, 2),
-                            "ms_per_step": round(1e3 * host_s / host_steps, 4), "steps": host_steps}}
+                            "ms_per_step": round(1e3 * host_s / host_steps, 4), "steps": host_steps},
+            "device_loop": {"tokens_per_s": round(steps / loop_s, 2), "ms_per_step": round(1e3 * loop_s / steps, 4),
+                            "steps": steps, "context": [ctx_end + warmup, ctx_end + warmup + steps]}}
 
 
 def probe_pass(H, model, n_vocab, steps, prompt_len, seed, weight_type):
@@ -696,6 +712,7 @@ def main() -> int:
                         "per-layer launches"),
         "prefill_tokens_per_s": round(b1["prefill_tokens_per_s"], 1),
         "decode_b1_host_argmax": b1["host_argmax"],
+        "decode_b1_device_loop": b1["device_loop"],
         "cpu_baseline": None,
     }
     if TRAFFIC_FILE.exists():

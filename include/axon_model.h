@@ -101,6 +101,13 @@ int axon_model_forward_mixed(axon_model* model, int prefill_cache, const int32_t
 int axon_model_greedy(axon_model* model, const int32_t* const* recent, const size_t* recent_len, float repeat_penalty,
                       int repeat_last_n, int32_t* ids, size_t n);
 
+/* Engine::generate (src/engine/engine.cpp:50-58) at temperature zero without a repetition
+ * penalty: n greedy steps after `token` on `cache`, the ids into out[n]. Each step's id stays on
+ * the device for the next step's embedding, so the steps run without host round trips (with the
+ * persistent decode kernel; else as the host loop of forward_prefill and greedy). Stop tokens
+ * are the caller's to apply to `out` afterwards; the cache advances by n. */
+int axon_model_generate_greedy(axon_model* model, int cache, int32_t token, size_t n, int32_t* out);
+
 /* SamplerConfig (include/axon/sampler.h:10-17) without the seed, which seeds an axon_rng. */
 typedef struct {
   float temperature; /* 0 or below: greedy */

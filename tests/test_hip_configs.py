@@ -290,3 +290,37 @@ def test_persistent_decode_equals_launch_by_launch(cfg):
             assert np.array_equal(a.cache_rows(ca, layer, v, 88), b.cache_rows(cb, layer, v, 88))
     a.close()
     b.close()
+
+
+@pytest.mark.parametrize("cfg", ["c1", "c4"])
+def test_generate_greedy_equals_host_loop(cfg):
+    """axon_model_generate_greedy (each step's id kept on the device for the next step's
+    embedding) against the host loop of Engine::generate at temperature zero: forward_prefill of
+    the previous id, then the greedy choice. 40 steps after a 24-token prompt give the same ids,
+    the same K/V rows, and the same logits for the step after, on the persistent path and on
+    the per-layer path."""
+    path = model_path(cfg)
+    for persistent in (True, False):
+        a = hip(path, max_seq=64, max_ctx=128, persistent=persistent)
+        b = hip(path, max_seq=64, max_ctx=128, persistent=persistent)
+        prompt = np.random.default_rng(11).integers(0, a.n_vocab, 24).astype(np.int32)
+        ca, cb = a.new_cache(), b.new_cache()
+        a.forward_mixed(ca, prompt, [], [], logits=False)  # logits of the prompt's last row only
+        t0 = int(a.greedy(1)[0])
+        b.forward_mixed(cb, prompt, [], [], logits=False)
+        assert int(b.greedy(1)[0]) == t0
+        got = a.generate_greedy(ca, t0, 40)
+        want, t = [], t0
+        for _ in range(40):
+            b.forward_prefill(cb, [t], logits=False)
+            t = int(b.greedy(1)[0])
+            want.append(t)
+        assert got.tolist() == want, (cfg, persistent)
+        assert a.cache_pos(ca) == b.cache_pos(cb) == 24 + 40
+        for layer in (0, a.info.n_layer - 1):
+            for v in (False, True):
+                assert np.array_equal(a.cache_rows(ca, layer, v, 64), b.cache_rows(cb, layer, v, 64))
+        la, lb = a.forward_prefill(ca, [want[-1]])[0], b.forward_prefill(cb, [want[-1]])[0]
+        assert np.array_equal(la, lb)
+        a.close()
+        b.close()
