@@ -845,13 +845,33 @@ __global__ __launch_bounds__(G * 128) void attn_mixd_kernel(AttnArgs a) {
   float* pbase = reinterpret_cast<float*>(reinterpret_cast<uint8_t*>(lds) + kR * M::kTileBytes);  // [G][pitch]
   const uint32_t pitch = mixd_pitch(a.max_vis);
   float* red_m = pbase + G * pitch;                       // [G][2] maxima (64 bytes)
-  double* red_s = reinterpret_cast<double*>(red_m + 16);  // [G][4] partial sums (256 bytes)
+  double* red_s = reinterpret_cast<double*>(red_m + 16);  // [G][4] partial sums (256 bytes); the row at +320
   const uint32_t tid = threadIdx.x;
   const uint32_t lane = tid & 63u;
   const uint32_t w = tid >> 6;
-  const uint32_t r = blockIdx.x;
-  const uint32_t g = blockIdx.y;
-  const uint32_t half = blockIdx.z;
+  // Workgroups start in the order of their linear index (x fastest), and a chain's length is its
+  // row's visible positions: the linear index is read as (rank, kv head, half) with rank 0 the
+  // row of most positions, so the longest rows start first and the short ones fill in behind.
+  const uint32_t lin = blockIdx.x + gridDim.x * (blockIdx.y + gridDim.y * blockIdx.z);
+  const uint32_t rank = lin / (gridDim.y * gridDim.z);
+  const uint32_t g = (lin / gridDim.z) % gridDim.y;
+  const uint32_t half = lin % gridDim.z;
+  uint32_t r = gridDim.x - 1 - rank;  // without n_vis, row r sees n_past + r + 1 positions
+  if (a.n_vis != nullptr) {
+    // Row i's rank: the rows with more positions, or as many and a lower index, come before it.
+    uint32_t* slot = reinterpret_cast<uint32_t*>(reinterpret_cast<uint8_t*>(red_m) + 320);
+    for (uint32_t i = tid; i < gridDim.x; i += blockDim.x) {
+      const int32_t ni = a.n_vis[i];
+      uint32_t rk = 0;
+      for (uint32_t j = 0; j < gridDim.x; ++j) {
+        const int32_t nj = a.n_vis[j];
+        rk += (nj > ni || (nj == ni && j < i)) ? 1u : 0u;
+      }
+      if (rk == rank) *slot = i;
+    }
+    __syncthreads();
+    r = *slot;
+  }
   const uint32_t n_vis = a.n_vis != nullptr ? static_cast<uint32_t>(a.n_vis[r]) : static_cast<uint32_t>(a.n_past) + r + 1;
   const size_t kv_row = static_cast<size_t>(a.n_kv) * 64;
   const int64_t v_off = (a.v_off != nullptr ? a.v_off[r] : 0) + a.v_off_c;
