@@ -818,7 +818,9 @@ struct MixD {
   static constexpr uint32_t kTileBytes = kDTile * (F16 ? 64 : 128);
   static constexpr uint32_t kCw = G < kCopies ? G : kCopies;  // copying waves
   static constexpr uint32_t kCmax = (kCopies + kCw - 1) / kCw;  // most copies per wave per tile
-  static constexpr uint32_t kBudget = 163840 - G * (kMixMaxVis + 4) * 4 - 512;  // LDS beside p
+  // LDS beside p: with G <= 4 two workgroups share a CU (half the LDS each), so a batch of
+  // rows runs in one wave of workgroups; larger groups take a whole CU's LDS.
+  static constexpr uint32_t kBudget = (G <= 4 ? 81920 : 163840) - G * (kMixMaxVis + 4) * 4 - 512;
   static constexpr uint32_t kR0 = (kBudget < 98304 ? kBudget : 98304) / kTileBytes;
   // Tiles in flight, even (two halves). A wave holds at most kMixMaxVis / 128 score copies and
   // kRing * kCmax V copies outstanding, within the 63 that vmcnt counts (and the 31 that
@@ -1025,6 +1027,16 @@ __global__ __launch_bounds__(G * 128) void attn_mixd_kernel(AttnArgs a) {
       for (uint32_t i = 0; i < cnt; ++i) acc += prod[i];
     }
   };
+  // A whole tile's adds with the next tile's products between them: each product fills the
+  // wait of one dependent add (written apart, the compiler emits the 32 adds, then the 32
+  // multiplies).
+  auto add_mul = [&](const float (&prod)[kDTile], float (&v)[kDTile], const float (&pp)[kDTile]) {
+#pragma unroll
+    for (uint32_t i = 0; i < kDTile; ++i) {
+      acc += prod[i];
+      v[i] = pp[i] * v[i];
+    }
+  };
   uint32_t issued = min(n_tiles, kR);
   for (uint32_t t0 = 0; t0 < n_tiles; t0 += kH) {
     const uint32_t t1 = min(n_tiles, t0 + kH);
@@ -1034,16 +1046,21 @@ __global__ __launch_bounds__(G * 128) void attn_mixd_kernel(AttnArgs a) {
     if (chain) {
       // Tile t + 1 is read while tile t's products are added, and its products are formed
       // after them, so neither the LDS reads nor the multiplies stall the adds.
+      // A tile followed by another in [t0, t1) is whole (t1 <= n_tiles).
       load_tile(t0, va, pa);
       mul_tile(va, pa);
       for (uint32_t t = t0; t < t1; t += 2) {
-        if (t + 1 < t1) load_tile(t + 1, vb, pb);
-        add_tile(va, t);
         if (t + 1 < t1) {
-          mul_tile(vb, pb);
-          if (t + 2 < t1) load_tile(t + 2, va, pa);
-          add_tile(vb, t + 1);
-          if (t + 2 < t1) mul_tile(va, pa);
+          load_tile(t + 1, vb, pb);
+          add_mul(va, vb, pb);
+          if (t + 2 < t1) {
+            load_tile(t + 2, va, pa);
+            add_mul(vb, va, pa);
+          } else {
+            add_tile(vb, t + 1);
+          }
+        } else {
+          add_tile(va, t);
         }
       }
     }
