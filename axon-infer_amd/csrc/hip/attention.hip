@@ -26,6 +26,7 @@ constexpr int kThreads = 256;
 // tile [hd][kVPitch] (kVTile positions, transposed).
 constexpr uint32_t kVTile = 64;
 constexpr uint32_t kVPitch = kVTile + 4;
+constexpr uint32_t kVGroup = 8;  // positions per register set in the whole-tile value mix
 constexpr uint32_t kVMaxItems = kVTile * 128 / 4 / kThreads;  // 4-float items per thread, hd <= 128
 
 __host__ __device__ inline uint32_t round4(uint32_t v) { return (v + 3) & ~3u; }
@@ -212,6 +213,39 @@ __global__ __launch_bounds__(kThreads) void attention_kernel(AttnArgs a) {
           const float* vv = vt + d * kVPitch;
           float sum = acc[q];
           uint32_t j = 0;
+          if (p4 && cnt == kVTile) {
+            // A whole tile, kG positions at a time from two register sets: each set's LDS reads
+            // are issued a group ahead of its adds, so the chain does not wait on them (read just
+            // before their adds, each 4 positions' reads stalled the chain).
+            constexpr uint32_t kG = kVGroup, kQ = kG / 4;
+            float4 pa[kQ], va[kQ], pb[kQ], vb[kQ];
+            auto get = [&](uint32_t j1, float4 (&p4r)[kQ], float4 (&v4r)[kQ]) {
+#pragma unroll
+              for (uint32_t i = 0; i < kQ; ++i) {
+                p4r[i] = *reinterpret_cast<const float4*>(pp + j1 + 4 * i);
+                v4r[i] = *reinterpret_cast<const float4*>(vv + j1 + 4 * i);
+              }
+            };
+            auto run = [&](const float4 (&p4r)[kQ], const float4 (&v4r)[kQ]) {
+#pragma unroll
+              for (uint32_t i = 0; i < kQ; ++i) {
+                sum += p4r[i].x * v4r[i].x;
+                sum += p4r[i].y * v4r[i].y;
+                sum += p4r[i].z * v4r[i].z;
+                sum += p4r[i].w * v4r[i].w;
+              }
+            };
+            get(0, pa, va);
+            get(kG, pb, vb);
+#pragma unroll
+            for (uint32_t j1 = 0; j1 < kVTile; j1 += 2 * kG) {
+              run(pa, va);
+              if (j1 + 2 * kG < kVTile) get(j1 + 2 * kG, pa, va);
+              run(pb, vb);
+              if (j1 + 3 * kG < kVTile) get(j1 + 3 * kG, pb, vb);
+            }
+            j = kVTile;
+          }
           if (p4) {
             for (; j + 4 <= cnt; j += 4) {
               const float4 p4v = *reinterpret_cast<const float4*>(pp + j);
