@@ -895,12 +895,16 @@ __global__ __launch_bounds__(G * 128) void attn_mixd_kernel(AttnArgs a) {
   uint32_t r = gridDim.x - 1 - rank;  // without n_vis, row r sees n_past + r + 1 positions
   if (a.n_vis != nullptr) {
     // Row i's rank: the rows with more positions, or as many and a lower index, come before it.
+    // The rows' lengths go through LDS (p's space, free until the scores are copied in).
     uint32_t* slot = reinterpret_cast<uint32_t*>(reinterpret_cast<uint8_t*>(red_m) + 320);
+    int32_t* nv = reinterpret_cast<int32_t*>(pbase);
+    for (uint32_t i = tid; i < gridDim.x; i += blockDim.x) nv[i] = a.n_vis[i];
+    __syncthreads();
     for (uint32_t i = tid; i < gridDim.x; i += blockDim.x) {
-      const int32_t ni = a.n_vis[i];
+      const int32_t ni = nv[i];
       uint32_t rk = 0;
       for (uint32_t j = 0; j < gridDim.x; ++j) {
-        const int32_t nj = a.n_vis[j];
+        const int32_t nj = nv[j];
         rk += (nj > ni || (nj == ni && j < i)) ? 1u : 0u;
       }
       if (rk == rank) *slot = i;
