@@ -181,15 +181,19 @@ __host__ __device__ constexpr uint32_t item_dwords() {
 
 // LDS: expanded weights [16][kRowsPitch], expanded activations [TM][kRowsPitch] (dwords), then
 // per (row, block) scales: wd, wm [16][KC], xd, xs [TM][KC].
-template <int TM>
+template <int TM, uint32_t TN = kRowsTN>
 __host__ __device__ constexpr size_t rows_lds() {
-  return (static_cast<size_t>(kRowsTN + TM) * kRowsPitch + static_cast<size_t>(kRowsTN + TM) * kRowsChunk * 2) * 4;
+  return (static_cast<size_t>(TN + TM) * kRowsPitch + static_cast<size_t>(TN + TM) * kRowsChunk * 2) * 4;
 }
 
-template <int T, int TM>
+// TN: weight rows per workgroup, 16 or 8. With 8 (a narrow matrix, so twice the workgroups),
+// lanes of weight column col read row col % 8 into the 16-wide MFMA and only columns below 8
+// are folded and stored.
+template <int T, int TM, uint32_t TN = kRowsTN>
 __global__ __launch_bounds__(kThreads) void mfma_rows_kernel(MatvecArgs args) {
+  static_assert(TN == 16 || TN == 8, "16 or 8 weight rows");
   constexpr int bs = block_bytes<T>();
-  constexpr uint32_t TN = kRowsTN, KC = kRowsChunk, P = kRowsPitch;
+  constexpr uint32_t KC = kRowsChunk, P = kRowsPitch;
   constexpr uint32_t MT = TM / 16;                      // MFMA tiles along the activation rows
   constexpr uint32_t WI = TN * KC / kThreads;           // weight items per thread per chunk
   constexpr uint32_t XI = TM * KC / kThreads;           // activation items per thread per chunk
@@ -315,6 +319,7 @@ __global__ __launch_bounds__(kThreads) void mfma_rows_kernel(MatvecArgs args) {
   };
 
   const uint32_t col = lane & 15;  // weight row (B) within the tile's 16
+  const uint32_t wrow = col % TN;  // the LDS row it reads (col itself when TN = 16)
   const uint32_t kq = lane >> 4;   // which 8 of a block's 32 elements this lane feeds
   // Wave w feeds activation row (col + w) % 16 as A row col, which moves D row 4 kq + w (the
   // output this wave folds) into the lane's first result: d[0] = sumi of activation row
@@ -325,7 +330,7 @@ __global__ __launch_bounds__(kThreads) void mfma_rows_kernel(MatvecArgs args) {
 #pragma unroll
   for (uint32_t t = 0; t < MT; ++t) acc[t] = 0.0f;
   auto sums = [&](uint32_t b, uint32_t t) {
-    const uint2 wq = *reinterpret_cast<const uint2*>(wa + col * P + b * 8 + 2 * kq);
+    const uint2 wq = *reinterpret_cast<const uint2*>(wa + wrow * P + b * 8 + 2 * kq);
     const uint2 xq = *reinterpret_cast<const uint2*>(xa + (16 * t + arow) * P + b * 8 + 2 * kq);
     const int64_t bw = static_cast<int64_t>((static_cast<uint64_t>(wq.y) << 32) | wq.x);
     const int64_t ax = static_cast<int64_t>((static_cast<uint64_t>(xq.y) << 32) | xq.x);
@@ -335,10 +340,10 @@ __global__ __launch_bounds__(kThreads) void mfma_rows_kernel(MatvecArgs args) {
   };
   auto fold = [&](uint32_t b, uint32_t t, int32_t sumi) {
     const uint32_t r = 16 * t + orow;
-    const float dw = wd[col * KC + b];
+    const float dw = wd[wrow * KC + b];
     const float dx = xd[r * KC + b];
     if constexpr (T == Q4_1) {
-      acc[t] += static_cast<float>(sumi) * dw * dx + wmn[col * KC + b] * dx * static_cast<float>(xs[r * KC + b]);
+      acc[t] += static_cast<float>(sumi) * dw * dx + wmn[wrow * KC + b] * dx * static_cast<float>(xs[r * KC + b]);
     } else {
       // Q4_0: sumi carries the -8 offset already (the weights entered as q - 8).
       acc[t] += static_cast<float>(sumi) * dw * dx;
@@ -693,20 +698,20 @@ int tile_launch(int type, MatvecArgs& a) {
   return check_launch("mfma_tile");
 }
 
-template <int TM>
+template <int TM, uint32_t TN = kRowsTN>
 int rows_launch(int type, MatvecArgs& a) {
   uint32_t wg = 0;
   for (int s = 0; s < a.n_seg; ++s) {
     a.seg[s].wg_begin = wg;
-    wg += static_cast<uint32_t>(ceil_div(a.seg[s].n_out, kRowsTN));
+    wg += static_cast<uint32_t>(ceil_div(a.seg[s].n_out, TN));
   }
   const dim3 grid(wg, static_cast<uint32_t>(ceil_div(a.m, TM)));
-  constexpr size_t lds = rows_lds<TM>();
+  constexpr size_t lds = rows_lds<TM, TN>();
   static_assert(lds <= 65536, "within the default LDS grant");
   switch (type) {
-  case Q8_0: launch(mfma_rows_kernel<Q8_0, TM>, grid, dim3(kThreads), lds, a); break;
-  case Q4_0: launch(mfma_rows_kernel<Q4_0, TM>, grid, dim3(kThreads), lds, a); break;
-  case Q4_1: launch(mfma_rows_kernel<Q4_1, TM>, grid, dim3(kThreads), lds, a); break;
+  case Q8_0: launch(mfma_rows_kernel<Q8_0, TM, TN>, grid, dim3(kThreads), lds, a); break;
+  case Q4_0: launch(mfma_rows_kernel<Q4_0, TM, TN>, grid, dim3(kThreads), lds, a); break;
+  case Q4_1: launch(mfma_rows_kernel<Q4_1, TM, TN>, grid, dim3(kThreads), lds, a); break;
   default: return fail(kUnsupported, "matmul rows: weight type %d", type);
   }
   return check_launch("mfma_rows");
@@ -777,8 +782,12 @@ int matmul_q8_tile_launch(int type, MatvecArgs& a) {
 
 int matmul_q8_rows_launch(int type, MatvecArgs& a) {
   if (!matmul_q8_rows_fits(type, a)) return fail(kUnsupported, "matmul rows: shape or alignment");
-  if (a.m <= 16) return rows_launch<16>(type, a);
-  return rows_launch<32>(type, a);
+  // Eight weight rows per workgroup when sixteen would leave CUs without one.
+  uint32_t wg16 = 0;
+  for (int s = 0; s < a.n_seg; ++s) wg16 += static_cast<uint32_t>(ceil_div(a.seg[s].n_out, kRowsTN));
+  const bool narrow = static_cast<uint64_t>(wg16) * ceil_div(a.m, a.m <= 16 ? 16u : 32u) < 256;
+  if (a.m <= 16) return narrow ? rows_launch<16, 8>(type, a) : rows_launch<16>(type, a);
+  return narrow ? rows_launch<32, 8>(type, a) : rows_launch<32>(type, a);
 }
 
 int matmul_q8_mfma_launch(int type, MatvecArgs& a) {
