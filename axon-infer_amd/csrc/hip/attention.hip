@@ -28,6 +28,10 @@ constexpr uint32_t kVTile = 64;
 constexpr uint32_t kVPitch = kVTile + 4;
 constexpr uint32_t kVGroup = 8;  // positions per register set in the whole-tile value mix
 constexpr uint32_t kVMaxItems = kVTile * 128 / 4 / kThreads;  // 4-float items per thread, hd <= 128
+// The blocked many-row kernel: blocks of rows only while they leave this many workgroups (two
+// per CU), LDS up to this many bytes (two workgroups per CU).
+constexpr uint32_t kBlockMinWorkgroups = 512;
+constexpr size_t kBlockMaxLds = 80 * 1024;
 
 __host__ __device__ inline uint32_t round4(uint32_t v) { return (v + 3) & ~3u; }
 __host__ __device__ inline size_t vtile_bytes(uint32_t hd) { return static_cast<size_t>(hd) * kVPitch * 4; }
@@ -41,11 +45,11 @@ __device__ __forceinline__ float kv_at(const void* base, size_t i) {
   }
 }
 
+// One query row r and kv head g on the whole workgroup; lds holds the q rows, the scores (when
+// they fit) and a V tile. With a.outq and 32-dim multiples of head_dim, each half-wave's 32
+// outputs are one Q8_0 block of wo's input, quantized as they are stored.
 template <bool F16, bool GLOBAL>
-__global__ __launch_bounds__(kThreads) void attention_kernel(AttnArgs a) {
-  extern __shared__ __attribute__((aligned(16))) float lds[];
-  const uint32_t r = blockIdx.x;
-  const uint32_t g = blockIdx.y;
+__device__ __forceinline__ void attention_row(const AttnArgs& a, uint32_t r, uint32_t g, float* lds) {
   const uint32_t tid = threadIdx.x;
   const uint32_t hd = a.head_dim;
   const uint32_t group = a.n_head / a.n_kv;
@@ -151,6 +155,15 @@ __global__ __launch_bounds__(kThreads) void attention_kernel(AttnArgs a) {
   // Value mix: one (head, d) per lane, positions in ascending order.
   float* out = a.out + static_cast<size_t>(r) * a.out_stride + static_cast<size_t>(h_lo) * hd;
   const uint32_t pairs = nh * hd;
+  // Every half-wave stores 32 consecutive outputs of one head (pairs is a multiple of 32).
+  const bool quant = a.outq != nullptr && hd % kQK == 0;
+  auto store_out = [&](uint32_t t, float v) {
+    out[t] = v;
+    if (quant) {
+      const size_t col = static_cast<size_t>(h_lo) * hd + t;
+      quantize_block_lanes(v, tid & 31u, a.outq + (static_cast<size_t>(r) * (a.out_stride / kQK) + col / kQK) * kBytesQ8_0);
+    }
+  };
   constexpr uint32_t es2 = F16 ? 8 : 16;  // bytes of one 4-element load
   const bool tiled = hd % 4 == 0 && hd <= 128 && pairs <= 4 * kThreads &&
                      ((reinterpret_cast<uintptr_t>(a.kv) + static_cast<uintptr_t>(v_off) * es) % es2) == 0 &&
@@ -264,7 +277,7 @@ __global__ __launch_bounds__(kThreads) void attention_kernel(AttnArgs a) {
 #pragma unroll
     for (uint32_t q = 0; q < 4; ++q) {
       const uint32_t t = tid + q * kThreads;
-      if (t < pairs) out[t] = acc[q];
+      if (t < pairs) store_out(t, acc[q]);
     }
     return;
   }
@@ -286,7 +299,338 @@ __global__ __launch_bounds__(kThreads) void attention_kernel(AttnArgs a) {
       acc += p[j + 3] * v3;
     }
     for (; j < n_vis; ++j) acc += p[j] * kv_at<F16>(a.kv, vbase + j * kv_row);
-    out[t] = acc;
+    store_out(t, acc);
+  }
+}
+
+template <bool F16, bool GLOBAL>
+__global__ __launch_bounds__(kThreads) void attention_kernel(AttnArgs a) {
+  extern __shared__ __attribute__((aligned(16))) float lds[];
+  attention_row<F16, GLOBAL>(a, blockIdx.x, blockIdx.y, lds);
+}
+
+// ---- Many-row launches, several query rows of one sequence per workgroup --------------------
+// attention_block_kernel<F16, G, R>: one workgroup per (block of R consecutive query rows, kv
+// head), for kv groups of G query heads of 64 dims. When the R rows read one K/V span (the rows
+// of a sequence's prefill chunk) and their scores fit the launch's LDS, each K and V row is read
+// once for all of them:
+//   scores   one position per lane; its K row, held in registers, serves the dot of every
+//            (row, head) pair that sees the position, each dot over d in order;
+//   softmax  one wave per (row, head) pair: max, exp, the fused kernel's 256-thread double-sum
+//            tree (lane l carries the partial sums of threads l, l + 64, l + 128, l + 192), scale;
+//   mix      lane = dim; the wave's pairs (wave, wave + 4, ...) are independent chains over
+//            positions in ascending order, all reading the one V tile staged in LDS.
+// Every float operation and its order are the one-row body's. The rows of any other block (the
+// decode rows of a ragged batch) run the one-row body in turn. Blocks are dispatched from the
+// last rows down: in a prefill those see the most positions. (A grid of one workgroup per row
+// whose other workgroups returned at once measured slower than one per block: 311 against
+// 92 us for 512 rows of 32/8 heads.)
+template <uint32_t G, uint32_t R>
+__host__ __device__ constexpr uint32_t block_pairs() { return G * R; }
+
+__host__ __device__ inline size_t block_lds(uint32_t pairs, uint32_t n_vis) {
+  return static_cast<size_t>(pairs) * (64 + round4(n_vis)) * 4 + vtile_bytes(64);
+}
+
+template <bool F16, uint32_t G, uint32_t R>
+__global__ __launch_bounds__(kThreads) void attention_block_kernel(AttnArgs a, uint32_t n_rows, uint32_t lds_bytes) {
+  static_assert(R >= 1 && R <= 4 && G * R <= 16, "block shape");
+  constexpr uint32_t kPairs = block_pairs<G, R>();
+  constexpr uint32_t kChains = (kPairs + 3) / 4;
+  constexpr uint32_t es = F16 ? 2 : 4;
+  extern __shared__ __attribute__((aligned(16))) float lds[];
+  const uint32_t tid = threadIdx.x, wave = tid >> 6, lane = tid & 63u;
+  const uint32_t g = blockIdx.x % a.n_kv;
+  const uint32_t n_blocks = (n_rows + R - 1) / R;
+  const uint32_t r0 = (n_blocks - 1 - blockIdx.x / a.n_kv) * R;
+  const size_t kv_row = static_cast<size_t>(a.n_kv) * 64;
+
+  // Row r0's span; the block shares it when every other row of the block has the same.
+  const int64_t k_off = (a.k_off != nullptr ? a.k_off[r0] : 0) + a.k_off_c;
+  const int64_t v_off = (a.v_off != nullptr ? a.v_off[r0] : 0) + a.v_off_c;
+  uint32_t nv[R];
+  bool shared = true;
+#pragma unroll
+  for (uint32_t i = 0; i < R; ++i) {
+    const uint32_t r = r0 + i;
+    nv[i] = 0;
+    if (r < n_rows) {
+      nv[i] = a.n_vis != nullptr ? static_cast<uint32_t>(a.n_vis[r]) : static_cast<uint32_t>(a.n_past) + r + 1;
+      if (i > 0)
+        shared = shared && (a.k_off != nullptr ? a.k_off[r] : 0) + a.k_off_c == k_off &&
+                 (a.v_off != nullptr ? a.v_off[r] : 0) + a.v_off_c == v_off;
+    }
+  }
+  uint32_t nmax = 0;
+#pragma unroll
+  for (uint32_t i = 0; i < R; ++i) nmax = max(nmax, nv[i]);
+  const uintptr_t base = reinterpret_cast<uintptr_t>(a.kv);
+  const bool aligned = ((base + static_cast<uintptr_t>(k_off) * es) & 15u) == 0 &&
+                       ((base + static_cast<uintptr_t>(v_off) * es) & 15u) == 0;
+  if (!shared || !aligned || block_lds(kPairs, nmax) > lds_bytes) {
+    for (uint32_t i = 0; i < R && r0 + i < n_rows; ++i) {
+      if (i > 0) __syncthreads();  // the previous row's readers of LDS are done
+      attention_row<F16, false>(a, r0 + i, g, lds);
+    }
+    return;
+  }
+
+  // Each row's visible positions, for lookups by a row index that is not a constant.
+  __shared__ uint32_t nv_s[R];
+  if (tid < R) nv_s[tid] = tid == 0 ? nv[0] : tid == 1 ? nv[R > 1 ? 1 : 0] : tid == 2 ? nv[R > 2 ? 2 : 0] : nv[R - 1];
+  auto vis = [&](uint32_t i) { return nv_s[i]; };
+
+  const uint32_t pitch = round4(nmax);
+  float* qs = lds;                  // [pair][64], pair = row * G + head
+  float* sc = qs + kPairs * 64;     // [pair][pitch]
+  float* vt = sc + kPairs * pitch;  // [64][kVPitch]
+  for (uint32_t e = tid; e < kPairs * 64; e += kThreads) {
+    const uint32_t i = e / (G * 64), rest = e % (G * 64);
+    qs[e] = r0 + i < n_rows
+                ? a.q[static_cast<size_t>(r0 + i) * a.q_stride + static_cast<size_t>(g) * G * 64 + rest]
+                : 0.0f;
+  }
+  __syncthreads();
+
+  // Scores: one position per lane, its K row once for every pair that sees it.
+  const size_t kcol = static_cast<size_t>(k_off) + static_cast<size_t>(g) * 64;
+  for (uint32_t j = tid; j < nmax; j += kThreads) {
+    const size_t krow = kcol + j * kv_row;
+    float kr[64];
+    if constexpr (F16) {
+      const uint4* kp = reinterpret_cast<const uint4*>(reinterpret_cast<const uint16_t*>(a.kv) + krow);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const uint4 t = kp[i];
+        const uint32_t w4[4] = {t.x, t.y, t.z, t.w};
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+          kr[8 * i + 2 * k] = half_value(w4[k] & 0xffffu);
+          kr[8 * i + 2 * k + 1] = half_value(w4[k] >> 16);
+        }
+      }
+    } else {
+      const float4* kp = reinterpret_cast<const float4*>(reinterpret_cast<const float*>(a.kv) + krow);
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const float4 t = kp[i];
+        kr[4 * i] = t.x;
+        kr[4 * i + 1] = t.y;
+        kr[4 * i + 2] = t.z;
+        kr[4 * i + 3] = t.w;
+      }
+    }
+#pragma unroll
+    for (uint32_t i = 0; i < R; ++i) {
+      if (j < nv[i]) {
+        for (uint32_t h = 0; h < G; ++h) {
+          const float* qh = qs + (i * G + h) * 64;
+          float acc = 0.0f;
+#pragma unroll
+          for (int d = 0; d < 64; ++d) acc += qh[d] * kr[d];
+          sc[(i * G + h) * pitch + j] = a.scale * acc;
+        }
+      }
+    }
+  }
+  __syncthreads();
+
+  // Softmax, one wave per pair.
+  for (uint32_t pr = wave; pr < kPairs; pr += kThreads / 64) {
+    const uint32_t n = vis(pr / G);
+    if (n == 0) continue;  // a row past the end
+    float* s = sc + pr * pitch;
+    float m = -INFINITY;
+    for (uint32_t j = lane; j < n; j += 64) m = fmaxf(m, s[j]);
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off, 64));
+    double part[4] = {0.0, 0.0, 0.0, 0.0};
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+      for (uint32_t j = lane + 64 * w; j < n; j += 256) {
+        const float e = exp_libm(s[j] - m);
+        s[j] = e;
+        part[w] += static_cast<double>(e);
+      }
+#pragma unroll
+      for (int off = 32; off > 0; off >>= 1) part[w] += __shfl_xor(part[w], off, 64);
+    }
+    double sum = 0.0;
+#pragma unroll
+    for (int w = 0; w < 4; ++w) sum += part[w];
+    const float inv = static_cast<float>(1.0 / sum);
+    for (uint32_t j = lane; j < n; j += 64) s[j] *= inv;
+  }
+
+  // Value mix over V tiles of kVTile positions, stored transposed ([d][position]); the next
+  // tile's loads fly while the current one is walked.
+  constexpr uint32_t kItems = kVTile * 16 / kThreads;  // float4 per thread per tile
+  const size_t vcol = static_cast<size_t>(v_off) + static_cast<size_t>(g) * 64;
+  float4 reg[kItems];
+  auto load_tile = [&](uint32_t j0) {
+#pragma unroll
+    for (uint32_t k = 0; k < kItems; ++k) {
+      const uint32_t it = tid + k * kThreads;
+      const uint32_t jj = it / 16, dq = it % 16;
+      float4 v = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+      if (j0 + jj < nmax) {
+        const size_t e = vcol + static_cast<size_t>(j0 + jj) * kv_row + 4 * dq;
+        if constexpr (F16) {
+          const uint2 h = *reinterpret_cast<const uint2*>(reinterpret_cast<const uint16_t*>(a.kv) + e);
+          v = make_float4(half_value(h.x & 0xffffu), half_value(h.x >> 16), half_value(h.y & 0xffffu),
+                          half_value(h.y >> 16));
+        } else {
+          v = *reinterpret_cast<const float4*>(reinterpret_cast<const float*>(a.kv) + e);
+        }
+      }
+      reg[k] = v;
+    }
+  };
+  // The lane's chains: pairs wave + 4c (a pair past kPairs reads the last pair's row and is
+  // never stored).
+  uint32_t cpair[kChains], cvis[kChains];
+#pragma unroll
+  for (uint32_t c = 0; c < kChains; ++c) {
+    const uint32_t pr = wave + 4 * c;
+    cpair[c] = min(pr, kPairs - 1);
+    cvis[c] = vis(cpair[c] / G);
+  }
+  float acc[kChains];
+#pragma unroll
+  for (uint32_t c = 0; c < kChains; ++c) acc[c] = 0.0f;
+  const float* vv = vt + lane * kVPitch;
+  load_tile(0);
+  for (uint32_t j0 = 0; j0 < nmax; j0 += kVTile) {
+    __syncthreads();  // the previous tile has been read (and, the first time, the softmax is done)
+#pragma unroll
+    for (uint32_t k = 0; k < kItems; ++k) {
+      const uint32_t it = tid + k * kThreads;
+      const uint32_t jj = it / 16, dq = it % 16;
+      float* col = vt + 4 * dq * kVPitch + jj;
+      col[0] = reg[k].x;
+      col[kVPitch] = reg[k].y;
+      col[2 * kVPitch] = reg[k].z;
+      col[3 * kVPitch] = reg[k].w;
+    }
+    __syncthreads();
+    if (j0 + kVTile < nmax) load_tile(j0 + kVTile);
+    const float* pp[kChains];
+    bool full = true;
+#pragma unroll
+    for (uint32_t c = 0; c < kChains; ++c) {
+      pp[c] = sc + cpair[c] * pitch + j0;
+      full = full && cvis[c] >= j0 + kVTile;
+    }
+    if (full) {
+      // Eight positions per register set, two sets: each set's LDS reads are issued a set ahead
+      // of its adds.
+      float4 va[2], vb[2], pa[kChains][2], pb[kChains][2];
+      auto get = [&](uint32_t j1, float4 (&v)[2], float4 (&p)[kChains][2]) {
+        v[0] = *reinterpret_cast<const float4*>(vv + j1);
+        v[1] = *reinterpret_cast<const float4*>(vv + j1 + 4);
+#pragma unroll
+        for (uint32_t c = 0; c < kChains; ++c) {
+          p[c][0] = *reinterpret_cast<const float4*>(pp[c] + j1);
+          p[c][1] = *reinterpret_cast<const float4*>(pp[c] + j1 + 4);
+        }
+      };
+      auto run = [&](const float4 (&v)[2], const float4 (&p)[kChains][2]) {
+#pragma unroll
+        for (uint32_t u = 0; u < 2; ++u) {
+#pragma unroll
+          for (uint32_t c = 0; c < kChains; ++c) acc[c] += p[c][u].x * v[u].x;
+#pragma unroll
+          for (uint32_t c = 0; c < kChains; ++c) acc[c] += p[c][u].y * v[u].y;
+#pragma unroll
+          for (uint32_t c = 0; c < kChains; ++c) acc[c] += p[c][u].z * v[u].z;
+#pragma unroll
+          for (uint32_t c = 0; c < kChains; ++c) acc[c] += p[c][u].w * v[u].w;
+        }
+      };
+      get(0, va, pa);
+      get(8, vb, pb);
+#pragma unroll
+      for (uint32_t j1 = 0; j1 < kVTile; j1 += 16) {
+        run(va, pa);
+        if (j1 + 16 < kVTile) get(j1 + 16, va, pa);
+        run(vb, pb);
+        if (j1 + 24 < kVTile) get(j1 + 24, vb, pb);
+      }
+    } else {
+#pragma unroll
+      for (uint32_t c = 0; c < kChains; ++c) {
+        const uint32_t cnt = cvis[c] > j0 ? min(kVTile, cvis[c] - j0) : 0;
+        for (uint32_t j = 0; j < cnt; ++j) acc[c] += pp[c][j] * vv[j];
+      }
+    }
+  }
+  const size_t nbq = a.out_stride / kQK;
+#pragma unroll
+  for (uint32_t c = 0; c < kChains; ++c) {
+    const uint32_t pr = wave + 4 * c;
+    const uint32_t r = r0 + pr / G;
+    if (pr < kPairs && r < n_rows) {
+      const size_t col = static_cast<size_t>(g * G + pr % G) * 64 + lane;
+      a.out[static_cast<size_t>(r) * a.out_stride + col] = acc[c];
+      if (a.outq != nullptr)
+        quantize_block_lanes(acc[c], lane & 31u, a.outq + (static_cast<size_t>(r) * nbq + col / kQK) * kBytesQ8_0);
+    }
+  }
+}
+
+// The block kernel's LDS beyond 64 KB must be granted once per instantiation; false when the
+// launch's LDS exceeds what the device grants.
+template <bool F16, uint32_t G, uint32_t R>
+bool block_lds_granted(size_t need) {
+  static int limit = -1;
+  if (limit < 0) {
+    int dev = 0, v = 0;
+    limit = (hipGetDevice(&dev) == hipSuccess &&
+             hipDeviceGetAttribute(&v, hipDeviceAttributeMaxSharedMemoryPerBlock, dev) == hipSuccess)
+                ? v
+                : 65536;
+    limit = std::min(limit, static_cast<int>(kBlockMaxLds));
+    if (hipFuncSetAttribute(reinterpret_cast<const void*>(attention_block_kernel<F16, G, R>),
+                            hipFuncAttributeMaxDynamicSharedMemorySize, limit) != hipSuccess)
+      limit = 65536;
+  }
+  return need <= static_cast<size_t>(limit);
+}
+
+// The launch's LDS: the one-row body's at max_vis, raised to the blocks' need up to
+// kBlockMaxLds; blocks whose scores do not fit run one row per workgroup.
+template <bool F16, uint32_t G, uint32_t R>
+bool try_block(const AttnArgs& a, uint32_t n_rows) {
+  const size_t one = static_cast<size_t>(G) * (64 + round4(a.max_vis)) * 4 + vtile_bytes(64);
+  const size_t lds = std::max(one, std::min(block_lds(G * R, a.max_vis), kBlockMaxLds));
+  if (!block_lds_granted<F16, G, R>(lds)) return false;
+  hipLaunchKernelGGL((attention_block_kernel<F16, G, R>), dim3((n_rows + R - 1) / R * a.n_kv), dim3(kThreads), lds, stream(), a,
+                     n_rows, static_cast<uint32_t>(lds));
+  return true;
+}
+
+// The largest block of R rows (R * G <= 16) that still leaves kBlockMinWorkgroups workgroups,
+// else single rows.
+template <uint32_t G>
+bool launch_block_g(const AttnArgs& a, uint32_t n_rows) {
+  auto enough = [&](uint32_t r) { return (n_rows + r - 1) / r * a.n_kv >= kBlockMinWorkgroups; };
+  if constexpr (G <= 4) {
+    if (enough(4)) return a.f16 ? try_block<true, G, 4>(a, n_rows) : try_block<false, G, 4>(a, n_rows);
+  }
+  if (enough(2)) return a.f16 ? try_block<true, G, 2>(a, n_rows) : try_block<false, G, 2>(a, n_rows);
+  return a.f16 ? try_block<true, G, 1>(a, n_rows) : try_block<false, G, 1>(a, n_rows);
+}
+
+// The blocked kernel for whole-head launches of 64-dim heads and kv groups of 3, 4, 7 or 8
+// query heads; false when it does not apply (the one-row kernel runs instead).
+bool launch_block(const AttnArgs& a, uint32_t n_rows) {
+  if (a.head_dim != 64 || a.head_begin != 0 || a.head_end != a.n_head) return false;
+  switch (a.n_head / a.n_kv) {
+  case 3: return launch_block_g<3>(a, n_rows);
+  case 4: return launch_block_g<4>(a, n_rows);
+  case 7: return launch_block_g<7>(a, n_rows);
+  case 8: return launch_block_g<8>(a, n_rows);
+  default: return false;
   }
 }
 
@@ -1236,8 +1580,9 @@ int attention_launch(const AttnArgs& a, uint32_t n_rows) {
     }
     return check_launch("attention (split)");
   }
-  if (a.outq != nullptr) {
-    // The fused kernel has no quantizing epilogue: quantize its output rows afterwards.
+  if (scores_fit_lds(a) && launch_block(a, n_rows)) return check_launch("attention (blocked rows)");
+  if (a.outq != nullptr && a.head_dim % kQK != 0) {
+    // The fused kernel quantizes whole 32-dim blocks only: quantize its output rows afterwards.
     AttnArgs b = a;
     b.outq = nullptr;
     const int rc = attention_launch(b, n_rows);

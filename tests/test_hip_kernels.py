@@ -410,7 +410,9 @@ def test_float_embedding_exact(h, name, type_id):
 
 @pytest.mark.parametrize("n_q,n_past,n_head,n_kv,hd", [(1, 0, 4, 2, 64), (1, 37, 9, 3, 64), (5, 11, 8, 2, 64),
                                                        (16, 100, 32, 8, 64), (3, 600, 14, 2, 64),
-                                                       (2, 5, 4, 4, 16), (1, 3000, 4, 1, 64)])
+                                                       (2, 5, 4, 4, 16), (1, 3000, 4, 1, 64),
+                                                       (37, 20, 9, 3, 64), (33, 5, 14, 2, 64), (18, 300, 32, 4, 64),
+                                                       (130, 0, 32, 8, 64), (300, 0, 32, 8, 64), (260, 40, 32, 4, 64)])
 def test_attention_matches_oracle(h, o, n_q, n_past, n_head, n_kv, hd):
     rng = np.random.default_rng(n_q * 1000 + n_past)
     total = n_past + n_q
@@ -551,3 +553,59 @@ def test_attention_rows_ragged_matches_oracle(o, h, n_head, n_kv, lens, f16):
         want = o.attention_kv_heads(q[i].reshape(1, n_head, hd), pool[i, 0, :L].copy(), pool[i, 1, :L].copy(), 1, L - 1,
                                     n_head, n_kv, hd, 0.125, 0, n_head, f16=f16)[0]
         assert np.array_equal(got[i], want), i
+
+
+@pytest.mark.parametrize("f16", [False, True])
+@pytest.mark.parametrize("n_head,n_kv,chunk", [(32, 8, (300, 45)), (32, 8, (40, 300)), (9, 3, (0, 700)),
+                                               (14, 2, (600, 520)), (32, 4, (120, 300))])
+def test_attention_rows_chunk_among_decode_rows(o, h, n_head, n_kv, chunk, f16):
+    """A mixed pass's attention: decode rows of three sequences around the prefill chunk of a
+    fourth (rows n_past .. n_past + m - 1 of that sequence, each seeing its own prefix), with the
+    Q8_0 output blocks (wo's input) requested. Blocks of rows that share one sequence's K/V read
+    it once (blocks of 4, 2 or 1 rows by the row count); blocks that straddle sequences, or whose
+    scores outgrow the launch's LDS (the last rows of the 14/2 chunk), run one row at a time.
+    Every output row and every Q8_0 block equal the oracle's."""
+    import axon_hip as H
+    hd = 64
+    n_past, m = chunk
+    dec = [700, 41, 900]
+    lens = [dec[0], n_past + m, dec[1], dec[2]]
+    rng = np.random.default_rng(n_head + n_past + m + int(f16))
+    max_ctx = max(lens) + 3
+    row = n_kv * hd
+    pool = rng.normal(0, 1, (4, 2, max_ctx, row)).astype(np.float32)
+    if f16:
+        pool = pool.astype(np.float16).view(np.uint16)
+    # rows: decode seq 0, the chunk of seq 1 (m rows), decode seqs 2 and 3
+    seq_of = [0] + [1] * m + [2, 3]
+    vis = [lens[0]] + [n_past + i + 1 for i in range(m)] + [lens[2], lens[3]]
+    n = len(seq_of)
+    q = rng.normal(0, 1, (n, n_head * hd)).astype(np.float32)
+    slot = pool[0].size
+    d_pool, d_q = H.DeviceBuffer.of(pool), H.DeviceBuffer.of(q)
+    d_out = H.DeviceBuffer(q.nbytes)
+    nbq = n_head * hd // 32
+    d_outq = H.DeviceBuffer(n * nbq * 34)
+    d_off = H.DeviceBuffer.of(np.array(seq_of, np.int64) * slot)
+    d_vis = H.DeviceBuffer.of(np.array(vis, np.int32))
+    args = H.AttentionRowsArgs(q=d_q.ptr, out=d_out.ptr, q_stride=n_head * hd, out_stride=n_head * hd, kv=d_pool.ptr,
+                               k_off=d_off.ptr, v_off=d_off.ptr, n_vis=d_vis.ptr, k_layer_off=0,
+                               v_layer_off=max_ctx * row, n_past=0, n_head=n_head, n_kv=n_kv, head_dim=hd,
+                               scale=0.125, f16=int(f16), scratch=0, max_vis=max(vis), outq=d_outq.ptr)
+    need = H.lib().axon_hip_attention_scratch_floats(C.byref(args), C.c_size_t(n))
+    scratch = H.DeviceBuffer(max(need, 1) * 4)
+    args.scratch = scratch.ptr if need else 0
+    H.check(H.lib().axon_hip_attention_rows(C.byref(args), C.c_size_t(n)), "attention_rows")
+    got = d_out.download(np.float32).reshape(n, n_head, hd)
+    got_q = d_outq.download(np.uint8, n * nbq * 34).reshape(n, nbq * 34)
+    want = np.zeros_like(got)
+    for i in (0, m + 1, m + 2):
+        s, L = seq_of[i], vis[i]
+        want[i] = o.attention_kv_heads(q[i].reshape(1, n_head, hd), pool[s, 0, :L].copy(), pool[s, 1, :L].copy(), 1,
+                                       L - 1, n_head, n_kv, hd, 0.125, 0, n_head, f16=f16)[0]
+    L = n_past + m
+    want[1:m + 1] = o.attention_kv_heads(q[1:m + 1].reshape(m, n_head, hd), pool[1, 0, :L].copy(),
+                                         pool[1, 1, :L].copy(), m, n_past, n_head, n_kv, hd, 0.125, 0, n_head, f16=f16)
+    for i in range(n):
+        assert np.array_equal(got[i], want[i]), i
+        assert np.array_equal(got_q[i], o.quantize_row_q8_0(want[i].ravel()).view(np.uint8).ravel()), i
