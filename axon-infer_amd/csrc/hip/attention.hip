@@ -32,6 +32,7 @@ constexpr uint32_t kVMaxItems = kVTile * 128 / 4 / kThreads;  // 4-float items p
 // per CU), LDS up to this many bytes (two workgroups per CU).
 constexpr uint32_t kBlockMinWorkgroups = 512;
 constexpr size_t kBlockMaxLds = 80 * 1024;
+constexpr int kBlockWaves = 3;  // waves per SIMD the blocked kernel's registers allow
 
 __host__ __device__ inline uint32_t round4(uint32_t v) { return (v + 3) & ~3u; }
 __host__ __device__ inline size_t vtile_bytes(uint32_t hd) { return static_cast<size_t>(hd) * kVPitch * 4; }
@@ -328,103 +329,76 @@ __global__ __launch_bounds__(kThreads) void attention_kernel(AttnArgs a) {
 template <uint32_t G, uint32_t R>
 __host__ __device__ constexpr uint32_t block_pairs() { return G * R; }
 
+// A pair's row of probabilities spans whole V tiles.
+__host__ __device__ inline uint32_t block_pitch(uint32_t n_vis) { return (n_vis + kVTile - 1) / kVTile * kVTile; }
+
 __host__ __device__ inline size_t block_lds(uint32_t pairs, uint32_t n_vis) {
-  return static_cast<size_t>(pairs) * (64 + round4(n_vis)) * 4 + vtile_bytes(64);
+  return static_cast<size_t>(pairs) * block_pitch(n_vis) * 4 + vtile_bytes(64);
 }
 
-template <bool F16, uint32_t G, uint32_t R>
-__global__ __launch_bounds__(kThreads) void attention_block_kernel(AttnArgs a, uint32_t n_rows, uint32_t lds_bytes) {
-  static_assert(R >= 1 && R <= 4 && G * R <= 16, "block shape");
-  constexpr uint32_t kPairs = block_pairs<G, R>();
+// The rows r0 .. r0 + RR - 1 of one K/V span (nv[i] positions each, 0 for a row past the
+// launch) on the whole workgroup: scores, softmax and value mix as described above. VEC: the
+// span's K and V rows are 16-byte aligned (vector loads); else element loads.
+template <bool F16, uint32_t G, uint32_t RR, bool VEC>
+__device__ __forceinline__ void block_rows(const AttnArgs& a, uint32_t r0, uint32_t g, const uint32_t (&nv)[RR],
+                                           int64_t k_off, int64_t v_off, float* lds, uint32_t* nv_s,
+                                           const uint64_t* exp_tab) {
+  constexpr uint32_t kPairs = block_pairs<G, RR>();
   constexpr uint32_t kChains = (kPairs + 3) / 4;
-  constexpr uint32_t es = F16 ? 2 : 4;
-  extern __shared__ __attribute__((aligned(16))) float lds[];
   const uint32_t tid = threadIdx.x, wave = tid >> 6, lane = tid & 63u;
-  const uint32_t g = blockIdx.x % a.n_kv;
-  const uint32_t n_blocks = (n_rows + R - 1) / R;
-  const uint32_t r0 = (n_blocks - 1 - blockIdx.x / a.n_kv) * R;
   const size_t kv_row = static_cast<size_t>(a.n_kv) * 64;
-
-  // Row r0's span; the block shares it when every other row of the block has the same.
-  const int64_t k_off = (a.k_off != nullptr ? a.k_off[r0] : 0) + a.k_off_c;
-  const int64_t v_off = (a.v_off != nullptr ? a.v_off[r0] : 0) + a.v_off_c;
-  uint32_t nv[R];
-  bool shared = true;
-#pragma unroll
-  for (uint32_t i = 0; i < R; ++i) {
-    const uint32_t r = r0 + i;
-    nv[i] = 0;
-    if (r < n_rows) {
-      nv[i] = a.n_vis != nullptr ? static_cast<uint32_t>(a.n_vis[r]) : static_cast<uint32_t>(a.n_past) + r + 1;
-      if (i > 0)
-        shared = shared && (a.k_off != nullptr ? a.k_off[r] : 0) + a.k_off_c == k_off &&
-                 (a.v_off != nullptr ? a.v_off[r] : 0) + a.v_off_c == v_off;
-    }
-  }
   uint32_t nmax = 0;
 #pragma unroll
-  for (uint32_t i = 0; i < R; ++i) nmax = max(nmax, nv[i]);
-  const uintptr_t base = reinterpret_cast<uintptr_t>(a.kv);
-  const bool aligned = ((base + static_cast<uintptr_t>(k_off) * es) & 15u) == 0 &&
-                       ((base + static_cast<uintptr_t>(v_off) * es) & 15u) == 0;
-  if (!shared || !aligned || block_lds(kPairs, nmax) > lds_bytes) {
-    for (uint32_t i = 0; i < R && r0 + i < n_rows; ++i) {
-      if (i > 0) __syncthreads();  // the previous row's readers of LDS are done
-      attention_row<F16, false>(a, r0 + i, g, lds);
-    }
-    return;
-  }
-
-  // Each row's visible positions, for lookups by a row index that is not a constant.
-  __shared__ uint32_t nv_s[R];
-  if (tid < R) nv_s[tid] = tid == 0 ? nv[0] : tid == 1 ? nv[R > 1 ? 1 : 0] : tid == 2 ? nv[R > 2 ? 2 : 0] : nv[R - 1];
+  for (uint32_t i = 0; i < RR; ++i) nmax = max(nmax, nv[i]);
+  if (tid < RR) nv_s[tid] = tid == 0 ? nv[0] : tid == 1 ? nv[RR > 1 ? 1 : 0] : tid == 2 ? nv[RR > 2 ? 2 : 0] : nv[RR - 1];
+  __syncthreads();  // nv_s is written (and the previous rows' readers of LDS are done)
   auto vis = [&](uint32_t i) { return nv_s[i]; };
 
-  const uint32_t pitch = round4(nmax);
-  float* qs = lds;                  // [pair][64], pair = row * G + head
-  float* sc = qs + kPairs * 64;     // [pair][pitch]
+  const uint32_t pitch = block_pitch(nmax);
+  float* sc = lds;                  // [pair][pitch], pair = row * G + head
   float* vt = sc + kPairs * pitch;  // [64][kVPitch]
-  for (uint32_t e = tid; e < kPairs * 64; e += kThreads) {
-    const uint32_t i = e / (G * 64), rest = e % (G * 64);
-    qs[e] = r0 + i < n_rows
-                ? a.q[static_cast<size_t>(r0 + i) * a.q_stride + static_cast<size_t>(g) * G * 64 + rest]
-                : 0.0f;
-  }
-  __syncthreads();
 
-  // Scores: one position per lane, its K row once for every pair that sees it.
+  // Scores: one position per lane; its K row, held in registers, serves the dot of every pair
+  // that sees the position. The q rows are wave-uniform and read through the constant address
+  // space (scalar loads: the kernel never writes them), so the dots read no LDS.
+  using cfloat = const __attribute__((address_space(4))) float;
   const size_t kcol = static_cast<size_t>(k_off) + static_cast<size_t>(g) * 64;
   for (uint32_t j = tid; j < nmax; j += kThreads) {
     const size_t krow = kcol + j * kv_row;
     float kr[64];
-    if constexpr (F16) {
+    if constexpr (!VEC) {
+#pragma unroll
+      for (int d = 0; d < 64; ++d) kr[d] = kv_at<F16>(a.kv, krow + d);
+    } else if constexpr (F16) {
       const uint4* kp = reinterpret_cast<const uint4*>(reinterpret_cast<const uint16_t*>(a.kv) + krow);
 #pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        const uint4 t = kp[i];
+      for (int c = 0; c < 8; ++c) {
+        const uint4 t = kp[c];
         const uint32_t w4[4] = {t.x, t.y, t.z, t.w};
 #pragma unroll
         for (int k = 0; k < 4; ++k) {
-          kr[8 * i + 2 * k] = half_value(w4[k] & 0xffffu);
-          kr[8 * i + 2 * k + 1] = half_value(w4[k] >> 16);
+          kr[8 * c + 2 * k] = half_value(w4[k] & 0xffffu);
+          kr[8 * c + 2 * k + 1] = half_value(w4[k] >> 16);
         }
       }
     } else {
       const float4* kp = reinterpret_cast<const float4*>(reinterpret_cast<const float*>(a.kv) + krow);
 #pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        const float4 t = kp[i];
-        kr[4 * i] = t.x;
-        kr[4 * i + 1] = t.y;
-        kr[4 * i + 2] = t.z;
-        kr[4 * i + 3] = t.w;
+      for (int c = 0; c < 16; ++c) {
+        const float4 t = kp[c];
+        kr[4 * c] = t.x;
+        kr[4 * c + 1] = t.y;
+        kr[4 * c + 2] = t.z;
+        kr[4 * c + 3] = t.w;
       }
     }
 #pragma unroll
-    for (uint32_t i = 0; i < R; ++i) {
+    for (uint32_t i = 0; i < RR; ++i) {
       if (j < nv[i]) {
+        cfloat* qrow = (cfloat*)(a.q + static_cast<size_t>(r0 + i) * a.q_stride + static_cast<size_t>(g) * G * 64);
+#pragma unroll 1
         for (uint32_t h = 0; h < G; ++h) {
-          const float* qh = qs + (i * G + h) * 64;
+          cfloat* qh = qrow + h * 64;
           float acc = 0.0f;
 #pragma unroll
           for (int d = 0; d < 64; ++d) acc += qh[d] * kr[d];
@@ -435,35 +409,78 @@ __global__ __launch_bounds__(kThreads) void attention_block_kernel(AttnArgs a, u
   }
   __syncthreads();
 
-  // Softmax, one wave per pair.
-  for (uint32_t pr = wave; pr < kPairs; pr += kThreads / 64) {
-    const uint32_t n = vis(pr / G);
-    if (n == 0) continue;  // a row past the end
-    float* s = sc + pr * pitch;
-    float m = -INFINITY;
-    for (uint32_t j = lane; j < n; j += 64) m = fmaxf(m, s[j]);
+  // Softmax, one wave per pair, the wave's pairs (wave, wave + 4, ...) side by side. Each pair's
+  // row is zeroed past its positions to the end of the last V tile, so that the value mix can run
+  // whole tiles.
+  uint32_t cpair[kChains], cvis[kChains];
+  float* cs[kChains];
+  uint32_t nhi = 0;
 #pragma unroll
-    for (int off = 32; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off, 64));
-    double part[4] = {0.0, 0.0, 0.0, 0.0};
+  for (uint32_t c = 0; c < kChains; ++c) {
+    const uint32_t pr = wave + 4 * c;
+    cpair[c] = min(pr, kPairs - 1);
+    cvis[c] = pr < kPairs ? vis(cpair[c] / G) : 0;
+    cs[c] = sc + cpair[c] * pitch;
+    nhi = max(nhi, cvis[c]);
+  }
+  {
+    float m[kChains];
 #pragma unroll
-    for (int w = 0; w < 4; ++w) {
-      for (uint32_t j = lane + 64 * w; j < n; j += 256) {
-        const float e = exp_libm(s[j] - m);
-        s[j] = e;
-        part[w] += static_cast<double>(e);
-      }
+    for (uint32_t c = 0; c < kChains; ++c) m[c] = -INFINITY;
+    for (uint32_t j = lane; j < nhi; j += 64) {
 #pragma unroll
-      for (int off = 32; off > 0; off >>= 1) part[w] += __shfl_xor(part[w], off, 64);
+      for (uint32_t c = 0; c < kChains; ++c)
+        if (j < cvis[c]) m[c] = fmaxf(m[c], cs[c][j]);
     }
-    double sum = 0.0;
 #pragma unroll
-    for (int w = 0; w < 4; ++w) sum += part[w];
-    const float inv = static_cast<float>(1.0 / sum);
-    for (uint32_t j = lane; j < n; j += 64) s[j] *= inv;
+    for (int off = 32; off > 0; off >>= 1) {
+#pragma unroll
+      for (uint32_t c = 0; c < kChains; ++c) m[c] = fmaxf(m[c], __shfl_xor(m[c], off, 64));
+    }
+    double part[kChains][4];
+#pragma unroll
+    for (uint32_t c = 0; c < kChains; ++c)
+#pragma unroll
+      for (int w = 0; w < 4; ++w) part[c][w] = 0.0;
+    for (uint32_t j = lane; j < nhi; j += 64) {
+#pragma unroll
+      for (uint32_t c = 0; c < kChains; ++c)
+        if (j < cvis[c]) cs[c][j] = exp_libm_from(cs[c][j] - m[c], exp_tab);
+    }
+    for (uint32_t j0 = 0; j0 < nhi; j0 += 256) {
+#pragma unroll
+      for (int w = 0; w < 4; ++w) {
+        const uint32_t j = j0 + 64 * w + lane;
+#pragma unroll
+        for (uint32_t c = 0; c < kChains; ++c)
+          if (j < cvis[c]) part[c][w] += static_cast<double>(cs[c][j]);
+      }
+    }
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) {
+#pragma unroll
+      for (uint32_t c = 0; c < kChains; ++c)
+#pragma unroll
+        for (int w = 0; w < 4; ++w) part[c][w] += __shfl_xor(part[c][w], off, 64);
+    }
+    float inv[kChains];
+#pragma unroll
+    for (uint32_t c = 0; c < kChains; ++c) {
+      double sum = 0.0;
+#pragma unroll
+      for (int w = 0; w < 4; ++w) sum += part[c][w];
+      inv[c] = static_cast<float>(1.0 / sum);
+    }
+    for (uint32_t j = lane; j < pitch; j += 64) {
+#pragma unroll
+      for (uint32_t c = 0; c < kChains; ++c)
+        if (wave + 4 * c < kPairs) cs[c][j] = j < cvis[c] ? cs[c][j] * inv[c] : 0.0f;
+    }
   }
 
   // Value mix over V tiles of kVTile positions, stored transposed ([d][position]); the next
-  // tile's loads fly while the current one is walked.
+  // tile's loads fly while the current one is walked. A pair's positions past its own are added
+  // as 0 * 0 (both factors selected to zero), which leaves its sum unchanged.
   constexpr uint32_t kItems = kVTile * 16 / kThreads;  // float4 per thread per tile
   const size_t vcol = static_cast<size_t>(v_off) + static_cast<size_t>(g) * 64;
   float4 reg[kItems];
@@ -475,7 +492,9 @@ __global__ __launch_bounds__(kThreads) void attention_block_kernel(AttnArgs a, u
       float4 v = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
       if (j0 + jj < nmax) {
         const size_t e = vcol + static_cast<size_t>(j0 + jj) * kv_row + 4 * dq;
-        if constexpr (F16) {
+        if constexpr (!VEC) {
+          v = make_float4(kv_at<F16>(a.kv, e), kv_at<F16>(a.kv, e + 1), kv_at<F16>(a.kv, e + 2), kv_at<F16>(a.kv, e + 3));
+        } else if constexpr (F16) {
           const uint2 h = *reinterpret_cast<const uint2*>(reinterpret_cast<const uint16_t*>(a.kv) + e);
           v = make_float4(half_value(h.x & 0xffffu), half_value(h.x >> 16), half_value(h.y & 0xffffu),
                           half_value(h.y >> 16));
@@ -486,15 +505,6 @@ __global__ __launch_bounds__(kThreads) void attention_block_kernel(AttnArgs a, u
       reg[k] = v;
     }
   };
-  // The lane's chains: pairs wave + 4c (a pair past kPairs reads the last pair's row and is
-  // never stored).
-  uint32_t cpair[kChains], cvis[kChains];
-#pragma unroll
-  for (uint32_t c = 0; c < kChains; ++c) {
-    const uint32_t pr = wave + 4 * c;
-    cpair[c] = min(pr, kPairs - 1);
-    cvis[c] = vis(cpair[c] / G);
-  }
   float acc[kChains];
 #pragma unroll
   for (uint32_t c = 0; c < kChains; ++c) acc[c] = 0.0f;
@@ -514,53 +524,75 @@ __global__ __launch_bounds__(kThreads) void attention_block_kernel(AttnArgs a, u
     }
     __syncthreads();
     if (j0 + kVTile < nmax) load_tile(j0 + kVTile);
-    const float* pp[kChains];
+    // Positions of this tile each chain adds (a chain past kPairs counts as whole: its sum is
+    // never stored).
     bool full = true;
+    uint32_t cnt[kChains];
 #pragma unroll
     for (uint32_t c = 0; c < kChains; ++c) {
-      pp[c] = sc + cpair[c] * pitch + j0;
-      full = full && cvis[c] >= j0 + kVTile;
+      cnt[c] = wave + 4 * c >= kPairs ? kVTile : cvis[c] > j0 ? min(kVTile, cvis[c] - j0) : 0;
+      full = full && cnt[c] == kVTile;
     }
+    // kSetQ * 4 positions per register set, two sets: each set's LDS reads are issued a set ahead
+    // of its adds.
+    constexpr uint32_t kSetQ = 1, kSet = 4 * kSetQ;
+    float4 va[kSetQ], vb[kSetQ], pa[kChains][kSetQ], pb[kChains][kSetQ];
+    auto get = [&](uint32_t j1, float4 (&v)[kSetQ], float4 (&pv)[kChains][kSetQ]) {
+#pragma unroll
+      for (uint32_t u = 0; u < kSetQ; ++u) v[u] = *reinterpret_cast<const float4*>(vv + j1 + 4 * u);
+#pragma unroll
+      for (uint32_t c = 0; c < kChains; ++c)
+#pragma unroll
+        for (uint32_t u = 0; u < kSetQ; ++u) pv[c][u] = *reinterpret_cast<const float4*>(cs[c] + j0 + j1 + 4 * u);
+    };
+    auto run = [&](const float4 (&v)[kSetQ], const float4 (&pv)[kChains][kSetQ]) {
+#pragma unroll
+      for (uint32_t u = 0; u < kSetQ; ++u) {
+#pragma unroll
+        for (uint32_t c = 0; c < kChains; ++c) acc[c] += pv[c][u].x * v[u].x;
+#pragma unroll
+        for (uint32_t c = 0; c < kChains; ++c) acc[c] += pv[c][u].y * v[u].y;
+#pragma unroll
+        for (uint32_t c = 0; c < kChains; ++c) acc[c] += pv[c][u].z * v[u].z;
+#pragma unroll
+        for (uint32_t c = 0; c < kChains; ++c) acc[c] += pv[c][u].w * v[u].w;
+      }
+    };
+    auto run_masked = [&](const float4 (&v)[kSetQ], const float4 (&pv)[kChains][kSetQ], uint32_t j1) {
+      auto term = [&](uint32_t c, uint32_t jj, float pq, float vq) {
+        const bool in = jj < cnt[c];
+        acc[c] += (in ? pq : 0.0f) * (in ? vq : 0.0f);
+      };
+#pragma unroll
+      for (uint32_t u = 0; u < kSetQ; ++u) {
+        const uint32_t jj = j1 + 4 * u;
+#pragma unroll
+        for (uint32_t c = 0; c < kChains; ++c) term(c, jj, pv[c][u].x, v[u].x);
+#pragma unroll
+        for (uint32_t c = 0; c < kChains; ++c) term(c, jj + 1, pv[c][u].y, v[u].y);
+#pragma unroll
+        for (uint32_t c = 0; c < kChains; ++c) term(c, jj + 2, pv[c][u].z, v[u].z);
+#pragma unroll
+        for (uint32_t c = 0; c < kChains; ++c) term(c, jj + 3, pv[c][u].w, v[u].w);
+      }
+    };
+    get(0, va, pa);
+    get(kSet, vb, pb);
     if (full) {
-      // Eight positions per register set, two sets: each set's LDS reads are issued a set ahead
-      // of its adds.
-      float4 va[2], vb[2], pa[kChains][2], pb[kChains][2];
-      auto get = [&](uint32_t j1, float4 (&v)[2], float4 (&p)[kChains][2]) {
-        v[0] = *reinterpret_cast<const float4*>(vv + j1);
-        v[1] = *reinterpret_cast<const float4*>(vv + j1 + 4);
 #pragma unroll
-        for (uint32_t c = 0; c < kChains; ++c) {
-          p[c][0] = *reinterpret_cast<const float4*>(pp[c] + j1);
-          p[c][1] = *reinterpret_cast<const float4*>(pp[c] + j1 + 4);
-        }
-      };
-      auto run = [&](const float4 (&v)[2], const float4 (&p)[kChains][2]) {
-#pragma unroll
-        for (uint32_t u = 0; u < 2; ++u) {
-#pragma unroll
-          for (uint32_t c = 0; c < kChains; ++c) acc[c] += p[c][u].x * v[u].x;
-#pragma unroll
-          for (uint32_t c = 0; c < kChains; ++c) acc[c] += p[c][u].y * v[u].y;
-#pragma unroll
-          for (uint32_t c = 0; c < kChains; ++c) acc[c] += p[c][u].z * v[u].z;
-#pragma unroll
-          for (uint32_t c = 0; c < kChains; ++c) acc[c] += p[c][u].w * v[u].w;
-        }
-      };
-      get(0, va, pa);
-      get(8, vb, pb);
-#pragma unroll
-      for (uint32_t j1 = 0; j1 < kVTile; j1 += 16) {
+      for (uint32_t j1 = 0; j1 < kVTile; j1 += 2 * kSet) {
         run(va, pa);
-        if (j1 + 16 < kVTile) get(j1 + 16, va, pa);
+        if (j1 + 2 * kSet < kVTile) get(j1 + 2 * kSet, va, pa);
         run(vb, pb);
-        if (j1 + 24 < kVTile) get(j1 + 24, vb, pb);
+        if (j1 + 3 * kSet < kVTile) get(j1 + 3 * kSet, vb, pb);
       }
     } else {
 #pragma unroll
-      for (uint32_t c = 0; c < kChains; ++c) {
-        const uint32_t cnt = cvis[c] > j0 ? min(kVTile, cvis[c] - j0) : 0;
-        for (uint32_t j = 0; j < cnt; ++j) acc[c] += pp[c][j] * vv[j];
+      for (uint32_t j1 = 0; j1 < kVTile; j1 += 2 * kSet) {
+        run_masked(va, pa, j1);
+        if (j1 + 2 * kSet < kVTile) get(j1 + 2 * kSet, va, pa);
+        run_masked(vb, pb, j1 + kSet);
+        if (j1 + 3 * kSet < kVTile) get(j1 + 3 * kSet, vb, pb);
       }
     }
   }
@@ -569,12 +601,61 @@ __global__ __launch_bounds__(kThreads) void attention_block_kernel(AttnArgs a, u
   for (uint32_t c = 0; c < kChains; ++c) {
     const uint32_t pr = wave + 4 * c;
     const uint32_t r = r0 + pr / G;
-    if (pr < kPairs && r < n_rows) {
+    if (pr < kPairs && cvis[c] > 0) {
       const size_t col = static_cast<size_t>(g * G + pr % G) * 64 + lane;
       a.out[static_cast<size_t>(r) * a.out_stride + col] = acc[c];
       if (a.outq != nullptr)
         quantize_block_lanes(acc[c], lane & 31u, a.outq + (static_cast<size_t>(r) * nbq + col / kQK) * kBytesQ8_0);
     }
+  }
+}
+
+template <bool F16, uint32_t G, uint32_t R>
+__global__ __launch_bounds__(kThreads, kBlockWaves) void attention_block_kernel(AttnArgs a, uint32_t n_rows, uint32_t lds_bytes) {
+  static_assert(R >= 1 && R <= 4 && G * R <= 16, "block shape");
+  constexpr uint32_t es = F16 ? 2 : 4;
+  extern __shared__ __attribute__((aligned(16))) float lds[];
+  __shared__ uint32_t nv_s[R];
+  __shared__ uint64_t exp_tab[32];
+  const uint32_t tid = threadIdx.x;
+  const uint32_t g = blockIdx.x % a.n_kv;
+  const uint32_t n_blocks = (n_rows + R - 1) / R;
+  const uint32_t r0 = (n_blocks - 1 - blockIdx.x / a.n_kv) * R;
+  if (tid < 32) exp_tab[tid] = kExp2Tab[tid];
+
+  // Each row's span and positions; the block shares row r0's span when every other row has it.
+  int64_t k_off[R], v_off[R];
+  uint32_t nv[R];
+  bool shared = true;
+#pragma unroll
+  for (uint32_t i = 0; i < R; ++i) {
+    const uint32_t r = min(r0 + i, n_rows - 1);
+    k_off[i] = (a.k_off != nullptr ? a.k_off[r] : 0) + a.k_off_c;
+    v_off[i] = (a.v_off != nullptr ? a.v_off[r] : 0) + a.v_off_c;
+    nv[i] = r0 + i < n_rows
+                ? (a.n_vis != nullptr ? static_cast<uint32_t>(a.n_vis[r]) : static_cast<uint32_t>(a.n_past) + r + 1)
+                : 0;
+    if (i > 0 && nv[i] > 0) shared = shared && k_off[i] == k_off[0] && v_off[i] == v_off[0];
+  }
+  uint32_t nmax = 0;
+#pragma unroll
+  for (uint32_t i = 0; i < R; ++i) nmax = max(nmax, nv[i]);
+  const uintptr_t base = reinterpret_cast<uintptr_t>(a.kv);
+  auto aligned = [&](uint32_t i) {
+    return ((base + static_cast<uintptr_t>(k_off[i]) * es) & 15u) == 0 &&
+           ((base + static_cast<uintptr_t>(v_off[i]) * es) & 15u) == 0;
+  };
+  if (shared && aligned(0) && block_lds(G * R, nmax) <= lds_bytes) {
+    block_rows<F16, G, R, true>(a, r0, g, nv, k_off[0], v_off[0], lds, nv_s, exp_tab);
+    return;
+  }
+  // One row at a time (a single row's scores always fit: the launch is sized for max_vis).
+#pragma unroll
+  for (uint32_t i = 0; i < R; ++i) {
+    if (nv[i] == 0) continue;
+    const uint32_t one[1] = {nv[i]};
+    if (aligned(i)) block_rows<F16, G, 1, true>(a, r0 + i, g, one, k_off[i], v_off[i], lds, nv_s, exp_tab);
+    else block_rows<F16, G, 1, false>(a, r0 + i, g, one, k_off[i], v_off[i], lds, nv_s, exp_tab);
   }
 }
 
@@ -601,7 +682,7 @@ bool block_lds_granted(size_t need) {
 // kBlockMaxLds; blocks whose scores do not fit run one row per workgroup.
 template <bool F16, uint32_t G, uint32_t R>
 bool try_block(const AttnArgs& a, uint32_t n_rows) {
-  const size_t one = static_cast<size_t>(G) * (64 + round4(a.max_vis)) * 4 + vtile_bytes(64);
+  const size_t one = block_lds(G, a.max_vis);
   const size_t lds = std::max(one, std::min(block_lds(G * R, a.max_vis), kBlockMaxLds));
   if (!block_lds_granted<F16, G, R>(lds)) return false;
   hipLaunchKernelGGL((attention_block_kernel<F16, G, R>), dim3((n_rows + R - 1) / R * a.n_kv), dim3(kThreads), lds, stream(), a,
