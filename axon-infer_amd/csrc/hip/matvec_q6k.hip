@@ -26,6 +26,8 @@ namespace axon_hip {
 
 namespace {
 
+constexpr uint32_t kQ6MaxRows = 8;  // activation rows per workgroup of the planar kernel
+
 constexpr int kThreads = 256;  // rows per workgroup
 constexpr int kWin = 53;       // dwords covering one super-block plus its 2-byte misalignment
 
@@ -291,10 +293,15 @@ __device__ __forceinline__ void planar_fetch(const uint8_t* col, uint32_t n_out,
   b.d = reinterpret_cast<const uint16_t*>(col + static_cast<size_t>(208) * n_out)[row];
 }
 
+// The activations of a column, read through the constant address space: every lane of a wave
+// reads the same values, so they arrive by scalar loads as instruction operands (the kernel
+// never writes them).
+using cfloat = const __attribute__((address_space(4))) float;
+
 // The row's super-block in element order, as q6k_window: value (d*scale)*(q-32), then
-// acc += value * x, element after element.
+// acc += value * x, element after element. Activation row m of the column at x + xoff[m].
 template <int MM>
-__device__ __forceinline__ void planar_superblock(const PlanarBlock& b, const float* x, uint32_t n_in,
+__device__ __forceinline__ void planar_superblock(const PlanarBlock& b, cfloat* x, const uint32_t (&xoff)[MM],
                                                   float (&acc)[MM]) {
   auto dw = [&](int o) {
     return b.q[o / 16][(o / 4) & 3];
@@ -303,35 +310,55 @@ __device__ __forceinline__ void planar_superblock(const PlanarBlock& b, const fl
   uint32_t sc[4];
 #pragma unroll
   for (int i = 0; i < 4; ++i) sc[i] = dw(192 + 4 * i);
+  // 64 steps of 4 elements (step s: elements 4s .. 4s+3, in order). Each step's activations
+  // (4 per row) are loaded kAhead steps ahead into a ring of register sets; the empty asm keeps
+  // the compiler from hoisting more loads above it, which would run the scalar registers out.
+  constexpr int kAhead = MM >= 4 ? 1 : 8 / MM;
+  float xr[kAhead + 1][MM][4];
+  auto xload = [&](int st, float (&xv)[MM][4]) {
 #pragma unroll
-  for (int n = 0; n < 2; ++n) {
+    for (int m = 0; m < MM; ++m) {
+      cfloat* xm = x + xoff[m] + 4 * st;
 #pragma unroll
-    for (int qi = 0; qi < 4; ++qi) {
+      for (int e = 0; e < 4; ++e) xv[m][e] = xm[e];
+    }
+  };
+  auto step = [&](int st, const float (&xv)[MM][4]) {
+    const int n = st / 32, qi = (st / 8) % 4, half = (st / 4) % 2, l4 = st % 4;
+    const int si = n * 8 + qi * 2 + half;
+    const float scale = static_cast<float>(static_cast<int8_t>((sc[si >> 2] >> (8 * (si & 3))) & 0xffu));
+    const float ds = d * scale;       // exact
+    const float neg32 = -32.0f * ds;  // exact
+    const int l = 16 * half + 4 * l4;
+    const uint32_t lw = dw(64 * n + 32 * (qi & 1) + l);
+    const uint32_t hw = dw(128 + 32 * n + l);
+    const uint32_t q = ((lw >> (4 * (qi >> 1))) & 0x0f0f0f0fu) | (((hw >> (2 * qi)) & 0x03030303u) << 4);
 #pragma unroll
-      for (int half = 0; half < 2; ++half) {
-        const int si = n * 8 + qi * 2 + half;
-        const float scale = static_cast<float>(static_cast<int8_t>((sc[si >> 2] >> (8 * (si & 3))) & 0xffu));
-        const float ds = d * scale;       // exact
-        const float neg32 = -32.0f * ds;  // exact
+    for (int e = 0; e < 4; ++e) {
+      const float v = fmaf(ds, static_cast<float>((q >> (8 * e)) & 0xffu), neg32);  // (d*scale)*(q-32)
 #pragma unroll
-        for (int l4 = 0; l4 < 4; ++l4) {
-          const int l = 16 * half + 4 * l4;
-          const uint32_t lw = dw(64 * n + 32 * (qi & 1) + l);
-          const uint32_t hw = dw(128 + 32 * n + l);
-          const uint32_t q = ((lw >> (4 * (qi >> 1))) & 0x0f0f0f0fu) | (((hw >> (2 * qi)) & 0x03030303u) << 4);
-          const uint32_t e0 = 128 * n + 32 * qi + l;
+      for (int m = 0; m < MM; ++m) acc[m] += v * xv[m][e];
+    }
+  };
+  if constexpr (kAhead == 1) {
+    xload(0, xr[0]);
 #pragma unroll
-          for (int m = 0; m < MM; ++m) {
-            const float4 x4 = *reinterpret_cast<const float4*>(x + m * n_in + e0);
-            const float xv[4] = {x4.x, x4.y, x4.z, x4.w};
+    for (int st = 0; st < 64; st += 2) {
+      xload(st + 1, xr[1]);
+      asm volatile("" ::: "memory");
+      step(st, xr[0]);
+      if (st + 2 < 64) xload(st + 2, xr[0]);
+      asm volatile("" ::: "memory");
+      step(st + 1, xr[1]);
+    }
+  } else {
 #pragma unroll
-            for (int e = 0; e < 4; ++e) {
-              const float v = fmaf(ds, static_cast<float>((q >> (8 * e)) & 0xffu), neg32);  // (d*scale)*(q-32)
-              acc[m] += v * xv[e];
-            }
-          }
-        }
-      }
+    for (int st = 0; st < kAhead; ++st) xload(st, xr[st]);
+#pragma unroll
+    for (int st = 0; st < 64; ++st) {
+      if (st + kAhead < 64) xload(st + kAhead, xr[(st + kAhead) % (kAhead + 1)]);
+      asm volatile("" ::: "memory");
+      step(st, xr[st % (kAhead + 1)]);
     }
   }
 }
@@ -339,23 +366,35 @@ __device__ __forceinline__ void planar_superblock(const PlanarBlock& b, const fl
 // One lane per output row, TH rows per workgroup (TH = 64 spreads a short matrix over more
 // CUs); workgroup (blockIdx.x, blockIdx.y) takes activation rows [MM * blockIdx.x, +MM) against
 // output rows [TH * blockIdx.y, +TH), so the workgroups that share a weight slice are launched
-// one after another. The chunk's activation rows sit in LDS (rows past m_total are zeros and
-// their outputs are not stored); the row's super-blocks are double-buffered in registers, two
-// per trip so the buffers swap roles without copies, every fetch unconditional (clamped to the
-// last column).
+// one after another. The chunk's activation rows are read by scalar loads (rows past m_total
+// read the chunk's last row; their outputs are not stored); the row's super-blocks are
+// double-buffered in registers, two per trip so the buffers swap roles without copies, every
+// fetch unconditional (clamped to the last column). Read as LDS broadcasts, the activations
+// cost the LDS a full 1 KB per wave and read for 4 elements of one row; as scalar operands
+// they cost nothing there (32 rows of 128256 x 2048: 571 -> 503 us; 4 rows 101 -> 81 us).
 template <int MM, int TH>
 __global__ __launch_bounds__(TH) void q6k_planar_kernel(MatvecArgs args, uint32_t n_in, size_t col_bytes,
                                                         uint32_t m_total) {
-  extern __shared__ __attribute__((aligned(16))) float xs[];  // [MM][n_in]
   const uint32_t tid = threadIdx.x;
   const uint32_t nsb = args.nb;
   const MatvecSeg seg = args.seg[0];
   const uint32_t m0 = blockIdx.x * MM;
   const uint32_t mm = min(static_cast<uint32_t>(MM), m_total - m0);
-  const float4* x4 = reinterpret_cast<const float4*>(args.xq) + static_cast<size_t>(m0) * n_in / 4;
-  for (uint32_t i = tid; i < MM * n_in / 4; i += TH)
-    reinterpret_cast<float4*>(xs)[i] = i < mm * n_in / 4 ? x4[i] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-  __syncthreads();
+  // Rows past m_total read the chunk's last row (their outputs are not stored).
+  cfloat* xs = (cfloat*)(reinterpret_cast<const float*>(args.xq) + static_cast<size_t>(m0) * n_in);
+  uint32_t xoff[MM];
+#pragma unroll
+  for (int m = 0; m < MM; ++m) xoff[m] = min(static_cast<uint32_t>(m), mm - 1) * n_in;
+  // The activations were just written, possibly through another XCD's L2: one round of vector
+  // loads brings them into this one's, so the scalar loads that follow hit it.
+  {
+    const float4* xv = reinterpret_cast<const float4*>(args.xq) + static_cast<size_t>(m0) * n_in / 4;
+    for (uint32_t i = tid; i < mm * n_in / 4; i += TH) {
+      const float4 t = xv[i];
+      asm volatile("" ::"v"(t.x));
+    }
+    __syncthreads();
+  }
   const uint32_t row = blockIdx.y * TH + tid;
   if (row >= seg.n_out) return;
   float acc[MM];
@@ -367,9 +406,9 @@ __global__ __launch_bounds__(TH) void q6k_planar_kernel(MatvecArgs args, uint32_
   planar_fetch(col_at(0), seg.n_out, row, a);
   for (uint32_t c = 0; c < nsb; c += 2) {
     planar_fetch(col_at(c + 1), seg.n_out, row, b);
-    planar_superblock<MM>(a, xs + c * kQKK, n_in, acc);
+    planar_superblock<MM>(a, xs + c * kQKK, xoff, acc);
     planar_fetch(col_at(c + 2), seg.n_out, row, a);
-    if (c + 1 < nsb) planar_superblock<MM>(b, xs + (c + 1) * kQKK, n_in, acc);
+    if (c + 1 < nsb) planar_superblock<MM>(b, xs + (c + 1) * kQKK, xoff, acc);
   }
 #pragma unroll
   for (int m = 0; m < MM; ++m)
@@ -399,16 +438,15 @@ int matvec_q6k_planar_launch(MatvecArgs& a, uint32_t n_in) {
   if ((reinterpret_cast<uintptr_t>(a.seg[0].w) & 15u) != 0 || (reinterpret_cast<uintptr_t>(a.xq) & 15u) != 0)
     return fail(kInvalidArgument, "matmul_q6_k_planar: the planar weights and the activations must be 16-byte aligned");
   const size_t col_bytes = q6k_planar_column_bytes(n_out);
-  // Activation rows per workgroup: up to 8 (each lane then runs 8 chains, and every weight
-  // slice is read once per 8 rows), as many as 64 KB of LDS holds, but fewer while that leaves
-  // under 1024 waves of 64 rows: a lane's chains run one element after another, so a short
-  // matrix needs the rows spread over more waves more than it needs fewer weight reads. One
-  // launch covers every row.
+  // Activation rows per workgroup: up to kQ6MaxRows (each lane then runs that many chains, and
+  // every weight slice is read once per that many rows), but fewer while that leaves under 1024
+  // waves of 64 rows: a lane's chains run one element after another, so a short matrix needs
+  // the rows spread over more waves more than it needs fewer weight reads. One launch covers
+  // every row.
   uint32_t mm = 1;
-  while (mm < 8 && mm < a.m && static_cast<size_t>(2 * mm) * n_in * 4 <= 65536) mm *= 2;
+  while (mm < kQ6MaxRows && mm < a.m) mm *= 2;
   while (mm > 1 && ceil_div(a.m, mm) * ceil_div(n_out, 64) < 1024) mm /= 2;
-  const size_t lds = static_cast<size_t>(mm) * n_in * 4;
-  if (lds > 65536) return fail(kUnsupported, "matmul_q6_k_planar: n_in %u too large for LDS", n_in);
+  const size_t lds = 0;
   const uint32_t chunks = static_cast<uint32_t>(ceil_div(a.m, mm));
   // 256 rows per workgroup when that still gives a workgroup per CU, else 64.
   const bool wide = ceil_div(n_out, 256) * chunks >= 256;
