@@ -5,12 +5,16 @@ embedding/output, llama3 rope scaling; seeded random-init GGUF written by synth.
 
 Two workloads, both greedy:
   decode-b1    one sequence: a 512-token prompt is prefilled (untimed), W warm-up decode steps,
-               then K timed decode steps. One step = forward_one on the device + the greedy
-               choice (Sampler::sample at temperature zero, src/sampling/sampler.cpp:67-102) made
-               on the device, only the token id crossing to the host: the reference's
-               Engine::generate step (src/engine/engine.cpp:50-58) with the sampler moved next to
-               the logits. value = K / seconds. The same steps with the [n_vocab] logits copied to
-               the host and argmax'd there are reported as decode_b1_host_argmax.
+               then K timed decode steps, generated as the reference's Engine::generate does at
+               temperature zero (src/engine/engine.cpp:50-58): each step is forward_one of the
+               previous token + the greedy choice (Sampler::sample, src/sampling/sampler.cpp:67-102).
+               Here the choice is made on the device next to the logits and stays there as the
+               next step's input (axon_model_generate_greedy); the K ids reach the host at the
+               end. value = K / seconds. Two host-driven variants of the same steps follow on the
+               same sequence: decode_b1_host_ids (the id of each step copied to the host and
+               passed back as the next forward's token) and decode_b1_host_argmax (the [n_vocab]
+               logits copied to the host and argmax'd by numpy). All three give the same ids
+               (tests/test_hip_configs.py, test_generate_greedy_equals_host_loop).
   ragged-32    continuous batching of 32 sequences with contexts drawn U[64, 2048] from the seed:
                eight cohorts of four join 16 steps apart, each sequence decodes 128 tokens. Joining
                sequences are prefilled in their join step (timed apart, as src/engine/batch.cpp:71-85
@@ -120,21 +124,21 @@ def bench_decode_b1(H, model, n_vocab, steps, warmup, prompt_len, seed):
     t0 = time.perf_counter()
     tok = prefill_greedy(model, cache, prompt)
     prefill_s = time.perf_counter() - t0
-    tok = greedy_decode(model, cache, tok, warmup)
-    H.synchronize()
-    t0 = time.perf_counter()
-    tok = greedy_decode(model, cache, tok, steps)
-    H.synchronize()
-    elapsed = time.perf_counter() - t0
-    ctx_end = model.cache_pos(cache)
-    # The same steps with the id kept on the device between steps, over the next steps of the
-    # same sequence (its warm-up first).
     tok = device_loop_decode(model, cache, tok, warmup)
     H.synchronize()
     t0 = time.perf_counter()
     tok = device_loop_decode(model, cache, tok, steps)
     H.synchronize()
-    loop_s = time.perf_counter() - t0
+    elapsed = time.perf_counter() - t0
+    ctx_end = model.cache_pos(cache)
+    # The same steps driven from the host, each id copied to the host and passed back as the
+    # next forward's token, over the next steps of the same sequence (its warm-up first).
+    tok = greedy_decode(model, cache, tok, warmup)
+    H.synchronize()
+    t0 = time.perf_counter()
+    tok = greedy_decode(model, cache, tok, steps)
+    H.synchronize()
+    ids_s = time.perf_counter() - t0
     # The same step with the logits row copied to the host and argmax'd there (the reference's
     # placement of the sampler), over the next steps of the same sequence.
     host_steps = min(steps, 64)
@@ -147,8 +151,8 @@ def bench_decode_b1(H, model, n_vocab, steps, warmup, prompt_len, seed):
             prompt_len / prefill_s, "context": [prompt_len + warmup, ctx_end],
             "host_argmax": {"tokens_per_s": round(host_steps / host_s, 2),
                             "ms_per_step": round(1e3 * host_s / host_steps, 4), "steps": host_steps},
-            "device_loop": {"tokens_per_s": round(steps / loop_s, 2), "ms_per_step": round(1e3 * loop_s / steps, 4),
-                            "steps": steps, "context": [ctx_end + warmup, ctx_end + warmup + steps]}}
+            "host_ids": {"tokens_per_s": round(steps / ids_s, 2), "ms_per_step": round(1e3 * ids_s / steps, 4),
+                         "steps": steps, "context": [ctx_end + warmup, ctx_end + warmup + steps]}}
 
 
 def probe_pass(H, model, n_vocab, steps, prompt_len, seed, weight_type):
@@ -712,7 +716,7 @@ def main() -> int:
                         "per-layer launches"),
         "prefill_tokens_per_s": round(b1["prefill_tokens_per_s"], 1),
         "decode_b1_host_argmax": b1["host_argmax"],
-        "decode_b1_device_loop": b1["device_loop"],
+        "decode_b1_host_ids": b1["host_ids"],
         "cpu_baseline": None,
     }
     if TRAFFIC_FILE.exists():
