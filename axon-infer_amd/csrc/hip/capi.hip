@@ -795,6 +795,7 @@ axon_hip::StepShape step_shape_of(const axon_hip_decode_shape* sh) {
   s.t_gu = sh->type_gate_up;
   s.t_down = sh->type_down;
   s.max_ctx = sh->max_ctx;
+  s.cache_f16 = sh->cache_f16 != 0;
   return s;
 }
 constexpr uint32_t kStepSpinLimit = 1u << 20;  // polls of one barrier (about a second) before giving up

@@ -27,6 +27,7 @@ struct StepShape {
   uint32_t n_layer, d, dq, dkv, ff, n_head, n_kv, rot_half;
   uint32_t max_ctx;              // positions of the caller's cache slots (bounds pos)
   int t_qkv, t_o, t_gu, t_down;  // weight types (Q8_0, Q4_0, Q4_1), the same in every layer
+  int cache_f16;                 // the KV pool holds fp16 bit patterns (keys and values rounded once)
 };
 
 struct StepCall {
@@ -34,7 +35,7 @@ struct StepCall {
   float eps, scale;
   const float* rope_table;  // [pos][rot_half] (cos, sin)
   float* x;                 // [d] residual stream, in and out
-  float* cache;             // KV pool (float elements)
+  float* cache;             // KV pool (float elements, or fp16 ones with shape.cache_f16)
   int64_t cache_off;        // the sequence's slot
   int32_t pos;              // the row's position: attention sees pos + 1 positions
   void* work;               // workspace of step_workspace_bytes

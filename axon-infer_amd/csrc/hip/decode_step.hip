@@ -88,6 +88,17 @@ __device__ __forceinline__ float4 gload4(const float* p) {
   return make_float4(v.x, v.y, v.z, v.w);
 }
 __device__ __forceinline__ float gload(const float* p) { return *reinterpret_cast<GlobalF>(reinterpret_cast<uintptr_t>(p)); }
+typedef uint32_t U2v __attribute__((ext_vector_type(2)));
+typedef uint32_t U4v __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ uint32_t gload_u1(const void* p) {
+  return *reinterpret_cast<const uint32_t __attribute__((address_space(1)))*>(reinterpret_cast<uintptr_t>(p));
+}
+__device__ __forceinline__ U2v gload_u2(const void* p) {
+  return *reinterpret_cast<const U2v __attribute__((address_space(1)))*>(reinterpret_cast<uintptr_t>(p));
+}
+__device__ __forceinline__ U4v gload_u4(const void* p) {
+  return *reinterpret_cast<const U4v __attribute__((address_space(1)))*>(reinterpret_cast<uintptr_t>(p));
+}
 
 
 // A workgroup barrier that waits for this wave's LDS accesses only (never for its copies).
@@ -381,6 +392,9 @@ __device__ __forceinline__ void copier_main(const StepK& k, StepLds& sh, uint8_t
   wait_vm<0>();  // no copy outlives the workgroup
 }
 
+// F16: the KV pool holds fp16 bit patterns (one instantiation per cache type, so the float
+// cache's kernel carries no branch on it).
+template <bool F16>
 __global__ __launch_bounds__(kStepThreads) void decode_step_kernel(StepK k) {
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
   __shared__ StepLds sh;
@@ -415,6 +429,7 @@ __global__ __launch_bounds__(kStepThreads) void decode_step_kernel(StepK k) {
 
   const uint32_t kv_row = s.dkv;
   const uint32_t group = s.n_head / s.n_kv;
+  constexpr bool f16 = F16;
   // A phase starts with a workgroup barrier, after which everyone knows whether to give up.
   // The flags are LDS words read right after a barrier, whose memory clobber makes the
   // compiler read them again (plain accesses keep them ds_read/ds_write; a generic or volatile
@@ -477,10 +492,18 @@ __global__ __launch_bounds__(kStepThreads) void decode_step_kernel(StepK k) {
       // the lines sit in this XCD's L2 by then; the values are discarded.
       float touch = 0.0f;
       const uint32_t p1t = min(p1, last);
-      for (uint32_t e = t; p0 < p1t && e < (p1t - p0) * 4; e += kCompute) {
-        const int64_t layer = (e & 2u) ? L.v_layer_off : L.k_layer_off;
-        touch += gload(k.cache + k.cache_off + layer + g * kHeadDim + static_cast<size_t>(p0 + e / 4) * kv_row +
-                       (e & 1u) * 32);
+      if constexpr (f16) {  // one 128-byte line per head row
+        const uint16_t* c16 = reinterpret_cast<const uint16_t*>(k.cache) + k.cache_off + g * kHeadDim;
+        for (uint32_t e = t; p0 < p1t && e < (p1t - p0) * 2; e += kCompute) {
+          const int64_t layer = (e & 1u) ? L.v_layer_off : L.k_layer_off;
+          touch += __uint_as_float(gload_u1(c16 + layer + static_cast<size_t>(p0 + e / 2) * kv_row));
+        }
+      } else {  // two per head row
+        for (uint32_t e = t; p0 < p1t && e < (p1t - p0) * 4; e += kCompute) {
+          const int64_t layer = (e & 2u) ? L.v_layer_off : L.k_layer_off;
+          touch += gload(k.cache + k.cache_off + layer + g * kHeadDim + static_cast<size_t>(p0 + e / 4) * kv_row +
+                         (e & 1u) * 32);
+        }
       }
       if (nr == 0) asm volatile("" ::"v"(touch));
       if (nr > 0) {
@@ -521,7 +544,16 @@ __global__ __launch_bounds__(kStepThreads) void decode_step_kernel(StepK k) {
             // The cache row for later steps; the tagged copy for this step's attention.
             const int64_t at = k.cache_off + (seg == 1 ? L.k_layer_off : L.v_layer_off) +
                                static_cast<int64_t>(k.pos) * kv_row + oo;
-            *reinterpret_cast<float2*>(k.cache + at) = make_float2(x0, x1);
+            if constexpr (f16) {
+              // Rounded once into the fp16 cache; this step's attention reads the rounded row,
+              // as every later step does.
+              const uint32_t h0 = float_to_half_bits(x0), h1 = float_to_half_bits(x1);
+              *reinterpret_cast<uint32_t*>(reinterpret_cast<uint16_t*>(k.cache) + at) = h0 | (h1 << 16);
+              x0 = half_value(h0);
+              x1 = half_value(h1);
+            } else {
+              *reinterpret_cast<float2*>(k.cache + at) = make_float2(x0, x1);
+            }
             uint64_t* kv = k.kvt + (seg == 1 ? 0 : s.dkv) + oo;
             put(kv, tag_a, __float_as_uint(x0));
             put(kv + 1, tag_a, __float_as_uint(x1));
@@ -544,16 +576,30 @@ __global__ __launch_bounds__(kStepThreads) void decode_step_kernel(StepK k) {
       float* vb = sc + ((s.max_ctx + 3) & ~3u);
       if (p0 < p1) {
         const float* kbase = k.cache + k.cache_off + L.k_layer_off + g * kHeadDim;
+        const uint16_t* kbase16 = reinterpret_cast<const uint16_t*>(k.cache) + k.cache_off + L.k_layer_off + g * kHeadDim;
         const uint32_t pairs = (p1 - p0) * group;
         float kr[kHeadDim];
         auto krow = [&](uint32_t j) {
+          if constexpr (f16) {
+            const uint16_t* kb = kbase16 + static_cast<size_t>(j) * kv_row;
 #pragma unroll
-          for (uint32_t i = 0; i < kHeadDim / 4; ++i) {
-            const float4 v = gload4(kbase + static_cast<size_t>(j) * kv_row + 4 * i);
-            kr[4 * i] = v.x;
-            kr[4 * i + 1] = v.y;
-            kr[4 * i + 2] = v.z;
-            kr[4 * i + 3] = v.w;
+            for (uint32_t i = 0; i < kHeadDim / 8; ++i) {
+              const U4v h = gload_u4(kb + 8 * i);
+#pragma unroll
+              for (uint32_t c = 0; c < 4; ++c) {
+                kr[8 * i + 2 * c] = half_value(h[c] & 0xffffu);
+                kr[8 * i + 2 * c + 1] = half_value(h[c] >> 16);
+              }
+            }
+          } else {
+#pragma unroll
+            for (uint32_t i = 0; i < kHeadDim / 4; ++i) {
+              const float4 v = gload4(kbase + static_cast<size_t>(j) * kv_row + 4 * i);
+              kr[4 * i] = v.x;
+              kr[4 * i + 1] = v.y;
+              kr[4 * i + 2] = v.z;
+              kr[4 * i + 3] = v.w;
+            }
           }
         };
         bool ok = true;
@@ -582,6 +628,8 @@ __global__ __launch_bounds__(kStepThreads) void decode_step_kernel(StepK k) {
         const uint32_t dim0 = (rank % k.dsplit) * k.dd;
         const uint32_t per = k.dd / 4;  // float4 of a V row slice
         const float* vbase = k.cache + k.cache_off + L.v_layer_off + g * kHeadDim + dim0;
+        const uint16_t* vbase16 =
+            reinterpret_cast<const uint16_t*>(k.cache) + k.cache_off + L.v_layer_off + g * kHeadDim + dim0;
         // V slices of positions [0, last) in chunks of vchunk positions, kVRegs float4 per thread.
         float4 vr[kVRegs];
         auto vload = [&](uint32_t c) {
@@ -589,8 +637,18 @@ __global__ __launch_bounds__(kStepThreads) void decode_step_kernel(StepK k) {
           for (uint32_t u = 0; u < kVRegs; ++u) {
             const uint32_t unit = t + u * kCompute;
             const uint32_t j = c * k.vchunk + unit / per;
-            vr[u] = j < last ? gload4(vbase + static_cast<size_t>(j) * kv_row + 4 * (unit % per))
-                             : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+            if constexpr (f16) {
+              if (j < last) {
+                const U2v h = gload_u2(vbase16 + static_cast<size_t>(j) * kv_row + 4 * (unit % per));
+                vr[u] = make_float4(half_value(h[0] & 0xffffu), half_value(h[0] >> 16), half_value(h[1] & 0xffffu),
+                                    half_value(h[1] >> 16));
+              } else {
+                vr[u] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+              }
+            } else {
+              vr[u] = j < last ? gload4(vbase + static_cast<size_t>(j) * kv_row + 4 * (unit % per))
+                               : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+            }
           }
         };
         vload(0);
@@ -833,8 +891,10 @@ int step_device(uint32_t* cus, size_t* lds_max) {
         hipDeviceGetAttribute(&smem, hipDeviceAttributeMaxSharedMemoryPerBlock, dev) != hipSuccess)
       return fail(kHipError, "decode step: device attributes");
     const size_t want = static_cast<size_t>(smem) - 1024;  // the kernel's static LDS beside it
-    if (hipFuncSetAttribute(reinterpret_cast<const void*>(decode_step_kernel), hipFuncAttributeMaxDynamicSharedMemorySize,
-                            static_cast<int>(want)) != hipSuccess) {
+    if (hipFuncSetAttribute(reinterpret_cast<const void*>(decode_step_kernel<false>),
+                            hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(want)) != hipSuccess ||
+        hipFuncSetAttribute(reinterpret_cast<const void*>(decode_step_kernel<true>),
+                            hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(want)) != hipSuccess) {
       (void)hipGetLastError();
       return fail(kUnsupported, "decode step: %zu bytes of LDS not granted", want);
     }
@@ -944,6 +1004,8 @@ int step_launch(const StepShape& s, const StepCall& c) {
   k.status = c.status;
   k.spin_limit = c.spin_limit;
   void* args[] = {&k};
+  const void* kernel = s.cache_f16 ? reinterpret_cast<const void*>(decode_step_kernel<true>)
+                                   : reinterpret_cast<const void*>(decode_step_kernel<false>);
   // A probed launch is bracketed by events on the stream (a cooperative launch takes none of its own).
   hipEvent_t start = nullptr, stop = nullptr;
   take_probe(&start, &stop);
@@ -958,9 +1020,9 @@ int step_launch(const StepShape& s, const StepCall& c) {
     return v != nullptr && std::strcmp(v, "plain") == 0;
   }();
   const hipError_t e =
-      plain ? hipLaunchKernel(reinterpret_cast<const void*>(decode_step_kernel), dim3(cus), dim3(kStepThreads), args,
+      plain ? hipLaunchKernel(kernel, dim3(cus), dim3(kStepThreads), args,
                               static_cast<unsigned>(lds), stream())
-            : hipLaunchCooperativeKernel(reinterpret_cast<const void*>(decode_step_kernel), dim3(cus),
+            : hipLaunchCooperativeKernel(kernel, dim3(cus),
                                          dim3(kStepThreads), args, static_cast<unsigned>(lds), stream());
   if (e != hipSuccess) return fail(kHipError, "decode step: launch: %s", hipGetErrorString(e));
   if (stop != nullptr && hipEventRecord(stop, stream()) != hipSuccess)

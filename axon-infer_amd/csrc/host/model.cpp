@@ -519,7 +519,6 @@ Expected<bool> LlamaModel::setup_persistent_decode() {
     return true;
   };
   if (exact_) return reason("exact activations (float matmul inputs)");
-  if (cache_type_ != CacheType::F32) return reason("an fp16 KV cache");
   if (c.rope_style != kernels::RopeStyle::Normal) return reason("NeoX rotary layout");
   if (c.head_dim != 64) return reason("a head size other than 64");
   for (const Layer& L : layers_) {
@@ -542,6 +541,7 @@ Expected<bool> LlamaModel::setup_persistent_decode() {
   sh.type_gate_up = static_cast<int>(layers_[0].w_gate.type);
   sh.type_down = static_cast<int>(layers_[0].w_down.type);
   sh.max_ctx = static_cast<std::uint32_t>(max_ctx_);
+  sh.cache_f16 = cache_type_ == CacheType::F16 ? 1 : 0;
   if (const char* why = axon_hip_decode_layers_unsupported(&sh); why != nullptr)
     return reason(why);
   const std::size_t dkv = c.n_embd_kv();
@@ -604,7 +604,8 @@ double LlamaModel::step_bytes(std::size_t n_vis) const {
   for (const Layer& L : layers_) {
     for (const Tensor* w : {&L.wq, &L.wk, &L.wv, &L.wo, &L.w_gate, &L.w_up, &L.w_down})
       b += static_cast<double>(w->row_bytes) * w->ne1;
-    b += 2 * d * 4 + 2 * dkv * 4 * (static_cast<double>(n_vis) + 1);
+    const double kv_elem = cache_type_ == CacheType::F16 ? 2 : 4;
+    b += 2 * d * 4 + 2 * dkv * kv_elem * (static_cast<double>(n_vis) + 1);
   }
   return b + 2 * d * 4;
 }

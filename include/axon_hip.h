@@ -315,7 +315,7 @@ int axon_hip_matvec_fused_supported(int type, int in_mode, size_t n_rows, size_t
  * SiLU * up, down with the residual add. The same bits as those steps launched one by one
  * (matvec_fused and attention_rows). One workgroup per CU; a phase's outputs carry the phase's
  * number and their readers poll for it; the caller's stream then continues with the output
- * norm and matrix. F32 cache, head
+ * norm and matrix. F32 or fp16 cache, head
  * size 64, n_embd a multiple of 32 up to 2048, Q8_0 / Q4_0 / Q4_1 layer matrices (one type per
  * matrix role); axon_hip_decode_layers_unsupported names what else it needs. */
 typedef struct {
@@ -338,6 +338,7 @@ typedef struct {
   uint32_t n_layer, n_embd, n_head, n_head_kv, n_ff, rotary_dim;
   int type_qkv, type_o, type_gate_up, type_down;
   uint32_t max_ctx; /* positions of a cache slot: calls take pos < max_ctx */
+  int cache_f16;    /* 1: the KV pool holds fp16 bit patterns (llama.cpp:525-532), else floats */
 } axon_hip_decode_shape;
 
 typedef struct {
@@ -345,7 +346,7 @@ typedef struct {
   float eps, scale;                    /* RMSNorm epsilon; 1 / sqrt(head size) */
   const float* rope_table;             /* device (cos, sin) [pos][rotary_dim / 2], built on the host */
   float* x;                            /* device [n_embd]: the row's residual stream, in and out */
-  float* cache;                        /* device KV pool (float elements) */
+  float* cache;                        /* device KV pool (float elements, or fp16 with shape->cache_f16) */
   int64_t cache_off;                   /* the row's slot, in elements */
   int32_t pos;                         /* the row's position */
   void* work;                          /* device workspace, zeroed once before its first call */

@@ -269,14 +269,16 @@ def test_c5_sampled_stream_matches_the_reference_sampler():
     hm.close()
 
 
-@pytest.mark.parametrize("cfg", ["c1", "c3", "c4"])
-def test_persistent_decode_equals_launch_by_launch(cfg):
+@pytest.mark.parametrize("cfg, cache", [("c1", "f32"), ("c3", "f32"), ("c4", "f32"), ("c1", "f16"), ("c4", "f16")])
+def test_persistent_decode_equals_launch_by_launch(cfg, cache):
     """The one-kernel decode step (axon_hip_decode_layers) against the same model launching each
     step of a layer on its own: the persistent path is taken (info.persistent_decode), and 48
-    greedy steps after a 40-token prompt give bit-identical logits."""
+    greedy steps after a 40-token prompt give bit-identical logits and cache rows. With the fp16
+    cache the kernel rounds the new key and value once into the pool and reads every position
+    (the new one included) back from fp16, as the per-layer launches do."""
     path = model_path(cfg)
-    a = hip(path, max_seq=64, max_ctx=160)
-    b = hip(path, max_seq=64, max_ctx=160, persistent=False)
+    a = hip(path, max_seq=64, max_ctx=160, cache=cache)
+    b = hip(path, max_seq=64, max_ctx=160, persistent=False, cache=cache)
     assert a.info.persistent_decode == 1 and b.info.persistent_decode == 0
     prompt = np.random.default_rng(77).integers(0, a.n_vocab, 40).astype(np.int32)
     ca, cb = a.new_cache(), b.new_cache()
