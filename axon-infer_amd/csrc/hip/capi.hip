@@ -10,6 +10,7 @@
 #include "../../../include/axon_hip.h"
 
 #include <algorithm>
+#include <atomic>
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
@@ -799,8 +800,14 @@ axon_hip::StepShape step_shape_of(const axon_hip_decode_shape* sh) {
   return s;
 }
 constexpr uint32_t kStepSpinLimit = 1u << 20;  // polls of one barrier (about a second) before giving up
+std::atomic<uint32_t> g_step_spin_limit{kStepSpinLimit};
 static_assert(sizeof(axon_hip_decode_layer) == sizeof(axon_hip::StepLayer), "one layer record layout");
 }  // namespace
+
+int axon_hip_decode_layers_set_spin_limit(uint32_t polls) {
+  g_step_spin_limit.store(polls == 0 ? kStepSpinLimit : polls, std::memory_order_relaxed);
+  return kOk;
+}
 
 size_t axon_hip_decode_layers_workspace_bytes(const axon_hip_decode_shape* shape) {
   return shape == nullptr ? 0 : step_workspace_bytes(step_shape_of(shape));
@@ -833,7 +840,7 @@ int axon_hip_decode_layers(const axon_hip_decode_shape* shape, const axon_hip_de
   c.work = a->work;
   c.epoch = *a->epoch;
   c.status = a->status;
-  c.spin_limit = kStepSpinLimit;
+  c.spin_limit = g_step_spin_limit.load(std::memory_order_relaxed);
   const StepShape s = step_shape_of(shape);
   const int rc = step_launch(s, c);
   if (rc != kOk) return rc;

@@ -354,6 +354,11 @@ typedef struct {
   uint32_t* status;                    /* pinned host word, 0 at the start: nonzero once a call gave up */
 } axon_hip_decode_layers_args;
 
+/* Test hook, no counterpart in the reference: the polls of one tagged word after which a
+ * workgroup of later axon_hip_decode_layers calls gives up (0 restores the default, about a
+ * second). A small limit forces the give-up path from the host: the kernel still drains, the
+ * call's status word is set, and the caller's recovery runs. */
+int axon_hip_decode_layers_set_spin_limit(uint32_t polls);
 size_t axon_hip_decode_layers_workspace_bytes(const axon_hip_decode_shape* shape);
 /* NULL when this device runs the shape, else the reason. */
 const char* axon_hip_decode_layers_unsupported(const axon_hip_decode_shape* shape);

@@ -326,3 +326,39 @@ def test_generate_greedy_equals_host_loop(cfg):
         assert np.array_equal(la, lb)
         a.close()
         b.close()
+
+
+def test_persistent_decode_gives_up_cleanly_and_recovers(tmp_path_factory):
+    """The step kernel's bounded waits, forced from the host: with a limit of one poll per
+    tagged word the workgroups of a one-row pass give up instead of waiting, the kernel still
+    drains, and the pass fails with the status word's error (its cache position not advanced).
+    With the limit restored, the same model retries that token and decodes 8 more steps with
+    logits bit-identical to the per-layer launches."""
+    from dataclasses import replace
+    import synth
+    import axon_hip as H
+    spec = replace(synth.CONFIGS["c4"], name="t-c4-giveup-2l", n_layer=2, n_vocab=2048, seed=41)
+    path = synth.cached_model(spec, tmp_path_factory.mktemp("models"))
+    a = hip(path, max_seq=32, max_ctx=64)
+    b = hip(path, max_seq=32, max_ctx=64, persistent=False)
+    assert a.info.persistent_decode == 1
+    prompt = np.random.default_rng(9).integers(0, 2048, 12).astype(np.int32)
+    ca, cb = a.new_cache(), b.new_cache()
+    la, lb = a.forward_prefill(ca, prompt)[-1], b.forward_prefill(cb, prompt)[-1]
+    assert np.array_equal(la, lb)
+    t = int(np.argmax(la))
+    lib = H.lib()
+    try:
+        assert lib.axon_hip_decode_layers_set_spin_limit(1) == 0
+        with pytest.raises(H.HipError, match="gave up"):
+            a.forward_prefill(ca, [t])
+    finally:
+        lib.axon_hip_decode_layers_set_spin_limit(0)
+    assert a.cache_pos(ca) == len(prompt)
+    for _ in range(9):
+        la, lb = a.forward_prefill(ca, [t])[0], b.forward_prefill(cb, [t])[0]
+        assert np.array_equal(la, lb)
+        t = int(np.argmax(la))
+    a.close()
+    b.close()
+
