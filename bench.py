@@ -391,6 +391,19 @@ def traffic_probe(H, model, n_vocab, steps, prompt_len, seed):
     model.free_cache(cache)
 
 
+def attention_traffic_probe(H, model, n_vocab, seed):
+    """The workload of the attention counter passes: the calibration copy of traffic_probe, then
+    the ragged-32 attention probe (every attn_scores64_kernel / attn_mixd_kernel launch of the
+    run is one layer of a 32-row batch at the ragged contexts); prints the probe's figures."""
+    src, dst = H.DeviceBuffer(COPY_BYTES), H.DeviceBuffer(COPY_BYTES)
+    src.fill(1)
+    H.call("memcpy_d2d", dst, src, COPY_BYTES)
+    H.synchronize()
+    src.free()
+    dst.free()
+    print(json.dumps(probe_attention_ragged(H, model, n_vocab, seed)), flush=True)
+
+
 def prefill_probe(H, model, n_vocab, seed, passes=4, prompt_len=512):
     """The workload of the prefill profiles: `passes` 512-token prefill passes (logits of the
     last row only), each on a new cache."""
@@ -622,6 +635,8 @@ def main() -> int:
                     help="only run the config-2 sweep and print its figures (the workload of its profile)")
     ap.add_argument("--c5-only", action="store_true",
                     help="only run the config-5 workload and print its figures (the workload of its profile)")
+    ap.add_argument("--attention-probe", action="store_true",
+                    help="only the calibration copy and the ragged-32 attention probe (counter passes)")
     ap.add_argument("--prefill-probe", action="store_true",
                     help="only run four 512-token prefill passes (the workload of the prefill profiles)")
     ap.add_argument("--cpu-budget", type=float, default=12.0, help="seconds per CPU baseline sample")
@@ -663,6 +678,11 @@ def main() -> int:
         traffic_probe(H, model, info.n_vocab, min(args.steps, 16), args.prompt, args.seed)
         model.close()
         log("traffic probe done")
+        return 0
+    if args.attention_probe:
+        attention_traffic_probe(H, model, info.n_vocab, args.seed)
+        model.close()
+        log("attention probe done")
         return 0
     if args.prefill_probe:
         prefill_probe(H, model, info.n_vocab, args.seed)
