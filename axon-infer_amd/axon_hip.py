@@ -258,6 +258,7 @@ def host() -> C.CDLL:
         L.axon_model_load.argtypes = [C.c_char_p, C.POINTER(ModelOptions), C.POINTER(C.c_void_p)]
         L.axon_model_free.argtypes = [C.c_void_p]
         L.axon_model_get_info.argtypes = [C.c_void_p, C.POINTER(ModelInfo)]
+        L.axon_model_set_persistent_decode.argtypes = [C.c_void_p, C.c_int]
         L.axon_model_cache_new.argtypes = [C.c_void_p, C.POINTER(C.c_int)]
         L.axon_model_cache_free.argtypes = [C.c_void_p, C.c_int]
         L.axon_model_cache_pos.argtypes = [C.c_void_p, C.c_int, C.POINTER(C.c_size_t)]
@@ -313,6 +314,16 @@ class Model:
         self.info = info
         self.n_vocab = info.n_vocab
         self.table_name = host().axon_model_table_name(self.h).decode()
+
+    def persistent_decode(self) -> bool:
+        """Whether one-row cached passes run as the persistent kernel now (a pass whose kernel
+        gave up turns it off)."""
+        info = ModelInfo()
+        host().axon_model_get_info(self.h, C.byref(info))
+        return bool(info.persistent_decode)
+
+    def set_persistent_decode(self, on: bool) -> None:
+        _mcheck(host().axon_model_set_persistent_decode(self.h, int(on)), "set_persistent_decode")
 
     def close(self) -> None:
         if getattr(self, "h", None):

@@ -18,6 +18,8 @@
 
 namespace axon_hip {
 
+extern std::atomic<size_t> g_device_allocations;  // alloc_count.hip
+
 namespace {
 
 thread_local char g_error[512] = "";
@@ -50,8 +52,11 @@ int init_device(int device) {
   e = hipStreamCreateWithFlags(&g_stream, hipStreamNonBlocking);
   if (e != hipSuccess) return hip_fail(e, "hipStreamCreateWithFlags");
   g_device = device;
-  // The fixed scratch of the allocation-free entry, looked up once with this device current.
-  return argmax_noalloc_setup();
+  // The fixed scratch of the allocation-free entry, looked up once with this device current. It
+  // serves that one optional entry only: a failed lookup is reported by the entry itself (which
+  // retries it), not by the library's initialisation.
+  if (argmax_noalloc_setup() != kOk) (void)hipGetLastError();
+  return kOk;
 }
 
 int ready() {
@@ -273,6 +278,7 @@ int axon_hip_malloc(void** ptr, size_t bytes) {
     return fail(kOutOfMemory, "hipMalloc: %zu bytes: out of device memory", bytes);
   }
   if (e != hipSuccess) return hip_fail(e, "hipMalloc");
+  g_device_allocations.fetch_add(1, std::memory_order_relaxed);
   return kOk;
 }
 
@@ -285,7 +291,9 @@ int axon_hip_free(void* ptr) {
 int axon_hip_host_malloc(void** ptr, size_t bytes) {
   AXON_READY();
   const hipError_t e = hipHostMalloc(ptr, bytes, hipHostMallocDefault);
-  return e == hipSuccess ? kOk : hip_fail(e, "hipHostMalloc");
+  if (e != hipSuccess) return hip_fail(e, "hipHostMalloc");
+  g_device_allocations.fetch_add(1, std::memory_order_relaxed);
+  return kOk;
 }
 
 int axon_hip_host_free(void* ptr) {
@@ -344,6 +352,7 @@ int axon_hip_event_create(void** event) {
   hipEvent_t ev;
   const hipError_t e = hipEventCreate(&ev);
   if (e != hipSuccess) return hip_fail(e, "hipEventCreate");
+  g_device_allocations.fetch_add(1, std::memory_order_relaxed);
   *event = ev;
   return kOk;
 }
@@ -828,6 +837,12 @@ int axon_hip_decode_layers(const axon_hip_decode_shape* shape, const axon_hip_de
   if (*reinterpret_cast<volatile uint32_t*>(a->status) != 0)
     return fail(kHipError, "decode_layers: an earlier call gave up at a device-wide barrier (status %u); "
                            "zero the workspace and reset epoch and status", *a->status);
+  const StepShape s = step_shape_of(shape);
+  // Phase tags are the low 32 bits of epoch + phase: the phases of this call must not wrap, or
+  // a tag could match a word written 2^32 phases earlier (or a zeroed word, tag 0).
+  if (*a->epoch + step_phases(s) > 0xffffffffull)
+    return fail(kInvalidArgument, "decode_layers: epoch %llu + %llu phases passes 2^32; zero the workspace and reset epoch",
+                static_cast<unsigned long long>(*a->epoch), static_cast<unsigned long long>(step_phases(s)));
   StepCall c{};
   c.layers = reinterpret_cast<const StepLayer*>(a->layers);
   c.eps = a->eps;
@@ -841,7 +856,6 @@ int axon_hip_decode_layers(const axon_hip_decode_shape* shape, const axon_hip_de
   c.epoch = *a->epoch;
   c.status = a->status;
   c.spin_limit = g_step_spin_limit.load(std::memory_order_relaxed);
-  const StepShape s = step_shape_of(shape);
   const int rc = step_launch(s, c);
   if (rc != kOk) return rc;
   *a->epoch += step_phases(s);

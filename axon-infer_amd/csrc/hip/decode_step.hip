@@ -32,8 +32,6 @@
 #include "decode_step.h"
 
 #include <algorithm>
-#include <cstdlib>
-#include <cstring>
 #include <mutex>
 
 namespace axon_hip {
@@ -1006,7 +1004,7 @@ int step_launch(const StepShape& s, const StepCall& c) {
   void* args[] = {&k};
   const void* kernel = s.cache_f16 ? reinterpret_cast<const void*>(decode_step_kernel<true>)
                                    : reinterpret_cast<const void*>(decode_step_kernel<false>);
-  // A probed launch is bracketed by events on the stream (a cooperative launch takes none of its own).
+  // A probed launch is bracketed by events on the stream.
   hipEvent_t start = nullptr, stop = nullptr;
   take_probe(&start, &stop);
   if (start != nullptr && hipEventRecord(start, stream()) != hipSuccess)
@@ -1015,18 +1013,10 @@ int step_launch(const StepShape& s, const StepCall& c) {
   // device with nothing else running, the stream's previous kernel done, every workgroup is
   // resident. The kernel needs no more than that (its hand-offs are its own tagged words, not
   // a grid barrier), and every wait is bounded: a workgroup that never became resident makes
-  // the call give up (status word), not hang. AXON_HIP_STEP_LAUNCH=cooperative takes the
-  // cooperative launch API instead, which checks residency at the launch but costs about 15 us
-  // per launch on this runtime (585 against 571 us per step, decode-b1 1533 against 1586 tok/s).
-  static const bool plain = [] {
-    const char* v = std::getenv("AXON_HIP_STEP_LAUNCH");
-    return v == nullptr || std::strcmp(v, "cooperative") != 0;
-  }();
-  const hipError_t e =
-      plain ? hipLaunchKernel(kernel, dim3(cus), dim3(kStepThreads), args,
-                              static_cast<unsigned>(lds), stream())
-            : hipLaunchCooperativeKernel(kernel, dim3(cus),
-                                         dim3(kStepThreads), args, static_cast<unsigned>(lds), stream());
+  // the call give up (status word), not hang. The cooperative launch API, which checks
+  // residency at the launch, cost about 15 us per launch on this runtime and profilers lose
+  // their results for processes that use it, so it is not used.
+  const hipError_t e = hipLaunchKernel(kernel, dim3(cus), dim3(kStepThreads), args, static_cast<unsigned>(lds), stream());
   if (e != hipSuccess) return fail(kHipError, "decode step: launch: %s", hipGetErrorString(e));
   if (stop != nullptr && hipEventRecord(stop, stream()) != hipSuccess)
     return fail(kHipError, "decode step: probe stop event");

@@ -15,6 +15,11 @@
 struct axon_model {
   std::unique_ptr<axon::model::LlamaModel> m;
   std::map<int, std::unique_ptr<axon::model::KVCache>> caches;
+  // Per-call argument staging, sized at load for max_batch + 1 rows, so that a pass through
+  // this interface allocates no host memory (tests/unit/test_model_forward.cpp:119-128).
+  std::vector<axon::model::KVCache*> batch;
+  std::vector<std::span<const int32_t>> windows;
+  std::vector<axon::sampling::Config> configs;
 };
 
 namespace {
@@ -69,7 +74,12 @@ int axon_model_load(const char* path, const axon_model_options* options, axon_mo
   }
   auto m = axon::model::LlamaModel::load(path, o);
   if (!m) return fail(m.error());
-  *out = new axon_model{std::move(*m), {}};
+  auto* model = new axon_model{std::move(*m), {}, {}, {}, {}};
+  const size_t rows = model->m->max_seq() + model->m->max_batch() + 1;
+  model->batch.reserve(rows);
+  model->windows.reserve(rows);
+  model->configs.reserve(rows);
+  *out = model;
   return 0;
 }
 
@@ -93,6 +103,12 @@ int axon_model_get_info(const axon_model* model, axon_model_info* out) {
   out->kv_bytes_per_position = static_cast<size_t>(c.n_layer) * 2 * c.n_embd_kv() * model->m->kv_element_bytes();
   out->cache_type = model->m->cache_type() == axon::model::CacheType::F16 ? 1 : 0;
   out->persistent_decode = model->m->persistent_decode() ? 1 : 0;
+  return 0;
+}
+
+int axon_model_set_persistent_decode(axon_model* model, int on) {
+  auto r = model->m->set_persistent_decode(on != 0);
+  if (!r) return fail(r.error());
   return 0;
 }
 
@@ -175,7 +191,8 @@ int axon_model_generate_greedy(axon_model* model, int cache, int32_t token, size
 }
 
 int axon_model_forward_batch(axon_model* model, const int* caches, const int32_t* tokens, size_t n, float* logits) {
-  std::vector<axon::model::KVCache*> cs(n);
+  std::vector<axon::model::KVCache*>& cs = model->batch;
+  cs.resize(n);
   for (size_t i = 0; i < n; ++i) {
     cs[i] = find(model, caches[i]);
     if (cs[i] == nullptr) return fail("forward_batch: unknown cache " + std::to_string(caches[i]));
@@ -196,7 +213,8 @@ int axon_model_forward_mixed(axon_model* model, int prefill_cache, const int32_t
     if (pc == nullptr) return fail("forward_mixed: unknown cache " + std::to_string(prefill_cache));
   }
   if (n != 0 && (caches == nullptr || tokens == nullptr)) return fail("forward_mixed: caches or tokens are NULL");
-  std::vector<axon::model::KVCache*> cs(n);
+  std::vector<axon::model::KVCache*>& cs = model->batch;
+  cs.resize(n);
   for (size_t i = 0; i < n; ++i) {
     cs[i] = find(model, caches[i]);
     if (cs[i] == nullptr) return fail("forward_mixed: unknown cache " + std::to_string(caches[i]));
@@ -212,7 +230,8 @@ int axon_model_forward_mixed(axon_model* model, int prefill_cache, const int32_t
 int axon_model_greedy(axon_model* model, const int32_t* const* recent, const size_t* recent_len, float repeat_penalty,
                       int repeat_last_n, int32_t* ids, size_t n) {
   if (ids == nullptr && n != 0) return fail("greedy: ids is NULL");
-  std::vector<std::span<const int32_t>> windows;
+  std::vector<std::span<const int32_t>>& windows = model->windows;
+  windows.clear();
   if (recent != nullptr) {
     if (recent_len == nullptr) return fail("greedy: recent_len is NULL");
     windows.resize(n);
@@ -241,9 +260,11 @@ int axon_model_sample(axon_model* model, const axon_sampler_config* configs, axo
                       const int32_t* const* recent, const size_t* recent_len, int32_t* ids, size_t n) {
   if (n != 0 && (configs == nullptr || rngs == nullptr || ids == nullptr))
     return fail("sample: configs, generators and ids are required");
-  std::vector<axon::sampling::Config> cs(n);
+  std::vector<axon::sampling::Config>& cs = model->configs;
+  cs.resize(n);
   for (size_t i = 0; i < n; ++i) cs[i] = config_of(configs[i]);
-  std::vector<std::span<const int32_t>> windows;
+  std::vector<std::span<const int32_t>>& windows = model->windows;
+  windows.clear();
   if (recent != nullptr) {
     if (recent_len == nullptr) return fail("sample: recent_len is NULL");
     windows.resize(n);

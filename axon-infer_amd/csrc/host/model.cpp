@@ -361,6 +361,7 @@ Expected<std::unique_ptr<LlamaModel>> LlamaModel::load(const std::string& path, 
       axon_hip_malloc(reinterpret_cast<void**>(&m->scores_), m->scores_floats_ * 4) != AXON_HIP_OK)
     return m->device_error("attention scratch");
   m->slot_used_.assign(m->n_slots_, false);
+  m->slot_cache_.assign(m->n_slots_, nullptr);
   if (options.persistent_decode) {
     auto st = m->setup_persistent_decode();
     if (!st) return st.error();
@@ -455,14 +456,20 @@ Expected<std::unique_ptr<KVCache>> LlamaModel::new_cache() {
   for (std::size_t s = 0; s < n_slots_; ++s) {
     if (!slot_used_[s]) {
       slot_used_[s] = true;
-      return std::make_unique<KVCache>(static_cast<int>(s), max_ctx_);
+      auto cache = std::make_unique<KVCache>(static_cast<int>(s), max_ctx_);
+      slot_cache_[s] = cache.get();
+      return cache;
     }
   }
   return make_error(ErrorCode::OutOfRange, "new_cache: all " + std::to_string(n_slots_) + " device KV slots are in use");
 }
 
 void LlamaModel::release_cache(const KVCache& cache) {
-  if (cache.slot() >= 0 && static_cast<std::size_t>(cache.slot()) < n_slots_) slot_used_[cache.slot()] = false;
+  if (cache.slot() >= 0 && static_cast<std::size_t>(cache.slot()) < n_slots_) {
+    slot_used_[cache.slot()] = false;
+    slot_cache_[cache.slot()] = nullptr;
+  }
+  if (step_pending_ == &cache) step_pending_ = nullptr;
 }
 
 Expected<std::vector<float>> LlamaModel::read_cache(const KVCache& cache, std::size_t layer, bool values, std::size_t n) {
@@ -581,17 +588,73 @@ Expected<bool> LlamaModel::setup_persistent_decode() {
   return true;
 }
 
-// After a synchronization: a persistent-kernel pass that gave up waiting for another workgroup's
-// output voids that pass; the workspace is reset so later passes run, and the error names what
-// happened.
+// After a synchronization (every pass issued so far has ended): a persistent-kernel pass that
+// gave up waiting for another workgroup's output voids that pass. Its cache goes back to the
+// position the pass started at (a pass whose logits stayed in HBM has already advanced it, and
+// the rows it wrote there are not the pass's results), the workspace is reset, and later one-row
+// passes of this model run layer by layer: a grid that could not become resident once (a CU
+// mask, another process holding CUs) is likely to fail again, and every such pass would cost a
+// full poll limit. set_persistent_decode(true) turns the kernel back on. The error names the
+// cache slot and the position.
 Expected<bool> LlamaModel::check_persistent_status() {
-  if (step_status_ == nullptr || *reinterpret_cast<volatile std::uint32_t*>(step_status_) == 0) return true;
+  if (step_status_ == nullptr || *reinterpret_cast<volatile std::uint32_t*>(step_status_) == 0) {
+    step_pending_ = nullptr;
+    return true;
+  }
   const std::uint32_t st = *step_status_;
+  std::string where;
+  if (step_pending_ != nullptr) {
+    if (step_pending_->pos() > step_pending_pos_) step_pending_->truncate(step_pending_pos_);
+    where = " at position " + std::to_string(step_pending_pos_) + " of the cache in slot " +
+            std::to_string(step_pending_->slot()) + " (rolled back to that position)";
+  }
+  step_pending_ = nullptr;
   if (axon_hip_memset(step_work_, 0, step_work_bytes_) != AXON_HIP_OK) return device_error("persistent decode reset");
   step_epoch_ = 0;
   *step_status_ = 0;
+  step_ok_ = false;
+  step_reason_ = "the persistent kernel gave up waiting for another workgroup (status " + std::to_string(st) +
+                 "); one-row passes run layer by layer";
   return make_error(ErrorCode::Device, "a one-row pass's persistent kernel gave up waiting for another workgroup (status " +
-                                           std::to_string(st) + "); that pass's results are void");
+                                           std::to_string(st) + ")" + where +
+                                           "; that pass's results are void, and later one-row passes run layer by layer");
+}
+
+// The phase tags of `passes` more persistent passes must not pass 2^32 (the kernel tags words
+// with the low 32 bits of epoch + phase): before they would, at a synchronization, the
+// workspace is zeroed and the epoch restarts (about 54 million steps of a 16-layer model).
+Expected<bool> LlamaModel::step_reserve(std::size_t passes) {
+  const std::uint64_t phases = 5ull * cfg_.n_layer * passes;
+  if (step_epoch_ + phases <= 0xffffffffull) return true;
+  if (axon_hip_synchronize() != AXON_HIP_OK) return device_error("synchronize");
+  if (auto st = check_persistent_status(); !st) return st.error();
+  if (axon_hip_memset(step_work_, 0, step_work_bytes_) != AXON_HIP_OK) return device_error("persistent decode reset");
+  step_epoch_ = 0;
+  if (phases > 0xffffffffull) return make_error(ErrorCode::InvalidArgument, "generate: too many steps in one call");
+  return true;
+}
+
+Expected<bool> LlamaModel::set_persistent_decode(bool on) {
+  if (axon_hip_synchronize() != AXON_HIP_OK) return device_error("synchronize");
+  if (auto st = check_persistent_status(); !st) return st.error();
+  if (!on) {
+    step_ok_ = false;
+    step_reason_ = "turned off by set_persistent_decode";
+    return true;
+  }
+  if (step_ok_) return true;
+  if (step_work_ == nullptr) {  // never set up (LoadOptions::persistent_decode was false)
+    auto st = setup_persistent_decode();
+    if (!st) return st.error();
+    if (!step_ok_) return make_error(ErrorCode::Unsupported, "persistent decode: " + step_reason_);
+    return true;
+  }
+  if (axon_hip_memset(step_work_, 0, step_work_bytes_) != AXON_HIP_OK) return device_error("persistent decode reset");
+  step_epoch_ = 0;
+  *step_status_ = 0;
+  step_ok_ = true;
+  step_reason_.clear();
+  return true;
 }
 
 // Algorithmic HBM bytes of one persistent decode step over n_vis positions: every layer's
@@ -739,6 +802,11 @@ Expected<std::size_t> LlamaModel::run(std::span<const Row> rows, bool copy_logit
   // One row of a cached pass: every layer in one persistent kernel.
   const bool persistent = step_ok_ && n == 1 && !free_pass;
   if (persistent) {
+    if (auto st = step_reserve(1); !st) return st.error();
+    // Until the next synchronization checks the status word, this pass may yet turn out void:
+    // its cache and starting position, to roll back to.
+    step_pending_ = slot_cache_[static_cast<std::size_t>(rows[0].slot)];
+    step_pending_pos_ = static_cast<std::size_t>(rows[0].pos);
     axon_hip_decode_layers_args sa{};
     sa.layers = static_cast<const axon_hip_decode_layer*>(step_layers_);
     sa.eps = eps;
@@ -1076,6 +1144,7 @@ Expected<std::size_t> LlamaModel::generate_greedy(KVCache& cache, std::int32_t t
   }
   if (axon_hip_synchronize() != AXON_HIP_OK) return device_error("synchronize");
   if (auto st = check_persistent_status(); !st) return st.error();
+  if (auto st = step_reserve(n); !st) return st.error();
   last_rows_ = 0;
   if (axon_hip_memcpy_h2d(gen_ids_, &token, 4) != AXON_HIP_OK) return device_error("generate");
   const std::size_t d = c.n_embd;

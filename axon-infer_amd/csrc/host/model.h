@@ -179,6 +179,9 @@ public:
   CacheType cache_type() const { return cache_type_; }
   // Whether one-row cached passes run as the persistent kernel, and if not, why.
   bool persistent_decode() const { return step_ok_; }
+  // Turns the persistent kernel for one-row passes on or off (on: Unsupported when the model's
+  // shape does not allow it). A pass whose kernel gave up turns it off (check_persistent_status).
+  Expected<bool> set_persistent_decode(bool on);
   const std::string& persistent_decode_reason() const { return step_reason_; }
   std::size_t kv_element_bytes() const { return cache_type_ == CacheType::F16 ? 2 : 4; }
 
@@ -258,11 +261,16 @@ private:
                  double out_bytes_override = -1.0);
   void probe_cancel();
   std::vector<bool> slot_used_;
+  std::vector<KVCache*> slot_cache_;  // the cache object of each used slot (new_cache to release_cache)
   // The persistent decode kernel (axon_hip_decode_layers): its shape, the device array of layer
   // records, its workspace and phase count, and the status word in pinned host memory.
   Expected<bool> setup_persistent_decode();
   Expected<bool> check_persistent_status();
+  Expected<bool> step_reserve(std::size_t passes);
   bool step_ok_ = false;
+  // The cache of the last persistent pass not yet checked, and the position it started at.
+  KVCache* step_pending_ = nullptr;
+  std::size_t step_pending_pos_ = 0;
   std::string step_reason_;
   axon_hip_decode_shape step_shape_{};
   void* step_layers_ = nullptr;

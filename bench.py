@@ -73,7 +73,7 @@ COPY_BYTES = 256 << 20
 MATVEC_KERNELS = ("matvec_dma_kernel<2>", "matvec_norm1_kernel<2>")
 # The persistent decode-step kernel, the dominant kernel when one-row passes run as one launch.
 STEP_KERNEL_NAME = "decode_step_kernel"
-# The persistent decode-step kernel: every layer of a one-row pass in one cooperative launch.
+# The persistent decode-step kernel: every layer of a one-row pass in one launch.
 STEP_KERNEL = ("decode_step_kernel: all 16 layers of one decode step (norms, q|k|v+rope+cache, attention, "
                "wo+add, gate|up+silu, down+add) in one persistent launch")
 METRIC = "decode tokens/s + HBM GB/s (% peak), Q4_0 1B model, batch 1 and 32 ragged"

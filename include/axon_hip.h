@@ -65,6 +65,13 @@ int axon_hip_memcpy_h2d_async(void* dst, const void* src, size_t bytes);
 int axon_hip_memset(void* dst, int value, size_t bytes);
 int axon_hip_synchronize(void);
 int axon_hip_event_create(void** event);
+/* Allocations this library's host code has made since it was loaded: *host_new counts its own
+ * operator new calls, *device its device and pinned-host allocations and events
+ * (axon_hip_malloc, axon_hip_host_malloc, axon_hip_event_create). No counterpart entry in the
+ * reference, whose tests count a whole test binary's operator new calls
+ * (tests/unit/alloc_counter.cpp:33-46): here the HIP runtime's own allocations are not this
+ * library's, so each library counts its own. */
+void axon_hip_allocation_counts(size_t* host_new, size_t* device);
 int axon_hip_event_record(void* event);
 int axon_hip_event_elapsed_ms(void* start, void* stop, float* ms);
 int axon_hip_event_destroy(void* event);

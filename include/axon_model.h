@@ -55,6 +55,18 @@ const char* axon_model_last_error(void);
 int axon_model_load(const char* path, const axon_model_options* options, axon_model** out);
 void axon_model_free(axon_model* model);
 int axon_model_get_info(const axon_model* model, axon_model_info* out);
+/* The host library's own operator new calls since it was loaded (libaxon_host.so counts its own,
+ * as libaxon_hip.so does with axon_hip_allocation_counts). With those, tests pin the reference's
+ * "a forward pass performs no heap allocation" (tests/unit/test_model_forward.cpp:119-128) for
+ * every pass after the first of each shape. */
+size_t axon_model_host_allocations(void);
+/* Turns the persistent decode kernel for one-row cached passes on (1) or off (0); on fails with
+ * Unsupported where the model's shape does not allow it. No counterpart in the reference, whose
+ * passes have no such kernel. A pass whose kernel gave up waiting for a workgroup that never
+ * became resident turns it off by itself: that pass fails, naming the cache slot and position,
+ * its cache is rolled back to that position, and later one-row passes run layer by layer until
+ * this turns the kernel back on. */
+int axon_model_set_persistent_decode(axon_model* model, int on);
 /* The name of the kernel table the model runs on ("hip"). */
 const char* axon_model_table_name(const axon_model* model);
 

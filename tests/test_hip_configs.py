@@ -331,9 +331,12 @@ def test_generate_greedy_equals_host_loop(cfg):
 def test_persistent_decode_gives_up_cleanly_and_recovers(tmp_path_factory):
     """The step kernel's bounded waits, forced from the host: with a limit of one poll per
     tagged word the workgroups of a one-row pass give up instead of waiting, the kernel still
-    drains, and the pass fails with the status word's error (its cache position not advanced).
-    With the limit restored, the same model retries that token and decodes 8 more steps with
-    logits bit-identical to the per-layer launches."""
+    drains, and the pass is void. With the logits copied the pass fails at once and its cache
+    position does not advance; with the logits left in HBM the pass returns, and the next
+    synchronization (the greedy choice) fails, names the cache slot and position, and rolls the
+    cache back to it. Either way the model turns the persistent kernel off for later one-row
+    passes; turned back on, the same model retries the token and decodes on with logits
+    bit-identical to the per-layer launches."""
     from dataclasses import replace
     import synth
     import axon_hip as H
@@ -348,17 +351,38 @@ def test_persistent_decode_gives_up_cleanly_and_recovers(tmp_path_factory):
     assert np.array_equal(la, lb)
     t = int(np.argmax(la))
     lib = H.lib()
+    n0 = len(prompt)
+    # Logits copied to the host: the pass itself reports the give-up.
     try:
         assert lib.axon_hip_decode_layers_set_spin_limit(1) == 0
         with pytest.raises(H.HipError, match="gave up"):
             a.forward_prefill(ca, [t])
     finally:
         lib.axon_hip_decode_layers_set_spin_limit(0)
-    assert a.cache_pos(ca) == len(prompt)
-    for _ in range(9):
+    assert a.cache_pos(ca) == n0
+    assert not a.persistent_decode()
+    a.set_persistent_decode(True)
+    assert a.persistent_decode()
+    # Logits left in HBM: the pass returns with its cache advanced; the greedy choice's
+    # synchronization finds the give-up and rolls the cache back.
+    try:
+        assert lib.axon_hip_decode_layers_set_spin_limit(1) == 0
+        a.forward_prefill(ca, [t], logits=False)
+    finally:
+        lib.axon_hip_decode_layers_set_spin_limit(0)
+    assert a.cache_pos(ca) == n0 + 1
+    with pytest.raises(H.HipError, match=f"gave up.*position {n0} of the cache in slot {ca}"):
+        a.greedy(1)
+    assert a.cache_pos(ca) == n0
+    assert not a.persistent_decode()
+    # Layer by layer now, then on the persistent kernel again: bit-identical throughout.
+    for step in range(10):
+        if step == 3:
+            a.set_persistent_decode(True)
+            assert a.persistent_decode()
         la, lb = a.forward_prefill(ca, [t])[0], b.forward_prefill(cb, [t])[0]
-        assert np.array_equal(la, lb)
+        assert np.array_equal(la, lb), f"step {step}"
         t = int(np.argmax(la))
+    assert a.cache_pos(ca) == b.cache_pos(cb)
     a.close()
     b.close()
-
