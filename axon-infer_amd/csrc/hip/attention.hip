@@ -897,21 +897,25 @@ __global__ __launch_bounds__(kThreads) void attn_mix_kernel(AttnArgs a) {
 
 // ---- Decode-shaped launches, 64-dim heads of an fp32 cache --------------------------------
 //   attn_scores64_kernel  one workgroup per (row, kv head, 64 positions): the 64 K rows go into
-//                         LDS by DMA, wave h computes query head h's scores, one lane per
-//                         position, each dot over d in order.
+//                         LDS by 16-byte DMA copies, wave h computes query head h's scores, one
+//                         lane per position, each dot over d in order.
 //   attn_mix64_kernel     one wave per (row, query head): the softmax statistics, then the
 //                         value mix with lane = dim, positions in order, V streaming through a
 //                         ring of LDS tiles that DMA keeps kRing tiles ahead.
 // The float operations and their order are the fused kernel's, and the double sum of the
 // softmax follows the fused kernel's 256-thread tree (each lane carries the partial sums of
 // threads lane, lane + 64, lane + 128, lane + 192).
-constexpr uint32_t kKPitch = 68;   // floats per K row in LDS (64 + 4: conflict-free b128 reads)
-constexpr uint32_t kKPitchH = 36;  // dwords per fp16 K row in LDS (32 + 4, the same banks)
+// attn_scores64_kernel's LDS: 64 K rows of 64 elements, the group's q rows.
+inline size_t scores64_lds(bool f16, uint32_t group) { return 64 * 64 * (f16 ? 2 : 4) + static_cast<size_t>(group) * 64 * 4; }
 
 // F16: the cache holds fp16 bit patterns; each K value is widened exactly before its product.
+// The 64 K rows go into LDS unpadded by 16-byte copies (4 rows of floats, or 8 of fp16, per
+// copy), each row's 16-byte chunks stored XOR-swizzled by the row: chunk c of row j sits in slot
+// c ^ (j % chunks), so the lanes (one row each) reading chunk c in the same step hit different
+// banks, while each lane still reads its row's chunks, and adds its products, in order.
 template <bool F16>
 __global__ __launch_bounds__(1024) void attn_scores64_kernel(AttnArgs a) {
-  extern __shared__ __attribute__((aligned(16))) float lds[];  // K [64][pitch], q [group][64]
+  extern __shared__ __attribute__((aligned(16))) float lds[];  // K [64][64 elements], q [group][64]
   const uint32_t r = blockIdx.x;
   const uint32_t g = blockIdx.y;
   const uint32_t j0 = blockIdx.z * 64;
@@ -924,22 +928,20 @@ __global__ __launch_bounds__(1024) void attn_scores64_kernel(AttnArgs a) {
   const uint32_t rows = min(64u, n_vis - j0);
   const size_t kv_row = static_cast<size_t>(a.n_kv) * 64;
   const int64_t k_off = (a.k_off != nullptr ? a.k_off[r] : 0) + a.k_off_c;
-  constexpr uint32_t es = F16 ? 2 : 4;                // bytes per cache element
-  constexpr uint32_t pitch = F16 ? kKPitchH : kKPitch;  // dwords per K row in LDS
+  constexpr uint32_t es = F16 ? 2 : 4;         // bytes per cache element
+  constexpr uint32_t kChunks = 64 * es / 16;   // 16-byte chunks per K row: 16, or 8 in fp16
+  constexpr uint32_t kRowsPer = 64 / kChunks;  // rows per copy: 4, or 8
   float* kt = lds;
-  float* qs = lds + 64 * pitch;
-  // K rows j0 .. j0 + 63 of kv head g (rows past n_vis repeat the last one): one dword DMA per
-  // row (32 lanes of an fp16 row), waves taking rows in turn.
+  float* qs = lds + 64 * 64 * es / 4;
+  // K rows j0 .. j0 + 63 of kv head g (rows past n_vis repeat the last one); copy i moves rows
+  // kRowsPer i .. kRowsPer i + kRowsPer - 1, waves taking copies in turn.
   const uint8_t* kbase = static_cast<const uint8_t*>(a.kv) + (k_off + static_cast<size_t>(j0) * kv_row + g * 64) * es;
-  const __amdgpu_buffer_rsrc_t rsrc = __builtin_amdgcn_make_buffer_rsrc(
-      const_cast<uint8_t*>(kbase), 0, static_cast<int>((static_cast<size_t>(rows - 1) * kv_row + 64) * es),
-      static_cast<int>(kRawBufferWord3));
-  for (uint32_t i = wave; i < 64; i += group) {
-    const uint32_t row = min(i, rows - 1);
-    if (!F16 || lane < 32) {
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, as_lds(kt + i * pitch), 4, 4 * lane,
-                                               static_cast<int>(row * kv_row * es), 0, 0);
-    }
+  const RsrcWords rsrc = raw_buffer_words(kbase, static_cast<uint32_t>((static_cast<size_t>(rows - 1) * kv_row + 64) * es));
+  const uint32_t kt_lds = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(as_lds(kt)));
+  for (uint32_t i = wave; i < 64 / kRowsPer; i += group) {
+    const uint32_t row = kRowsPer * i + lane / kChunks;
+    const uint32_t chunk = (lane % kChunks) ^ (row % kChunks);
+    lds_dma16(rsrc, static_cast<uint32_t>(min(row, rows - 1) * kv_row * es) + chunk * 16, kt_lds + i * 1024);
   }
   const float* q = a.q + static_cast<size_t>(r) * a.q_stride + static_cast<size_t>(g) * group * 64;
   for (uint32_t i = tid; i < group * 64; i += blockDim.x) qs[i] = q[i];
@@ -947,16 +949,16 @@ __global__ __launch_bounds__(1024) void attn_scores64_kernel(AttnArgs a) {
   __syncthreads();
   const uint32_t j = j0 + lane;
   if (j >= n_vis) return;
-  const float* kr = kt + lane * pitch;
+  const uint4* kr = reinterpret_cast<const uint4*>(kt) + lane * kChunks;
   const float* qh = qs + wave * 64;
+  const uint32_t sw = lane % kChunks;
   float acc = 0.0f;
   if constexpr (F16) {
-    const uint32_t* kh = reinterpret_cast<const uint32_t*>(kr);
 #pragma unroll
-    for (int d = 0; d < 64; d += 8) {
-      const uint4 h = *reinterpret_cast<const uint4*>(kh + d / 2);
-      const float4 qa = *reinterpret_cast<const float4*>(qh + d);
-      const float4 qb = *reinterpret_cast<const float4*>(qh + d + 4);
+    for (uint32_t c = 0; c < kChunks; ++c) {
+      const uint4 h = kr[c ^ sw];
+      const float4 qa = *reinterpret_cast<const float4*>(qh + 8 * c);
+      const float4 qb = *reinterpret_cast<const float4*>(qh + 8 * c + 4);
       acc += qa.x * half_value(h.x & 0xffffu);
       acc += qa.y * half_value(h.x >> 16);
       acc += qa.z * half_value(h.y & 0xffffu);
@@ -968,13 +970,13 @@ __global__ __launch_bounds__(1024) void attn_scores64_kernel(AttnArgs a) {
     }
   } else {
 #pragma unroll
-    for (int d = 0; d < 64; d += 4) {
-      const float4 k4 = *reinterpret_cast<const float4*>(kr + d);
-      const float4 q4 = *reinterpret_cast<const float4*>(qh + d);
-      acc += q4.x * k4.x;
-      acc += q4.y * k4.y;
-      acc += q4.z * k4.z;
-      acc += q4.w * k4.w;
+    for (uint32_t c = 0; c < kChunks; ++c) {
+      const uint4 u = kr[c ^ sw];
+      const float4 q4 = *reinterpret_cast<const float4*>(qh + 4 * c);
+      acc += q4.x * __uint_as_float(u.x);
+      acc += q4.y * __uint_as_float(u.y);
+      acc += q4.z * __uint_as_float(u.z);
+      acc += q4.w * __uint_as_float(u.w);
     }
   }
   a.scratch[(static_cast<size_t>(r) * a.n_head + g * group + wave) * a.max_vis + j] = a.scale * acc;
@@ -1621,12 +1623,12 @@ int attention_launch(const AttnArgs& a, uint32_t n_rows) {
       const dim3 sgrid(n_rows, a.n_kv, (a.max_vis + 63) / 64);
       const dim3 dgrid(n_rows, a.n_kv, 2);
       if (a.f16) {
-        const size_t slds = (64 * kKPitchH + static_cast<size_t>(group) * 64) * 4;
+        const size_t slds = scores64_lds(true, group);
         hipLaunchKernelGGL(attn_scores64_kernel<true>, sgrid, dim3(group * 64), slds, stream(), a);
         launch_mixd<true>(group, dgrid, dlds, a);
         return check_launch("attention (decode, fp16)");
       }
-      const size_t slds = (64 * kKPitch + static_cast<size_t>(group) * 64) * 4;
+      const size_t slds = scores64_lds(false, group);
       hipLaunchKernelGGL(attn_scores64_kernel<false>, sgrid, dim3(group * 64), slds, stream(), a);
       const size_t glds = mixg_lds(group, a.max_vis);
       const dim3 ggrid(n_rows, a.n_kv);
