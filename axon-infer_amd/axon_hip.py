@@ -167,6 +167,13 @@ class AttentionRowsArgs(C.Structure):
                 ("f16", C.c_int), ("scratch", C.c_void_p), ("max_vis", C.c_uint32), ("outq", C.c_void_p)]
 
 
+class DecodeShape(C.Structure):
+    """axon_hip_decode_shape (include/axon_hip.h)."""
+    _fields_ = [("n_layer", C.c_uint32), ("n_embd", C.c_uint32), ("n_head", C.c_uint32), ("n_head_kv", C.c_uint32),
+                ("n_ff", C.c_uint32), ("rotary_dim", C.c_uint32), ("type_qkv", C.c_int), ("type_o", C.c_int),
+                ("type_gate_up", C.c_int), ("type_down", C.c_int), ("max_ctx", C.c_uint32), ("cache_f16", C.c_int)]
+
+
 class MatvecFusedArgs(C.Structure):
     """axon_hip_matvec_fused_args (include/axon_hip.h)."""
     _fields_ = [("type", C.c_int), ("n_seg", C.c_size_t), ("w", C.c_void_p * 3), ("n_out", C.c_size_t * 3),

@@ -810,12 +810,29 @@ axon_hip::StepShape step_shape_of(const axon_hip_decode_shape* sh) {
 }
 constexpr uint32_t kStepSpinLimit = 1u << 20;  // polls of one barrier (about a second) before giving up
 std::atomic<uint32_t> g_step_spin_limit{kStepSpinLimit};
+std::atomic<uint64_t*> g_step_stamps{nullptr};
 static_assert(sizeof(axon_hip_decode_layer) == sizeof(axon_hip::StepLayer), "one layer record layout");
 }  // namespace
 
 int axon_hip_decode_layers_set_spin_limit(uint32_t polls) {
   g_step_spin_limit.store(polls == 0 ? kStepSpinLimit : polls, std::memory_order_relaxed);
   return kOk;
+}
+
+int axon_hip_decode_layers_set_stamps(uint64_t* stamps) {
+  g_step_stamps.store(stamps, std::memory_order_relaxed);
+  return kOk;
+}
+
+size_t axon_hip_decode_layers_stamp_count(const axon_hip_decode_shape* shape, double* ticks_per_second) {
+  if (shape == nullptr || ready() != kOk) return 0;
+  if (ticks_per_second != nullptr) {
+    int khz = 0;
+    *ticks_per_second = hipDeviceGetAttribute(&khz, hipDeviceAttributeWallClockRate, g_device) == hipSuccess
+                            ? 1e3 * khz
+                            : 0.0;
+  }
+  return step_stamp_count(step_shape_of(shape));
 }
 
 size_t axon_hip_decode_layers_workspace_bytes(const axon_hip_decode_shape* shape) {
@@ -856,6 +873,7 @@ int axon_hip_decode_layers(const axon_hip_decode_shape* shape, const axon_hip_de
   c.epoch = *a->epoch;
   c.status = a->status;
   c.spin_limit = g_step_spin_limit.load(std::memory_order_relaxed);
+  c.stamps = g_step_stamps.load(std::memory_order_relaxed);
   const int rc = step_launch(s, c);
   if (rc != kOk) return rc;
   *a->epoch += step_phases(s);

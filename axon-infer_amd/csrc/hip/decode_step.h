@@ -42,12 +42,15 @@ struct StepCall {
   uint64_t epoch;           // phases run on this workspace before the call
   uint32_t* status;         // pinned host word: 0, or why the kernel gave up
   uint32_t spin_limit;      // polls of one tagged word before giving up
+  uint64_t* stamps;         // per-phase clock stamps (step_stamp_count words), or null
 };
 
 // Why a step kernel gave up (the status word): a word it waited for outlasted the poll limit.
 constexpr uint32_t kStepTimedOut = 1;
 
 size_t step_workspace_bytes(const StepShape& s);
+// Words of a stamp buffer: 4 points x 5 phases x n_layer x one workgroup per CU.
+size_t step_stamp_count(const StepShape& s);
 // 0 when this GPU runs the shape as one persistent kernel, else the reason (a static string).
 const char* step_unsupported(const StepShape& s);
 // Phases one call runs (each tags the words it writes with its own number).

@@ -65,6 +65,7 @@ struct StepK {
   uint64_t epoch;
   uint32_t* status;
   uint32_t spin_limit;
+  uint64_t* stamps;                         // per-phase clock stamps, or null
   uint32_t r_qkv, r_o, r_d;                 // weight rows per workgroup
   uint32_t rb_d, rb_q, rb_ff;               // bytes per row of the d-, dq- and ff-wide matrices
   uint32_t rb_o, rb_down;
@@ -267,8 +268,16 @@ __device__ __forceinline__ bool take_f(const uint64_t* src, uint32_t tag, float*
 // RMSNorm'd and quantized activation blocks of x (d floats) into act, with rmsnorm_row_256's
 // reduction (one 8-float chunk per thread, d <= 2048). x is the launch's input (xt null) or the
 // tagged copy the previous phase wrote. False when the poll gave up.
+// When stamping (at non-null, the same in every thread), the device clock goes to *at once every
+// thread of the compute waves has passed this point (their polls done): one more barrier, which
+// the copying waves' barrier loop absorbs.
+__device__ __forceinline__ void stamp_at(uint64_t* at) {
+  if (at == nullptr) return;
+  bar();
+  if (threadIdx.x == 0) *at = __builtin_amdgcn_s_memrealtime();
+}
 __device__ __forceinline__ bool norm_quantize(const StepK& k, const float* gain, const uint64_t* xt, uint32_t tag,
-                                              ActBlock* act, double* red, uint32_t t) {
+                                              ActBlock* act, double* red, uint32_t t, uint64_t* stamp) {
   const uint32_t d = k.s.d;
   const bool has = t * 8 < d;
   float xv[8], wv[8];
@@ -294,6 +303,7 @@ __device__ __forceinline__ bool norm_quantize(const StepK& k, const float* gain,
       ss += v * v;
     }
   }
+  stamp_at(stamp);
   ss = block_sum_double_256(ss, red);
   const float inv = static_cast<float>(1.0 / sqrt(ss / static_cast<double>(d) + static_cast<double>(k.eps)));
   if (has) {
@@ -461,6 +471,15 @@ __global__ __launch_bounds__(kStepThreads) void decode_step_kernel(StepK k) {
     sh.abort = 1;
     __hip_atomic_store(k.status, kStepTimedOut, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
   };
+  // Measurement: the device clock at point pt of phase ph of layer l (stamp buffer words
+  // ((l * 5 + ph) * 4 + pt) * workgroups + w); stamp_in first waits for every compute thread.
+  auto slot_of = [&](uint32_t l, uint32_t ph, uint32_t pt) -> uint64_t* {
+    return k.stamps == nullptr ? nullptr : k.stamps + (static_cast<size_t>(l * 5 + ph) * 4 + pt) * gridDim.x + w;
+  };
+  auto stamp = [&](uint32_t l, uint32_t ph, uint32_t pt) {
+    if (k.stamps != nullptr && tid == 0) *slot_of(l, ph, pt) = __builtin_amdgcn_s_memrealtime();
+  };
+  auto stamp_in = [&](uint32_t l, uint32_t ph, uint32_t pt) { stamp_at(slot_of(l, ph, pt)); };
   // The rows of x this workgroup's wo and down rows update, held in registers across layers.
   const uint32_t r0x = w * k.r_o;
   const uint32_t nrx = r0x < s.d ? min(k.r_o, s.d - r0x) : 0;
@@ -482,6 +501,7 @@ __global__ __launch_bounds__(kStepThreads) void decode_step_kernel(StepK k) {
 
     // ---- A: RMSNorm, q|k|v, bias, RoPE, q and the KV row -----------------------------------
     if (!begin()) break;
+    stamp(l, 0, 0);
     {
       const uint32_t r0 = w * k.r_qkv;
       const uint32_t nr = r0 < s.dq + 2 * s.dkv ? min(k.r_qkv, s.dq + 2 * s.dkv - r0) : 0;
@@ -511,7 +531,8 @@ __global__ __launch_bounds__(kStepThreads) void decode_step_kernel(StepK k) {
         const uint32_t tp = term_pitch(nb);
         float* outv = tv + k.r_qkv * tp + 64;
         // x: the launch's input, or the previous layer's down phase.
-        if (!norm_quantize(k, L.attn_norm, l == 0 ? nullptr : k.xt, tag_a - 1, act, red, t)) give_up();
+        if (!norm_quantize(k, L.attn_norm, l == 0 ? nullptr : k.xt, tag_a - 1, act, red, t, slot_of(l, 0, 1))) give_up();
+        stamp(l, 0, 2);
         asm volatile("" ::"v"(touch));  // the reads are complete: x came after them
         terms(s.t_qkv, k.lds_qkv, k.rb_d, nr, nb, act, tv, tp);
         if (t < nr) outv[t] = ordered_sum(tv + t * tp, nb);
@@ -557,7 +578,11 @@ __global__ __launch_bounds__(kStepThreads) void decode_step_kernel(StepK k) {
             put(kv + 1, tag_a, __float_as_uint(x1));
           }
         }
+      } else {
+        stamp(l, 0, 1);
+        stamp(l, 0, 2);
       }
+      stamp(l, 0, 3);
       lead_end();
     }
 
@@ -567,6 +592,7 @@ __global__ __launch_bounds__(kStepThreads) void decode_step_kernel(StepK k) {
     // the group, which waits for the head's scores, softmaxes them itself and runs the
     // in-order chains of its dims over V slices staged in LDS.
     if (!begin()) break;
+    stamp(l, 1, 0);
     {
       float* qs = reinterpret_cast<float*>(smem + k.lds_dn);  // the down region is copied only
       float* klast = qs + group * kHeadDim;                     // after this phase
@@ -606,6 +632,7 @@ __global__ __launch_bounds__(kStepThreads) void decode_step_kernel(StepK k) {
         if (p1 == n_vis && t < kHeadDim) ok &= take_f(k.kvt + g * kHeadDim + t, tag_a, klast + t, k.spin_limit);
         if (!ok) give_up();
         bar();
+        stamp(l, 1, 1);
         for (uint32_t e = t; e < pairs; e += kCompute) {
           const uint32_t j = p0 + e / group, hi = e % group;
           if (j == last) {
@@ -620,6 +647,8 @@ __global__ __launch_bounds__(kStepThreads) void decode_step_kernel(StepK k) {
           for (uint32_t i = 0; i < kHeadDim; ++i) acc += qh[i] * kr[i];
           put(k.scores + static_cast<size_t>(g * group + hi) * s.max_ctx + j, tag_b, __float_as_uint(k.scale * acc));
         }
+      } else {
+        stamp(l, 1, 1);
       }
       if (rank < group * k.dsplit) {
         const uint32_t h = g * group + rank / k.dsplit;
@@ -658,6 +687,7 @@ __global__ __launch_bounds__(kStepThreads) void decode_step_kernel(StepK k) {
         if (t < k.dd) ok &= take_f(k.kvt + s.dkv + g * kHeadDim + dim0 + t, tag_a, &vlast, k.spin_limit);
         if (!ok) give_up();
         bar();
+        stamp(l, 1, 2);
         if (sh.abort == 0) {
           // Softmax: the maximum, e = exp(s - max), the double sum over the 256-thread tree,
           // p = e / sum.
@@ -733,12 +763,16 @@ __global__ __launch_bounds__(kStepThreads) void decode_step_kernel(StepK k) {
             put(k.attnt + h * kHeadDim + dim0 + t, tag_b, __float_as_uint(acc));
           }
         }
+      } else {
+        stamp(l, 1, 2);
       }
+      stamp(l, 1, 3);
       lead_end();
     }
 
     // ---- C: wo and the residual add ---------------------------------------------------------
     if (!begin()) break;
+    stamp(l, 2, 0);
     if (nrx > 0) {
       const uint32_t nb = s.dq / kQK;
       ActBlock* act = reinterpret_cast<ActBlock*>(scratch);
@@ -753,6 +787,8 @@ __global__ __launch_bounds__(kStepThreads) void decode_step_kernel(StepK k) {
         for (int i = 0; i < 8; ++i) v[i] = __uint_as_float(u[i]);
         quantize8_to_act(v, t & 3u, act[t / 4]);
       }
+      stamp_in(l, 2, 1);
+      stamp(l, 2, 2);
       terms(s.t_o, k.lds_o, k.rb_o, nrx, nb, act, tv, tp);
       if (t < nrx) outv[t] = ordered_sum(tv + t * tp, nb);
       bar();
@@ -760,18 +796,24 @@ __global__ __launch_bounds__(kStepThreads) void decode_step_kernel(StepK k) {
         xr = xr + outv[t];
         put(k.xt + r0x + t, tag_c, __float_as_uint(xr));
       }
+    } else {
+      stamp(l, 2, 1);
+      stamp(l, 2, 2);
     }
+    stamp(l, 2, 3);
     lead_end();
 
     // ---- D: RMSNorm, gate|up, SiLU * up, its Q8_0 block ------------------------------------
     if (!begin()) break;
+    stamp(l, 3, 0);
     if (w * kGuRows < s.ff) {
       const uint32_t nb = s.d / kQK;
       ActBlock* act = reinterpret_cast<ActBlock*>(scratch);
       float* tv = reinterpret_cast<float*>(scratch + nb * sizeof(ActBlock));
       const uint32_t tp = term_pitch(nb);
       float* outv = tv + 2 * kGuRows * tp + 64;
-      if (!norm_quantize(k, L.ffn_norm, k.xt, tag_c, act, red, t)) give_up();
+      if (!norm_quantize(k, L.ffn_norm, k.xt, tag_c, act, red, t, slot_of(l, 3, 1))) give_up();
+      stamp(l, 3, 2);
       terms(s.t_gu, k.lds_gu, k.rb_d, 2 * kGuRows, nb, act, tv, tp);
       if (t < 2 * kGuRows) outv[t] = ordered_sum(tv + t * tp, nb);
       bar();
@@ -781,11 +823,16 @@ __global__ __launch_bounds__(kStepThreads) void decode_step_kernel(StepK k) {
         const float hv = gt / (1.0f + exp_libm_from(-gt, sh.exp_tab)) * u;
         put_act_block(hv, t, k.ht + static_cast<size_t>(w) * 10, tag_d);
       }
+    } else {
+      stamp(l, 3, 1);
+      stamp(l, 3, 2);
     }
+    stamp(l, 3, 3);
     lead_end();
 
     // ---- E: down and the residual add -------------------------------------------------------
     if (!begin()) break;
+    stamp(l, 4, 0);
     if (nrx > 0) {
       const uint32_t nb = s.ff / kQK;
       ActBlock* act = reinterpret_cast<ActBlock*>(scratch);
@@ -801,6 +848,8 @@ __global__ __launch_bounds__(kStepThreads) void decode_step_kernel(StepK k) {
         a.d = __uint_as_float(u[8]);
         a.sum = static_cast<int32_t>(u[9]);
       }
+      stamp_in(l, 4, 1);
+      stamp(l, 4, 2);
       terms(s.t_down, k.lds_dn, k.rb_down, nrx, nb, act, tv, tp);
       if (t < nrx) outv[t] = ordered_sum(tv + t * tp, nb);
       bar();
@@ -809,7 +858,11 @@ __global__ __launch_bounds__(kStepThreads) void decode_step_kernel(StepK k) {
         if (more) put(k.xt + r0x + t, tag_e, __float_as_uint(xr));
         else k.x[r0x + t] = xr;  // the step's output, read by the launches after this one
       }
+    } else {
+      stamp(l, 4, 1);
+      stamp(l, 4, 2);
     }
+    stamp(l, 4, 3);
     lead_end();
   }
 }
@@ -936,6 +989,13 @@ WorkLayout work_layout(const StepShape& s) {
 
 size_t step_workspace_bytes(const StepShape& s) { return work_layout(s).total; }
 
+size_t step_stamp_count(const StepShape& s) {
+  uint32_t cus = 0;
+  size_t lds_max = 0;
+  if (step_device(&cus, &lds_max) != kOk) return 0;
+  return static_cast<size_t>(s.n_layer) * 5 * 4 * cus;
+}
+
 uint64_t step_phases(const StepShape& s) { return 5ull * s.n_layer; }
 
 const char* step_unsupported(const StepShape& s) {
@@ -1001,6 +1061,7 @@ int step_launch(const StepShape& s, const StepCall& c) {
   k.epoch = c.epoch;
   k.status = c.status;
   k.spin_limit = c.spin_limit;
+  k.stamps = c.stamps;
   void* args[] = {&k};
   const void* kernel = s.cache_f16 ? reinterpret_cast<const void*>(decode_step_kernel<true>)
                                    : reinterpret_cast<const void*>(decode_step_kernel<false>);

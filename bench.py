@@ -169,6 +169,66 @@ def probe_pass(H, model, n_vocab, steps, prompt_len, seed, weight_type):
     return ms, launches, nbytes
 
 
+PHASES = ("A: norm, q|k|v, RoPE, KV row", "B: attention", "C: wo + residual", "D: norm, gate|up, SiLU",
+          "E: down + residual")
+
+
+def phase_probe(H, model, n_vocab, steps, prompt_len, seed):
+    """The persistent decode step's phases, from the device clock stamps the kernel records when
+    given a stamp buffer (axon_hip_decode_layers_set_stamps): decode-b1 steps after a
+    prompt_len-token prompt, one forward_prefill + device greedy choice per step, the stamps of
+    each step read back after it. Per phase of a layer, the maximum over workgroups of
+      wait  = inputs in - phase start      (polls for the previous phase's outputs)
+      mid   = second inputs in - first     (attention: scoring and the scores exchange)
+      tail  = phase end - last inputs in   (compute after the last poll)
+    and the phase's span on the critical path: the latest end of this phase minus the latest end
+    of the one before. Averaged over layers and steps."""
+    import ctypes as C
+    L = H.lib()
+    info = model.info
+    shape = H.DecodeShape()
+    shape.n_layer = info.n_layer
+    tps = C.c_double(0.0)
+    L.axon_hip_decode_layers_stamp_count.restype = C.c_size_t
+    n = L.axon_hip_decode_layers_stamp_count(C.byref(shape), C.byref(tps))
+    if n == 0 or tps.value <= 0:
+        raise SystemExit("bench.py: no stamp buffer size or clock rate for the decode step")
+    wgs = n // (info.n_layer * 20)
+    buf = H.DeviceBuffer(n * 8)
+    rng = np.random.default_rng(seed + 3)
+    cache = model.new_cache()
+    tok = prefill_greedy(model, cache, rng.integers(0, n_vocab, prompt_len).astype(np.int32))
+    tok = greedy_decode(model, cache, tok, 8)
+    H.synchronize()
+    t0 = time.perf_counter()
+    tok = greedy_decode(model, cache, tok, steps)
+    plain_ms = 1e3 * (time.perf_counter() - t0) / steps
+    wait, mid, tail, span, total = [], [], [], [], []
+    L.axon_hip_decode_layers_set_stamps(C.c_void_p(H.ptr_of(buf)))
+    try:
+        for _ in range(steps):
+            model.forward_prefill(cache, [tok], logits=False)
+            tok = int(model.greedy(1)[0])
+            t = buf.download(np.uint64).reshape(info.n_layer, 5, 4, wgs).astype(np.float64) * (1e6 / tps.value)
+            t -= t[0, 0, 0].min()
+            wait.append((t[:, :, 1] - t[:, :, 0]).max(axis=2))
+            mid.append((t[:, :, 2] - t[:, :, 1]).max(axis=2))
+            tail.append((t[:, :, 3] - t[:, :, 2]).max(axis=2))
+            ends = t[:, :, 3].max(axis=2).reshape(-1)
+            span.append(np.diff(np.concatenate([[0.0], ends])).reshape(info.n_layer, 5))
+            total.append(ends[-1])
+    finally:
+        L.axon_hip_decode_layers_set_stamps(None)
+    model.free_cache(cache)
+    mean = lambda a: np.mean(np.stack(a), axis=(0, 1))  # over steps and layers
+    w, m, tl, sp = mean(wait), mean(mid), mean(tail), mean(span)
+    return {"kernel": STEP_KERNEL_NAME, "steps": steps, "context": [prompt_len + 8 + steps, prompt_len + 8 + 2 * steps],
+            "workgroups": wgs, "clock_hz": tps.value, "us_per_step_stamped": round(float(np.mean(total)), 2),
+            "ms_per_step_plain": round(plain_ms, 4), "us_per_layer_stamped": round(float(np.mean(total)) / info.n_layer, 2),
+            "phases": [{"phase": PHASES[p], "span_us": round(float(sp[p]), 3), "wait_us": round(float(w[p]), 3),
+                        "mid_us": round(float(m[p]), 3), "tail_us": round(float(tl[p]), 3)} for p in range(5)]}
+
+
 def ragged_schedule(n_seq, cohort, gap, decode_steps):
     return [(i // cohort) * gap for i in range(n_seq)], decode_steps
 
@@ -637,6 +697,8 @@ def main() -> int:
                     help="only run the config-5 workload and print its figures (the workload of its profile)")
     ap.add_argument("--attention-probe", action="store_true",
                     help="only the calibration copy and the ragged-32 attention probe (counter passes)")
+    ap.add_argument("--phase-probe", action="store_true",
+                    help="only the persistent decode step's per-phase clock stamps (decode-b1 steps)")
     ap.add_argument("--prefill-probe", action="store_true",
                     help="only run four 512-token prefill passes (the workload of the prefill profiles)")
     ap.add_argument("--cpu-budget", type=float, default=12.0, help="seconds per CPU baseline sample")
@@ -683,6 +745,10 @@ def main() -> int:
         attention_traffic_probe(H, model, info.n_vocab, args.seed)
         model.close()
         log("attention probe done")
+        return 0
+    if args.phase_probe:
+        print(json.dumps(phase_probe(H, model, info.n_vocab, min(args.steps, 64), args.prompt, args.seed)), flush=True)
+        model.close()
         return 0
     if args.prefill_probe:
         prefill_probe(H, model, info.n_vocab, args.seed)

@@ -366,6 +366,16 @@ typedef struct {
  * second). A small limit forces the give-up path from the host: the kernel still drains, the
  * call's status word is set, and the caller's recovery runs. */
 int axon_hip_decode_layers_set_spin_limit(uint32_t polls);
+/* Measurement hook, no counterpart in the reference: with a device buffer of
+ * axon_hip_decode_layers_stamp_count(shape, &ticks_per_second) uint64 words, every later
+ * axon_hip_decode_layers call records the device's constant-rate clock (s_memrealtime) at four points of every phase of every layer in every
+ * workgroup, each call overwriting the last: word ((layer * 5 + phase) * 4 + point) * workgroups +
+ * workgroup, phases A (norm, q|k|v, RoPE, cache row), B (attention), C (wo), D (norm, gate|up,
+ * SiLU), E (down); points: the phase's start, its first inputs in (every thread's polls done),
+ * its second inputs in (B: the scores; else the same as the first), its end. NULL turns it off.
+ * The instrumented launch adds one workgroup barrier per poll. */
+int axon_hip_decode_layers_set_stamps(uint64_t* stamps);
+size_t axon_hip_decode_layers_stamp_count(const axon_hip_decode_shape* shape, double* ticks_per_second);
 size_t axon_hip_decode_layers_workspace_bytes(const axon_hip_decode_shape* shape);
 /* NULL when this device runs the shape, else the reason. */
 const char* axon_hip_decode_layers_unsupported(const axon_hip_decode_shape* shape);
