@@ -31,16 +31,27 @@ The line also carries:
                summed kernel time. The Q6_K output matvec is probed the same way (roofline_q6_k).
   cpu_baseline the reference's own LlamaModel on its scalar table (oracle/_ref, compiled from the
                reference sources) on the same GGUF, threads = the host's cores, on a bounded sample.
+               For ragged-32 the CPU sample is fixed 32-row forward_batch steps at the workload's
+               contexts; vs_cpu_fixed_batch compares the GPU's same 32-row steps with it, and
+               vs_cpu_schedule the staggered workload's rate.
 
   f16_cache    decode-b1 and ragged-32 again with the KV cache held as fp16 (LoadOptions::cache
                = F16): half the cache bytes per position (kv_bytes_per_position).
+
+  c1, c3       configs 1 and 3 as decode-b1 on their own shapes (SmolLM2-135M Q8_0: 128-token
+               prompt, 64 greedy steps; TinyLlama-1.1B Q4_0/Q4_1/Q6_K: 512-token prompt, 256 greedy
+               steps): tokens/s, HBM fraction per step, the step kernel's roofline, and the
+               reference's LlamaModel decoding the same model on the host cores.
 
   c5_mixed     config 5: the Qwen2.5-0.5B-shaped model, 64 sequences with prompts U[32, 1024]
                admitted together, each step one 512-token prompt chunk plus one token of every
                sequence in decode, seeded top-k 40 / top-p 0.9 / T 0.8 sampling (candidates on the
                device, the draw on the host), 128 tokens each. one_pass runs each step as one
                forward (axon_model_forward_mixed), two_pass as the reference's two; both must give
-               the same token streams. tokens_per_s = sampled tokens over the whole run.
+               the same token streams. tokens_per_s = sampled tokens over the whole run; its roofline
+               = algorithmic HBM bytes (weights per pass, each row's visible K and V) over the run.
+               mixed_step: one steady-state step (a 512-token chunk + 63 decode rows) on the GPU in
+               one and in two passes, and on the reference's LlamaModel (cpu_baseline).
 
   traffic      HBM bytes per launch of that kernel, from two rocprofv3 counter passes over
                `bench.py --traffic-probe` (FETCH_SIZE, then WRITE_SIZE, KiB per dispatch), each
@@ -303,6 +314,14 @@ def probe_attention_ragged(H, model, n_vocab, seed, n_seq=32, steps=8):
         toks.append(tok)
     model.forward_batch(caches, toks, logits=False)  # untimed first batch
     toks = [int(t) for t in model.greedy(n_seq)]
+    # The same 32-row steps as the CPU baseline's forward_batch sample, timed plainly (the
+    # like-for-like figure beside it): forward_batch, the device greedy choice, the ids.
+    H.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        model.forward_batch(caches, toks, logits=False)
+        toks = [int(t) for t in model.greedy(n_seq)]
+    fixed_tps = n_seq * steps / (time.perf_counter() - t0)
     H.synchronize()
     model.probe(H.PROBE_ATTENTION, True)
     model.probe_read()
@@ -316,6 +335,7 @@ def probe_attention_ragged(H, model, n_vocab, seed, n_seq=32, steps=8):
     gbs = nbytes / (ms * 1e-3) / 1e9
     return {"kernel": "attn_scores64_kernel + attn_mixd_kernel (one attention_rows call per layer)",
             "rows": n_seq, "contexts_mean": float(ctx.mean()), "layer_calls": launches,
+            "fixed_batch_tokens_per_s": round(fixed_tps, 1),
             "us_per_layer": round(1e3 * ms / max(launches, 1), 2), "bytes_per_layer": round(nbytes / max(launches, 1)),
             "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4)}
 
@@ -341,6 +361,10 @@ def run_engine(H, model, prompts, decode_tokens, seed, one_pass):
     fed = [0] * n
     out = [[] for _ in range(n)]
     steps = 0
+    # Algorithmic HBM bytes: per pass the weights once (a two-pass step reads them twice), and
+    # each row's visible K and V rows (the chunk's span once for the chunk).
+    info = model.info
+    hbm_bytes = 0.0
     H.synchronize()
     t0 = time.perf_counter()
     while True:
@@ -383,6 +407,9 @@ def run_engine(H, model, prompts, decode_tokens, seed, one_pass):
             if dec:
                 model.forward_batch([caches[i] for i in dec], toks, logits=False)
                 ids += list(model.sample(dcfg, dgen, drec))
+        passes = 1 if one_pass else int(pi is not None) + int(bool(dec))
+        kv_rows = sum(fed[i] + 1 for i in dec) + (fed[pi] + len(chunk) if pi is not None else 0)
+        hbm_bytes += passes * info.weight_bytes_per_token + kv_rows * info.kv_bytes_per_position
         r = 0
         if pi is not None:
             fed[pi] += len(chunk)
@@ -396,7 +423,7 @@ def run_engine(H, model, prompts, decode_tokens, seed, one_pass):
     elapsed = time.perf_counter() - t0
     for c in caches:
         model.free_cache(c)
-    return [o[:decode_tokens] for o in out], steps, elapsed
+    return [o[:decode_tokens] for o in out], steps, elapsed, hbm_bytes
 
 
 def bench_c5(H, seed, n_seq=64, decode_tokens=128):
@@ -416,13 +443,20 @@ def bench_c5(H, seed, n_seq=64, decode_tokens=128):
     res = {}
     streams = []
     for name, one in (("one_pass", True), ("two_pass", False)):
-        out, steps, elapsed = run_engine(H, model, prompts, decode_tokens, seed, one)
+        out, steps, elapsed, nbytes = run_engine(H, model, prompts, decode_tokens, seed, one)
         gen = sum(len(o) for o in out)
+        gbs = nbytes / elapsed / 1e9
         res[name] = {"tokens_per_s": round(gen / elapsed, 1),
                      "total_tokens_per_s": round((gen + int(lens.sum())) / elapsed, 1),
-                     "seconds": round(elapsed, 3), "steps": steps}
+                     "seconds": round(elapsed, 3), "steps": steps,
+                     "hbm_gbs": round(gbs, 1), "hbm_frac": round(gbs / HBM_PEAK_GBS, 4)}
         streams.append(out)
         log(f"c5 {name}: {gen} tokens in {elapsed:.2f}s over {steps} steps ({gen / elapsed:.0f} tok/s)")
+    res["roofline"] = {"bound": "hbm", "kernel": "whole run (one_pass): every pass's weights plus each row's visible "
+                                                "K and V rows, over the run's wall time",
+                       "achieved": res["one_pass"]["hbm_gbs"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                       "frac": res["one_pass"]["hbm_frac"]}
+    res["mixed_step"] = c5_mixed_step(H, model, lens, seed)
     model.close()
     res["streams_identical"] = streams[0] == streams[1]
     res["generated_tokens"] = n_seq * decode_tokens
@@ -431,6 +465,57 @@ def bench_c5(H, seed, n_seq=64, decode_tokens=128):
     res["workload"] = ("config 5: Qwen2.5-0.5B-shaped (24 layers, hidden 896, 14/2 heads, FFN 4864, vocab 151936, "
                        "Q4_0 + q/k/v bias, NeoX, Q8_0 output), 64 sequences, prompts U[32, 1024], chunks of 512 "
                        "mixed with decode, top-k 40 / top-p 0.9 / T 0.8 / min-p 0.05 / penalty 1.1, 128 tokens each")
+    return res
+
+
+def c5_step_inputs(info, lens, seed, n_dec=63, chunk_len=512):
+    """One continuous-batching step of config 5 in its steady state: a 512-token prompt chunk into a
+    fresh cache and 63 sequences in decode at the prompt contexts lens[:63], their caches holding
+    the same seeded random K and V rows on the GPU and on the CPU."""
+    rng = np.random.default_rng(seed + 13)
+    chunk = rng.integers(0, info.n_vocab, chunk_len).astype(np.int32)
+    toks = rng.integers(0, info.n_vocab, n_dec).astype(np.int32)
+    row = info.n_head_kv * info.head_dim
+
+    def rows(i):
+        return np.random.default_rng(seed + 100 + i).standard_normal((info.n_layer, 2, int(lens[i]), row), dtype=np.float32)
+    return chunk, toks, rows
+
+
+def c5_mixed_step(H, model, lens, seed, reps=5):
+    """That step on the GPU, as one pass (forward_mixed: the chunk's last row and the 63 decode
+    rows get logits) and as the reference's two (forward_prefill of the chunk, then
+    forward_batch); tokens/s = the 64 tokens the step samples over the step's time."""
+    info = model.info
+    chunk, toks, rows = c5_step_inputs(info, lens, seed)
+    dec = []
+    for i in range(len(toks)):
+        c = model.new_cache()
+        model.cache_fill(c, rows(i))
+        dec.append(c)
+    res = {}
+    for name in ("one_pass", "two_pass"):
+        times = []
+        for _ in range(reps + 1):
+            pc = model.new_cache()
+            H.synchronize()
+            t0 = time.perf_counter()
+            if name == "one_pass":
+                model.forward_mixed(pc, chunk, dec, toks, logits=False)
+            else:
+                model.forward_mixed(pc, chunk, [], [], logits=False)
+                model.forward_batch(dec, toks, logits=False)
+            H.synchronize()
+            times.append(time.perf_counter() - t0)
+            model.free_cache(pc)
+            for i, c in enumerate(dec):
+                model.truncate(c, int(lens[i]))
+        t = float(np.median(times[1:]))
+        res[name] = {"ms": round(1e3 * t, 3), "tokens_per_s": round((len(toks) + 1) / t, 1)}
+    for c in dec:
+        model.free_cache(c)
+    res["step"] = (f"one {len(chunk)}-token prompt chunk into a fresh cache + {len(toks)} decode rows at contexts "
+                   f"U[32, 1024] (mean {float(np.mean(lens[:len(toks)])):.0f}); {len(toks) + 1} sampled tokens")
     return res
 
 
@@ -624,6 +709,121 @@ def host_cores() -> int:
         return os.cpu_count() or 1
 
 
+# Configs 1 and 3 (decode-b1 on their own shapes): (config, prompt, greedy steps, weight type of
+# q|k|v, whose launches the kernel-time probe brackets).
+B1_CONFIGS = {"c1": (128, 64, 8), "c3": (512, 256, 2)}
+
+
+def bench_config_b1(H, name, warmup, seed):
+    """BASELINE configs 1 and 3 as decode-b1: the config's prompt, then its greedy steps generated
+    as the bench's C4 leg does (axon_model_generate_greedy); HBM bytes per step = the weights
+    (llama.cpp:151-167) + the K and V rows of the visible positions; the dominant kernel's
+    roofline from a probed pass of the same steps."""
+    import synth
+    prompt_len, steps, wtype = B1_CONFIGS[name]
+    spec = synth.CONFIGS[name]
+    path = synth.cached_model(spec)
+    model = H.Model(path, max_seq=prompt_len, max_ctx=prompt_len + warmup + steps + 8)
+    info = model.info
+    prompt = np.random.default_rng(seed + 21).integers(0, info.n_vocab, prompt_len).astype(np.int32)
+    warm = model.new_cache()
+    prefill_greedy(model, warm, prompt)
+    model.free_cache(warm)
+    cache = model.new_cache()
+    tok = prefill_greedy(model, cache, prompt)
+    tok = device_loop_decode(model, cache, tok, warmup)
+    H.synchronize()
+    t0 = time.perf_counter()
+    ids = model.generate_greedy(cache, tok, steps)
+    H.synchronize()
+    dt = time.perf_counter() - t0
+    model.free_cache(cache)
+    ctx = [prompt_len + warmup + 1, prompt_len + warmup + steps]
+    step_bytes = info.weight_bytes_per_token + info.kv_bytes_per_position * 0.5 * (ctx[0] + ctx[1])
+    ms, launches, nbytes = probe_pass(H, model, info.n_vocab, min(steps, 32), prompt_len, seed, wtype)
+    achieved = nbytes / (ms * 1e-3) / 1e9 if launches else 0.0
+    res = {"workload": f"{spec.name}-shaped random-init GGUF, {prompt_len}-token prompt, {steps} greedy steps, batch 1",
+           "tokens_per_s": round(steps / dt, 2), "ms_per_step": round(1e3 * dt / steps, 4), "context": ctx,
+           "weight_bytes_per_token": info.weight_bytes_per_token, "kv_bytes_per_position": info.kv_bytes_per_position,
+           "hbm_gbs_per_step": round(step_bytes / (dt / steps) / 1e9, 1),
+           "hbm_frac_per_step": round(step_bytes / (dt / steps) / 1e9 / HBM_PEAK_GBS, 4),
+           "decode_path": "one persistent kernel per step" if info.persistent_decode else "per-layer launches",
+           "roofline": {"bound": "hbm", "kernel": STEP_KERNEL_NAME if info.persistent_decode else "decode matvecs",
+                        "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                        "frac": round(achieved / HBM_PEAK_GBS, 4), "launches": launches,
+                        "bytes_per_launch": round(nbytes / max(launches, 1)),
+                        "avg_us": round(1e3 * ms / max(launches, 1), 3), "traffic": None},
+           "first_ids": [int(v) for v in ids[:8]]}
+    model.close()
+    log(f"{name} decode-b1: {res['tokens_per_s']:.1f} tok/s, {res['hbm_frac_per_step'] * 100:.1f}% of HBM per step, "
+        f"kernel {res['roofline']['frac'] * 100:.1f}%")
+    return res, path, prompt
+
+
+def cpu_decode_b1(path, n_vocab, seed, budget_s, ctx0, prompt=None, max_ctx=2176):
+    """The reference's LlamaModel decoding greedily at batch 1 on the host cores: after a real
+    prefill of `prompt`, or over a cache filled with ctx0 seeded random positions."""
+    from helpers import GGUF, ModelConfig, RefModel, ref
+    import ctypes as C
+    cores = host_cores()
+    rng = np.random.default_rng(seed)
+    r = RefModel(path, max_seq=max(32, len(prompt) if prompt is not None else 0), max_ctx=max_ctx, max_batch=1,
+                 n_threads=cores)
+    c = r.new_cache()
+    if prompt is not None:
+        logits = r.forward_prefill(c, prompt)
+        tok = int(np.argmax(logits[-1]))
+        ctx0 = len(prompt)
+        how = f"after a real prefill of the same {ctx0}-token prompt"
+    else:
+        cfg = ModelConfig(GGUF(path))
+        row = cfg.n_head_kv * cfg.head_dim
+        kv = (0.5 * rng.standard_normal(cfg.n_layer * 2 * ctx0 * row)).astype(np.float32)
+        ref().ref_cache_fill(C.c_void_p(r.h), c, C.c_void_p(kv.ctypes.data), C.c_size_t(ctx0))
+        del kv
+        tok = int(rng.integers(0, n_vocab))
+        how = f"over a cache filled with {ctx0} seeded random positions"
+    steps, t0 = 0, time.perf_counter()
+    while steps < 3 or (time.perf_counter() - t0 < budget_s and steps < 64):
+        logits = r.forward_prefill(c, [tok])
+        tok = int(np.argmax(logits[-1]))
+        steps += 1
+    dt = time.perf_counter() - t0
+    return {"value": steps / dt, "unit": "tokens/s", "cores": cores, "kind": "reference",
+            "sample": f"{steps} greedy decode steps at contexts {ctx0 + 1}..{ctx0 + steps}, {how}; reference "
+                      f"LlamaModel on its scalar table, {cores} threads"}
+
+
+def cpu_c5_step(path, lens, seed):
+    """Config 5's steady-state step (c5_step_inputs) on the reference's LlamaModel, as its
+    BatchEngine runs it: forward_prefill of the chunk, then forward_batch of the decode rows."""
+    from helpers import GGUF, ModelConfig, RefModel, ref
+    import ctypes as C
+    cores = host_cores()
+    cfg = ModelConfig(GGUF(path))
+
+    class Info:
+        n_vocab, n_head_kv, head_dim, n_layer = cfg.n_vocab, cfg.n_head_kv, cfg.head_dim, cfg.n_layer
+    chunk, toks, rows = c5_step_inputs(Info, lens, seed)
+    r = RefModel(path, max_seq=512, max_ctx=1024 + 128 + 64, max_batch=64, n_threads=cores)
+    dec = []
+    for i in range(len(toks)):
+        c = r.new_cache()
+        rr = np.ascontiguousarray(rows(i))
+        ref().ref_cache_fill(C.c_void_p(r.h), c, C.c_void_p(rr.ctypes.data), C.c_size_t(int(lens[i])))
+        dec.append(c)
+    pc = r.new_cache()
+    t0 = time.perf_counter()
+    r.forward_prefill(pc, chunk)
+    t1 = time.perf_counter()
+    r.forward_batch(dec, toks)
+    t2 = time.perf_counter()
+    return {"value": (len(toks) + 1) / (t2 - t0), "unit": "tokens/s", "cores": cores, "kind": "reference",
+            "sample": f"one step: forward_prefill of a {len(chunk)}-token chunk ({t1 - t0:.2f} s, logits of every row "
+                      f"as the reference computes them) then forward_batch of {len(toks)} decode rows ({t2 - t1:.2f} s); "
+                      f"reference LlamaModel on its scalar table, {cores} threads"}
+
+
 def cpu_baseline(path, n_vocab, seed, budget_s, ctx0):
     """The reference's LlamaModel (scalar table) on the host cores: batch-1 decode and one
     32-sequence batched step over caches filled to the ragged contexts."""
@@ -691,6 +891,9 @@ def main() -> int:
     ap.add_argument("--no-f16", action="store_true", help="skip the fp16-cache runs")
     ap.add_argument("--no-c5", action="store_true", help="skip the config-5 mixed prefill/decode workload")
     ap.add_argument("--no-sweep", action="store_true", help="skip the config-2 matvec/matmul sweep")
+    ap.add_argument("--no-configs", action="store_true", help="skip the config-1 and config-3 decode-b1 legs")
+    ap.add_argument("--config-only", choices=sorted(B1_CONFIGS),
+                    help="only run that config's decode-b1 leg and print its figures (the workload of its profile)")
     ap.add_argument("--sweep-only", action="store_true",
                     help="only run the config-2 sweep and print its figures (the workload of its profile)")
     ap.add_argument("--c5-only", action="store_true",
@@ -724,6 +927,10 @@ def main() -> int:
     if args.sweep_only:
         H.init(0)
         print(json.dumps(bench_sweep(H, args.seed)), flush=True)
+        return 0
+    if args.config_only:
+        H.init(0)
+        print(json.dumps(bench_config_b1(H, args.config_only, args.warmup, args.seed)[0]), flush=True)
         return 0
     spec = synth.LLAMA32_1B
     log(f"model: {spec.name} (writing the seeded GGUF on first use)")
@@ -833,6 +1040,11 @@ def main() -> int:
                                "prefill_s": round(rg16["prefill_s"], 3)}
         m16.close()
         result["f16_cache"] = f16
+    b1_paths = {}
+    if not args.no_configs:
+        for name in sorted(B1_CONFIGS):
+            result[name], p, pr = bench_config_b1(H, name, args.warmup, args.seed)
+            b1_paths[name] = (p, pr)
     if not args.no_c5:
         result["c5_mixed"] = bench_c5(H, args.seed)
     if not args.no_sweep:
@@ -844,7 +1056,33 @@ def main() -> int:
             result["vs_cpu"] = round(result["value"] / b1c["value"], 1)
         if rgc is not None and "ragged32" in result:
             result["ragged32"]["cpu_baseline"] = rgc
-            result["ragged32"]["vs_cpu"] = round(result["ragged32"]["tokens_per_s"] / rgc["value"], 1)
+            # Like for like: the CPU's fixed 32-row steps against the GPU's same steps.
+            fixed = result["ragged32"]["attention_roofline"]["fixed_batch_tokens_per_s"]
+            result["ragged32"]["vs_cpu_fixed_batch"] = round(fixed / rgc["value"], 1)
+            result["ragged32"]["vs_cpu_schedule"] = round(result["ragged32"]["tokens_per_s"] / rgc["value"], 1)
+        if b1c is not None:
+            import synth
+            for name, (p, pr) in b1_paths.items():
+                prompt_len = B1_CONFIGS[name][0]
+                vocab = synth.CONFIGS[name].n_vocab
+                if name == "c1":  # small enough for the reference to prefill the real prompt
+                    cb = cpu_decode_b1(p, vocab, args.seed, args.cpu_budget, prompt_len, prompt=pr,
+                                       max_ctx=prompt_len + 96)
+                else:
+                    cb = cpu_decode_b1(p, vocab, args.seed, args.cpu_budget, prompt_len + args.warmup,
+                                       max_ctx=prompt_len + args.warmup + 96)
+                result[name]["cpu_baseline"] = cb
+                result[name]["vs_cpu"] = round(result[name]["tokens_per_s"] / cb["value"], 1)
+                log(f"cpu baseline {name}: {cb['value']:.3f} tok/s")
+            if "c5_mixed" in result:
+                lens = np.random.default_rng(args.seed + 11).integers(32, 1025, 64)
+                cs = cpu_c5_step(synth.cached_model(synth.CONFIGS["c5"]), lens, args.seed)
+                step = result["c5_mixed"]["mixed_step"]
+                step["cpu_baseline"] = cs
+                step["vs_cpu_one_pass"] = round(step["one_pass"]["tokens_per_s"] / cs["value"], 1)
+                step["vs_cpu_two_pass"] = round(step["two_pass"]["tokens_per_s"] / cs["value"], 1)
+                result["c5_mixed"]["cpu_baseline"] = cs
+                log(f"cpu baseline c5 step: {cs['value']:.3f} tok/s")
     print(json.dumps(result), flush=True)
     return 0
 
