@@ -194,6 +194,8 @@ def ptr_of(b) -> int:
 
 # axon_model_probe's type for the attention launches (AXON_MODEL_PROBE_ATTENTION).
 PROBE_ATTENTION = -2
+# ... and for the persistent decode kernel's launches alone (AXON_MODEL_PROBE_STEP).
+PROBE_STEP = -3
 
 
 class ModelOptions(C.Structure):

@@ -820,7 +820,8 @@ Expected<std::size_t> LlamaModel::run(std::span<const Row> rows, bool copy_logit
     sa.epoch = &step_epoch_;
     sa.status = step_status_;
     // The probe counts the whole kernel as one launch of the layers' q|k|v type.
-    const bool probed = probe_type_ == step_shape_.type_qkv && 2 * probe_used_ + 2 <= probe_events_.size();
+    const bool probed = (probe_type_ == kProbeStep || probe_type_ == step_shape_.type_qkv) &&
+                        2 * probe_used_ + 2 <= probe_events_.size();
     if (probed) axon_hip_probe_next_launch(probe_events_[2 * probe_used_], probe_events_[2 * probe_used_ + 1]);
     const int rc = axon_hip_decode_layers(&step_shape_, &sa);
     if (probed) axon_hip_probe_next_launch(nullptr, nullptr);

@@ -252,6 +252,7 @@ private:
   // Probe state (set_probe / read_probe).
   int probe_type_ = -1;
   static constexpr int kProbeAttention = -2;  // AXON_MODEL_PROBE_ATTENTION (axon_model.h)
+  static constexpr int kProbeStep = -3;       // AXON_MODEL_PROBE_STEP (axon_model.h)
   std::vector<void*> probe_events_;
   std::size_t probe_used_ = 0;
   std::vector<double> probe_bytes_;

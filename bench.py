@@ -605,7 +605,9 @@ def traffic_summary(fetch_csv, write_csv):
            "traffic_bytes_per_launch": round(fetch + write),
            "copy_bytes": COPY_BYTES, "copy_fetch_kib": fcopy, "copy_write_kib": wcopy,
            "fetch_scale": round(f_scale, 4), "write_scale": round(w_scale, 4),
-           "counters": [str(fetch_csv), str(write_csv)]}
+           "passes": ["rocprofv3 --pmc FETCH_SIZE -f csv -- python3 bench.py --traffic-probe --steps 8",
+                      "rocprofv3 --pmc WRITE_SIZE -f csv -- python3 bench.py --traffic-probe --steps 8",
+                      "python3 bench.py --traffic-summary <FETCH_SIZE counter csv> <WRITE_SIZE counter csv>"]}
     if fq6 and wq6:  # the Q6_K output matvec over the planar copy, for comparison
         out["q6k_planar_kernel<1>"] = {"dispatches": len(fq6),
                                        "traffic_bytes_per_launch": round(float(np.mean(fq6)) * 1024.0 * f_scale +
@@ -740,7 +742,8 @@ def bench_config_b1(H, name, warmup, seed):
     model.free_cache(cache)
     ctx = [prompt_len + warmup + 1, prompt_len + warmup + steps]
     step_bytes = info.weight_bytes_per_token + info.kv_bytes_per_position * 0.5 * (ctx[0] + ctx[1])
-    ms, launches, nbytes = probe_pass(H, model, info.n_vocab, min(steps, 32), prompt_len, seed, wtype)
+    ms, launches, nbytes = probe_pass(H, model, info.n_vocab, min(steps, 32), prompt_len, seed,
+                                      H.PROBE_STEP if info.persistent_decode else wtype)
     achieved = nbytes / (ms * 1e-3) / 1e9 if launches else 0.0
     res = {"workload": f"{spec.name}-shaped random-init GGUF, {prompt_len}-token prompt, {steps} greedy steps, batch 1",
            "tokens_per_s": round(steps / dt, 2), "ms_per_step": round(1e3 * dt / steps, 4), "context": ctx,
@@ -966,13 +969,14 @@ def main() -> int:
     b1 = bench_decode_b1(H, model, info.n_vocab, args.steps, args.warmup, args.prompt, args.seed)
     log(f"decode-b1: {b1['tokens_per_s']:.1f} tok/s ({b1['ms_per_step']:.3f} ms/step)")
 
-    ms, launches, nbytes = probe_pass(H, model, info.n_vocab, min(args.steps, 32), args.prompt, args.seed, synth.Q4_0)
+    ms, launches, nbytes = probe_pass(H, model, info.n_vocab, min(args.steps, 32), args.prompt, args.seed,
+                                      H.PROBE_STEP if info.persistent_decode else synth.Q4_0)
     if launches == 0:
         raise SystemExit("bench.py: the Q4_0 probe recorded no launch")
     achieved = nbytes / (ms * 1e-3) / 1e9
     q6_ms, q6_n, q6_b = probe_pass(H, model, info.n_vocab, min(args.steps, 32), args.prompt, args.seed, synth.Q6_K)
     q6_gbs = q6_b / (q6_ms * 1e-3) / 1e9
-    log(f"Q4_0 matvec: {launches} launches, {achieved:.0f} GB/s; Q6_K: {q6_n} launches, {q6_gbs:.0f} GB/s")
+    log(f"step kernel: {launches} launches, {achieved:.0f} GB/s; Q6_K: {q6_n} launches, {q6_gbs:.0f} GB/s")
 
     kv_pos_bytes = info.kv_bytes_per_position
     mean_ctx = 0.5 * (b1["context"][0] + b1["context"][1])

@@ -164,6 +164,9 @@ int axon_sample_candidates(const axon_sampler_config* config, axon_rng* rng, con
  * instead (their bytes: the rows' visible K and V rows, q and the output). probe_read returns the
  * summed kernel milliseconds, the launch count and the launches' algorithmic bytes, and resets. */
 #define AXON_MODEL_PROBE_ATTENTION (-2)
+/* With type AXON_MODEL_PROBE_STEP only the persistent decode kernel's launches are bracketed (a
+ * probe of the layers' q|k|v type brackets them too, with every other matmul of that type). */
+#define AXON_MODEL_PROBE_STEP (-3)
 int axon_model_probe(axon_model* model, int type, int enable);
 int axon_model_probe_read(axon_model* model, double* ms, size_t* launches, double* bytes);
 
