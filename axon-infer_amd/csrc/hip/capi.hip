@@ -683,6 +683,18 @@ int axon_hip_topk_rows(const float* x, size_t n, size_t n_rows, size_t stride, s
                           out_logit, out_id);
 }
 
+size_t axon_hip_sort_rows_work_bytes(size_t n, size_t n_rows) { return 8 * n * n_rows; }
+
+int axon_hip_sort_rows(const float* x, size_t n, size_t n_rows, size_t stride, void* work, float* out_logit,
+                       int32_t* out_id) {
+  AXON_READY();
+  if (n == 0 || !fits_u32(n) || !fits_u32(n_rows) || stride < n)
+    return fail(kInvalidArgument, "sort_rows: %zu x %zu, stride %zu", n_rows, n, stride);
+  if (work == nullptr || out_logit == nullptr || out_id == nullptr)
+    return fail(kInvalidArgument, "sort_rows: the workspace and outputs are required");
+  return sort_rows_launch(x, static_cast<uint32_t>(n), static_cast<uint32_t>(n_rows), stride, work, out_logit, out_id);
+}
+
 int axon_hip_matmul_q8_fused(int type, const void* xq, size_t n_rows, size_t n_in, size_t n_seg,
                              const void* const* w, float* const* y, const size_t* n_out, const size_t* y_stride,
                              int accumulate) {

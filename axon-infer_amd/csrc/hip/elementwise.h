@@ -43,6 +43,10 @@ size_t argmax_scratch_words(uint32_t n_rows);
 constexpr uint32_t kMaxTopK = 256;
 int topk_rows_launch(const float* x, uint32_t n, uint32_t n_rows, size_t stride, uint32_t k, float* out_logit,
                      int32_t* out_id);
+// Every value of each row in the same order (out_logit/out_id [n_rows][n], NaN last with id -1),
+// through a workspace of 8 * n * n_rows bytes.
+int sort_rows_launch(const float* x, uint32_t n, uint32_t n_rows, size_t stride, void* work, float* out_logit,
+                     int32_t* out_id);
 int argmax_rows_launch(const float* x, uint32_t n, uint32_t n_rows, size_t stride, uint64_t* scratch, int32_t* out);
 // argmax_rows over a fixed per-device array instead of a workspace (at most kArgmaxNoAllocRows rows);
 // argmax_noalloc_setup finds the array's address on the current device (once per device).

@@ -206,7 +206,174 @@ __global__ __launch_bounds__(kTopKThreads) void topk_rows_kernel(const float* __
   }
 }
 
+// ---- Whole-row sort (top_k 0, or more than kMaxTopK candidates) -------------------------------
+// sampler.cpp:105-118 sorts every id by logit when top_k keeps them all. One workgroup per row
+// runs a stable LSD radix sort of 32-bit keys, four passes of 8-bit digits, in the order the
+// top-k kernel keeps: larger values first, equal values (-0 equal to +0) by ascending index,
+// NaN last with id -1. The key is the complement of the order-preserving map of argmax_key, so
+// an ascending sort of keys is a descending sort of values; the input order is ascending index
+// and every pass is stable, so ties keep it.
+//
+// The four digit histograms come from one sweep (the keys are the same in every pass). A pass
+// takes the row 1024 keys at a time in index order: lanes of a wave that share a digit find each
+// other with eight ballots, a lane's rank among them is the popcount of the lower ones, the
+// first of them writes the group's count into a [wave][digit] table, and 256 threads turn each
+// digit's column into offsets (the digit's running base plus the earlier waves' counts). Two
+// tables alternate, so the one the next group of keys counts into is cleared while this one is
+// read. Passes ping-pong between the workspace and the output arrays: row -> work -> out ->
+// work -> out, the last pass writing the original values (signed zeros kept) and ids.
+
+constexpr uint32_t kSortThreads = 1024;
+constexpr uint32_t kSortWaves = kSortThreads / 64;
+constexpr uint32_t kSortNaN = 0xffffffffu;
+
+__device__ __forceinline__ uint32_t sort_key(float v) {
+  if (v != v) return kSortNaN;  // no other value maps there: only a NaN has order 0
+  uint32_t b = __float_as_uint(v);
+  if (b == 0x80000000u) b = 0;
+  const uint32_t ord = (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+  return ~ord;
+}
+
+// The valid lanes of this wave whose digit equals this lane's.
+__device__ __forceinline__ uint64_t same_digit_lanes(uint32_t d, bool valid) {
+  uint64_t peers = __ballot(valid);
+#pragma unroll
+  for (uint32_t b = 0; b < 8; ++b) {
+    const bool bit = ((d >> b) & 1u) != 0;
+    const uint64_t m = __ballot(bit);
+    peers &= bit ? m : ~m;
+  }
+  return peers;
+}
+
+__global__ __launch_bounds__(kSortThreads) void sort_rows_kernel(const float* __restrict__ x, uint32_t n,
+                                                                 size_t stride, uint32_t* __restrict__ work_key,
+                                                                 int32_t* __restrict__ work_id,
+                                                                 float* __restrict__ out_logit,
+                                                                 int32_t* __restrict__ out_id) {
+  __shared__ uint32_t hist[4][256];
+  __shared__ uint32_t offs[2][kSortWaves][256];
+  const uint32_t r = blockIdx.x;
+  const uint32_t t = threadIdx.x;
+  const uint32_t w = t >> 6;
+  const uint64_t below = (1ull << (t & 63)) - 1;
+  const float* row = x + static_cast<size_t>(r) * stride;
+  uint32_t* ak = work_key + static_cast<size_t>(r) * n;
+  int32_t* ai = work_id + static_cast<size_t>(r) * n;
+  // The output arrays hold keys between passes; every access inside the kernel is as uint32.
+  uint32_t* bk = reinterpret_cast<uint32_t*>(out_logit) + static_cast<size_t>(r) * n;
+  int32_t* bi = out_id + static_cast<size_t>(r) * n;
+
+  for (uint32_t i = t; i < 4 * 256; i += kSortThreads) (&hist[0][0])[i] = 0;
+  for (uint32_t i = t; i < 2 * kSortWaves * 256; i += kSortThreads) (&offs[0][0][0])[i] = 0;
+  __syncthreads();
+  for (uint32_t j0 = 0; j0 < n; j0 += kSortThreads) {
+    const uint32_t j = j0 + t;
+    const bool valid = j < n;
+    const uint32_t k = valid ? sort_key(row[j]) : 0;
+#pragma unroll
+    for (uint32_t p = 0; p < 4; ++p) {
+      const uint32_t d = (k >> (8 * p)) & 255u;
+      const uint64_t peers = same_digit_lanes(d, valid);
+      if (valid && (peers & below) == 0) atomicAdd(&hist[p][d], static_cast<uint32_t>(__popcll(peers)));
+    }
+  }
+  __syncthreads();
+  if (w < 4) {  // exclusive scan of pass w's histogram, four bins a lane
+    const uint32_t lane = t & 63;
+    uint32_t c[4];
+    uint32_t s = 0;
+#pragma unroll
+    for (uint32_t i = 0; i < 4; ++i) {
+      c[i] = hist[w][4 * lane + i];
+      s += c[i];
+    }
+    uint32_t inc = s;
+#pragma unroll
+    for (uint32_t off = 1; off < 64; off <<= 1) {
+      const uint32_t o = __shfl_up(inc, off, 64);
+      if (lane >= off) inc += o;
+    }
+    uint32_t e = inc - s;
+#pragma unroll
+    for (uint32_t i = 0; i < 4; ++i) {
+      hist[w][4 * lane + i] = e;
+      e += c[i];
+    }
+  }
+  __syncthreads();
+
+  uint32_t buf = 0;  // offs[buf] is clear when a group of keys starts
+  for (uint32_t pass = 0; pass < 4; ++pass) {
+    const uint32_t shift = 8 * pass;
+    const uint32_t* sk = pass == 2 ? bk : ak;
+    const int32_t* si = pass == 2 ? bi : ai;
+    uint32_t* dk = (pass & 1u) ? bk : ak;
+    int32_t* di = (pass & 1u) ? bi : ai;
+    uint32_t base = t < 256 ? hist[pass][t] : 0;  // digit t's next free slot
+    for (uint32_t j0 = 0; j0 < n; j0 += kSortThreads, buf ^= 1u) {
+      const uint32_t j = j0 + t;
+      const bool valid = j < n;
+      uint32_t k = kSortNaN;
+      int32_t id = -1;
+      if (valid) {
+        if (pass == 0) {
+          k = sort_key(row[j]);
+          id = static_cast<int32_t>(j);
+        } else {
+          k = sk[j];
+          id = si[j];
+        }
+      }
+      const uint32_t d = (k >> shift) & 255u;
+      const uint64_t peers = same_digit_lanes(d, valid);
+      const uint32_t rank = static_cast<uint32_t>(__popcll(peers & below));
+      if (valid && rank == 0) offs[buf][w][d] = static_cast<uint32_t>(__popcll(peers));
+      __syncthreads();
+      if (t < 256) {
+        uint32_t c[kSortWaves];
+#pragma unroll
+        for (uint32_t v = 0; v < kSortWaves; ++v) c[v] = offs[buf][v][t];
+        uint32_t s = base;
+#pragma unroll
+        for (uint32_t v = 0; v < kSortWaves; ++v) {
+          offs[buf][v][t] = s;
+          s += c[v];
+          offs[buf ^ 1u][v][t] = 0;  // read by the previous group, which every thread has finished
+        }
+        base = s;
+      }
+      __syncthreads();
+      if (valid) {
+        const uint32_t at = offs[buf][w][d] + rank;
+        if (pass == 3) {
+          const bool nan = k == kSortNaN;
+          dk[at] = nan ? 0u : __float_as_uint(row[id]);
+          di[at] = nan ? -1 : id;
+        } else {
+          dk[at] = k;
+          di[at] = id;
+        }
+      }
+    }
+    __syncthreads();  // this pass's stores before the next pass's loads (one workgroup)
+  }
+}
+
 }  // namespace
+
+int sort_rows_launch(const float* x, uint32_t n, uint32_t n_rows, size_t stride, void* work, float* out_logit,
+                     int32_t* out_id) {
+  if (n_rows == 0) return kOk;
+  if (n == 0) return fail(kInvalidArgument, "sort_rows: empty rows");
+  if (n_rows > 65535) return fail(kInvalidArgument, "sort_rows: %u rows exceed one launch's 65535", n_rows);
+  auto* key = static_cast<uint32_t*>(work);
+  auto* id = reinterpret_cast<int32_t*>(key + static_cast<size_t>(n_rows) * n);
+  hipLaunchKernelGGL(sort_rows_kernel, dim3(n_rows), dim3(kSortThreads), 0, stream(), x, n, stride, key, id, out_logit,
+                     out_id);
+  return check_launch("sort_rows");
+}
 
 int topk_rows_launch(const float* x, uint32_t n, uint32_t n_rows, size_t stride, uint32_t k, float* out_logit,
                      int32_t* out_id) {

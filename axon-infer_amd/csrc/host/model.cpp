@@ -386,7 +386,7 @@ LlamaModel::~LlamaModel() {
                   static_cast<void*>(v_), static_cast<void*>(attn_), static_cast<void*>(gate_),
                   static_cast<void*>(up_), static_cast<void*>(tmp_), static_cast<void*>(logits_),
                   static_cast<void*>(scores_), static_cast<void*>(argmax_scratch_), static_cast<void*>(ids_),
-                  static_cast<void*>(gen_ids_), cand_, window_,
+                  static_cast<void*>(gen_ids_), cand_, sort_out_, sort_work_, window_,
                   xq_, rowinfo_, kv_, static_cast<void*>(kv_free_),
                   static_cast<void*>(rope_table_), weights_, planar_}) {
     if (p != nullptr) axon_hip_free(p);
@@ -1261,14 +1261,23 @@ Expected<std::size_t> LlamaModel::sample(std::span<std::int32_t> ids, std::span<
       any_greedy = true;
       continue;
     }
-    const std::size_t kept = sampling::kept_after_top_k(configs[r], V);
-    if (kept > AXON_HIP_MAX_TOPK)
-      return make_error(ErrorCode::Unsupported, "sample: row " + std::to_string(r) + " keeps " + std::to_string(kept) +
-                                                    " candidates after top-k; the device sampler keeps at most " +
-                                                    std::to_string(AXON_HIP_MAX_TOPK) + " (top_k 1.." +
-                                                    std::to_string(AXON_HIP_MAX_TOPK) + ")");
-    k_max = std::max(k_max, kept);
+    k_max = std::max(k_max, sampling::kept_after_top_k(configs[r], V));
   }
+  // Up to AXON_HIP_MAX_TOPK candidates a row come from the top-k kernel; beyond that every row
+  // is sorted whole (the same order, so a row's first top_k candidates are the same either way).
+  const bool whole = k_max > AXON_HIP_MAX_TOPK;
+  if (whole && n > sort_rows_) {
+    for (void** p : {&sort_out_, &sort_work_}) {
+      if (*p != nullptr) axon_hip_free(*p);
+      *p = nullptr;
+    }
+    sort_rows_ = 0;
+    if (axon_hip_malloc(&sort_out_, n * V * 8) != AXON_HIP_OK ||
+        axon_hip_malloc(&sort_work_, axon_hip_sort_rows_work_bytes(V, n)) != AXON_HIP_OK)
+      return device_error("sample: whole-vocabulary candidates");
+    sort_rows_ = n;
+  }
+  const std::size_t width = whole ? V : k_max;  // candidates a row holds on the device
   last_rows_ = 0;
   // The penalty, once per distinct (penalty, window) setting among the rows.
   if (!recent.empty()) {
@@ -1289,25 +1298,28 @@ Expected<std::size_t> LlamaModel::sample(std::span<std::int32_t> ids, std::span<
       std::fill(select.begin(), select.end(), 0);
     }
   }
-  auto* cand_logits = static_cast<float*>(cand_);
-  auto* cand_ids = reinterpret_cast<std::int32_t*>(cand_logits + n * k_max);
-  if ((any_greedy && axon_hip_argmax_rows(logits_, V, n, V, argmax_scratch_, ids_) != AXON_HIP_OK) ||
-      (k_max != 0 && axon_hip_topk_rows(logits_, V, n, V, k_max, cand_logits, cand_ids) != AXON_HIP_OK))
+  void* cand = whole ? sort_out_ : cand_;
+  auto* cand_logits = static_cast<float*>(cand);
+  auto* cand_ids = reinterpret_cast<std::int32_t*>(cand_logits + n * width);
+  if (any_greedy && axon_hip_argmax_rows(logits_, V, n, V, argmax_scratch_, ids_) != AXON_HIP_OK)
+    return device_error("sample");
+  if (k_max != 0 && (whole ? axon_hip_sort_rows(logits_, V, n, V, sort_work_, cand_logits, cand_ids)
+                           : axon_hip_topk_rows(logits_, V, n, V, k_max, cand_logits, cand_ids)) != AXON_HIP_OK)
     return device_error("sample");
   // Synchronous copies on the library stream.
   if (any_greedy && axon_hip_memcpy_d2h(ids.data(), ids_, n * 4) != AXON_HIP_OK) return device_error("sample");
   if (auto st = check_persistent_status(); !st) return st.error();
   if (k_max == 0) return n;
-  cand_host_.resize(n * k_max * 8);
-  if (axon_hip_memcpy_d2h(cand_host_.data(), cand_, n * k_max * 8) != AXON_HIP_OK) return device_error("sample");
+  cand_host_.resize(n * width * 8);
+  if (axon_hip_memcpy_d2h(cand_host_.data(), cand, n * width * 8) != AXON_HIP_OK) return device_error("sample");
   const auto* hl = reinterpret_cast<const float*>(cand_host_.data());
-  const auto* hi = reinterpret_cast<const std::int32_t*>(hl + n * k_max);
+  const auto* hi = reinterpret_cast<const std::int32_t*>(hl + n * width);
   probs_.resize(k_max);
   for (std::size_t r = 0; r < n; ++r) {
     if (configs[r].temperature <= 0.0F) continue;
     std::size_t kept = sampling::kept_after_top_k(configs[r], V);
-    while (kept > 1 && hi[r * k_max + kept - 1] < 0) --kept;  // NaN logits are never candidates
-    ids[r] = sampling::draw(configs[r], rngs[r], hl + r * k_max, hi + r * k_max, kept, probs_.data());
+    while (kept > 1 && hi[r * width + kept - 1] < 0) --kept;  // NaN logits are never candidates
+    ids[r] = sampling::draw(configs[r], rngs[r], hl + r * width, hi + r * width, kept, probs_.data());
   }
   return n;
 }

@@ -242,6 +242,12 @@ private:
   std::int32_t* ids_ = nullptr;
   std::int32_t* gen_ids_ = nullptr;  // generate_greedy's ids: [max_ctx + 1]
   void* cand_ = nullptr;  // top-k candidates: [rows][k] logits, then [rows][k] ids
+  // Every candidate of each row when a row keeps more than AXON_HIP_MAX_TOPK of them (top_k 0):
+  // [rows][n_vocab] sorted logits then ids, and the sort's workspace. Allocated by the first
+  // such sample call for its row count, and again only for a call with more rows.
+  void* sort_out_ = nullptr;
+  void* sort_work_ = nullptr;
+  std::size_t sort_rows_ = 0;
   std::vector<std::byte> cand_host_;
   std::vector<double> probs_;
   void* window_ = nullptr;       // device: recent ids [R][kMaxPenaltyWindow] | lengths [R]

@@ -210,6 +210,15 @@ int axon_hip_argmax_rows_noalloc(const float* x, size_t n, size_t n_rows, size_t
 #define AXON_HIP_MAX_TOPK 256
 int axon_hip_topk_rows(const float* x, size_t n, size_t n_rows, size_t stride, size_t k, float* out_logit,
                        int32_t* out_id);
+/* Every candidate in order, for top_k 0 or a top_k above 256 (src/sampling/sampler.cpp:105-118,
+ * std::ranges::sort of all ids by logit, descending, and the partial_sort whose first top_k it
+ * also gives): row r's n values (rows stride floats apart) into out_logit[r * n + i] with their
+ * indices in out_id, in the order of axon_hip_topk_rows (descending, equal values by ascending
+ * index, -0 equal to +0), the NaN values last with ids -1 and logits 0. work: a device buffer of
+ * axon_hip_sort_rows_work_bytes(n, n_rows) bytes. The outputs must not alias x or work. */
+size_t axon_hip_sort_rows_work_bytes(size_t n, size_t n_rows);
+int axon_hip_sort_rows(const float* x, size_t n, size_t n_rows, size_t stride, void* work, float* out_logit,
+                       int32_t* out_id);
 /* gate|up with the SwiGLU product and its Q8_0 quantization in one launch, for 65 or more
  * rows (llama.cpp:600-620: out = silu(x W_gate^T) * (x W_up^T), then quantize_row_q8_0 of each
  * row for w_down): the same bits as matmul_q8_fused of the two weights, silu_mul_rows and

@@ -145,10 +145,12 @@ double axon_rng_uniform(axon_rng* rng);
  * repetition penalty (recent as for axon_model_greedy), the greedy choice for rows at temperature
  * zero, and the top-k candidates of the others, descending, equal logits by ascending id (the
  * reference leaves their order unspecified). On the host: temperature, softmax in double, top-p,
- * min-p and one draw from rngs[i] per stochastic row. Only the ids and at most 256 candidates
- * per row cross to the host. A stochastic row must keep at most 256 candidates after top-k
- * (top_k 1..256, or a vocabulary of at most 256), else Unsupported and nothing runs. The pass's
- * logits are consumed. */
+ * min-p and one draw from rngs[i] per stochastic row. When every stochastic row keeps at most
+ * 256 candidates after top-k, only the ids and those candidates cross to the host; when one
+ * keeps more (top_k 0 keeps the whole vocabulary, sampler.cpp:115-117), every row of the call is
+ * sorted whole on the device (axon_hip_sort_rows, the same order) and [n][n_vocab] sorted
+ * logits and ids cross instead. The first such call allocates device room for its rows (a later
+ * call with more rows, again). The pass's logits are consumed. */
 int axon_model_sample(axon_model* model, const axon_sampler_config* configs, axon_rng* rngs,
                       const int32_t* const* recent, const size_t* recent_len, int32_t* ids, size_t n);
 

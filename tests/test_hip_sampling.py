@@ -1,5 +1,5 @@
 """The device sampler (sampling.hip: axon_hip_repeat_penalty_rows, axon_hip_argmax_rows,
-axon_hip_topk_rows, and the model's axon_model_greedy and axon_model_sample) against the oracle's
+axon_hip_topk_rows, axon_hip_sort_rows, and the model's axon_model_greedy and axon_model_sample) against the oracle's
 sampler, which tests/test_oracle_sampling.py pins to the reference's Sampler draw for draw.
 
 Selection is index work, so the bar is bit-exact: the same id for every row, the penalised
@@ -344,9 +344,84 @@ def test_model_sample_bounds(H, c1_model):
         m.sample([H.SamplerConfig()], [H.Rng(1)])
     g = H.Rng(5)
     before = g.state()
-    with pytest.raises(H.HipError, match="at most 256"):
-        m.sample([H.SamplerConfig(top_k=0)] * 3, [g, H.Rng(6), H.Rng(7)])
+    with pytest.raises(H.HipError, match="3 rows"):
+        m.sample([H.SamplerConfig(top_k=0)] * 2, [g, H.Rng(6)])
     assert g.state() == before  # nothing ran
     # The pass's logits are still there after a refused call.
     ids = m.sample([H.SamplerConfig(temperature=0.0)] * 3, [H.Rng(1)] * 3)
     assert len(ids) == 3
+
+
+@pytest.mark.parametrize("n", [151936, 128256, 32000, 4097, 1025, 1024, 300, 40, 1])
+def test_sort_rows_match_sorted_order(H, n):
+    """The whole-row sort behind top_k 0: every row kind of the top-k test, every position in the
+    order the top-k kernel keeps (NaN last with ids -1 and logits 0), values bit for bit (signed
+    zeros kept), at row lengths around one 1024-key group and at the largest vocabularies."""
+    kinds = ["normal", "ties", "nan", "zeros", "equal", "one-stride", "ascending", "descending"]
+    rng = np.random.default_rng(n)
+    x = np.stack([topk_rows(kind, n, rng) for kind in kinds])
+    stride = n + 5
+    xs = np.zeros((len(kinds), stride), np.float32)
+    xs[:, :n] = x
+    H.lib().axon_hip_sort_rows_work_bytes.restype = C.c_size_t
+    work = H.DeviceBuffer(H.lib().axon_hip_sort_rows_work_bytes(C.c_size_t(n), C.c_size_t(len(kinds))))
+    dx = H.DeviceBuffer.of(xs)
+    ol = H.DeviceBuffer(4 * len(kinds) * n)
+    oi = H.DeviceBuffer(4 * len(kinds) * n)
+    H.call("sort_rows", dx, n, len(kinds), stride, work, ol, oi)
+    got_v = ol.download(np.float32, len(kinds) * n).reshape(len(kinds), n)
+    got_i = oi.download(np.int32, len(kinds) * n).reshape(len(kinds), n)
+    for r, kind in enumerate(kinds):
+        want_v, want_i = topk_reference(x[r], n)
+        assert np.array_equal(got_i[r], want_i), (kind, np.nonzero(got_i[r] != want_i)[0][:5])
+        assert np.array_equal(got_v[r].view(np.uint32), want_v.view(np.uint32)), kind
+
+
+def test_sort_rows_bounds(H):
+    dx = H.DeviceBuffer.of(np.zeros(300, np.float32))
+    out = H.DeviceBuffer(4 * 300)
+    with pytest.raises(H.HipError, match="stride"):
+        H.call("sort_rows", dx, 300, 1, 200, out, out, out)
+    with pytest.raises(H.HipError, match="stride"):
+        H.call("sort_rows", dx, 0, 1, 300, out, out, out)
+    with pytest.raises(H.HipError, match="required"):
+        H.call("sort_rows", dx, 300, 1, 300, None, out, out)
+
+
+WHOLE_CONFIGS = [
+    dict(temperature=0.8, top_k=0, top_p=0.95, min_p=0.05, repeat_penalty=1.1, repeat_last_n=64),
+    dict(temperature=1.3, top_k=0, top_p=1.0, min_p=0.0, repeat_penalty=1.0, repeat_last_n=64),
+    dict(temperature=0.9, top_k=300, top_p=0.98, min_p=0.0, repeat_penalty=1.2, repeat_last_n=32),
+    dict(temperature=0.8, top_k=40, top_p=0.95, min_p=0.05, repeat_penalty=1.1, repeat_last_n=64),
+    dict(temperature=0.0, top_k=0, top_p=0.95, min_p=0.05, repeat_penalty=1.3, repeat_last_n=16),
+    dict(temperature=2.0, top_k=0, top_p=0.5, min_p=0.01, repeat_penalty=1.1, repeat_last_n=64),
+]
+
+
+def test_model_sample_whole_vocabulary_matches_oracle_sampler(H, c1_model):
+    """top_k 0 (sampler.cpp:115-117 sorts every id) beside top_k 300 and 40 and a greedy row, six
+    sequences for 24 steps, then the same with fewer rows (the device room of the first call
+    serves): every drawn id and generator state equal the oracle sampler's, whose qsort of the
+    whole vocabulary is the reference's sort."""
+    n_seq = len(WHOLE_CONFIGS)
+    m = hip_model(c1_model, max_seq=32, max_ctx=128, max_batch=n_seq, max_caches=n_seq)
+    rng = np.random.default_rng(22)
+    prompts = [rng.integers(0, 2048, 5 + 2 * i).astype(np.int32) for i in range(n_seq)]
+    caches = [m.new_cache() for _ in range(n_seq)]
+    hist = [list(p) for p in prompts]
+    cfgs = [H.SamplerConfig(**c) for c in WHOLE_CONFIGS]
+    gens = [H.Rng(2000 + i) for i in range(n_seq)]
+    orc = [OracleSampler(2048, seed=2000 + i, **c) for i, c in enumerate(WHOLE_CONFIGS)]
+    for i in range(n_seq):
+        m.forward_prefill(caches[i], prompts[i][:-1], logits=False)
+    toks = [int(p[-1]) for p in prompts]
+    for step in range(24):
+        rows = n_seq if step < 16 else 2  # the last steps decode two sequences only
+        logits = m.forward_batch(caches[:rows], toks[:rows])
+        got = m.sample(cfgs[:rows], gens[:rows], hist[:rows])
+        want = [orc[i].sample(logits[i], np.array(hist[i], np.int32)) for i in range(rows)]
+        assert got.tolist() == want, (step, got.tolist(), want)
+        for i in range(rows):
+            assert gens[i].state() == tuple(orc[i].rng.s), (step, i)
+            hist[i].append(int(got[i]))
+        toks[:rows] = [int(t) for t in got]
