@@ -822,12 +822,18 @@ axon_hip::StepShape step_shape_of(const axon_hip_decode_shape* sh) {
 }
 constexpr uint32_t kStepSpinLimit = 1u << 20;  // polls of one barrier (about a second) before giving up
 std::atomic<uint32_t> g_step_spin_limit{kStepSpinLimit};
+std::atomic<uint32_t> g_step_fail_waits{0};
 std::atomic<uint64_t*> g_step_stamps{nullptr};
 static_assert(sizeof(axon_hip_decode_layer) == sizeof(axon_hip::StepLayer), "one layer record layout");
 }  // namespace
 
 int axon_hip_decode_layers_set_spin_limit(uint32_t polls) {
   g_step_spin_limit.store(polls == 0 ? kStepSpinLimit : polls, std::memory_order_relaxed);
+  return kOk;
+}
+
+int axon_hip_decode_layers_set_fail_waits(int on) {
+  g_step_fail_waits.store(on != 0 ? 1u : 0u, std::memory_order_relaxed);
   return kOk;
 }
 
@@ -885,6 +891,7 @@ int axon_hip_decode_layers(const axon_hip_decode_shape* shape, const axon_hip_de
   c.epoch = *a->epoch;
   c.status = a->status;
   c.spin_limit = g_step_spin_limit.load(std::memory_order_relaxed);
+  c.fail_waits = g_step_fail_waits.load(std::memory_order_relaxed);
   c.stamps = g_step_stamps.load(std::memory_order_relaxed);
   const int rc = step_launch(s, c);
   if (rc != kOk) return rc;

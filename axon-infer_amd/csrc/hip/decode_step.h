@@ -42,6 +42,7 @@ struct StepCall {
   uint64_t epoch;           // phases run on this workspace before the call
   uint32_t* status;         // pinned host word: 0, or why the kernel gave up
   uint32_t spin_limit;      // polls of one tagged word before giving up
+  uint32_t fail_waits;      // test hook: nonzero, no wait ever sees its word written
   uint64_t* stamps;         // per-phase clock stamps (step_stamp_count words), or null
 };
 

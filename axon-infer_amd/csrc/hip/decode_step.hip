@@ -12,9 +12,9 @@
 //
 // Layout of a workgroup (512 threads): waves 0-3 compute, with the 256-thread reductions of the
 // launch-per-kernel path; waves 4-7 copy weights into LDS with LDS-DMA. Each phase's slice of
-// the next layer's weights (q|k|v rows, wo rows, 32 gate and 32 up rows, down rows) is issued as
-// soon as the phase that used the slice ends, so the weights of a layer stream from HBM while
-// the attention and the waits run. The copying waves keep no other memory operation
+// the next layer's weights (q|k|v rows, wo rows, 32 gate and 32 up rows, down rows) is issued
+// when the phase after the one that used the slice starts, so the weights of a layer stream from
+// HBM while the attention and the waits run, and issuing them overlaps the polls. The copying waves keep no other memory operation
 // outstanding, so their waits (s_waitcnt vmcnt) count their own copies only, in issue order;
 // they follow the compute waves' workgroup barriers until a phase-done flag in LDS is set.
 //
@@ -45,6 +45,13 @@ constexpr uint32_t kHeadDim = 64;
 constexpr uint32_t kVRegs = 2;         // float4 of V slices each compute thread stages per chunk
 constexpr uint32_t kVChunkF4 = kVRegs * 256;  // float4 per V chunk (8 KB)
 
+// How long a wait polls: `limit` polls of a word before the workgroup gives up; with `never` set
+// (a test hook) no word counts as written, so every wait gives up after its polls.
+struct PollLimit {
+  uint32_t limit;
+  uint32_t never;
+};
+
 struct StepK {
   StepShape s;
   const StepLayer* layers;
@@ -64,7 +71,7 @@ struct StepK {
   uint32_t dsplit, dd, vchunk;  // mix: workgroups per head, dims per workgroup, positions per V chunk
   uint64_t epoch;
   uint32_t* status;
-  uint32_t spin_limit;
+  PollLimit poll;
   uint64_t* stamps;                         // per-phase clock stamps, or null
   uint32_t r_qkv, r_o, r_d;                 // weight rows per workgroup
   uint32_t rb_d, rb_q, rb_ff;               // bytes per row of the d-, dq- and ff-wide matrices
@@ -240,17 +247,17 @@ __device__ __forceinline__ void put(uint64_t* p, uint32_t tag, uint32_t bits) {
 // Polls n consecutive tagged words until every one carries `tag`, their payloads into out;
 // false when the poll limit ran out first.
 template <int N>
-__device__ __forceinline__ bool take(const uint64_t* src, uint32_t tag, uint32_t (&out)[N], uint32_t limit) {
+__device__ __forceinline__ bool take(const uint64_t* src, uint32_t tag, uint32_t (&out)[N], PollLimit poll) {
   uint64_t u[N];
   for (uint32_t spins = 0;; ++spins) {
-    bool ok = true;
+    bool ok = poll.never == 0;
 #pragma unroll
     for (int i = 0; i < N; ++i) {
       u[i] = ld_dev(src + i);
       ok &= static_cast<uint32_t>(u[i] >> 32) == tag;
     }
     if (ok) break;
-    if (spins >= limit) return false;
+    if (spins >= poll.limit) return false;
     __builtin_amdgcn_s_sleep(1);
   }
 #pragma unroll
@@ -258,12 +265,31 @@ __device__ __forceinline__ bool take(const uint64_t* src, uint32_t tag, uint32_t
   return true;
 }
 
-__device__ __forceinline__ bool take_f(const uint64_t* src, uint32_t tag, float* out, uint32_t limit) {
-  uint32_t v[1];
-  const bool ok = take<1>(src, tag, v, limit);
-  *out = __uint_as_float(v[0]);
-  return ok;
+// Polls the words p[i] with use[i] set, word i until it carries tag[i], all of them in flight
+// together each round (one round trip when they are all there), payloads into out; false when
+// the poll limit ran out first.
+template <int N>
+__device__ __forceinline__ bool take_words(const uint64_t* const (&p)[N], const bool (&use)[N],
+                                           const uint32_t (&tag)[N], uint32_t (&out)[N], PollLimit poll) {
+  uint64_t u[N];
+  for (uint32_t spins = 0;; ++spins) {
+    bool ok = poll.never == 0;
+#pragma unroll
+    for (int i = 0; i < N; ++i) {
+      if (use[i]) {
+        u[i] = ld_dev(p[i]);
+        ok &= static_cast<uint32_t>(u[i] >> 32) == tag[i];
+      }
+    }
+    if (ok) break;
+    if (spins >= poll.limit) return false;
+    __builtin_amdgcn_s_sleep(1);
+  }
+#pragma unroll
+  for (int i = 0; i < N; ++i) out[i] = use[i] ? static_cast<uint32_t>(u[i]) : 0u;
+  return true;
 }
+
 
 // RMSNorm'd and quantized activation blocks of x (d floats) into act, with rmsnorm_row_256's
 // reduction (one 8-float chunk per thread, d <= 2048). x is the launch's input (xt null) or the
@@ -284,19 +310,20 @@ __device__ __forceinline__ bool norm_quantize(const StepK& k, const float* gain,
   double ss = 0.0;
   bool ok = true;
   if (has) {
+    // The gains first: their loads are in flight during the poll instead of after it.
+    const float4 ga = gload4(gain + t * 8);
+    const float4 gb = gload4(gain + t * 8 + 4);
     if (xt == nullptr) {
       const float4 a = gload4(k.x + t * 8);
       const float4 b = gload4(k.x + t * 8 + 4);
       xv[0] = a.x; xv[1] = a.y; xv[2] = a.z; xv[3] = a.w; xv[4] = b.x; xv[5] = b.y; xv[6] = b.z; xv[7] = b.w;
     } else {
       uint32_t u[8];
-      ok = take<8>(xt + t * 8, tag, u, k.spin_limit);
+      ok = take<8>(xt + t * 8, tag, u, k.poll);
 #pragma unroll
       for (int i = 0; i < 8; ++i) xv[i] = __uint_as_float(u[i]);
     }
-    const float4 a = gload4(gain + t * 8);
-    const float4 b = gload4(gain + t * 8 + 4);
-    wv[0] = a.x; wv[1] = a.y; wv[2] = a.z; wv[3] = a.w; wv[4] = b.x; wv[5] = b.y; wv[6] = b.z; wv[7] = b.w;
+    wv[0] = ga.x; wv[1] = ga.y; wv[2] = ga.z; wv[3] = ga.w; wv[4] = gb.x; wv[5] = gb.y; wv[6] = gb.z; wv[7] = gb.w;
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
       const double v = static_cast<double>(xv[i]);
@@ -377,24 +404,27 @@ __device__ __forceinline__ void copier_main(const StepK& k, StepLds& sh, uint8_t
     }
     bar();
   };
-  // Issue order per layer l: q|k|v of l+1 after A, down of l after B (its region holds the
-  // attention's scores and value tiles during B), wo of l+1 after C, gate|up of l+1 after D.
+  // Issue order per layer l, each right after the barrier that starts a phase (the region's
+  // last reader finished before it), so the issue overlaps the compute waves' polls instead of
+  // holding up that barrier: q|k|v of l+1 at B, down of l at C (its region holds the attention's
+  // scores and value tiles during B), wo of l+1 at D, gate|up of l+1 at E. A phase's begin
+  // leaves in flight only the copies issued after its own region's.
   for (uint32_t l = 0; l < s.n_layer; ++l) {
     const bool more = l + 1 < s.n_layer;
     const StepLayer& N = layers[more ? l + 1 : l];
-    if (!begin(no + ng)) break;  // A
+    if (!begin(nd + no + ng)) break;  // A
     follow();
-    if (more) nq = region_copies(k, N, kQkv, w, lds_base, dw, lane, true);
     if (!begin(63)) break;  // B
+    nq = more ? region_copies(k, N, kQkv, w, lds_base, dw, lane, true) : 0;
     follow();
+    if (!begin(ng + nq)) break;  // C
     nd = region_copies(k, layers[l], kDown, w, lds_base, dw, lane, true);
-    if (!begin(ng + (more ? nq : 0) + nd)) break;  // C
     follow();
-    if (more) no = region_copies(k, N, kWo, w, lds_base, dw, lane, true);
-    if (!begin((more ? nq + no : 0) + nd)) break;  // D
+    if (!begin(nq + nd)) break;  // D
+    no = more ? region_copies(k, N, kWo, w, lds_base, dw, lane, true) : 0;
     follow();
-    if (more) ng = region_copies(k, N, kGu, w, lds_base, dw, lane, true);
-    if (!begin(more ? no + ng : 0)) break;  // E
+    if (!begin(no)) break;  // E
+    ng = more ? region_copies(k, N, kGu, w, lds_base, dw, lane, true) : 0;
     follow();
   }
   wait_vm<0>();  // no copy outlives the workgroup
@@ -525,6 +555,22 @@ __global__ __launch_bounds__(kStepThreads) void decode_step_kernel(StepK k) {
       }
       if (nr == 0) asm volatile("" ::"v"(touch));
       if (nr > 0) {
+        // This thread's output pair: its segment (q, k or v), bias and RoPE factors, loaded
+        // before the norm so they are not on the path after x arrives.
+        const uint32_t o = r0 + 2 * t;
+        const bool pair = t < nr / 2;
+        const int seg = o < s.dq ? 0 : o < s.dq + s.dkv ? 1 : 2;
+        const uint32_t oo = seg == 0 ? o : seg == 1 ? o - s.dq : o - s.dq - s.dkv;
+        const float* bias = seg == 0 ? L.bq : seg == 1 ? L.bk : L.bv;
+        float b0 = 0.0f, b1 = 0.0f;
+        if (pair && bias != nullptr) {
+          b0 = gload(bias + oo);
+          b1 = gload(bias + oo + 1);
+        }
+        const uint32_t ri = (oo % kHeadDim) / 2;
+        const bool rot = seg < 2 && ri < s.rot_half;
+        float2 rc = make_float2(1.0f, 0.0f);
+        if (pair && rot) rc = reinterpret_cast<const float2*>(k.rope_table)[static_cast<size_t>(k.pos) * s.rot_half + ri];
         ActBlock* act = reinterpret_cast<ActBlock*>(scratch);
         const uint32_t nb = s.d / kQK;
         float* tv = reinterpret_cast<float*>(scratch + nb * sizeof(ActBlock));
@@ -537,24 +583,16 @@ __global__ __launch_bounds__(kStepThreads) void decode_step_kernel(StepK k) {
         terms(s.t_qkv, k.lds_qkv, k.rb_d, nr, nb, act, tv, tp);
         if (t < nr) outv[t] = ordered_sum(tv + t * tp, nb);
         bar();
-        if (t < nr / 2) {
-          const uint32_t o = r0 + 2 * t;
-          const int seg = o < s.dq ? 0 : o < s.dq + s.dkv ? 1 : 2;
-          const uint32_t oo = seg == 0 ? o : seg == 1 ? o - s.dq : o - s.dq - s.dkv;
+        if (pair) {
           float x0 = outv[2 * t], x1 = outv[2 * t + 1];
-          const float* bias = seg == 0 ? L.bq : seg == 1 ? L.bk : L.bv;
           if (bias != nullptr) {
-            x0 = x0 + gload(bias + oo);
-            x1 = x1 + gload(bias + oo + 1);
+            x0 = x0 + b0;
+            x1 = x1 + b1;
           }
-          if (seg < 2) {
-            const uint32_t i = (oo % kHeadDim) / 2;
-            if (i < s.rot_half) {
-              const float2 cs = reinterpret_cast<const float2*>(k.rope_table)[static_cast<size_t>(k.pos) * s.rot_half + i];
-              const float a0 = x0, a1 = x1;
-              x0 = a0 * cs.x - a1 * cs.y;
-              x1 = a0 * cs.y + a1 * cs.x;
-            }
+          if (rot) {
+            const float a0 = x0, a1 = x1;
+            x0 = a0 * rc.x - a1 * rc.y;
+            x1 = a0 * rc.y + a1 * rc.x;
           }
           if (seg == 0) {
             put(k.qt + oo, tag_a, __float_as_uint(x0));
@@ -598,53 +636,88 @@ __global__ __launch_bounds__(kStepThreads) void decode_step_kernel(StepK k) {
       float* klast = qs + group * kHeadDim;                     // after this phase
       float* sc = klast + kHeadDim;
       float* vb = sc + ((s.max_ctx + 3) & ~3u);
-      if (p0 < p1) {
-        const float* kbase = k.cache + k.cache_off + L.k_layer_off + g * kHeadDim;
-        const uint16_t* kbase16 = reinterpret_cast<const uint16_t*>(k.cache) + k.cache_off + L.k_layer_off + g * kHeadDim;
-        const uint32_t pairs = (p1 - p0) * group;
-        float kr[kHeadDim];
-        auto krow = [&](uint32_t j) {
-          if constexpr (f16) {
-            const uint16_t* kb = kbase16 + static_cast<size_t>(j) * kv_row;
+      const float* kbase = k.cache + k.cache_off + L.k_layer_off + g * kHeadDim;
+      const uint16_t* kbase16 = reinterpret_cast<const uint16_t*>(k.cache) + k.cache_off + L.k_layer_off + g * kHeadDim;
+      // A K row's raw words (fp32: 16 float4; fp16: 8 x 8 halves) and q . k over them, the
+      // products added in dimension order, as the reference's dot.
+      auto kfetch = [&](uint32_t j, float4 (&f)[kHeadDim / 4], U4v (&hh)[kHeadDim / 8]) {
+        if constexpr (f16) {
+          const uint16_t* kb = kbase16 + static_cast<size_t>(j) * kv_row;
 #pragma unroll
-            for (uint32_t i = 0; i < kHeadDim / 8; ++i) {
-              const U4v h = gload_u4(kb + 8 * i);
+          for (uint32_t i = 0; i < kHeadDim / 8; ++i) hh[i] = gload_u4(kb + 8 * i);
+        } else {
 #pragma unroll
-              for (uint32_t c = 0; c < 4; ++c) {
-                kr[8 * i + 2 * c] = half_value(h[c] & 0xffffu);
-                kr[8 * i + 2 * c + 1] = half_value(h[c] >> 16);
-              }
-            }
-          } else {
+          for (uint32_t i = 0; i < kHeadDim / 4; ++i) f[i] = gload4(kbase + static_cast<size_t>(j) * kv_row + 4 * i);
+        }
+      };
+      auto kdot = [&](const float* qh, const float4 (&f)[kHeadDim / 4], const U4v (&hh)[kHeadDim / 8]) -> float {
+        float acc = 0.0f;
+        if constexpr (f16) {
 #pragma unroll
-            for (uint32_t i = 0; i < kHeadDim / 4; ++i) {
-              const float4 v = gload4(kbase + static_cast<size_t>(j) * kv_row + 4 * i);
-              kr[4 * i] = v.x;
-              kr[4 * i + 1] = v.y;
-              kr[4 * i + 2] = v.z;
-              kr[4 * i + 3] = v.w;
+          for (uint32_t i = 0; i < kHeadDim / 8; ++i) {
+#pragma unroll
+            for (uint32_t c = 0; c < 4; ++c) {
+              acc += qh[8 * i + 2 * c] * half_value(hh[i][c] & 0xffffu);
+              acc += qh[8 * i + 2 * c + 1] * half_value(hh[i][c] >> 16);
             }
           }
-        };
+        } else {
+#pragma unroll
+          for (uint32_t i = 0; i < kHeadDim / 4; ++i) {
+            acc += qh[4 * i] * f[i].x;
+            acc += qh[4 * i + 1] * f[i].y;
+            acc += qh[4 * i + 2] * f[i].z;
+            acc += qh[4 * i + 3] * f[i].w;
+          }
+        }
+        return acc;
+      };
+      auto kdot_last = [&](const float* qh) -> float {
+        float acc = 0.0f;
+#pragma unroll
+        for (uint32_t i = 0; i < kHeadDim; ++i) acc += qh[i] * klast[i];
+        return acc;
+      };
+      if (p0 < p1) {
+        const uint32_t pairs = (p1 - p0) * group;
+        // The group's q and (on the workgroup that scores the current position) its K row, in
+        // rounds of up to 4 q words and that K word per thread.
         bool ok = true;
-        for (uint32_t i = t; i < group * kHeadDim; i += kCompute)
-          ok &= take_f(k.qt + g * group * kHeadDim + i, tag_a, qs + i, k.spin_limit);
-        if (p1 == n_vis && t < kHeadDim) ok &= take_f(k.kvt + g * kHeadDim + t, tag_a, klast + t, k.spin_limit);
+        for (uint32_t i0 = 0; ok && i0 < group * kHeadDim; i0 += 4 * kCompute) {
+          const uint64_t* p[5];
+          bool use[5];
+          uint32_t tg[5], got[5];
+#pragma unroll
+          for (uint32_t u = 0; u < 4; ++u) {
+            const uint32_t i = i0 + t + u * kCompute;
+            use[u] = i < group * kHeadDim;
+            p[u] = k.qt + g * group * kHeadDim + (use[u] ? i : 0);
+            tg[u] = tag_a;
+          }
+          use[4] = i0 == 0 && p1 == n_vis && t < kHeadDim;
+          p[4] = k.kvt + g * kHeadDim + (t < kHeadDim ? t : 0);
+          tg[4] = tag_a;
+          ok = take_words<5>(p, use, tg, got, k.poll);
+#pragma unroll
+          for (uint32_t u = 0; u < 4; ++u)
+            if (use[u]) qs[i0 + t + u * kCompute] = __uint_as_float(got[u]);
+          if (use[4]) klast[t] = __uint_as_float(got[4]);
+        }
         if (!ok) give_up();
         bar();
         stamp(l, 1, 1);
+        float4 kf[kHeadDim / 4];
+        U4v kh[kHeadDim / 8];
         for (uint32_t e = t; e < pairs; e += kCompute) {
           const uint32_t j = p0 + e / group, hi = e % group;
-          if (j == last) {
-#pragma unroll
-            for (uint32_t i = 0; i < kHeadDim; ++i) kr[i] = klast[i];
-          } else {
-            krow(j);
-          }
           const float* qh = qs + hi * kHeadDim;
-          float acc = 0.0f;
-#pragma unroll
-          for (uint32_t i = 0; i < kHeadDim; ++i) acc += qh[i] * kr[i];
+          float acc;
+          if (j == last) {
+            acc = kdot_last(qh);
+          } else {
+            kfetch(j, kf, kh);
+            acc = kdot(qh, kf, kh);
+          }
           put(k.scores + static_cast<size_t>(g * group + hi) * s.max_ctx + j, tag_b, __float_as_uint(k.scale * acc));
         }
       } else {
@@ -679,12 +752,31 @@ __global__ __launch_bounds__(kStepThreads) void decode_step_kernel(StepK k) {
           }
         };
         vload(0);
-        // The head's scores, and this slice of the current position's V row.
-        const uint64_t* src = k.scores + static_cast<size_t>(h) * s.max_ctx;
         bool ok = true;
-        for (uint32_t j = t; j < n_vis; j += kCompute) ok &= take_f(src + j, tag_b, sc + j, k.spin_limit);
         float vlast = 0.0f;
-        if (t < k.dd) ok &= take_f(k.kvt + s.dkv + g * kHeadDim + dim0 + t, tag_a, &vlast, k.spin_limit);
+        // The head's scores, in rounds of up to 8 per thread (one round for up to 2048
+        // positions), the first with this slice's word of the current V row.
+        const uint64_t* src = k.scores + static_cast<size_t>(h) * s.max_ctx;
+        for (uint32_t j0 = 0; ok && j0 < n_vis; j0 += 8 * kCompute) {
+          const uint64_t* p[9];
+          bool use[9];
+          uint32_t tg[9], got[9];
+#pragma unroll
+          for (uint32_t u = 0; u < 8; ++u) {
+            const uint32_t j = j0 + t + u * kCompute;
+            use[u] = j < n_vis;
+            p[u] = src + (use[u] ? j : 0);
+            tg[u] = tag_b;
+          }
+          use[8] = j0 == 0 && t < k.dd;
+          p[8] = k.kvt + s.dkv + g * kHeadDim + dim0 + (t < k.dd ? t : 0);
+          tg[8] = tag_a;
+          ok = take_words<9>(p, use, tg, got, k.poll);
+#pragma unroll
+          for (uint32_t u = 0; u < 8; ++u)
+            if (use[u]) sc[j0 + t + u * kCompute] = __uint_as_float(got[u]);
+          if (use[8]) vlast = __uint_as_float(got[8]);
+        }
         if (!ok) give_up();
         bar();
         stamp(l, 1, 2);
@@ -781,7 +873,7 @@ __global__ __launch_bounds__(kStepThreads) void decode_step_kernel(StepK k) {
       float* outv = tv + k.r_o * tp + 64;
       if (t * 8 < s.dq) {  // the heads' outputs as Q8_0 blocks, 8 values per thread
         uint32_t u[8];
-        if (!take<8>(k.attnt + t * 8, tag_b, u, k.spin_limit)) give_up();
+        if (!take<8>(k.attnt + t * 8, tag_b, u, k.poll)) give_up();
         float v[8];
 #pragma unroll
         for (int i = 0; i < 8; ++i) v[i] = __uint_as_float(u[i]);
@@ -841,7 +933,7 @@ __global__ __launch_bounds__(kStepThreads) void decode_step_kernel(StepK k) {
       float* outv = tv + k.r_d * tp + 64;
       if (t < nb) {
         uint32_t u[10];
-        if (!take<10>(k.ht + static_cast<size_t>(t) * 10, tag_d, u, k.spin_limit)) give_up();
+        if (!take<10>(k.ht + static_cast<size_t>(t) * 10, tag_d, u, k.poll)) give_up();
         ActBlock& a = act[t];
 #pragma unroll
         for (int i = 0; i < 8; ++i) a.qs[i] = static_cast<int32_t>(u[i]);
@@ -1060,7 +1152,7 @@ int step_launch(const StepShape& s, const StepCall& c) {
   k.scores = reinterpret_cast<uint64_t*>(work + wl.scores);
   k.epoch = c.epoch;
   k.status = c.status;
-  k.spin_limit = c.spin_limit;
+  k.poll = PollLimit{c.spin_limit, c.fail_waits};
   k.stamps = c.stamps;
   void* args[] = {&k};
   const void* kernel = s.cache_f16 ? reinterpret_cast<const void*>(decode_step_kernel<true>)

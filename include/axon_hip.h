@@ -375,6 +375,11 @@ typedef struct {
  * second). A small limit forces the give-up path from the host: the kernel still drains, the
  * call's status word is set, and the caller's recovery runs. */
 int axon_hip_decode_layers_set_spin_limit(uint32_t polls);
+/* Test hook, no counterpart in the reference: with on nonzero, no wait of later
+ * axon_hip_decode_layers calls sees its word as written, so every workgroup gives up after the
+ * spin limit's polls whatever the timing (with a small limit, at once): the give-up path runs
+ * deterministically. 0 restores normal waits. */
+int axon_hip_decode_layers_set_fail_waits(int on);
 /* Measurement hook, no counterpart in the reference: with a device buffer of
  * axon_hip_decode_layers_stamp_count(shape, &ticks_per_second) uint64 words, every later
  * axon_hip_decode_layers call records the device's constant-rate clock (s_memrealtime) at four points of every phase of every layer in every

@@ -294,6 +294,33 @@ def test_persistent_decode_equals_launch_by_launch(cfg, cache):
     b.close()
 
 
+@pytest.mark.parametrize("cfg, cache", [("c3", "f32"), ("c4", "f32"), ("c4", "f16")])
+def test_persistent_decode_at_long_context(cfg, cache):
+    """The step kernel past a thousand positions: the scores of each head from 32 workgroups of
+    its group, four or more V chunks per mixing workgroup, the score polls in rounds of 2048
+    positions. 32 greedy steps from position 1008 (a 1008-token prompt): logits and cache rows
+    bit-identical to the per-layer launches."""
+    path = model_path(cfg)
+    a = hip(path, max_seq=1024, max_ctx=1056, cache=cache)
+    b = hip(path, max_seq=1024, max_ctx=1056, persistent=False, cache=cache)
+    assert a.info.persistent_decode == 1 and b.info.persistent_decode == 0
+    prompt = np.random.default_rng(78).integers(0, a.n_vocab, 1008).astype(np.int32)
+    ca, cb = a.new_cache(), b.new_cache()
+    a.forward_mixed(ca, prompt, [], [], logits=False)  # logits of the prompt's last row only
+    b.forward_mixed(cb, prompt, [], [], logits=False)
+    t = int(a.greedy(1)[0])
+    assert int(b.greedy(1)[0]) == t
+    for s in range(32):
+        la, lb = a.forward_prefill(ca, [t])[0], b.forward_prefill(cb, [t])[0]
+        assert np.array_equal(la, lb), f"{cfg} position {1008 + s}: max diff {np.max(np.abs(la - lb))}"
+        t = int(np.argmax(la))
+    for layer in (0, a.info.n_layer - 1):
+        for v in (False, True):
+            assert np.array_equal(a.cache_rows(ca, layer, v, 1040), b.cache_rows(cb, layer, v, 1040))
+    a.close()
+    b.close()
+
+
 @pytest.mark.parametrize("cfg", ["c1", "c4"])
 def test_generate_greedy_equals_host_loop(cfg):
     """axon_model_generate_greedy (each step's id kept on the device for the next step's
@@ -330,8 +357,8 @@ def test_generate_greedy_equals_host_loop(cfg):
 
 def test_persistent_decode_gives_up_cleanly_and_recovers(tmp_path_factory):
     """The step kernel's bounded waits, forced from the host: with a limit of one poll per
-    tagged word the workgroups of a one-row pass give up instead of waiting, the kernel still
-    drains, and the pass is void. With the logits copied the pass fails at once and its cache
+    tagged word and waits that never see their word written, the workgroups of a one-row pass
+    give up instead of waiting, the kernel still drains, and the pass is void. With the logits copied the pass fails at once and its cache
     position does not advance; with the logits left in HBM the pass returns, and the next
     synchronization (the greedy choice) fails, names the cache slot and position, and rolls the
     cache back to it. Either way the model turns the persistent kernel off for later one-row
@@ -355,9 +382,11 @@ def test_persistent_decode_gives_up_cleanly_and_recovers(tmp_path_factory):
     # Logits copied to the host: the pass itself reports the give-up.
     try:
         assert lib.axon_hip_decode_layers_set_spin_limit(1) == 0
+        assert lib.axon_hip_decode_layers_set_fail_waits(1) == 0
         with pytest.raises(H.HipError, match="gave up"):
             a.forward_prefill(ca, [t])
     finally:
+        lib.axon_hip_decode_layers_set_fail_waits(0)
         lib.axon_hip_decode_layers_set_spin_limit(0)
     assert a.cache_pos(ca) == n0
     assert not a.persistent_decode()
@@ -367,8 +396,10 @@ def test_persistent_decode_gives_up_cleanly_and_recovers(tmp_path_factory):
     # synchronization finds the give-up and rolls the cache back.
     try:
         assert lib.axon_hip_decode_layers_set_spin_limit(1) == 0
+        assert lib.axon_hip_decode_layers_set_fail_waits(1) == 0
         a.forward_prefill(ca, [t], logits=False)
     finally:
+        lib.axon_hip_decode_layers_set_fail_waits(0)
         lib.axon_hip_decode_layers_set_spin_limit(0)
     assert a.cache_pos(ca) == n0 + 1
     with pytest.raises(H.HipError, match=f"gave up.*position {n0} of the cache in slot {ca}"):
