@@ -50,7 +50,8 @@ struct StepCall {
 constexpr uint32_t kStepTimedOut = 1;
 
 size_t step_workspace_bytes(const StepShape& s);
-// Words of a stamp buffer: 4 points x 5 phases x n_layer x one workgroup per CU.
+// Words of a stamp buffer: 4 points x 5 phases x n_layer x one slot per CU (the grid may be
+// smaller: 128 workgroups for a shape that fits them).
 size_t step_stamp_count(const StepShape& s);
 // 0 when this GPU runs the shape as one persistent kernel, else the reason (a static string).
 const char* step_unsupported(const StepShape& s);

@@ -73,6 +73,7 @@ struct StepK {
   uint32_t* status;
   PollLimit poll;
   uint64_t* stamps;                         // per-phase clock stamps, or null
+  uint32_t stamp_stride;                    // workgroup slots per stamp point (one per CU)
   uint32_t r_qkv, r_o, r_d;                 // weight rows per workgroup
   uint32_t rb_d, rb_q, rb_ff;               // bytes per row of the d-, dq- and ff-wide matrices
   uint32_t rb_o, rb_down;
@@ -504,7 +505,7 @@ __global__ __launch_bounds__(kStepThreads) void decode_step_kernel(StepK k) {
   // Measurement: the device clock at point pt of phase ph of layer l (stamp buffer words
   // ((l * 5 + ph) * 4 + pt) * workgroups + w); stamp_in first waits for every compute thread.
   auto slot_of = [&](uint32_t l, uint32_t ph, uint32_t pt) -> uint64_t* {
-    return k.stamps == nullptr ? nullptr : k.stamps + (static_cast<size_t>(l * 5 + ph) * 4 + pt) * gridDim.x + w;
+    return k.stamps == nullptr ? nullptr : k.stamps + (static_cast<size_t>(l * 5 + ph) * 4 + pt) * k.stamp_stride + w;
   };
   auto stamp = [&](uint32_t l, uint32_t ph, uint32_t pt) {
     if (k.stamps != nullptr && tid == 0) *slot_of(l, ph, pt) = __builtin_amdgcn_s_memrealtime();
@@ -1077,6 +1078,37 @@ WorkLayout work_layout(const StepShape& s) {
   w.total = w.scores + words(static_cast<size_t>(s.n_head) * s.max_ctx);
   return w;
 }
+// Why a grid of `wgs` workgroups cannot run the shape, or null.
+const char* grid_unsupported(const StepShape& s, uint32_t wgs, size_t lds_max) {
+  if (s.n_head > wgs || ceil_div(s.ff, kGuRows) > wgs) return "more heads or SiLU blocks than CUs";
+  StepK k{};
+  k.s = s;
+  size_t lds = 0;
+  const char* why = nullptr;
+  if (!step_geometry(s, wgs, k, &lds, &why)) return why;
+  if (lds > lds_max) return "the layer's weight slices and scratch exceed LDS";
+  // Every copying wave keeps at most 63 copies in flight: one layer's four regions.
+  for (uint32_t dw = 0; dw < 4; ++dw) {
+    auto wide = [](uint32_t rb, uint32_t rows) { return (rb * rows) % 16 == 0 && rb % 16 == 0; };
+    const uint32_t n = copies_host(k.r_qkv * k.rb_d, wide(k.rb_d, k.r_qkv), dw) * 3 +
+                       copies_host(k.r_o * k.rb_o, wide(k.rb_o, k.r_o), dw) +
+                       2 * copies_host(kGuRows * k.rb_d, wide(k.rb_d, kGuRows), dw) +
+                       copies_host(k.r_d * k.rb_down, wide(k.rb_down, k.r_d), dw);
+    if (n > 63) return "a layer's weight slices need more copies in flight than a wave can count";
+  }
+  return nullptr;
+}
+
+// Workgroups of the step grid: kSmallGrid when the shape runs on that many, else one per CU.
+// Each phase's hand-off is an all-to-all of tagged words whose cost grows with the workgroups
+// that write them (one round of 256 writers and readers takes about 2.6 us on MI355X, of 128
+// about 1.7 us), so a model small enough to run on half the CUs does (C1, SmolLM2-135M: 1382
+// against 1272 tokens/s); larger ones need every CU's LDS for their weight slices.
+constexpr uint32_t kSmallGrid = 128;
+uint32_t step_grid(const StepShape& s, uint32_t cus, size_t lds_max) {
+  return cus > kSmallGrid && grid_unsupported(s, kSmallGrid, lds_max) == nullptr ? kSmallGrid : cus;
+}
+
 }  // namespace
 
 size_t step_workspace_bytes(const StepShape& s) { return work_layout(s).total; }
@@ -1102,23 +1134,7 @@ const char* step_unsupported(const StepShape& s) {
   uint32_t cus = 0;
   size_t lds_max = 0;
   if (step_device(&cus, &lds_max) != kOk) return "the device does not grant the kernel's LDS";
-  if (s.n_head > cus || ceil_div(s.ff, kGuRows) > cus) return "more heads or SiLU blocks than CUs";
-  StepK k{};
-  k.s = s;
-  size_t lds = 0;
-  const char* why = nullptr;
-  if (!step_geometry(s, cus, k, &lds, &why)) return why;
-  if (lds > lds_max) return "the layer's weight slices and scratch exceed LDS";
-  // Every copying wave keeps at most 63 copies in flight: one layer's four regions.
-  for (uint32_t dw = 0; dw < 4; ++dw) {
-    auto wide = [](uint32_t rb, uint32_t rows) { return (rb * rows) % 16 == 0 && rb % 16 == 0; };
-    const uint32_t n = copies_host(k.r_qkv * k.rb_d, wide(k.rb_d, k.r_qkv), dw) * 3 +
-                       copies_host(k.r_o * k.rb_o, wide(k.rb_o, k.r_o), dw) +
-                       2 * copies_host(kGuRows * k.rb_d, wide(k.rb_d, kGuRows), dw) +
-                       copies_host(k.r_d * k.rb_down, wide(k.rb_down, k.r_d), dw);
-    if (n > 63) return "a layer's weight slices need more copies in flight than a wave can count";
-  }
-  return nullptr;
+  return grid_unsupported(s, cus, lds_max);
 }
 
 int step_launch(const StepShape& s, const StepCall& c) {
@@ -1130,10 +1146,11 @@ int step_launch(const StepShape& s, const StepCall& c) {
     return fail(kInvalidArgument, "decode step: position %d outside [0, %u)", c.pos, s.max_ctx);
   const char* why = step_unsupported(s);
   if (why != nullptr) return fail(kUnsupported, "decode step: %s", why);
+  const uint32_t wgs = step_grid(s, cus, lds_max);
   StepK k{};
   k.s = s;
   size_t lds = 0;
-  if (!step_geometry(s, cus, k, &lds, &why)) return fail(kUnsupported, "decode step: %s", why);
+  if (!step_geometry(s, wgs, k, &lds, &why)) return fail(kUnsupported, "decode step: %s", why);
   k.layers = c.layers;
   k.eps = c.eps;
   k.scale = c.scale;
@@ -1154,6 +1171,7 @@ int step_launch(const StepShape& s, const StepCall& c) {
   k.status = c.status;
   k.poll = PollLimit{c.spin_limit, c.fail_waits};
   k.stamps = c.stamps;
+  k.stamp_stride = cus;
   void* args[] = {&k};
   const void* kernel = s.cache_f16 ? reinterpret_cast<const void*>(decode_step_kernel<true>)
                                    : reinterpret_cast<const void*>(decode_step_kernel<false>);
@@ -1169,7 +1187,7 @@ int step_launch(const StepShape& s, const StepCall& c) {
   // the call give up (status word), not hang. The cooperative launch API, which checks
   // residency at the launch, cost about 15 us per launch on this runtime and profilers lose
   // their results for processes that use it, so it is not used.
-  const hipError_t e = hipLaunchKernel(kernel, dim3(cus), dim3(kStepThreads), args, static_cast<unsigned>(lds), stream());
+  const hipError_t e = hipLaunchKernel(kernel, dim3(wgs), dim3(kStepThreads), args, static_cast<unsigned>(lds), stream());
   if (e != hipSuccess) return fail(kHipError, "decode step: launch: %s", hipGetErrorString(e));
   if (stop != nullptr && hipEventRecord(stop, stream()) != hipSuccess)
     return fail(kHipError, "decode step: probe stop event");

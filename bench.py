@@ -218,9 +218,12 @@ def phase_probe(H, model, n_vocab, steps, prompt_len, seed):
     L.axon_hip_decode_layers_set_stamps(C.c_void_p(H.ptr_of(buf)))
     try:
         for _ in range(steps):
+            buf.fill(0)
             model.forward_prefill(cache, [tok], logits=False)
             tok = int(model.greedy(1)[0])
-            t = buf.download(np.uint64).reshape(info.n_layer, 5, 4, wgs).astype(np.float64) * (1e6 / tps.value)
+            t = buf.download(np.uint64).reshape(info.n_layer, 5, 4, wgs)
+            t = t[..., (t != 0).any(axis=(0, 1, 2))]  # the grid's workgroups (a small model's is smaller)
+            t = t.astype(np.float64) * (1e6 / tps.value)
             t -= t[0, 0, 0].min()
             wait.append((t[:, :, 1] - t[:, :, 0]).max(axis=2))
             mid.append((t[:, :, 2] - t[:, :, 1]).max(axis=2))
@@ -234,7 +237,7 @@ def phase_probe(H, model, n_vocab, steps, prompt_len, seed):
     mean = lambda a: np.mean(np.stack(a), axis=(0, 1))  # over steps and layers
     w, m, tl, sp = mean(wait), mean(mid), mean(tail), mean(span)
     return {"kernel": STEP_KERNEL_NAME, "steps": steps, "context": [prompt_len + 8 + steps, prompt_len + 8 + 2 * steps],
-            "workgroups": wgs, "clock_hz": tps.value, "us_per_step_stamped": round(float(np.mean(total)), 2),
+            "workgroups": int(t.shape[-1]), "clock_hz": tps.value, "us_per_step_stamped": round(float(np.mean(total)), 2),
             "ms_per_step_plain": round(plain_ms, 4), "us_per_layer_stamped": round(float(np.mean(total)) / info.n_layer, 2),
             "phases": [{"phase": PHASES[p], "span_us": round(float(sp[p]), 3), "wait_us": round(float(w[p]), 3),
                         "mid_us": round(float(m[p]), 3), "tail_us": round(float(tl[p]), 3)} for p in range(5)]}

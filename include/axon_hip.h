@@ -383,11 +383,13 @@ int axon_hip_decode_layers_set_fail_waits(int on);
 /* Measurement hook, no counterpart in the reference: with a device buffer of
  * axon_hip_decode_layers_stamp_count(shape, &ticks_per_second) uint64 words, every later
  * axon_hip_decode_layers call records the device's constant-rate clock (s_memrealtime) at four points of every phase of every layer in every
- * workgroup, each call overwriting the last: word ((layer * 5 + phase) * 4 + point) * workgroups +
+ * workgroup, each call overwriting the last: word ((layer * 5 + phase) * 4 + point) * CUs +
  * workgroup, phases A (norm, q|k|v, RoPE, cache row), B (attention), C (wo), D (norm, gate|up,
  * SiLU), E (down); points: the phase's start, its first inputs in (every thread's polls done),
- * its second inputs in (B: the scores; else the same as the first), its end. NULL turns it off.
- * The instrumented launch adds one workgroup barrier per poll. */
+ * its second inputs in (B: the scores; else the same as the first), its end. A shape small
+ * enough to run on 128 workgroups runs on 128 (then the words of workgroups 128 and up keep
+ * what they held). NULL turns it off. The instrumented launch adds one workgroup barrier per
+ * poll. */
 int axon_hip_decode_layers_set_stamps(uint64_t* stamps);
 size_t axon_hip_decode_layers_stamp_count(const axon_hip_decode_shape* shape, double* ticks_per_second);
 size_t axon_hip_decode_layers_workspace_bytes(const axon_hip_decode_shape* shape);
