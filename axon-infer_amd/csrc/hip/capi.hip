@@ -596,6 +596,12 @@ int axon_hip_matmul_q6_k_planar(const void* planar, const float* x, float* y, si
   return matvec_q6k_planar_launch(a, static_cast<uint32_t>(n_in));
 }
 
+int axon_hip_q6k_force_path(int path) {
+  if (path < 0 || path > 3) return fail(kInvalidArgument, "q6k_force_path: path %d (0-3)", path);
+  matvec_q6k_force_path(path);
+  return kOk;
+}
+
 int axon_hip_rmsnorm_rows(const float* x, const float* weight, float* y, void* yq, size_t n, size_t n_rows,
                           float eps) {
   AXON_READY();

@@ -73,6 +73,9 @@ int matvec_q6k_launch(MatvecArgs& a, uint32_t n_in);
 size_t q6k_planar_column_bytes(uint32_t n_out);
 int q6k_repack_launch(const uint8_t* src, uint8_t* dst, uint32_t n_out, uint32_t nsb);
 int matvec_q6k_planar_launch(MatvecArgs& a, uint32_t n_in);
+// Test hook: 0 chooses the one-row kernel by shape; 1 the one-lane-per-row kernel, 2 the
+// products-then-chains kernel (where its LDS fits), 3 the streamed-ring kernel.
+void matvec_q6k_force_path(int path);
 // int8 MFMA tiles for 16 or more Q8_0 activation rows.
 int matmul_q8_mfma_launch(int type, MatvecArgs& a);
 // int8 MFMA for 1..kRowsMaxM activation rows (batched decode): every segment in one grid, one

@@ -19,6 +19,7 @@
 //    LDS broadcasts.
 //  * matvec_q6k_kernel (any 2-byte-aligned rows): each lane fetches its own super-blocks with
 //    per-lane loads, double-buffered in registers.
+#include <atomic>
 #include "common.h"
 #include "matvec.h"
 
@@ -27,6 +28,7 @@ namespace axon_hip {
 namespace {
 
 constexpr uint32_t kQ6MaxRows = 8;  // activation rows per workgroup of the planar kernel
+constexpr uint32_t kChainMaxOut = 2048;  // one activation row up to this many outputs: the chain kernel
 
 constexpr int kThreads = 256;  // rows per workgroup
 constexpr int kWin = 53;       // dwords covering one super-block plus its 2-byte misalignment
@@ -415,6 +417,327 @@ __global__ __launch_bounds__(TH) void q6k_planar_kernel(MatvecArgs args, uint32_
     if (m < static_cast<int>(mm)) seg.y[static_cast<size_t>(m0 + m) * seg.y_stride + row] = acc[m];
 }
 
+// One activation row against a short matrix: R output rows per workgroup, the products apart
+// from the sums. The threads take units of (super-block, quarter, row) and write the quarter's
+// 64 products v * x in element order into LDS ([super-block][row][256 + 4 pad] floats); then lane
+// r of the first wave adds row r's products in order, four per 16-byte read. The floats are those
+// of q6k_planar_kernel (each product rounded, then added in element order); the chain no longer
+// waits for the decoding and the multiplies, which with one lane per row set its pace, and a short
+// matrix spreads over R-row workgroups instead of 64-row ones.
+constexpr uint32_t kChainPitch = kQKK + 4;  // floats per (super-block, row) of products
+
+// Quarter Qr of a super-block is its elements 64 Qr .. 64 Qr + 63 (planar_superblock's steps
+// 16 Qr .. 16 Qr + 15). It reads 6 of the 13 slices of its row (the low bits of its half, 4;
+// the high bits, 2), word Qr of the scales slice, and d; the rest stays zero.
+template <int Qr>
+__device__ __forceinline__ void quarter_fetch(const uint8_t* col, uint32_t n_out, uint32_t row, PlanarBlock& b) {
+  constexpr int n = Qr / 2;
+  b.d = reinterpret_cast<const uint16_t*>(col + static_cast<size_t>(208) * n_out)[row];
+#pragma unroll
+  for (int s = 0; s < 12; ++s) {
+    if ((s >= 4 * n && s < 4 * n + 4) || s == 8 + 2 * n || s == 9 + 2 * n)
+      b.q[s] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(col + static_cast<size_t>(s) * 16 * n_out) + row);
+    else
+      b.q[s] = u32x4{0, 0, 0, 0};
+  }
+  // Of the scales the quarter reads one word, its four 16-element scales (a wider load would
+  // leave registers that the compiler reuses while the load is still landing).
+  b.q[12] = u32x4{0, 0, 0, 0};
+  b.q[12][Qr] = __builtin_nontemporal_load(reinterpret_cast<const uint32_t*>(col + static_cast<size_t>(12) * 16 * n_out) +
+                                           4 * static_cast<size_t>(row) + Qr);
+}
+
+// Products v * x of the quarter's steps S0 .. S0 + NS - 1 (4 elements each), v = (d*scale)*(q-32)
+// as planar_superblock forms it; xs holds those steps' activations, pv receives the products.
+template <int Qr, int S0 = 0, int NS = 16>
+__device__ __forceinline__ void quarter_products(const PlanarBlock& b, const float4* xs, float4* pv) {
+  auto dw = [&](int o) { return b.q[o / 16][(o / 4) & 3]; };
+  const float d = half_value(b.d);
+#pragma unroll
+  for (int st = 16 * Qr + S0; st < 16 * Qr + S0 + NS; ++st) {
+    const int n = st / 32, qi = (st / 8) % 4, half = (st / 4) % 2, l4 = st % 4;
+    const int si = n * 8 + qi * 2 + half;
+    const float scale = static_cast<float>(static_cast<int8_t>((dw(192 + 4 * (si >> 2)) >> (8 * (si & 3))) & 0xffu));
+    const float ds = d * scale;
+    const float neg32 = -32.0f * ds;
+    const int l = 16 * half + 4 * l4;
+    const uint32_t lw = dw(64 * n + 32 * (qi & 1) + l);
+    const uint32_t hw = dw(128 + 32 * n + l);
+    const uint32_t q = ((lw >> (4 * (qi >> 1))) & 0x0f0f0f0fu) | (((hw >> (2 * qi)) & 0x03030303u) << 4);
+    const float4 xv = xs[st - 16 * Qr - S0];
+    float4& o = pv[st - 16 * Qr - S0];
+    o.x = fmaf(ds, static_cast<float>(q & 0xffu), neg32) * xv.x;
+    o.y = fmaf(ds, static_cast<float>((q >> 8) & 0xffu), neg32) * xv.y;
+    o.z = fmaf(ds, static_cast<float>((q >> 16) & 0xffu), neg32) * xv.z;
+    o.w = fmaf(ds, static_cast<float>(q >> 24), neg32) * xv.w;
+  }
+}
+
+// One unit of the chain kernel: the quarter's products of one row into dst[16 Qr ..].
+template <int Qr>
+__device__ __forceinline__ void chain_quarter(const uint8_t* col, uint32_t n_out, uint32_t row, const float4* xc,
+                                              float4* dst) {
+  PlanarBlock b;
+  quarter_fetch<Qr>(col, n_out, row, b);
+  // Every activation load is issued before the first step (the scheduling barrier keeps the
+  // compiler from sinking them between the steps, where each would wait out its own latency).
+  float4 xs[16];
+#pragma unroll
+  for (int i = 0; i < 16; ++i) xs[i] = xc[16 * Qr + i];
+  __builtin_amdgcn_sched_barrier(0);
+  float4 pv[16];
+  quarter_products<Qr>(b, xs, pv);
+#pragma unroll
+  for (int i = 0; i < 16; ++i) dst[16 * Qr + i] = pv[i];
+}
+
+template <int R>
+__global__ __launch_bounds__(256) void q6k_planar_chain_kernel(MatvecArgs args, uint32_t n_in, size_t col_bytes) {
+  extern __shared__ __attribute__((aligned(16))) float prods[];
+  const uint32_t nsb = args.nb;
+  const MatvecSeg seg = args.seg[0];
+  const uint32_t r0 = blockIdx.x * R;
+  const float* x = reinterpret_cast<const float*>(args.xq);
+  // Wave w takes quarter w of every unit (the quarter's code is chosen per wave, not per lane);
+  // its lanes take (super-block, row) pairs cr = c * R + r, 64 at a time.
+  const uint32_t qr = threadIdx.x / 64;
+  for (uint32_t cr = threadIdx.x % 64; cr < R * nsb; cr += 64) {
+    const uint32_t r = cr % R, c = cr / R;
+    const uint32_t row = min(r0 + r, seg.n_out - 1);  // rows past n_out repeat the last (not stored)
+    const uint8_t* col = seg.w + static_cast<size_t>(c) * col_bytes;
+    const float4* xc = reinterpret_cast<const float4*>(x + static_cast<size_t>(c) * kQKK);
+    float4* dst = reinterpret_cast<float4*>(prods + static_cast<size_t>(c * R + r) * kChainPitch);
+    switch (qr) {
+      case 0: chain_quarter<0>(col, seg.n_out, row, xc, dst); break;
+      case 1: chain_quarter<1>(col, seg.n_out, row, xc, dst); break;
+      case 2: chain_quarter<2>(col, seg.n_out, row, xc, dst); break;
+      default: chain_quarter<3>(col, seg.n_out, row, xc, dst); break;
+    }
+  }
+  __syncthreads();
+  const uint32_t r = threadIdx.x;
+  if (r < R && r0 + r < seg.n_out) {
+    // A super-block's 256 products in 8 rounds of 32: the next round's 8 reads are issued
+    // before this round's 32 adds (a scheduling barrier keeps them there), so the adds wait for
+    // LDS only at the first round of each super-block; 16 reads in flight at most, which the LDS
+    // wait counter can still tell apart. (Carrying reads over to the next super-block would
+    // make the loop copy its registers, and the copy waits for the reads.)
+    auto add8 = [](float acc, const float4 (&v)[8]) {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        acc += v[i].x;
+        acc += v[i].y;
+        acc += v[i].z;
+        acc += v[i].w;
+      }
+      return acc;
+    };
+    float acc = 0.0f;
+    for (uint32_t c = 0; c < nsb; ++c) {
+      const float4* src = reinterpret_cast<const float4*>(prods + static_cast<size_t>(c * R + r) * kChainPitch);
+      float4 v[2][8];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) v[0][i] = src[i];
+#pragma unroll
+      for (int t = 0; t < 8; ++t) {
+        if (t + 1 < 8) {
+#pragma unroll
+          for (int i = 0; i < 8; ++i) v[(t + 1) & 1][i] = src[8 * (t + 1) + i];
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        acc = add8(acc, v[t & 1]);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    }
+    seg.y[r0 + r] = acc;
+  }
+}
+
+// One activation row against any number of output rows: 64 rows per workgroup, the products
+// streamed to the chains through LDS. Wave 0 runs the chains (lane r adds row r's products in
+// element order); waves 1-4 each form one quarter of every super-block for all 64 rows and
+// hand it over in slot h = quarter / 2 (the super-block's half h: [row][128 + 4 pad] floats).
+// A slot holds one half at a time: its producers form the next super-block's products in
+// registers while the chain reads the slot, and write them once the chain has released it.
+// The counters in LDS only grow: ready[h] counts the quarters written (two per super-block),
+// freed[h] the halves the chain has read. Neither side waits on anything the other side
+// delivers later, so the waits end; their poll bound only guarantees that every wave exits.
+constexpr uint32_t kRingRows = 64;
+constexpr uint32_t kRingPitch = kQKK / 2 + 4;  // floats per row of a half-super-block slot
+constexpr size_t kRingLds = 2 * kRingRows * kRingPitch * 4;
+constexpr uint32_t kRingPoll = 1u << 22;  // s_sleep rounds per wait (~0.1 s), then go on
+
+__device__ __forceinline__ void ring_wait(const uint32_t* counter, uint32_t target) {
+  for (uint32_t i = 0; i < kRingPoll; ++i) {
+    if (__hip_atomic_load(counter, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) >= target) break;
+    __builtin_amdgcn_s_sleep(1);
+  }
+  asm volatile("" ::: "memory");
+}
+
+// Counts one hand-over once this wave's LDS accesses have completed (reads in registers,
+// writes in LDS).
+__device__ __forceinline__ void ring_signal(uint32_t* counter, uint32_t lane) {
+  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+  if (lane == 0) __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+}
+
+template <int Qr>
+__device__ __forceinline__ void ring_producer(const MatvecSeg& seg, cfloat* x, uint32_t nsb, size_t col_bytes,
+                                              uint32_t row, uint32_t lane, float* ring, uint32_t* ready,
+                                              const uint32_t* freed) {
+  constexpr int h = Qr / 2;
+  float4* dst = reinterpret_cast<float4*>(ring + static_cast<size_t>(h * kRingRows + lane) * kRingPitch) + 16 * (Qr % 2);
+  // Weights three super-blocks ahead: the loads of super-blocks c + 1 .. c + 3 are in flight
+  // while c's products are formed and handed over (one super-block ahead leaves every step
+  // waiting out a whole HBM latency). Three register sets, the loop unrolled by three so that
+  // each keeps its registers. The activations (the same for every lane) come through the
+  // scalar cache as operands.
+  PlanarBlock b0, b1, b2;
+  // Past the last super-block the last is loaded again (unconditional loads keep the
+  // compiler's count of loads in flight exact, so each step waits only for its own).
+  auto fetch = [&](PlanarBlock& b, uint32_t c) {
+    quarter_fetch<Qr>(seg.w + static_cast<size_t>(min(c, nsb - 1)) * col_bytes, seg.n_out, row, b);
+  };
+  // Super-block c: the first 32 products are formed before the wait for the slot and the
+  // other 32 after it (while the chain reads the other half), so 32 registers hold products.
+  // Steps past the last super-block (the loop is unrolled by three) form products of the last
+  // one again but hand nothing over: only LDS work is conditional, so the compiler's count of
+  // loads in flight stays exact across the steps.
+  auto step = [&](PlanarBlock& b, uint32_t c) {
+    const bool live = c < nsb;
+    cfloat* xc = x + static_cast<size_t>(min(c, nsb - 1)) * kQKK + 64 * Qr;
+    float4 xs[8], pv[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) xs[i] = float4{xc[4 * i], xc[4 * i + 1], xc[4 * i + 2], xc[4 * i + 3]};
+    quarter_products<Qr, 0, 8>(b, xs, pv);
+    // Formed here, before the wait (the compiler would otherwise sink them to their stores).
+#pragma unroll
+    for (int i = 0; i < 8; ++i) asm volatile("" : "+v"(pv[i].x), "+v"(pv[i].y), "+v"(pv[i].z), "+v"(pv[i].w));
+    if (live) {
+      if (c > 0) ring_wait(&freed[h], c);  // the chain has read this half of super-block c - 1
+#pragma unroll
+      for (int i = 0; i < 8; ++i) dst[i] = pv[i];
+    }
+#pragma unroll
+    for (int i = 0; i < 8; ++i) xs[i] = float4{xc[32 + 4 * i], xc[33 + 4 * i], xc[34 + 4 * i], xc[35 + 4 * i]};
+    quarter_products<Qr, 8, 8>(b, xs, pv);
+    if (live) {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) dst[8 + i] = pv[i];
+      ring_signal(&ready[h], lane);
+    }
+    fetch(b, c + 3);
+  };
+  fetch(b0, 0);
+  fetch(b1, 1);
+  fetch(b2, 2);
+  for (uint32_t c = 0; c < nsb; c += 3) {
+    step(b0, c);
+    step(b1, c + 1);
+    step(b2, c + 2);
+  }
+}
+
+// Three waves per SIMD (two workgroups per CU) leave each lane up to 168 registers, which the
+// three prefetched weight sets need.
+__global__ __launch_bounds__(320) __attribute__((amdgpu_waves_per_eu(3))) void q6k_planar_ring_kernel(
+    MatvecArgs args, uint32_t n_in, size_t col_bytes) {
+  extern __shared__ __attribute__((aligned(16))) float ring[];
+  __shared__ uint32_t ready[2], freed[2];
+  const uint32_t tid = threadIdx.x, lane = tid % 64;
+  const uint32_t wave = __builtin_amdgcn_readfirstlane(tid / 64);  // uniform: branches per wave
+  if (tid < 2) {
+    ready[tid] = 0;
+    freed[tid] = 0;
+  }
+  __syncthreads();
+  const uint32_t nsb = args.nb;
+  const MatvecSeg seg = args.seg[0];
+  const uint32_t r0 = blockIdx.x * kRingRows;
+  if (wave == 0) {
+    float acc = 0.0f;
+    for (uint32_t c = 0; c < nsb; ++c) {
+#pragma unroll
+      for (uint32_t h = 0; h < 2; ++h) {
+        ring_wait(&ready[h], 2 * (c + 1));
+        const float4* src = reinterpret_cast<const float4*>(ring + static_cast<size_t>(h * kRingRows + lane) * kRingPitch);
+        // 128 products in 4 rounds of 32, each round's reads issued a round ahead of its adds
+        // (empty asm statements and scheduling barriers pin both for the compiler and for the
+        // scheduler); the slot is released once the last round's reads have landed.
+        float4 va[8], vb[8];
+        auto read8 = [&](float4 (&v)[8], int t) {
+#pragma unroll
+          for (int i = 0; i < 8; ++i) v[i] = src[8 * t + i];
+          asm volatile("" ::: "memory");
+          __builtin_amdgcn_sched_barrier(0);
+        };
+        auto add8 = [&](const float4 (&v)[8]) {
+#pragma unroll
+          for (int i = 0; i < 8; ++i) {
+            acc += v[i].x;
+            acc += v[i].y;
+            acc += v[i].z;
+            acc += v[i].w;
+          }
+          asm volatile("" : "+v"(acc)::"memory");  // the adds happen here, before the next reads
+          __builtin_amdgcn_sched_barrier(0);
+        };
+        read8(va, 0);
+        read8(vb, 1);
+        add8(va);
+        read8(va, 2);
+        add8(vb);
+        read8(vb, 3);
+        add8(va);
+        ring_signal(&freed[h], lane);
+        add8(vb);
+      }
+    }
+    if (r0 + lane < seg.n_out) seg.y[r0 + lane] = acc;
+  } else {
+    const uint32_t row = min(r0 + lane, seg.n_out - 1);  // rows past n_out repeat the last (not stored)
+    cfloat* x = (cfloat*)(reinterpret_cast<const float*>(args.xq));
+    switch (wave) {
+      case 1: ring_producer<0>(seg, x, nsb, col_bytes, row, lane, ring, ready, freed); break;
+      case 2: ring_producer<1>(seg, x, nsb, col_bytes, row, lane, ring, ready, freed); break;
+      case 3: ring_producer<2>(seg, x, nsb, col_bytes, row, lane, ring, ready, freed); break;
+      default: ring_producer<3>(seg, x, nsb, col_bytes, row, lane, ring, ready, freed); break;
+    }
+  }
+}
+
+// Grants the ring kernel its 66 KB of LDS (above the 64 KB default); false when it cannot.
+bool ring_granted() {
+  static int granted = -1;
+  if (granted < 0) {
+    granted = hipFuncSetAttribute(reinterpret_cast<const void*>(q6k_planar_ring_kernel),
+                                  hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(kRingLds)) == hipSuccess;
+    (void)hipGetLastError();
+  }
+  return granted == 1;
+}
+
+template <int R>
+size_t chain_lds(uint32_t nsb) { return static_cast<size_t>(R) * nsb * kChainPitch * 4; }
+
+// Grants the chain kernel its LDS (above 64 KB needs the attribute); false when it cannot.
+template <int R>
+bool chain_granted(size_t lds) {
+  static int limit = -1;
+  if (limit < 0) {
+    int dev = 0, v = 0;
+    limit = hipGetDevice(&dev) == hipSuccess &&
+                    hipDeviceGetAttribute(&v, hipDeviceAttributeMaxSharedMemoryPerBlock, dev) == hipSuccess &&
+                    hipFuncSetAttribute(reinterpret_cast<const void*>(q6k_planar_chain_kernel<R>),
+                                        hipFuncAttributeMaxDynamicSharedMemorySize, v) == hipSuccess
+                ? v
+                : 65536;
+    (void)hipGetLastError();
+  }
+  return lds <= static_cast<size_t>(limit);
+}
+
 }  // namespace
 
 size_t q6k_planar_column_bytes(uint32_t n_out) {
@@ -431,6 +754,35 @@ int q6k_repack_launch(const uint8_t* src, uint8_t* dst, uint32_t n_out, uint32_t
   return check_launch("q6k_repack");
 }
 
+std::atomic<int> g_q6k_path{0};
+
+uint32_t device_cus() {
+  static std::atomic<uint32_t> cus{0};
+  uint32_t n = cus.load(std::memory_order_relaxed);
+  if (n == 0) {
+    int dev = 0, v = 0;
+    n = hipGetDevice(&dev) == hipSuccess &&
+                hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && v > 0
+            ? static_cast<uint32_t>(v)
+            : 256;
+    cus.store(n, std::memory_order_relaxed);
+  }
+  return n;
+}
+
+// The one-row kernel for a shape: products then chains for a short matrix whose products fit
+// 8-row workgroups (up to 2048 rows and 19 super-blocks); the streamed ring while one round of
+// its 64-row workgroups, two per CU, covers the rows; else one lane per row, whose time does
+// not grow with the rows until the matrix streams at HBM rate (C2 sweep and the Llama-3 output,
+// measured on MI355X).
+int one_row_path(uint32_t n_out, uint32_t nsb) {
+  if (n_out <= kChainMaxOut && chain_lds<8>(nsb) <= 163840) return 2;
+  if (ceil_div(n_out, kRingRows) <= 2 * static_cast<size_t>(device_cus())) return 3;
+  return 1;
+}
+
+void matvec_q6k_force_path(int path) { g_q6k_path.store(path, std::memory_order_relaxed); }
+
 int matvec_q6k_planar_launch(MatvecArgs& a, uint32_t n_in) {
   const uint32_t n_out = a.seg[0].n_out;
   if (a.m == 0 || n_out == 0) return kOk;
@@ -438,6 +790,30 @@ int matvec_q6k_planar_launch(MatvecArgs& a, uint32_t n_in) {
   if ((reinterpret_cast<uintptr_t>(a.seg[0].w) & 15u) != 0 || (reinterpret_cast<uintptr_t>(a.xq) & 15u) != 0)
     return fail(kInvalidArgument, "matmul_q6_k_planar: the planar weights and the activations must be 16-byte aligned");
   const size_t col_bytes = q6k_planar_column_bytes(n_out);
+  int path = g_q6k_path.load(std::memory_order_relaxed);
+  if (a.m == 1 && path == 0) path = one_row_path(n_out, a.nb);
+  // One activation row: the streamed-ring kernel, 64 output rows per workgroup.
+  if (a.m == 1 && path == 3 && ring_granted()) {
+    launch(q6k_planar_ring_kernel, dim3(static_cast<uint32_t>(ceil_div(n_out, kRingRows))), dim3(320), kRingLds, a,
+           n_in, col_bytes);
+    return check_launch("q6k_planar_ring");
+  }
+  // One activation row: the products-then-chains kernel, R rows per workgroup as the LDS allows
+  // (R * n_in / 256 super-blocks of 1040 bytes).
+  if (a.m == 1 && path == 2) {
+    const uint32_t nsb = a.nb;
+    int rows = 8;
+    while (rows > 1 && chain_lds<8>(nsb) / 8 * rows > 163840) rows /= 2;
+    const uint32_t blocks = static_cast<uint32_t>(ceil_div(n_out, rows));
+    bool ok = false;
+    switch (rows) {
+      case 8: ok = chain_granted<8>(chain_lds<8>(nsb)); if (ok) launch(q6k_planar_chain_kernel<8>, dim3(blocks), dim3(256), chain_lds<8>(nsb), a, n_in, col_bytes); break;
+      case 4: ok = chain_granted<4>(chain_lds<4>(nsb)); if (ok) launch(q6k_planar_chain_kernel<4>, dim3(blocks), dim3(256), chain_lds<4>(nsb), a, n_in, col_bytes); break;
+      case 2: ok = chain_granted<2>(chain_lds<2>(nsb)); if (ok) launch(q6k_planar_chain_kernel<2>, dim3(blocks), dim3(256), chain_lds<2>(nsb), a, n_in, col_bytes); break;
+      default: ok = chain_granted<1>(chain_lds<1>(nsb)); if (ok) launch(q6k_planar_chain_kernel<1>, dim3(blocks), dim3(256), chain_lds<1>(nsb), a, n_in, col_bytes); break;
+    }
+    if (ok) return check_launch("q6k_planar_chain");
+  }
   // Activation rows per workgroup: up to kQ6MaxRows (each lane then runs that many chains, and
   // every weight slice is read once per that many rows), but fewer while that leaves under 1024
   // waves of 64 rows: a lane's chains run one element after another, so a short matrix needs

@@ -170,6 +170,12 @@ int axon_hip_q6k_repack(const void* w, size_t n_out, size_t n_in, void* planar);
  * x 16-byte aligned. */
 int axon_hip_matmul_q6_k_planar(const void* planar, const float* x, float* y, size_t n_rows, size_t n_out,
                                 size_t n_in, size_t y_stride);
+/* Test hook, no counterpart in the reference: which kernel axon_hip_matmul_q6_k_planar runs for
+ * one activation row. 0 (the default) chooses by shape; 1 one lane per output row; 2 the
+ * products formed by every thread into LDS, then one in-order chain per row (used only where
+ * its LDS fits, else as 1); 3 products streamed to the chains through two LDS slots, 64 rows
+ * per workgroup. Every path gives the same bits. */
+int axon_hip_q6k_force_path(int path);
 
 /* rmsnorm over rows (src/model/llama.cpp:128-134), writing y, its Q8_0 blocks (the next
  * matmul's input, llama.cpp:399-417), or both (either may be NULL). */

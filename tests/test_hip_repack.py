@@ -8,7 +8,8 @@ aligned planes for the device.
   column, then the d plane) gives the oracle's dequantization of the native blocks, float for
   float; the oracle's dequantizer is pinned to the reference's by its fixture.
 * The planar matmul equals the oracle's matmul_q6_k bit for bit (one row and several, strided
-  outputs), and the native stream kernel on the Llama-3 output shape.
+  outputs; each of the three one-row kernels forced in turn), and the native stream kernel on
+  the Llama-3 output shape.
 * A model's logits are the same with and without the repack."""
 from dataclasses import replace
 
@@ -102,6 +103,36 @@ def test_planar_matmul_bit_exact(H, o, n_out, n_in, n_rows):
     got = dy.download(np.float32, n_rows * stride)
     want = o.matmul("q6_k", w, x, n_out, n_in, n_rows=n_rows, y_stride=stride)
     assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+
+
+@pytest.mark.parametrize("path", [1, 2, 3])
+@pytest.mark.parametrize("n_out, n_in", [(13, 256), (64, 512), (1000, 2048), (300, 8192), (77, 14336),
+                                         (4097, 4096), (9000, 2048), (70, 40960)])
+def test_one_row_kernels_bit_exact(H, o, path, n_out, n_in):
+    """Each one-row kernel (axon_hip_q6k_force_path: one lane per row; products then chains,
+    whose rows per workgroup shrink as n_in grows and which 40960 columns do not fit; the
+    streamed ring, 64 rows per workgroup with a partial last one) against the oracle, bit for bit."""
+    import ctypes as C
+    w = q6k_weights(n_out, n_in, 11 * n_out + n_in)
+    x = random_floats(n_in, n_in + 3 * path)
+    dst, _ = repack(H, w, n_out, n_in)
+    dx = H.DeviceBuffer.of(x)
+    dy = H.DeviceBuffer.of(np.full(n_out + 1, np.float32(-7.25), np.float32))
+    H.check(H.lib().axon_hip_q6k_force_path(C.c_int(path)), "q6k_force_path")
+    try:
+        H.call("matmul_q6_k_planar", dst, dx, dy, 1, n_out, n_in, n_out)
+    finally:
+        H.check(H.lib().axon_hip_q6k_force_path(C.c_int(0)), "q6k_force_path")
+    got = dy.download(np.float32, n_out + 1)
+    want = o.matmul("q6_k", w, x, n_out, n_in, n_rows=1, y_stride=n_out)
+    assert np.array_equal(got[:n_out].view(np.uint32), want.view(np.uint32))
+    assert got[n_out] == np.float32(-7.25)  # nothing written past the last row
+
+
+def test_force_path_bounds(H):
+    import ctypes as C
+    with pytest.raises(H.HipError, match="0-3"):
+        H.check(H.lib().axon_hip_q6k_force_path(C.c_int(4)), "q6k_force_path")
 
 
 def test_planar_matmul_equals_the_stream_kernel_on_the_output_shape(H):
