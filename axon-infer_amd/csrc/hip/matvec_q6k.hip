@@ -19,6 +19,14 @@
 //    LDS broadcasts.
 //  * matvec_q6k_kernel (any 2-byte-aligned rows): each lane fetches its own super-blocks with
 //    per-lane loads, double-buffered in registers.
+//
+// The planar copy made at upload (q6k_repack_kernel) is what the model streams. Over it, several
+// activation rows run q6k_planar_kernel (one lane per output row, up to 8 rows per lane). One
+// activation row splits the products from the sums instead, since a lane that decodes and
+// chains by itself runs ~14 ns an element: q6k_planar_chain_kernel (a short matrix: every
+// thread forms products into LDS, then one lane per row adds them) and q6k_planar_ring_kernel
+// (products streamed to the chains through two LDS slots, 64 rows per workgroup). The sums keep
+// the scalar table's order in every kernel.
 #include <atomic>
 #include "common.h"
 #include "matvec.h"

@@ -622,6 +622,9 @@ def traffic_summary(fetch_csv, write_csv):
 
 SWEEP_SHAPES = [(2048, 2048), (8192, 2048), (2048, 8192), (128256, 2048)]
 SWEEP_ROWS = [1, 16, 64, 512]
+# Beside the sweep: the Q6_K table entry over the GGUF blocks themselves (matmul_q6_k /
+# matmul_q6_k_rows, what a caller binding the kernel table gets) on the output shape.
+SWEEP_NATIVE = ("q6_k_native", 128256, 2048, [1, 4, 16, 32])
 SWEEP_TYPES = {"q4_0": (2, 18 / 32), "q4_1": (3, 20 / 32), "q8_0": (8, 34 / 32), "q6_k": (14, 210 / 256)}
 INT8_PEAK_TOPS = 5000.0
 FP32_PEAK_TFLOPS = 157.3
@@ -631,7 +634,8 @@ def bench_sweep(H, seed, reps=20, rounds=3):
     """BASELINE configuration 2 through the table entries (the reference's bench_kernels.cpp:379-402
     sweep): every (N, K) x type x M. Integer types run matmul_*_q8 (one row) or matmul_*_q8_rows
     on Q8_0 activations; Q6_K runs matmul_q6_k_planar on float activations (the repacked copy the
-    model streams). Each call is captured `reps` times into one graph, each capture on the next of
+    model streams), and beside the sweep ("q6_k_native") matmul_q6_k_rows over the GGUF blocks on
+    the output shape. Each call is captured `reps` times into one graph, each capture on the next of
     enough weight copies that the copies exceed the 256 MB Infinity Cache, and the graph's
     replays are timed with events on the library stream: per-call time, dispatch included.
     Bytes are algorithmic: N*K weight bytes + the activations (Q8_0 blocks, or floats for Q6_K)
@@ -641,65 +645,70 @@ def bench_sweep(H, seed, reps=20, rounds=3):
     lib = H.lib()
     lib.axon_hip_q6k_planar_bytes.restype = C.c_size_t
     rows = []
-    for kind, (tid, bpe) in SWEEP_TYPES.items():
-        for n, k in SWEEP_SHAPES:
-            w = random_weights(kind, n, k, seed + n + k)
-            wbytes = w.nbytes
-            copies = int(max(2, min(64, -(-640_000_000 // wbytes))))
-            bufs = []
-            for _ in range(copies):
-                b = H.DeviceBuffer.of(w)
-                if kind == "q6_k":
-                    pl = H.DeviceBuffer(lib.axon_hip_q6k_planar_bytes(C.c_size_t(n), C.c_size_t(k)))
-                    H.call("q6k_repack", b, n, k, pl)
-                    b.free()
-                    b = pl
-                bufs.append(b)
-            del w
-            for m in SWEEP_ROWS:
-                x = np.random.default_rng(seed + m).standard_normal(m * k).astype(np.float32)
-                dx = H.DeviceBuffer.of(x)
-                dxq = H.DeviceBuffer(m * k // 32 * 34)
-                H.call("quantize_rows_q8_0", dx, dxq, k, m, k)
-                y = H.DeviceBuffer(m * n * 4)
-
-                def one(i):
-                    wb = bufs[i % copies]
-                    if kind == "q6_k":
-                        H.call("matmul_q6_k_planar", wb, dx, y, m, n, k, n)
-                    elif m == 1:
-                        H.call(f"matmul_{kind}_q8", wb, dxq, y, n, k)
-                    else:
-                        H.call(f"matmul_{kind}_q8_rows", wb, dxq, y, m, n, k, n)
-
-                for i in range(copies):  # untimed: first launches, LDS grants
-                    one(i)
-                H.synchronize()
-                H.check(lib.axon_hip_graph_begin(), "graph_begin")
-                for i in range(reps):
-                    one(i)
-                g = C.c_void_p(0)
-                H.check(lib.axon_hip_graph_end(C.byref(g)), "graph_end")
-                H.check(lib.axon_hip_graph_launch(g), "graph_launch")
-                H.synchronize()
-                e0, e1 = H.Event(), H.Event()
-                e0.record()
-                for _ in range(rounds):
-                    H.check(lib.axon_hip_graph_launch(g), "graph_launch")
-                e1.record()
-                H.synchronize()
-                lib.axon_hip_graph_destroy(g)
-                us = 1e3 * e0.elapsed_ms(e1) / (rounds * reps)
-                act = m * k * 4 if kind == "q6_k" else m * k // 32 * 34
-                nbytes = n * k * bpe + act + m * n * 4
-                gbs = nbytes / (us * 1e-6) / 1e9
-                tops = 2.0 * m * n * k / (us * 1e-6) / 1e12
-                rows.append([kind, n, k, m, round(us, 2), round(gbs, 1), round(tops, 2)])
-                log(f"sweep {kind} {n}x{k} M={m}: {us:.1f} us, {gbs:.0f} GB/s, {tops:.1f} TOPS")
-                dx.free(); dxq.free(); y.free()
-            for b in bufs:
+    jobs = [(kind, n, k, SWEEP_ROWS) for kind in SWEEP_TYPES for n, k in SWEEP_SHAPES]
+    jobs.append((SWEEP_NATIVE[0], SWEEP_NATIVE[1], SWEEP_NATIVE[2], SWEEP_NATIVE[3]))
+    for kind, n, k, ms in jobs:
+        tid, bpe = SWEEP_TYPES["q6_k" if kind == "q6_k_native" else kind]
+        w = random_weights("q6_k" if kind == "q6_k_native" else kind, n, k, seed + n + k)
+        wbytes = w.nbytes
+        copies = int(max(2, min(64, -(-640_000_000 // wbytes))))
+        bufs = []
+        for _ in range(copies):
+            b = H.DeviceBuffer.of(w)
+            if kind == "q6_k":
+                pl = H.DeviceBuffer(lib.axon_hip_q6k_planar_bytes(C.c_size_t(n), C.c_size_t(k)))
+                H.call("q6k_repack", b, n, k, pl)
                 b.free()
-    best_m1 = {f"{n}x{k}": max(r[5] for r in rows if r[1] == n and r[2] == k and r[3] == 1) for n, k in SWEEP_SHAPES}
+                b = pl
+            bufs.append(b)
+        del w
+        for m in ms:
+            x = np.random.default_rng(seed + m).standard_normal(m * k).astype(np.float32)
+            dx = H.DeviceBuffer.of(x)
+            dxq = H.DeviceBuffer(m * k // 32 * 34)
+            H.call("quantize_rows_q8_0", dx, dxq, k, m, k)
+            y = H.DeviceBuffer(m * n * 4)
+
+            def one(i):
+                wb = bufs[i % copies]
+                if kind == "q6_k":
+                    H.call("matmul_q6_k_planar", wb, dx, y, m, n, k, n)
+                elif kind == "q6_k_native":
+                    H.call("matmul_q6_k_rows", wb, dx, y, m, n, k, n)
+                elif m == 1:
+                    H.call(f"matmul_{kind}_q8", wb, dxq, y, n, k)
+                else:
+                    H.call(f"matmul_{kind}_q8_rows", wb, dxq, y, m, n, k, n)
+
+            for i in range(copies):  # untimed: first launches, LDS grants
+                one(i)
+            H.synchronize()
+            H.check(lib.axon_hip_graph_begin(), "graph_begin")
+            for i in range(reps):
+                one(i)
+            g = C.c_void_p(0)
+            H.check(lib.axon_hip_graph_end(C.byref(g)), "graph_end")
+            H.check(lib.axon_hip_graph_launch(g), "graph_launch")
+            H.synchronize()
+            e0, e1 = H.Event(), H.Event()
+            e0.record()
+            for _ in range(rounds):
+                H.check(lib.axon_hip_graph_launch(g), "graph_launch")
+            e1.record()
+            H.synchronize()
+            lib.axon_hip_graph_destroy(g)
+            us = 1e3 * e0.elapsed_ms(e1) / (rounds * reps)
+            act = m * k * 4 if kind.startswith("q6_k") else m * k // 32 * 34
+            nbytes = n * k * bpe + act + m * n * 4
+            gbs = nbytes / (us * 1e-6) / 1e9
+            tops = 2.0 * m * n * k / (us * 1e-6) / 1e12
+            rows.append([kind, n, k, m, round(us, 2), round(gbs, 1), round(tops, 2)])
+            log(f"sweep {kind} {n}x{k} M={m}: {us:.1f} us, {gbs:.0f} GB/s, {tops:.1f} TOPS")
+            dx.free(); dxq.free(); y.free()
+        for b in bufs:
+            b.free()
+    best_m1 = {f"{n}x{k}": max(r[5] for r in rows if r[1] == n and r[2] == k and r[3] == 1 and r[0] in SWEEP_TYPES)
+               for n, k in SWEEP_SHAPES}
     return {"columns": ["type", "N", "K", "M", "us_per_call", "GB_per_s", "TOPS"], "rows": rows,
             "hbm_peak_GB_per_s": HBM_PEAK_GBS, "int8_peak_TOPS": INT8_PEAK_TOPS, "fp32_peak_TFLOPS": FP32_PEAK_TFLOPS,
             "best_M1_GB_per_s": best_m1,

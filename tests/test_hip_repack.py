@@ -140,7 +140,7 @@ def test_planar_matmul_equals_the_stream_kernel_on_the_output_shape(H):
     w = q6k_weights(n_out, n_in, 5)
     dst, _ = repack(H, w, n_out, n_in)
     dw = H.DeviceBuffer.of(w)
-    for n_rows in (1, 4, 5):
+    for n_rows in (1, 4, 5, 32):
         x = random_floats(n_rows * n_in, 40 + n_rows)
         dx = H.DeviceBuffer.of(x)
         a = H.DeviceBuffer(4 * n_rows * n_out)
@@ -148,6 +148,23 @@ def test_planar_matmul_equals_the_stream_kernel_on_the_output_shape(H):
         H.call("matmul_q6_k_planar", dst, dx, a, n_rows, n_out, n_in, n_out)
         H.call("matmul_q6_k_rows", dw, dx, b, n_rows, n_out, n_in, n_out)
         assert np.array_equal(a.download(np.uint32, n_rows * n_out), b.download(np.uint32, n_rows * n_out))
+
+
+@pytest.mark.parametrize("n_rows", [8, 16, 21, 32])
+def test_native_rows_bit_exact(H, o, n_rows):
+    """matmul_q6_k_rows over the GGUF blocks with many activation rows (launches of up to four,
+    then the rest), strided outputs, against the oracle."""
+    n_out, n_in = 300, 2048
+    w = q6k_weights(n_out, n_in, 7 * n_rows)
+    x = random_floats(n_rows * n_in, 90 + n_rows)
+    stride = n_out + 3
+    dw = H.DeviceBuffer.of(w)
+    dx = H.DeviceBuffer.of(x)
+    dy = H.DeviceBuffer.of(np.full(n_rows * stride, np.float32(-7.25), np.float32))
+    H.call("matmul_q6_k_rows", dw, dx, dy, n_rows, n_out, n_in, stride)
+    got = dy.download(np.float32, n_rows * stride)
+    want = o.matmul("q6_k", w, x, n_out, n_in, n_rows=n_rows, y_stride=stride)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
 
 
 def test_planar_bounds(H):
