@@ -412,20 +412,29 @@ constexpr uint32_t kTileRows = 64;
 
 template <uint32_t TN>
 __host__ __device__ constexpr uint32_t tile_wp() { return TN + 4; }  // scale pitch, weights
-__host__ __device__ constexpr uint32_t tile_xp() { return kTileRows + 4; }  // scale pitch, activations
+template <uint32_t TM = kTileRows>
+__host__ __device__ constexpr uint32_t tile_xp() { return TM + 4; }  // scale pitch, activations
 
-template <int T, uint32_t TN>
+template <int T, uint32_t TN, uint32_t TM = kTileRows>
 __host__ __device__ constexpr size_t tile_lds() {
-  const size_t scales = static_cast<size_t>(kTileChunk) * (tile_wp<TN>() + tile_xp()) * (T == Q4_1 ? 2 : 1);
-  return (static_cast<size_t>(TN + kTileRows) * kTilePitch + scales) * 4;
+  const size_t scales = static_cast<size_t>(kTileChunk) * (tile_wp<TN>() + tile_xp<TM>()) * (T == Q4_1 ? 2 : 1);
+  return (static_cast<size_t>(TN + TM) * kTilePitch + scales) * 4;
 }
 
-template <int T, uint32_t TN, bool SWIGLU = false>
+template <int T, uint32_t TN, bool SWIGLU = false, uint32_t TM = kTileRows>
 __global__ __launch_bounds__(kThreads) void mfma_tile_kernel(MatvecArgs args) {
   constexpr int bs = block_bytes<T>();
-  constexpr uint32_t TM = kTileRows, KC = kTileChunk, P = kTilePitch;
-  constexpr uint32_t WP = tile_wp<TN>(), XP = tile_xp();
-  constexpr uint32_t NT = TN / 16;                      // weight sub-tiles per wave
+  constexpr uint32_t KC = kTileChunk, P = kTilePitch;
+  constexpr uint32_t WP = tile_wp<TN>(), XP = tile_xp<TM>();
+  constexpr uint32_t NT = TN / 16;                      // weight sub-tiles of the tile
+  // The four waves split the tile's (activation tile, weight sub-tile) pairs: with MT
+  // activation tiles of 16 rows, wave w takes activation tile w % MT and NTW weight sub-tiles
+  // from (w / MT) * NTW on (all NT when the tile has 64 activation rows).
+  constexpr uint32_t MT = TM / 16;
+  constexpr uint32_t NTW = NT * MT / 4;
+  static_assert(TM == 16 || TM == 32 || TM == 64, "16, 32 or 64 activation rows");
+  static_assert(NTW >= 1 && NTW * 4 == NT * MT, "whole sub-tiles per wave");
+  static_assert(!SWIGLU || TM == kTileRows, "the SwiGLU epilogue holds all four sub-tiles in one wave");
   constexpr uint32_t WI = TN * KC / kThreads;           // weight items per thread per chunk
   constexpr uint32_t XI = TM * KC / kThreads;           // activation items per thread per chunk
   constexpr uint32_t WD = item_dwords<T>(), XD = item_dwords<Q8_0>();
@@ -554,38 +563,39 @@ __global__ __launch_bounds__(kThreads) void mfma_tile_kernel(MatvecArgs args) {
 
   const uint32_t col = lane & 15;  // weight row within a 16-row sub-tile; A row within the wave's 16
   const uint32_t kq = lane >> 4;   // which 8 of a block's 32 elements this lane feeds
-  const uint32_t arow = 16 * wave + col;        // the A operand row (activation row in the tile)
-  const uint32_t orow = 16 * wave + 4 * kq;     // the lane's output rows: orow .. orow + 3
-  float acc[NT][4];
+  const uint32_t arow = 16 * (wave % MT) + col;     // the A operand row (activation row in the tile)
+  const uint32_t orow = 16 * (wave % MT) + 4 * kq;  // the lane's output rows: orow .. orow + 3
+  const uint32_t j0 = (wave / MT) * NTW;           // the wave's first weight sub-tile
+  float acc[NTW][4];
 #pragma unroll
-  for (uint32_t j = 0; j < NT; ++j)
+  for (uint32_t j = 0; j < NTW; ++j)
 #pragma unroll
     for (int v = 0; v < 4; ++v) acc[j][v] = 0.0f;
 
   constexpr uint32_t kBatch = 4;  // blocks whose MFMAs are issued before their folds
   static_assert(KC % kBatch == 0, "whole batches");
-  auto block_sums = [&](uint32_t b, i32x4 (&d)[NT]) {
+  auto block_sums = [&](uint32_t b, i32x4 (&d)[NTW]) {
     const uint2 xq = *reinterpret_cast<const uint2*>(xa + arow * P + b * 8 + 2 * kq);
     const int64_t ax = static_cast<int64_t>((static_cast<uint64_t>(xq.y) << 32) | xq.x);
 #pragma unroll
-    for (uint32_t j = 0; j < NT; ++j) {
-      const uint2 wq = *reinterpret_cast<const uint2*>(wa + (16 * j + col) * P + b * 8 + 2 * kq);
+    for (uint32_t j = 0; j < NTW; ++j) {
+      const uint2 wq = *reinterpret_cast<const uint2*>(wa + (16 * (j0 + j) + col) * P + b * 8 + 2 * kq);
       const int64_t bw = static_cast<int64_t>((static_cast<uint64_t>(wq.y) << 32) | wq.x);
       i32x4 z = {0, 0, 0, 0};
       d[j] = __builtin_amdgcn_mfma_i32_16x16x32_i8(ax, bw, z, 0, 0, 0);
     }
   };
-  auto block_fold = [&](uint32_t b, const i32x4 (&d)[NT]) {
+  auto block_fold = [&](uint32_t b, const i32x4 (&d)[NTW]) {
     const float4 dx = *reinterpret_cast<const float4*>(xd + b * XP + orow);
     const float dxv[4] = {dx.x, dx.y, dx.z, dx.w};
     int4 sx = make_int4(0, 0, 0, 0);
     if constexpr (T == Q4_1) sx = *reinterpret_cast<const int4*>(xs + b * XP + orow);
     const int32_t sxv[4] = {sx.x, sx.y, sx.z, sx.w};
 #pragma unroll
-    for (uint32_t j = 0; j < NT; ++j) {
-      const float dw = wd[b * WP + 16 * j + col];
+    for (uint32_t j = 0; j < NTW; ++j) {
+      const float dw = wd[b * WP + 16 * (j0 + j) + col];
       float mw = 0.0f;
-      if constexpr (T == Q4_1) mw = wmn[b * WP + 16 * j + col];
+      if constexpr (T == Q4_1) mw = wmn[b * WP + 16 * (j0 + j) + col];
 #pragma unroll
       for (int v = 0; v < 4; ++v) {
         if constexpr (T == Q4_1) {
@@ -606,7 +616,7 @@ __global__ __launch_bounds__(kThreads) void mfma_tile_kernel(MatvecArgs args) {
     if (c + 1 < n_chunks) load(c + 1, r);
     if (cb == KC) {
       for (uint32_t b0 = 0; b0 < KC; b0 += kBatch) {
-        i32x4 d[kBatch][NT];
+        i32x4 d[kBatch][NTW];
 #pragma unroll
         for (uint32_t k = 0; k < kBatch; ++k) block_sums(b0 + k, d[k]);
 #pragma unroll
@@ -614,7 +624,7 @@ __global__ __launch_bounds__(kThreads) void mfma_tile_kernel(MatvecArgs args) {
       }
     } else {
       for (uint32_t b = 0; b < cb; ++b) {
-        i32x4 d[NT];
+        i32x4 d[NTW];
         block_sums(b, d);
         block_fold(b, d);
       }
@@ -653,13 +663,13 @@ __global__ __launch_bounds__(kThreads) void mfma_tile_kernel(MatvecArgs args) {
     return;
   }
 #pragma unroll
-  for (uint32_t j = 0; j < NT; ++j) {
-    if (16 * j + col < nn) {
+  for (uint32_t j = 0; j < NTW; ++j) {
+    if (16 * (j0 + j) + col < nn) {
 #pragma unroll
       for (int v = 0; v < 4; ++v) {
         const uint32_t rr = orow + v;
         if (rr < mm) {
-          float* y = seg.y + static_cast<size_t>(m0 + rr) * seg.y_stride + n0 + 16 * j + col;
+          float* y = seg.y + static_cast<size_t>(m0 + rr) * seg.y_stride + n0 + 16 * (j0 + j) + col;
           *y = args.accumulate ? *y + acc[j][v] : acc[j][v];
         }
       }
@@ -667,14 +677,14 @@ __global__ __launch_bounds__(kThreads) void mfma_tile_kernel(MatvecArgs args) {
   }
 }
 
-template <uint32_t TN>
+template <uint32_t TN, uint32_t TM = kTileRows>
 int tile_launch(int type, MatvecArgs& a) {
   uint32_t wg = 0;
   for (int s = 0; s < a.n_seg; ++s) {
     a.seg[s].wg_begin = wg;
     wg += static_cast<uint32_t>(ceil_div(a.seg[s].n_out, TN));
   }
-  const dim3 grid(wg, static_cast<uint32_t>(ceil_div(a.m, kTileRows)));
+  const dim3 grid(wg, static_cast<uint32_t>(ceil_div(a.m, TM)));
   // Dynamic LDS above 64 KB is granted per kernel, once.
   static const bool granted = [] {
     bool ok = true;
@@ -683,16 +693,16 @@ int tile_launch(int type, MatvecArgs& a) {
         ok = ok && hipFuncSetAttribute(reinterpret_cast<const void*>(kernel), hipFuncAttributeMaxDynamicSharedMemorySize,
                                        static_cast<int>(lds)) == hipSuccess;
     };
-    grant(mfma_tile_kernel<Q8_0, TN>, tile_lds<Q8_0, TN>());
-    grant(mfma_tile_kernel<Q4_0, TN>, tile_lds<Q4_0, TN>());
-    grant(mfma_tile_kernel<Q4_1, TN>, tile_lds<Q4_1, TN>());
+    grant(mfma_tile_kernel<Q8_0, TN, false, TM>, tile_lds<Q8_0, TN, TM>());
+    grant(mfma_tile_kernel<Q4_0, TN, false, TM>, tile_lds<Q4_0, TN, TM>());
+    grant(mfma_tile_kernel<Q4_1, TN, false, TM>, tile_lds<Q4_1, TN, TM>());
     return ok;
   }();
   if (!granted) return fail(kUnsupported, "matmul tile: the LDS grant was refused");
   switch (type) {
-  case Q8_0: launch(mfma_tile_kernel<Q8_0, TN>, grid, dim3(kThreads), tile_lds<Q8_0, TN>(), a); break;
-  case Q4_0: launch(mfma_tile_kernel<Q4_0, TN>, grid, dim3(kThreads), tile_lds<Q4_0, TN>(), a); break;
-  case Q4_1: launch(mfma_tile_kernel<Q4_1, TN>, grid, dim3(kThreads), tile_lds<Q4_1, TN>(), a); break;
+  case Q8_0: launch(mfma_tile_kernel<Q8_0, TN, false, TM>, grid, dim3(kThreads), tile_lds<Q8_0, TN, TM>(), a); break;
+  case Q4_0: launch(mfma_tile_kernel<Q4_0, TN, false, TM>, grid, dim3(kThreads), tile_lds<Q4_0, TN, TM>(), a); break;
+  case Q4_1: launch(mfma_tile_kernel<Q4_1, TN, false, TM>, grid, dim3(kThreads), tile_lds<Q4_1, TN, TM>(), a); break;
   default: return fail(kUnsupported, "matmul tile: weight type %d", type);
   }
   return check_launch("mfma_tile");
@@ -733,6 +743,8 @@ bool matmul_q8_rows_fits(int type, const MatvecArgs& a, bool many_rows) {
   if (static_cast<uint64_t>(a.nb) * kBytesQ8_0 * 64 >= (uint64_t(1) << 31)) return false;
   return (bases & 3u) == 0 && (a.nb * bs) % 4 == 0 && (a.nb * kBytesQ8_0) % 4 == 0;
 }
+
+constexpr uint32_t kDecodeTileWg = 256;  // workgroups a decode matrix needs for the tile kernel
 
 bool matmul_q8_tile_fills(const MatvecArgs& a) {
   if (a.m < 33 || a.m > kRowsMaxM) return false;
@@ -782,6 +794,20 @@ int matmul_q8_tile_launch(int type, MatvecArgs& a) {
 
 int matmul_q8_rows_launch(int type, MatvecArgs& a) {
   if (!matmul_q8_rows_fits(type, a)) return fail(kUnsupported, "matmul rows: shape or alignment");
+  // A matrix wide enough for kDecodeTileWg workgroups of 64 weight rows (16 activation rows) or
+  // 32 (32 activation rows) takes the tile kernel: each workgroup reads and expands the
+  // activations once for all its weight rows, where the rows kernel's 16-row workgroups read
+  // them two or four times as often (gate|up of C4 at 32 rows: 27.3 -> 14.2 us).
+  uint32_t wg64 = 0, wg32 = 0;
+  for (int s = 0; s < a.n_seg; ++s) {
+    wg64 += static_cast<uint32_t>(ceil_div(a.seg[s].n_out, 64));
+    wg32 += static_cast<uint32_t>(ceil_div(a.seg[s].n_out, 32));
+  }
+  if (a.m <= 16) {
+    if (wg64 >= kDecodeTileWg) return tile_launch<64, 16>(type, a);
+  } else if (a.m <= 32) {
+    if (wg32 >= kDecodeTileWg) return tile_launch<32, 32>(type, a);
+  }
   // Eight weight rows per workgroup when sixteen would leave CUs without one.
   uint32_t wg16 = 0;
   for (int s = 0; s < a.n_seg; ++s) wg16 += static_cast<uint32_t>(ceil_div(a.seg[s].n_out, kRowsTN));

@@ -157,6 +157,40 @@ def test_q8_fused_segments_few_rows_bit_exact(o, n_rows, n_in):
                 assert np.array_equal(got[:, n_out[j]:], base[j].reshape(n_rows, stride[j])[:, n_out[j]:])
 
 
+@pytest.mark.parametrize("n_rows", [5, 16, 17, 32])
+def test_q8_fused_segments_wide_decode_bit_exact(o, n_rows):
+    """Decode batches (5..32 rows) on a matrix wide enough for the tile kernel with 16 or 32
+    activation rows per workgroup (64 weight rows per workgroup up to 16 rows, 32 above):
+    segments of 16384, 7 and 300 rows (partial weight tiles), a last K chunk of 12 blocks, the
+    sentinels past n_out untouched, and accumulate — each output equal to the oracle's."""
+    import axon_hip as H
+    n_in, n_out = 896, [16384, 7, 300]
+    stride = [n + 3 for n in n_out]
+    xs = random_floats(n_rows * n_in, 5 * n_rows + n_in, 3.0)
+    xq = np.concatenate([o.quantize_row_q8_0(xs[i * n_in:(i + 1) * n_in]) for i in range(n_rows)])
+    dx = H.DeviceBuffer.of(xq)
+    for kind in QUANT_TYPES:
+        ws = [random_weights(kind, n, n_in, 300 * j + n_rows) for j, n in enumerate(n_out)]
+        wants = [o.matmul(f"{kind}_q8", ws[j], xq, n_out[j], n_in, n_rows=n_rows,
+                          y_stride=n_out[j]).reshape(n_rows, n_out[j]) for j in range(len(ws))]
+        dws = [H.DeviceBuffer.of(w) for w in ws]
+        for accumulate in (0, 1):
+            base = [random_floats(n_rows * st, 9 + j, 1.0) for j, st in enumerate(stride)]
+            dys = [H.DeviceBuffer.of(b) for b in base]
+            n = len(ws)
+            H.check(H.lib().axon_hip_matmul_q8_fused(
+                C.c_int(TYPE_ID[kind]), C.c_void_p(dx.ptr), C.c_size_t(n_rows), C.c_size_t(n_in), C.c_size_t(n),
+                (C.c_void_p * n)(*[b.ptr for b in dws]), (C.c_void_p * n)(*[b.ptr for b in dys]),
+                (C.c_size_t * n)(*n_out), (C.c_size_t * n)(*stride), C.c_int(accumulate)), "matmul_q8_fused")
+            for j in range(n):
+                got = dys[j].download(np.float32).reshape(n_rows, stride[j])
+                want = wants[j]
+                if accumulate:
+                    want = base[j].reshape(n_rows, stride[j])[:, :n_out[j]] + want
+                assert np.array_equal(got[:, :n_out[j]], want), (kind, j, accumulate)
+                assert np.array_equal(got[:, n_out[j]:], base[j].reshape(n_rows, stride[j])[:, n_out[j]:])
+
+
 @pytest.mark.parametrize("n_rows, n_in, n_out", [(65, 896, [300, 7, 64]), (77, 2048, [300, 7, 64]),
                                                   (200, 896, [1152, 896, 40]), (576, 896, [4096, 1024, 1024]),
                                                   (130, 4864, [896, 33, 64]), (40, 896, [32768, 7, 64]),
