@@ -794,7 +794,9 @@ void matvec_q6k_force_path(int path) { g_q6k_path.store(path, std::memory_order_
 int matvec_q6k_planar_launch(MatvecArgs& a, uint32_t n_in) {
   const uint32_t n_out = a.seg[0].n_out;
   if (a.m == 0 || n_out == 0) return kOk;
-  if (n_in % kQKK != 0) return fail(kInvalidArgument, "matmul_q6_k_planar: n_in %u is not a multiple of 256", n_in);
+  // n_in 0 has no super-block to read (every kernel below reads the first one).
+  if (n_in == 0 || n_in % kQKK != 0)
+    return fail(kInvalidArgument, "matmul_q6_k_planar: n_in %u is not a positive multiple of 256", n_in);
   if ((reinterpret_cast<uintptr_t>(a.seg[0].w) & 15u) != 0 || (reinterpret_cast<uintptr_t>(a.xq) & 15u) != 0)
     return fail(kInvalidArgument, "matmul_q6_k_planar: the planar weights and the activations must be 16-byte aligned");
   const size_t col_bytes = q6k_planar_column_bytes(n_out);
@@ -860,7 +862,8 @@ int matvec_q6k_planar_launch(MatvecArgs& a, uint32_t n_in) {
 int matvec_q6k_launch(MatvecArgs& a, uint32_t n_in) {
   const uint32_t n_out = a.seg[0].n_out;
   if (a.m == 0 || n_out == 0) return kOk;
-  if (n_in % kQKK != 0) return fail(kInvalidArgument, "matmul_q6_k: n_in %u is not a multiple of 256", n_in);
+  if (n_in == 0 || n_in % kQKK != 0)
+    return fail(kInvalidArgument, "matmul_q6_k: n_in %u is not a positive multiple of 256", n_in);
   if ((reinterpret_cast<uintptr_t>(a.seg[0].w) & 1u) != 0)
     return fail(kInvalidArgument, "matmul_q6_k: weights must be 2-byte aligned");
   if ((reinterpret_cast<uintptr_t>(a.xq) & 3u) != 0)

@@ -179,6 +179,10 @@ def test_planar_bounds(H):
         H.call("q6k_repack", buf.at(1), 1, 256, buf)
     with pytest.raises(H.HipError, match="aligned"):
         H.call("matmul_q6_k_planar", buf.at(8), buf, buf, 1, 1, 256, 1)
+    with pytest.raises(H.HipError, match="positive multiple of 256"):  # no super-block to read
+        H.call("matmul_q6_k_planar", buf, buf, buf, 1, 4, 0, 4)
+    with pytest.raises(H.HipError, match="positive multiple of 256"):
+        H.call("matmul_q6_k_rows", buf, buf, buf, 1, 4, 0, 4)
 
 
 def test_model_logits_unchanged_by_the_repack(H, tmp_path_factory):
