@@ -807,6 +807,44 @@ int axon_hip_matvec_fused(const axon_hip_matvec_fused_args* p) {
   return matvec_fused_launch(p->type, a);
 }
 
+int axon_hip_matmul_q8_qkv_rope(const axon_hip_matvec_fused_args* p) {
+  AXON_READY();
+  if (p->n_seg != 3 || p->in_mode != kInQ8 || p->out_mode != kOutRope)
+    return fail(kInvalidArgument, "matmul_q8_qkv_rope: three segments, in_mode 0 and out_mode 3");
+  if (p->n_in % kQK != 0 || p->n_in == 0) return fail(kInvalidArgument, "matmul_q8_qkv_rope: n_in %zu is not a positive multiple of 32", p->n_in);
+  if (p->xq == nullptr || p->y[0] == nullptr || p->pos == nullptr || p->cache == nullptr || p->cache_off == nullptr ||
+      p->rope_table == nullptr)
+    return fail(kInvalidArgument, "matmul_q8_qkv_rope: needs the blocks, q's buffer, positions, a cache and a cos/sin table");
+  if (p->head_dim == 0 || (p->head_dim & 1) != 0 || p->rot_half * 2 > p->head_dim || p->n_out[1] != p->n_out[2] ||
+      ((p->n_out[0] | p->n_out[1]) & 1) != 0 || p->y_stride[0] < p->n_out[0])
+    return fail(kInvalidArgument, "matmul_q8_qkv_rope: q|k|v shapes");
+  if (p->n_rows == 0) return kOk;
+  if (p->n_rows > kRowsMaxM) return fail(kUnsupported, "matmul_q8_qkv_rope: %zu rows (at most %u)", p->n_rows, kRowsMaxM);
+  if (!fits_u32(p->n_in) || !fits_u32(p->n_out[0]) || !fits_u32(p->n_out[1]) || !fits_u32(p->y_stride[0]))
+    return fail(kInvalidArgument, "matmul_q8_qkv_rope: sizes too large");
+  MatvecArgs a{};
+  for (int s = 0; s < 3; ++s)
+    a.seg[s] = MatvecSeg{static_cast<const uint8_t*>(p->w[s]), s == 0 ? p->y[0] : nullptr,
+                         static_cast<uint32_t>(p->n_out[s]), s == 0 ? static_cast<uint32_t>(p->y_stride[0]) : 0u, 0};
+  a.n_seg = 3;
+  a.xq = static_cast<const uint8_t*>(p->xq);
+  a.nb = static_cast<uint32_t>(p->n_in / kQK);
+  a.m = static_cast<uint32_t>(p->n_rows);
+  RowsRope rp{};
+  for (int s = 0; s < 3; ++s) rp.bias[s] = p->bias[s];
+  rp.table = p->rope_table;
+  rp.pos = p->pos;
+  rp.cache_off = p->cache_off;
+  rp.cache = p->cache;
+  rp.k_layer_off = p->k_layer_off;
+  rp.v_layer_off = p->v_layer_off;
+  rp.rot_half = p->rot_half;
+  rp.head_dim = p->head_dim;
+  rp.kv_row = static_cast<uint32_t>(p->n_out[1]);
+  rp.cache_f16 = p->cache_f16 != 0;
+  return matmul_q8_rows_rope_launch(p->type, a, rp);
+}
+
 namespace {
 axon_hip::StepShape step_shape_of(const axon_hip_decode_shape* sh) {
   axon_hip::StepShape s{};

@@ -189,8 +189,8 @@ __host__ __device__ constexpr size_t rows_lds() {
 // TN: weight rows per workgroup, 16 or 8. With 8 (a narrow matrix, so twice the workgroups),
 // lanes of weight column col read row col % 8 into the 16-wide MFMA and only columns below 8
 // are folded and stored.
-template <int T, int TM, uint32_t TN = kRowsTN>
-__global__ __launch_bounds__(kThreads) void mfma_rows_kernel(MatvecArgs args) {
+template <int T, int TM, uint32_t TN = kRowsTN, bool ROPE = false>
+__global__ __launch_bounds__(kThreads) void mfma_rows_kernel(MatvecArgs args, RowsRope rp) {
   static_assert(TN == 16 || TN == 8, "16 or 8 weight rows");
   constexpr int bs = block_bytes<T>();
   constexpr uint32_t KC = kRowsChunk, P = kRowsPitch;
@@ -385,6 +385,40 @@ __global__ __launch_bounds__(kThreads) void mfma_rows_kernel(MatvecArgs args) {
     if (c + 1 < n_chunks) chunk(c + 1, rb);
   }
 
+  if constexpr (ROPE) {
+    // Segments q, k, v: the bias, then the rotation of each pair (2i, 2i + 1) of a head as
+    // rope_rows_kernel forms it (x0 * c - x1 * s, x0 * s + x1 * c); n0 is a multiple of TN, so
+    // output n sits in lane col and its partner n ^ 1 in lane col ^ 1 of the same 16.
+    const uint32_t n = n0 + col;
+#pragma unroll
+    for (uint32_t t = 0; t < MT; ++t) {
+      const uint32_t r = 16 * t + orow;
+      float x = acc[t];
+      if (rp.bias[s] != nullptr && col < nn) x = x + rp.bias[s][n];
+      const float other = __shfl_xor(x, 1, 64);
+      if (col < nn && r < mm) {
+        const int32_t pos = rp.pos[m0 + r];
+        if (s < 2) {
+          const uint32_t i = (n % rp.head_dim) / 2;
+          if (i < rp.rot_half) {
+            const float2 cs = reinterpret_cast<const float2*>(rp.table)[static_cast<size_t>(pos) * rp.rot_half + i];
+            const float x0 = (col & 1) ? other : x;
+            const float x1 = (col & 1) ? x : other;
+            x = (col & 1) ? x0 * cs.y + x1 * cs.x : x0 * cs.x - x1 * cs.y;
+          }
+        }
+        if (s == 0) {
+          seg.y[static_cast<size_t>(m0 + r) * seg.y_stride + n] = x;
+        } else {
+          const size_t at = rp.cache_off[m0 + r] + (s == 1 ? rp.k_layer_off : rp.v_layer_off) +
+                            static_cast<size_t>(pos) * rp.kv_row + n;
+          if (rp.cache_f16) static_cast<uint16_t*>(rp.cache)[at] = static_cast<uint16_t>(float_to_half_bits(x));
+          else static_cast<float*>(rp.cache)[at] = x;
+        }
+      }
+    }
+    return;
+  }
   if (col < nn) {
 #pragma unroll
     for (uint32_t t = 0; t < MT; ++t) {
@@ -434,7 +468,6 @@ __global__ __launch_bounds__(kThreads) void mfma_tile_kernel(MatvecArgs args) {
   constexpr uint32_t NTW = NT * MT / 4;
   static_assert(TM == 16 || TM == 32 || TM == 64, "16, 32 or 64 activation rows");
   static_assert(NTW >= 1 && NTW * 4 == NT * MT, "whole sub-tiles per wave");
-  static_assert(!SWIGLU || TM == kTileRows, "the SwiGLU epilogue holds all four sub-tiles in one wave");
   constexpr uint32_t WI = TN * KC / kThreads;           // weight items per thread per chunk
   constexpr uint32_t XI = TM * KC / kThreads;           // activation items per thread per chunk
   constexpr uint32_t WD = item_dwords<T>(), XD = item_dwords<Q8_0>();
@@ -635,14 +668,11 @@ __global__ __launch_bounds__(kThreads) void mfma_tile_kernel(MatvecArgs args) {
   if constexpr (SWIGLU) {
     // Output n0 + col (sub-tiles 0 and 2) and n0 + 16 + col (1 and 3): silu(gate) * up as
     // silu_mul_kernel forms it, then each row's 32 outputs as one Q8_0 block, quantized as
-    // quantize_block_lanes does (the 16 lanes of a kq group hold the block).
+    // quantize_block_lanes does (the 16 lanes of a kq group hold the block, row rr of the tile).
     const size_t row_blocks = seg.n_out / kQK;
-#pragma unroll
-    for (int v = 0; v < 4; ++v) {
-      const uint32_t rr = orow + v;
-      const float g0 = acc[0][v], g1 = acc[1][v];
-      const float y0 = g0 / (1.0f + exp_libm(-g0)) * acc[2][v];
-      const float y1 = g1 / (1.0f + exp_libm(-g1)) * acc[3][v];
+    auto swiglu_row = [&](uint32_t rr, float g0, float g1, float u0, float u1) {
+      const float y0 = g0 / (1.0f + exp_libm(-g0)) * u0;
+      const float y1 = g1 / (1.0f + exp_libm(-g1)) * u1;
       float amax = fmaxf(fabsf(y0), fabsf(y1));
 #pragma unroll
       for (int off = 8; off > 0; off >>= 1) amax = fmaxf(amax, __shfl_xor(amax, off, 64));
@@ -658,6 +688,26 @@ __global__ __launch_bounds__(kThreads) void mfma_tile_kernel(MatvecArgs args) {
         blk[2 + col] = static_cast<uint8_t>(static_cast<int32_t>(roundf(y0 * id)) & 0xff);
         blk[2 + 16 + col] = static_cast<uint8_t>(static_cast<int32_t>(roundf(y1 * id)) & 0xff);
         if (col == 0) *reinterpret_cast<uint16_t*>(blk) = static_cast<uint16_t>(float_to_half_bits(dq));
+      }
+    };
+    if constexpr (TM == kTileRows) {
+#pragma unroll
+      for (int v = 0; v < 4; ++v) swiglu_row(orow + v, acc[0][v], acc[1][v], acc[2][v], acc[3][v]);
+    } else {
+      // Fewer activation rows: a row's gate and up sub-tiles sit on different waves. They meet
+      // in LDS ([sub-tile][row][16] floats; the chunk loop's last barrier freed it), and wave w
+      // then takes rows w * TM / 4 .., four per pass (one per 16-lane group).
+      float* st = reinterpret_cast<float*>(lds_tile);
+#pragma unroll
+      for (uint32_t j = 0; j < NTW; ++j)
+#pragma unroll
+        for (int v = 0; v < 4; ++v) st[((j0 + j) * TM + orow + v) * 16 + col] = acc[j][v];
+      __syncthreads();
+#pragma unroll
+      for (uint32_t p = 0; p < TM / 16; ++p) {
+        const uint32_t rr = wave * (TM / 4) + 4 * p + kq;
+        swiglu_row(rr, st[rr * 16 + col], st[(TM + rr) * 16 + col], st[(2 * TM + rr) * 16 + col],
+                   st[(3 * TM + rr) * 16 + col]);
       }
     }
     return;
@@ -708,8 +758,8 @@ int tile_launch(int type, MatvecArgs& a) {
   return check_launch("mfma_tile");
 }
 
-template <int TM, uint32_t TN = kRowsTN>
-int rows_launch(int type, MatvecArgs& a) {
+template <int TM, uint32_t TN = kRowsTN, bool ROPE = false>
+int rows_launch(int type, MatvecArgs& a, const RowsRope& rp = RowsRope{}) {
   uint32_t wg = 0;
   for (int s = 0; s < a.n_seg; ++s) {
     a.seg[s].wg_begin = wg;
@@ -719,12 +769,19 @@ int rows_launch(int type, MatvecArgs& a) {
   constexpr size_t lds = rows_lds<TM, TN>();
   static_assert(lds <= 65536, "within the default LDS grant");
   switch (type) {
-  case Q8_0: launch(mfma_rows_kernel<Q8_0, TM, TN>, grid, dim3(kThreads), lds, a); break;
-  case Q4_0: launch(mfma_rows_kernel<Q4_0, TM, TN>, grid, dim3(kThreads), lds, a); break;
-  case Q4_1: launch(mfma_rows_kernel<Q4_1, TM, TN>, grid, dim3(kThreads), lds, a); break;
+  case Q8_0: launch(mfma_rows_kernel<Q8_0, TM, TN, ROPE>, grid, dim3(kThreads), lds, a, rp); break;
+  case Q4_0: launch(mfma_rows_kernel<Q4_0, TM, TN, ROPE>, grid, dim3(kThreads), lds, a, rp); break;
+  case Q4_1: launch(mfma_rows_kernel<Q4_1, TM, TN, ROPE>, grid, dim3(kThreads), lds, a, rp); break;
   default: return fail(kUnsupported, "matmul rows: weight type %d", type);
   }
-  return check_launch("mfma_rows");
+  return check_launch(ROPE ? "mfma_rows (rope)" : "mfma_rows");
+}
+
+// Eight weight rows per workgroup when sixteen would leave CUs without one.
+bool rows_narrow(const MatvecArgs& a) {
+  uint32_t wg16 = 0;
+  for (int s = 0; s < a.n_seg; ++s) wg16 += static_cast<uint32_t>(ceil_div(a.seg[s].n_out, kRowsTN));
+  return static_cast<uint64_t>(wg16) * ceil_div(a.m, 16u) < 256;
 }
 
 }  // namespace
@@ -753,13 +810,9 @@ bool matmul_q8_tile_fills(const MatvecArgs& a) {
   return wg64 >= 512;
 }
 
-int matmul_q8_swiglu_launch(int type, MatvecArgs& a) {
-  MatvecArgs probe = a;
-  probe.n_seg = 2;
-  if (a.n_seg != 2 || a.outq == nullptr || a.m <= kRowsMaxM || a.seg[0].n_out != a.seg[1].n_out ||
-      a.seg[0].n_out % kQK != 0 || !matmul_q8_rows_fits(type, probe, true))
-    return fail(kUnsupported, "matmul swiglu: shape or alignment");
-  const dim3 grid(static_cast<uint32_t>(a.seg[0].n_out / 32), static_cast<uint32_t>(ceil_div(a.m, kTileRows)));
+template <uint32_t TM>
+int swiglu_launch(int type, MatvecArgs& a) {
+  const dim3 grid(static_cast<uint32_t>(a.seg[0].n_out / 32), static_cast<uint32_t>(ceil_div(a.m, TM)));
   static const bool granted = [] {
     bool ok = true;
     auto grant = [&](auto kernel, size_t lds) {
@@ -767,19 +820,34 @@ int matmul_q8_swiglu_launch(int type, MatvecArgs& a) {
         ok = ok && hipFuncSetAttribute(reinterpret_cast<const void*>(kernel), hipFuncAttributeMaxDynamicSharedMemorySize,
                                        static_cast<int>(lds)) == hipSuccess;
     };
-    grant(mfma_tile_kernel<Q8_0, 64, true>, tile_lds<Q8_0, 64>());
-    grant(mfma_tile_kernel<Q4_0, 64, true>, tile_lds<Q4_0, 64>());
-    grant(mfma_tile_kernel<Q4_1, 64, true>, tile_lds<Q4_1, 64>());
+    grant(mfma_tile_kernel<Q8_0, 64, true, TM>, tile_lds<Q8_0, 64, TM>());
+    grant(mfma_tile_kernel<Q4_0, 64, true, TM>, tile_lds<Q4_0, 64, TM>());
+    grant(mfma_tile_kernel<Q4_1, 64, true, TM>, tile_lds<Q4_1, 64, TM>());
     return ok;
   }();
   if (!granted) return fail(kUnsupported, "matmul swiglu: the LDS grant was refused");
   switch (type) {
-  case Q8_0: launch(mfma_tile_kernel<Q8_0, 64, true>, grid, dim3(kThreads), tile_lds<Q8_0, 64>(), a); break;
-  case Q4_0: launch(mfma_tile_kernel<Q4_0, 64, true>, grid, dim3(kThreads), tile_lds<Q4_0, 64>(), a); break;
-  case Q4_1: launch(mfma_tile_kernel<Q4_1, 64, true>, grid, dim3(kThreads), tile_lds<Q4_1, 64>(), a); break;
+  case Q8_0: launch(mfma_tile_kernel<Q8_0, 64, true, TM>, grid, dim3(kThreads), tile_lds<Q8_0, 64, TM>(), a); break;
+  case Q4_0: launch(mfma_tile_kernel<Q4_0, 64, true, TM>, grid, dim3(kThreads), tile_lds<Q4_0, 64, TM>(), a); break;
+  case Q4_1: launch(mfma_tile_kernel<Q4_1, 64, true, TM>, grid, dim3(kThreads), tile_lds<Q4_1, 64, TM>(), a); break;
   default: return fail(kUnsupported, "matmul swiglu: weight type %d", type);
   }
   return check_launch("mfma_tile (swiglu)");
+}
+
+int matmul_q8_swiglu_launch(int type, MatvecArgs& a) {
+  MatvecArgs probe = a;
+  probe.n_seg = 2;
+  if (a.n_seg != 2 || a.outq == nullptr || a.seg[0].n_out != a.seg[1].n_out || a.seg[0].n_out % kQK != 0 ||
+      !matmul_q8_rows_fits(type, probe, true))
+    return fail(kUnsupported, "matmul swiglu: shape or alignment");
+  // Decode-sized calls (up to kRowsMaxM rows) take the fused tile only when its one workgroup
+  // per 32 outputs fills the chip; otherwise the caller runs the matmul and silu_mul apart.
+  if (a.m <= kRowsMaxM && a.seg[0].n_out / 32 < kDecodeTileWg)
+    return fail(kUnsupported, "matmul swiglu: %u outputs give too few workgroups for %u rows", a.seg[0].n_out, a.m);
+  if (a.m <= 16) return swiglu_launch<16>(type, a);
+  if (a.m <= 32) return swiglu_launch<32>(type, a);
+  return swiglu_launch<kTileRows>(type, a);
 }
 
 int matmul_q8_tile_launch(int type, MatvecArgs& a) {
@@ -808,14 +876,15 @@ int matmul_q8_rows_launch(int type, MatvecArgs& a) {
   } else if (a.m <= 32) {
     if (wg32 >= kDecodeTileWg) return tile_launch<32, 32>(type, a);
   }
-  // Eight weight rows per workgroup when sixteen would leave CUs without one.
-  uint32_t wg16 = 0;
-  for (int s = 0; s < a.n_seg; ++s) wg16 += static_cast<uint32_t>(ceil_div(a.seg[s].n_out, kRowsTN));
   // Up to 32 rows go in tiles of 16 activation rows (two tiles along the grid's second axis
   // above 16): a workgroup of 32 rows would run twice the folds and read twice the activations
   // for the same weight rows (C4 down at 32 rows 26.9 -> 21.0 us).
-  const bool narrow = static_cast<uint64_t>(wg16) * ceil_div(a.m, 16u) < 256;
-  return narrow ? rows_launch<16, 8>(type, a) : rows_launch<16>(type, a);
+  return rows_narrow(a) ? rows_launch<16, 8>(type, a) : rows_launch<16>(type, a);
+}
+
+int matmul_q8_rows_rope_launch(int type, MatvecArgs& a, const RowsRope& rp) {
+  if (a.n_seg != 3 || !matmul_q8_rows_fits(type, a)) return fail(kUnsupported, "matmul rows (rope): shape or alignment");
+  return rows_narrow(a) ? rows_launch<16, 8, true>(type, a, rp) : rows_launch<16, kRowsTN, true>(type, a, rp);
 }
 
 int matmul_q8_mfma_launch(int type, MatvecArgs& a) {

@@ -62,6 +62,21 @@ struct FusedArgs {
 bool matvec_fused_fits(int type, int in_mode, uint32_t m, uint32_t nb, bool silu);
 int matvec_fused_launch(int type, FusedArgs& a);
 
+// The q|k|v epilogue of the few-rows MFMA kernel (rope_rows_kernel's work, for three segments
+// q, k, v): per segment bias (or null), Normal-style RoPE over the first rot_half pairs of each
+// head at pos[row] from the cos/sin table, q into seg[0].y, k and v into the cache at
+// cache_off[row] + {k,v}_layer_off + pos * kv_row (float elements, or fp16 with cache_f16).
+struct RowsRope {
+  const float* bias[3];
+  const float* table;
+  const int32_t* pos;
+  const int64_t* cache_off;
+  void* cache;
+  int64_t k_layer_off, v_layer_off;
+  uint32_t rot_half, head_dim, kv_row;
+  int cache_f16;
+};
+
 // Quantized weights (Q8_0 / Q4_0 / Q4_1) against Q8_0 activations, m <= 4 rows.
 int matvec_q8_launch(int type, MatvecArgs& a);
 // The most activation rows (1..4) one matvec launch takes at nb blocks per row.
@@ -76,6 +91,9 @@ int matvec_q6k_planar_launch(MatvecArgs& a, uint32_t n_in);
 // Test hook: 0 chooses the one-row kernel by shape; 1 the one-lane-per-row kernel, 2 the
 // products-then-chains kernel (where its LDS fits), 3 the streamed-ring kernel.
 void matvec_q6k_force_path(int path);
+// q|k|v of 1..kRowsMaxM rows on the few-rows MFMA kernel with the RowsRope epilogue
+// (kUnsupported, nothing launched, where matmul_q8_rows_fits refuses the shape).
+int matmul_q8_rows_rope_launch(int type, MatvecArgs& a, const RowsRope& rp);
 // int8 MFMA tiles for 16 or more Q8_0 activation rows.
 int matmul_q8_mfma_launch(int type, MatvecArgs& a);
 // int8 MFMA for 1..kRowsMaxM activation rows (batched decode): every segment in one grid, one

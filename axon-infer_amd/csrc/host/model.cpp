@@ -878,43 +878,86 @@ Expected<std::size_t> LlamaModel::run(std::span<const Row> rows, bool copy_logit
       const bool need_f = !q8_path(L.wq) || !q8_path(L.wk) || !q8_path(L.wv);
       DEV(axon_hip_rmsnorm_rows(x_, static_cast<const float*>(L.attn_norm.dev), need_f ? h_ : nullptr,
                                 need_q8 ? xq_ : nullptr, d, n, eps));
-      if (qkv_q8) {
-        const void* ws[3] = {L.wq.dev, L.wk.dev, L.wv.dev};
-        float* ys[3] = {q_, k_, v_};
-        const std::size_t no[3] = {dq, dkv, dkv};
+      // Up to 64 rows: q|k|v with the bias, RoPE and KV write in the matmul's epilogue.
+      bool roped = false;
+      if (qkv_q8 && c.rope_style == kernels::RopeStyle::Normal && rope_table_ != nullptr) {
+        axon_hip_matvec_fused_args fa = fused_args(L.wq);
+        fa.n_seg = 3;
+        fa.w[0] = L.wq.dev;
+        fa.w[1] = L.wk.dev;
+        fa.w[2] = L.wv.dev;
+        fa.n_out[0] = dq;
+        fa.n_out[1] = dkv;
+        fa.n_out[2] = dkv;
+        fa.in_mode = 0;
+        fa.xq = xq_;
+        fa.out_mode = 3;
+        fa.y[0] = q_;
+        fa.y_stride[0] = dq;
+        if (L.bias) {
+          fa.bias[0] = static_cast<const float*>(L.bq.dev);
+          fa.bias[1] = static_cast<const float*>(L.bk.dev);
+          fa.bias[2] = static_cast<const float*>(L.bv.dev);
+        }
+        fa.rope_table = rope_table_;
+        fa.rot_half = c.rotary_dim / 2;
+        fa.head_dim = c.head_dim;
+        fa.pos = d_pos;
+        fa.cache_off = d_coff;
+        fa.cache = kv;
+        fa.cache_f16 = kv_f16;
+        fa.k_layer_off = k_layer;
+        fa.v_layer_off = v_layer;
         probe_begin(L.wq);
-        DEV(axon_hip_matmul_q8_fused(static_cast<int>(L.wq.type), xq_, n, d, 3, ws, ys, no, no, 0));
-        probe_end(L.wq, n, dq + 2 * dkv, false);
-      } else {
-        DEV(mm(L.wq, h_, xq_, q_, n, false));
-        DEV(mm(L.wk, h_, xq_, k_, n, false));
-        DEV(mm(L.wv, h_, xq_, v_, n, false));
+        const int rc = axon_hip_matmul_q8_qkv_rope(&fa);
+        if (rc == AXON_HIP_OK) {
+          probe_end(L.wq, n, dq + 2 * dkv, false);
+          roped = true;
+        } else if (rc == AXON_HIP_E_UNSUPPORTED) {
+          probe_cancel();  // refused: nothing was launched
+        } else {
+          return device_error("matmul_q8_qkv_rope");
+        }
       }
-      axon_hip_rope_rows_args ra{};
-      ra.q = q_;
-      ra.k = k_;
-      ra.v = v_;
-      if (L.bias) {
-        ra.bq = static_cast<const float*>(L.bq.dev);
-        ra.bk = static_cast<const float*>(L.bk.dev);
-        ra.bv = static_cast<const float*>(L.bv.dev);
+      if (!roped) {
+        if (qkv_q8) {
+          const void* ws[3] = {L.wq.dev, L.wk.dev, L.wv.dev};
+          float* ys[3] = {q_, k_, v_};
+          const std::size_t no[3] = {dq, dkv, dkv};
+          probe_begin(L.wq);
+          DEV(axon_hip_matmul_q8_fused(static_cast<int>(L.wq.type), xq_, n, d, 3, ws, ys, no, no, 0));
+          probe_end(L.wq, n, dq + 2 * dkv, false);
+        } else {
+          DEV(mm(L.wq, h_, xq_, q_, n, false));
+          DEV(mm(L.wk, h_, xq_, k_, n, false));
+          DEV(mm(L.wv, h_, xq_, v_, n, false));
+        }
+        axon_hip_rope_rows_args ra{};
+        ra.q = q_;
+        ra.k = k_;
+        ra.v = v_;
+        if (L.bias) {
+          ra.bq = static_cast<const float*>(L.bq.dev);
+          ra.bk = static_cast<const float*>(L.bk.dev);
+          ra.bv = static_cast<const float*>(L.bv.dev);
+        }
+        ra.pos = d_pos;
+        ra.q_stride = static_cast<std::uint32_t>(dq);
+        ra.k_stride = static_cast<std::uint32_t>(dkv);
+        ra.n_head = c.n_head;
+        ra.n_kv = c.n_head_kv;
+        ra.head_dim = c.head_dim;
+        ra.rotary_dim = c.rotary_dim;
+        ra.neox = c.rope_style == kernels::RopeStyle::NeoX ? 1 : 0;
+        ra.theta = c.rope_theta;
+        ra.table = rope_table_;
+        ra.cache = kv;
+        ra.cache_f16 = kv_f16;
+        ra.cache_off = d_coff;
+        ra.k_layer_off = k_layer;
+        ra.v_layer_off = v_layer;
+        DEV(axon_hip_rope_rows(&ra, n));
       }
-      ra.pos = d_pos;
-      ra.q_stride = static_cast<std::uint32_t>(dq);
-      ra.k_stride = static_cast<std::uint32_t>(dkv);
-      ra.n_head = c.n_head;
-      ra.n_kv = c.n_head_kv;
-      ra.head_dim = c.head_dim;
-      ra.rotary_dim = c.rotary_dim;
-      ra.neox = c.rope_style == kernels::RopeStyle::NeoX ? 1 : 0;
-      ra.theta = c.rope_theta;
-      ra.table = rope_table_;
-      ra.cache = kv;
-      ra.cache_f16 = kv_f16;
-      ra.cache_off = d_coff;
-      ra.k_layer_off = k_layer;
-      ra.v_layer_off = v_layer;
-      DEV(axon_hip_rope_rows(&ra, n));
     }
 
     const bool wo_fused = fused_ok(L.wo, 0, dq, false);
@@ -1020,11 +1063,12 @@ Expected<std::size_t> LlamaModel::run(std::span<const Row> rows, bool copy_logit
     const bool ff_f = !q8_path(L.w_gate) || !q8_path(L.w_up);
     DEV(axon_hip_rmsnorm_rows(x_, static_cast<const float*>(L.ffn_norm.dev), ff_f ? h_ : nullptr,
                               ff_q8 ? xq_ : nullptr, d, n, eps));
-    // Many rows: gate|up, SiLU and down's Q8_0 input in one tile launch, the blocks into tmp_
-    // (xq_ is still being read as its input).
+    // gate|up, SiLU and down's Q8_0 input in one tile launch, the blocks into tmp_ (xq_ is
+    // still being read as its input); the launcher refuses decode-sized calls whose FFN is too
+    // narrow to fill the chip, and those run the matmul and silu_mul apart.
     const void* down_xq = xq_;
     bool swiglu = false;
-    if (gu_q8 && q8_path(L.w_down) && n > 64 && ff % 32 == 0) {
+    if (gu_q8 && q8_path(L.w_down) && ff % 32 == 0) {
       probe_begin(L.w_gate);
       const int rc = axon_hip_matmul_q8_swiglu(static_cast<int>(L.w_gate.type), xq_, n, d, L.w_gate.dev, L.w_up.dev,
                                                ff, nullptr, tmp_);

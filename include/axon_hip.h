@@ -225,12 +225,12 @@ int axon_hip_topk_rows(const float* x, size_t n, size_t n_rows, size_t stride, s
 size_t axon_hip_sort_rows_work_bytes(size_t n, size_t n_rows);
 int axon_hip_sort_rows(const float* x, size_t n, size_t n_rows, size_t stride, void* work, float* out_logit,
                        int32_t* out_id);
-/* gate|up with the SwiGLU product and its Q8_0 quantization in one launch, for 65 or more
- * rows (llama.cpp:600-620: out = silu(x W_gate^T) * (x W_up^T), then quantize_row_q8_0 of each
- * row for w_down): the same bits as matmul_q8_fused of the two weights, silu_mul_rows and
- * quantize_rows. out: float [n_rows][n_ff] or NULL; outq: [n_rows][n_ff / 32] Q8_0 blocks, which
- * must not alias xq. n_ff a multiple of 32. AXON_HIP_E_UNSUPPORTED (nothing launched) for fewer
- * rows or bases the tile kernel cannot load. */
+/* gate|up with the SwiGLU product and its Q8_0 quantization in one launch (llama.cpp:600-620:
+ * out = silu(x W_gate^T) * (x W_up^T), then quantize_row_q8_0 of each row for w_down): the same
+ * bits as matmul_q8_fused of the two weights, silu_mul_rows and quantize_rows. out: float
+ * [n_rows][n_ff] or NULL; outq: [n_rows][n_ff / 32] Q8_0 blocks, which must not alias xq. n_ff a
+ * multiple of 32. AXON_HIP_E_UNSUPPORTED (nothing launched) for up to 64 rows with n_ff below
+ * 8192 (too few workgroups to fill the chip), or bases the tile kernel cannot load. */
 int axon_hip_matmul_q8_swiglu(int type, const void* xq, size_t n_rows, size_t n_in, const void* w_gate,
                               const void* w_up, size_t n_ff, float* out, void* outq);
 
@@ -330,6 +330,14 @@ typedef struct {
 int axon_hip_matvec_fused(const axon_hip_matvec_fused_args* args);
 /* 1 when axon_hip_matvec_fused takes this shape (rows, row length, input mode, SiLU pairing). */
 int axon_hip_matvec_fused_supported(int type, int in_mode, size_t n_rows, size_t n_in, int silu);
+/* q|k|v of 1..64 rows of Q8_0 blocks with the bias, Normal-style RoPE and KV write folded into
+ * the int8 MFMA matmul's epilogue (llama.cpp:493-537; replaces matmul_q8_fused followed by
+ * rope_rows, kernels/ref/rope.cpp:13-37, with the same bits). The fields of
+ * axon_hip_matvec_fused_args with n_seg 3, in_mode 0 (xq) and out_mode 3: q into y[0] (row
+ * stride y_stride[0]), k and v into the cache as axon_hip_matvec_fused writes them; norm_w, x
+ * and outq are not read. AXON_HIP_E_UNSUPPORTED (nothing launched) above 64 rows or for bases
+ * the kernel's dword loads cannot take. */
+int axon_hip_matmul_q8_qkv_rope(const axon_hip_matvec_fused_args* args);
 
 /* Every layer of one decode row as a single persistent kernel (llama.cpp:487-623 for a batch of
  * one): per layer, attn_norm, q|k|v, bias, RoPE (Normal style) and the KV write at pos, the

@@ -302,6 +302,106 @@ def quantized_rows(o, x_rows):
     return np.concatenate([o.quantize_row_q8_0(r) for r in x_rows])
 
 
+def qkv_rope(H, **kw):
+    a = H.MatvecFusedArgs()
+    for k, v in kw.items():
+        if k in ("w", "y", "bias"):
+            arr = getattr(a, k)
+            for i, b in enumerate(v):
+                arr[i] = H.ptr_of(b)
+        elif k in ("n_out", "y_stride"):
+            arr = getattr(a, k)
+            for i, b in enumerate(v):
+                arr[i] = b
+        elif isinstance(v, H.DeviceBuffer):
+            setattr(a, k, v.ptr)
+        else:
+            setattr(a, k, v)
+    H.check(H.lib().axon_hip_matmul_q8_qkv_rope(C.byref(a)), "matmul_q8_qkv_rope")
+
+
+@pytest.mark.parametrize("kind", KINDS)
+@pytest.mark.parametrize("n_rows", [1, 5, 16, 17, 33, 64])
+@pytest.mark.parametrize("d,n_head,n_kv,hd,rot,bias", [(2048, 32, 8, 64, 64, False), (896, 14, 2, 64, 64, True),
+                                                       (256, 4, 2, 64, 32, True)])
+@pytest.mark.parametrize("f16", [0, 1])
+def test_rows_qkv_rope_matches_unfused(H, o, kind, n_rows, d, n_head, n_kv, hd, rot, bias, f16):
+    """axon_hip_matmul_q8_qkv_rope: q|k|v of 1..64 Q8_0 rows on the MFMA rows kernel with the
+    bias, Normal-style RoPE and the KV write in its epilogue, against matmul_q8_fused + rope_rows
+    over the same pool, bit for bit, with a float and an fp16 cache (workgroups of 8 and of 16
+    weight rows both occur: the narrow form below 256 workgroups); q also against the oracle."""
+    dq, dkv = n_head * hd, n_kv * hd
+    max_ctx = 40
+    rng = np.random.default_rng(d + n_rows + rot + 7 * f16)
+    x = random_floats(n_rows * d, d + n_rows * 5, 2.0).reshape(n_rows, d)
+    dxq = H.DeviceBuffer.of(quantized_rows(o, x))
+    ws = [random_weights(kind, n, d, n + d + s + 1) for s, n in enumerate((dq, dkv, dkv))]
+    bs = [random_floats(n, n + s + 2, 0.5) for s, n in enumerate((dq, dkv, dkv))] if bias else [None] * 3
+    pos = rng.integers(0, max_ctx, n_rows).astype(np.int32)
+    slot = 2 * 3 * max_ctx * dkv
+    coff = (rng.permutation(n_rows + 1)[:n_rows] * slot).astype(np.int64)
+    k_layer, v_layer = 2 * max_ctx * dkv, 3 * max_ctx * dkv
+    if f16:
+        pool0 = rng.integers(0, 0x7bff, (n_rows + 1) * slot).astype(np.uint16)
+    else:
+        pool0 = rng.normal(0, 1, (n_rows + 1) * slot).astype(np.float32)
+    table = rope_table(max_ctx, rot, 10000.0)
+    dtab, dpos, dcoff = (H.DeviceBuffer.of(a) for a in (table, pos, coff))
+    dws = [H.DeviceBuffer.of(w) for w in ws]
+    dbs = [H.DeviceBuffer.of(b) if b is not None else None for b in bs]
+    pool, pool2 = H.DeviceBuffer.of(pool0), H.DeviceBuffer.of(pool0)
+    q = H.DeviceBuffer.of(np.full((n_rows, dq + 3), -1.0, np.float32))
+    qkv_rope(H, type=TYPE_ID[kind], n_seg=3, w=dws, n_out=[dq, dkv, dkv], n_rows=n_rows, n_in=d, in_mode=0, xq=dxq,
+             out_mode=3, y=[q], y_stride=[dq + 3], bias=dbs, rope_table=dtab, rot_half=rot // 2, head_dim=hd,
+             pos=dpos, cache_off=dcoff, cache=pool, cache_f16=f16, k_layer_off=k_layer, v_layer_off=v_layer)
+    got_q = q.download(np.float32).reshape(n_rows, dq + 3)
+    assert (got_q[:, dq:] == -1.0).all()  # the stride's padding is not written
+    got_q = got_q[:, :dq]
+
+    q2, k2, v2 = (H.DeviceBuffer(n_rows * n * 4) for n in (dq, dkv, dkv))
+    unfused_matmul(H, kind, dxq, n_rows, d, dws, [q2, k2, v2], [dq, dkv, dkv], [dq, dkv, dkv], False)
+    ra = H.RopeRowsArgs(q=q2.ptr, k=k2.ptr, v=v2.ptr, bq=H.ptr_of(dbs[0]), bk=H.ptr_of(dbs[1]), bv=H.ptr_of(dbs[2]),
+                        pos=dpos.ptr, pos0=0, q_stride=dq, k_stride=dkv, n_head=n_head, n_kv=n_kv, head_dim=hd,
+                        rotary_dim=rot, neox=0, theta=10000.0, freq_factors=0, table=dtab.ptr, cache=pool2.ptr,
+                        cache_off=dcoff.ptr, k_layer_off=k_layer, v_layer_off=v_layer, cache_f16=f16)
+    H.check(H.lib().axon_hip_rope_rows(C.byref(ra), C.c_size_t(n_rows)), "rope_rows")
+    assert np.array_equal(got_q.view(np.uint32), q2.download(np.uint32).reshape(n_rows, dq))
+    dt = np.uint16 if f16 else np.uint32
+    got_pool, want_pool = pool.download(dt), pool2.download(dt)
+    assert np.array_equal(got_pool, want_pool)
+    changed = np.flatnonzero(got_pool != pool0.view(dt))
+    allowed = np.concatenate([c + lo + p * dkv + np.arange(dkv) for c, p in zip(coff, pos) for lo in (k_layer, v_layer)])
+    assert np.isin(changed, allowed).all()
+    if n_rows <= 17:
+        oq = oracle_rows(o, kind, ws[0], x, dq, d)
+        if bias:
+            oq = oq + bs[0]
+        for i in range(n_rows):
+            want = o.rope(oq[i], n_head, int(pos[i]), hd, rot, 10000.0, 0)
+            assert np.max(np.abs(got_q[i] - want)) <= 2e-6 * max(1.0, float(np.max(np.abs(want)))), i
+
+
+def test_rows_qkv_rope_refusals(H, o):
+    """More than 64 rows, or blocks off a 4-byte boundary: E_UNSUPPORTED with nothing launched
+    (the forward pass then runs matmul_q8_fused and rope_rows); malformed arguments: errors."""
+    d, dq, dkv, hd = 256, 256, 128, 64
+    dws = [H.DeviceBuffer.of(random_weights("q8_0", n, d, n + 1)) for n in (dq, dkv, dkv)]
+    dxq = H.DeviceBuffer(65 * 8 * 34 + 16)
+    q, pool = H.DeviceBuffer(65 * dq * 4), H.DeviceBuffer(4 * dkv * 4)
+    table = H.DeviceBuffer.of(rope_table(4, hd, 10000.0))
+    zeros = H.DeviceBuffer.of(np.zeros(65, np.int64))
+    base = dict(type=TYPE_ID["q8_0"], n_seg=3, w=dws, n_out=[dq, dkv, dkv], n_rows=4, n_in=d, in_mode=0, xq=dxq,
+                out_mode=3, y=[q], y_stride=[dq], rope_table=table, rot_half=hd // 2, head_dim=hd, pos=zeros,
+                cache_off=zeros, cache=pool)
+    for bad in (dict(n_rows=65), dict(xq=dxq.ptr + 2)):
+        with pytest.raises(H.HipError, match="status -2"):
+            qkv_rope(H, **{**base, **bad})
+    for bad in (dict(n_seg=2), dict(in_mode=2), dict(out_mode=0), dict(n_in=48), dict(head_dim=63),
+                dict(rot_half=33), dict(n_out=[dq, dkv, dkv - 2]), dict(pos=0), dict(y_stride=[dq - 1])):
+        with pytest.raises(H.HipError, match="status -1"):
+            qkv_rope(H, **{**base, **bad})
+
+
 @pytest.mark.parametrize("kind", KINDS)
 @pytest.mark.parametrize("n_rows", [1, 2, 3, 4])
 @pytest.mark.parametrize("n_in,n_out,out_mode", [(2048, 2048, 0), (2048, 1153, 1), (8192, 2048, 1), (576, 576, 1),
