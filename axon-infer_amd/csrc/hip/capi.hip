@@ -596,6 +596,37 @@ int axon_hip_matmul_q6_k_planar(const void* planar, const float* x, float* y, si
   return matvec_q6k_planar_launch(a, static_cast<uint32_t>(n_in));
 }
 
+size_t axon_hip_q6k_argmax_parts(size_t n_out) {
+  return n_out == 0 || !fits_u32(n_out) ? 0 : q6k_planar_argmax_parts(static_cast<uint32_t>(n_out));
+}
+
+int axon_hip_matmul_q6_k_planar_argmax(const void* planar, const float* x, float* y, size_t n_out, size_t n_in,
+                                       uint64_t* keys, size_t key_words) {
+  AXON_READY();
+  if (n_in % kQKK != 0) return fail(kInvalidArgument, "matmul_q6_k_planar_argmax: n_in %zu is not a multiple of 256", n_in);
+  if (n_out == 0 || !fits_u32(n_out) || !fits_u32(n_in)) return fail(kInvalidArgument, "matmul_q6_k_planar_argmax: %zu outputs", n_out);
+  if (keys == nullptr || key_words < axon_hip_q6k_argmax_parts(n_out))
+    return fail(kInvalidArgument, "matmul_q6_k_planar_argmax: %zu key words for %zu outputs", key_words, n_out);
+  MatvecArgs a{};
+  a.seg[0] = MatvecSeg{static_cast<const uint8_t*>(planar), y, static_cast<uint32_t>(n_out), static_cast<uint32_t>(n_out), 0};
+  a.n_seg = 1;
+  a.xq = reinterpret_cast<const uint8_t*>(x);
+  a.nb = static_cast<uint32_t>(n_in / kQKK);
+  a.m = 1;
+  a.argmax_part = keys;
+  return matvec_q6k_planar_launch(a, static_cast<uint32_t>(n_in));
+}
+
+int axon_hip_argmax_embed(const float* x, const uint64_t* keys, size_t n_keys, int32_t* out, int type,
+                          const void* table, size_t table_rows, size_t n, float* emb) {
+  AXON_READY();
+  if (!fits_u32(n_keys) || !fits_u32(n) || !fits_u32(table_rows)) return fail(kInvalidArgument, "argmax_embed: sizes too large");
+  if (x == nullptr || keys == nullptr || out == nullptr || table == nullptr || emb == nullptr)
+    return fail(kInvalidArgument, "argmax_embed: null pointer");
+  return argmax_embed_launch(x, keys, static_cast<uint32_t>(n_keys), out, type, static_cast<const uint8_t*>(table),
+                             static_cast<uint32_t>(table_rows), static_cast<uint32_t>(n), emb);
+}
+
 int axon_hip_q6k_force_path(int path) {
   if (path < 0 || path > 3) return fail(kInvalidArgument, "q6k_force_path: path %d (0-3)", path);
   matvec_q6k_force_path(path);

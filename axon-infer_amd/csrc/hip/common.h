@@ -282,6 +282,26 @@ __device__ __forceinline__ void quantize_block_lanes(float x, uint32_t lane, uin
 }
 
 // ------------------------------------------------------------------------------------------
+// Greedy selection keys: (value, index) packed so that the largest key is the first maximum
+// (std::ranges::max_element): the value's bits mapped to an unsigned order (-0 as +0) above the
+// complemented index. Key 0 stands for "no value" (NaN is never a key).
+__device__ __forceinline__ uint64_t argmax_key(float v, uint32_t i) {
+  uint32_t b = __float_as_uint(v);
+  if (b == 0x80000000u) b = 0;  // -0 == +0
+  const uint32_t ord = (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+  return (static_cast<uint64_t>(ord) << 32) | static_cast<uint64_t>(~i);
+}
+
+__device__ __forceinline__ uint64_t max_key_wave(uint64_t k) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) {
+    const uint64_t o = __shfl_xor(k, off, 64);
+    k = o > k ? o : k;
+  }
+  return k;
+}
+
+// ------------------------------------------------------------------------------------------
 // Whole-row work for one 256-thread workgroup, shared by the standalone kernels and the fused
 // matvec's prologue, so that both produce the same bits.
 

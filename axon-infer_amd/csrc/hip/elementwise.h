@@ -56,6 +56,10 @@ int argmax_rows_noalloc_launch(const float* x, uint32_t n, uint32_t n_rows, size
 int rope_rows_launch(const RopeRowsArgs& a, uint32_t n_rows);
 int embedding_launch(int type, const uint8_t* table, uint32_t n, const int32_t* ids, int64_t id0, uint32_t n_rows,
                      float* out);
+// The greedy id of one logits row x from n_parts partial keys (argmax_key), into *out_id, and that
+// token's row of an embedding table of table_rows rows into emb[n].
+int argmax_embed_launch(const float* x, const uint64_t* part, uint32_t n_parts, int32_t* out_id, int type,
+                        const uint8_t* table, uint32_t table_rows, uint32_t n, float* emb);
 
 // Attention over per-row KV spans. Row r reads its query at q + r * q_stride and attends over
 // positions 0 .. n_vis(r) - 1 of K/V rows [pos][n_kv][head_dim] starting at

@@ -249,39 +249,28 @@ __global__ __launch_bounds__(256) void rope_rows_kernel(RopeRowsArgs a) {
   }
 }
 
-// embedding_row (src/kernels/ref/embedding.cpp:12-64) for a list of token ids: row ids[r] of
-// the table, dequantized exactly as dtype.cpp:274-336 does, into out[r][n].
-__global__ __launch_bounds__(256) void embedding_kernel(int type, const uint8_t* __restrict__ table, uint32_t n,
-                                                        const int32_t* __restrict__ ids, int64_t id0,
-                                                        float* __restrict__ out) {
-  const uint32_t r = blockIdx.y;
-  const int64_t row = ids != nullptr ? ids[r] : id0;
-  float* o = out + static_cast<size_t>(r) * n;
-  const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
-  if (i >= n) return;
+// embedding_row (src/kernels/ref/embedding.cpp:12-64): element i of row `row` of an n-wide
+// table, dequantized exactly as dtype.cpp:274-336 does (types checked by the launchers).
+__device__ __forceinline__ float embed_value(int type, const uint8_t* __restrict__ table, uint32_t n, int64_t row,
+                                             uint32_t i) {
   switch (type) {
   case F32:
-    o[i] = reinterpret_cast<const float*>(table)[row * n + i];
-    break;
+    return reinterpret_cast<const float*>(table)[row * n + i];
   case F16:
-    o[i] = half_bits_to_float(reinterpret_cast<const uint16_t*>(table)[row * n + i]);
-    break;
+    return half_bits_to_float(reinterpret_cast<const uint16_t*>(table)[row * n + i]);
   case BF16:
-    o[i] = bf16_bits_to_float(reinterpret_cast<const uint16_t*>(table)[row * n + i]);
-    break;
+    return bf16_bits_to_float(reinterpret_cast<const uint16_t*>(table)[row * n + i]);
   case Q8_0: {
     const uint8_t* blk = table + (row * (n / kQK) + i / kQK) * kBytesQ8_0;
     const float d = half_bits_to_float(*reinterpret_cast<const uint16_t*>(blk));
-    o[i] = static_cast<float>(static_cast<int8_t>(blk[2 + i % kQK])) * d;
-    break;
+    return static_cast<float>(static_cast<int8_t>(blk[2 + i % kQK])) * d;
   }
   case Q4_0: {
     const uint8_t* blk = table + (row * (n / kQK) + i / kQK) * kBytesQ4_0;
     const float d = half_bits_to_float(*reinterpret_cast<const uint16_t*>(blk));
     const uint32_t e = i % kQK;
     const int nib = e < 16 ? (blk[2 + e] & 0x0f) : (blk[2 + e - 16] >> 4);
-    o[i] = static_cast<float>(nib - 8) * d;
-    break;
+    return static_cast<float>(nib - 8) * d;
   }
   case Q4_1: {
     const uint8_t* blk = table + (row * (n / kQK) + i / kQK) * kBytesQ4_1;
@@ -289,8 +278,7 @@ __global__ __launch_bounds__(256) void embedding_kernel(int type, const uint8_t*
     const float m = half_bits_to_float(*reinterpret_cast<const uint16_t*>(blk + 2));
     const uint32_t e = i % kQK;
     const int nib = e < 16 ? (blk[4 + e] & 0x0f) : (blk[4 + e - 16] >> 4);
-    o[i] = static_cast<float>(nib) * d + m;
-    break;
+    return static_cast<float>(nib) * d + m;
   }
   case Q6_K: {
     const uint8_t* blk = table + (row * (n / kQKK) + i / kQKK) * kBytesQ6_K;
@@ -307,12 +295,48 @@ __global__ __launch_bounds__(256) void embedding_kernel(int type, const uint8_t*
     const uint32_t hibits = (qh[l] >> (2 * quarter)) & 3u;
     const int q = static_cast<int>(lowbits | (hibits << 4)) - 32;
     const float d = half_bits_to_float(*reinterpret_cast<const uint16_t*>(blk + 208));
-    o[i] = d * static_cast<float>(sc[l / 16 + 2 * quarter]) * static_cast<float>(q);
-    break;
+    return d * static_cast<float>(sc[l / 16 + 2 * quarter]) * static_cast<float>(q);
   }
   default:
-    break;
+    return 0.0f;
   }
+}
+
+// embedding_row for a list of token ids: row ids[r] of the table into out[r][n].
+__global__ __launch_bounds__(256) void embedding_kernel(int type, const uint8_t* __restrict__ table, uint32_t n,
+                                                        const int32_t* __restrict__ ids, int64_t id0,
+                                                        float* __restrict__ out) {
+  const uint32_t r = blockIdx.y;
+  const int64_t row = ids != nullptr ? ids[r] : id0;
+  const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  out[static_cast<size_t>(r) * n + i] = embed_value(type, table, n, row, i);
+}
+
+// The greedy choice of one logits row from its n_parts partial keys (argmax_final_kernel's rule:
+// the largest key, index 0 when the row's first value is NaN or no key exists), then that
+// token's embedding row: every workgroup reduces the keys (a few KB) and embeds its 256
+// elements; workgroup 0 writes the id.
+__global__ __launch_bounds__(256) void argmax_embed_kernel(const float* __restrict__ x,
+                                                           const uint64_t* __restrict__ part, uint32_t n_parts,
+                                                           int32_t* __restrict__ out_id, int type,
+                                                           const uint8_t* __restrict__ table, uint32_t table_rows,
+                                                           uint32_t n, float* __restrict__ emb) {
+  __shared__ uint64_t red[4];
+  uint64_t k = 0;
+  for (uint32_t j = threadIdx.x; j < n_parts; j += 256) k = part[j] > k ? part[j] : k;
+  k = max_key_wave(k);
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = k;
+  __syncthreads();
+  k = red[0];
+  for (int w = 1; w < 4; ++w) k = red[w] > k ? red[w] : k;
+  const float first = x[0];
+  const int32_t id = (first != first || k == 0) ? 0 : static_cast<int32_t>(~static_cast<uint32_t>(k & 0xffffffffu));
+  if (blockIdx.x == 0 && threadIdx.x == 0) *out_id = id;
+  // The keys index a row of at most table_rows values; the clamp only keeps a caller's mismatch
+  // inside the table.
+  const uint32_t i = blockIdx.x * 256 + threadIdx.x;
+  if (i < n) emb[i] = embed_value(type, table, n, min(static_cast<uint32_t>(id), table_rows - 1), i);
 }
 
 }  // namespace
@@ -369,9 +393,8 @@ int rope_rows_launch(const RopeRowsArgs& a, uint32_t n_rows) {
   return check_launch("rope_rows");
 }
 
-int embedding_launch(int type, const uint8_t* table, uint32_t n, const int32_t* ids, int64_t id0, uint32_t n_rows,
-                     float* out) {
-  if (n == 0 || n_rows == 0) return kOk;
+namespace {
+int embedding_check(int type, uint32_t n) {
   switch (type) {
   case F32: case F16: case BF16: break;
   case Q8_0: case Q4_0: case Q4_1:
@@ -383,9 +406,27 @@ int embedding_launch(int type, const uint8_t* table, uint32_t n, const int32_t* 
   default:
     return fail(kUnsupported, "embedding_row: unsupported dtype %d", type);
   }
+  return kOk;
+}
+}  // namespace
+
+int embedding_launch(int type, const uint8_t* table, uint32_t n, const int32_t* ids, int64_t id0, uint32_t n_rows,
+                     float* out) {
+  if (n == 0 || n_rows == 0) return kOk;
+  if (const int rc = embedding_check(type, n); rc != kOk) return rc;
   const dim3 grid(static_cast<uint32_t>(ceil_div(n, 256)), n_rows);
   hipLaunchKernelGGL(embedding_kernel, grid, dim3(256), 0, stream(), type, table, n, ids, id0, out);
   return check_launch("embedding");
+}
+
+int argmax_embed_launch(const float* x, const uint64_t* part, uint32_t n_parts, int32_t* out_id, int type,
+                        const uint8_t* table, uint32_t table_rows, uint32_t n, float* emb) {
+  if (n == 0 || n_parts == 0 || table_rows == 0)
+    return fail(kInvalidArgument, "argmax_embed: %u keys, %u table rows of %u", n_parts, table_rows, n);
+  if (const int rc = embedding_check(type, n); rc != kOk) return rc;
+  hipLaunchKernelGGL(argmax_embed_kernel, dim3(static_cast<uint32_t>(ceil_div(n, 256))), dim3(256), 0, stream(), x,
+                     part, n_parts, out_id, type, table, table_rows, n, emb);
+  return check_launch("argmax_embed");
 }
 
 }  // namespace axon_hip

@@ -25,6 +25,7 @@ struct MatvecArgs {
   int n_seg;
   int accumulate;     // y += W x instead of y = W x
   uint8_t* outq;      // the SwiGLU tile path: Q8_0 blocks of each output row
+  uint64_t* argmax_part;  // one-row planar Q6_K: each workgroup's greedy key of its outputs, or null
 };
 
 // The fused decode matvec (matvec_fused.hip): input prologue and output epilogue modes.
@@ -88,6 +89,9 @@ int matvec_q6k_launch(MatvecArgs& a, uint32_t n_in);
 size_t q6k_planar_column_bytes(uint32_t n_out);
 int q6k_repack_launch(const uint8_t* src, uint8_t* dst, uint32_t n_out, uint32_t nsb);
 int matvec_q6k_planar_launch(MatvecArgs& a, uint32_t n_in);
+// With a.argmax_part set (one activation row): the one-lane-per-row kernel, which also leaves
+// q6k_planar_argmax_parts(n_out) greedy keys (argmax_key of each workgroup's first maximum).
+uint32_t q6k_planar_argmax_parts(uint32_t n_out);
 // Test hook: 0 chooses the one-row kernel by shape; 1 the one-lane-per-row kernel, 2 the
 // products-then-chains kernel (where its LDS fits), 3 the streamed-ring kernel.
 void matvec_q6k_force_path(int path);

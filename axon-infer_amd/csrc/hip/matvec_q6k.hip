@@ -405,8 +405,12 @@ __global__ __launch_bounds__(TH) void q6k_planar_kernel(MatvecArgs args, uint32_
     }
     __syncthreads();
   }
-  const uint32_t row = blockIdx.y * TH + tid;
-  if (row >= seg.n_out) return;
+  const uint32_t row_id = blockIdx.y * TH + tid;
+  // With greedy keys to form, every lane stays to the end (the reduction needs them all): a lane
+  // past the last row reads the last row and neither stores nor offers a key.
+  if (row_id >= seg.n_out && (MM != 1 || args.argmax_part == nullptr)) return;
+  const bool live = row_id < seg.n_out;
+  const uint32_t row = live ? row_id : seg.n_out - 1;
   float acc[MM];
 #pragma unroll
   for (int m = 0; m < MM; ++m) acc[m] = 0.0f;
@@ -422,7 +426,22 @@ __global__ __launch_bounds__(TH) void q6k_planar_kernel(MatvecArgs args, uint32_
   }
 #pragma unroll
   for (int m = 0; m < MM; ++m)
-    if (m < static_cast<int>(mm)) seg.y[static_cast<size_t>(m0 + m) * seg.y_stride + row] = acc[m];
+    if (live && m < static_cast<int>(mm)) seg.y[static_cast<size_t>(m0 + m) * seg.y_stride + row] = acc[m];
+  if constexpr (MM == 1) {
+    if (args.argmax_part != nullptr) {
+      // argmax_partial_kernel's key over this workgroup's outputs (NaN never a key).
+      __shared__ uint64_t red[TH / 64];
+      uint64_t key = live && acc[0] == acc[0] ? argmax_key(acc[0], row) : 0;
+      key = max_key_wave(key);
+      if (TH > 64) {
+        if ((tid & 63) == 0) red[tid >> 6] = key;
+        __syncthreads();
+        if (tid == 0)
+          for (uint32_t w = 1; w < TH / 64; ++w) key = red[w] > key ? red[w] : key;
+      }
+      if (tid == 0) args.argmax_part[blockIdx.y] = key;
+    }
+  }
 }
 
 // One activation row against a short matrix: R output rows per workgroup, the products apart
@@ -791,6 +810,13 @@ int one_row_path(uint32_t n_out, uint32_t nsb) {
 
 void matvec_q6k_force_path(int path) { g_q6k_path.store(path, std::memory_order_relaxed); }
 
+// The one-lane-per-row kernel's workgroups for one activation row: the launcher's choice of 256
+// or 64 rows per workgroup with a single chunk of rows.
+uint32_t q6k_planar_argmax_parts(uint32_t n_out) {
+  const bool wide = ceil_div(n_out, 256) >= 256;
+  return static_cast<uint32_t>(ceil_div(n_out, wide ? 256 : 64));
+}
+
 int matvec_q6k_planar_launch(MatvecArgs& a, uint32_t n_in) {
   const uint32_t n_out = a.seg[0].n_out;
   if (a.m == 0 || n_out == 0) return kOk;
@@ -801,6 +827,11 @@ int matvec_q6k_planar_launch(MatvecArgs& a, uint32_t n_in) {
     return fail(kInvalidArgument, "matmul_q6_k_planar: the planar weights and the activations must be 16-byte aligned");
   const size_t col_bytes = q6k_planar_column_bytes(n_out);
   int path = g_q6k_path.load(std::memory_order_relaxed);
+  if (a.argmax_part != nullptr) {
+    // Greedy keys come from the one-lane-per-row kernel alone.
+    if (a.m != 1) return fail(kInvalidArgument, "matmul_q6_k_planar: greedy keys for %u rows (one row only)", a.m);
+    path = 1;
+  }
   if (a.m == 1 && path == 0) path = one_row_path(n_out, a.nb);
   // One activation row: the streamed-ring kernel, 64 output rows per workgroup.
   if (a.m == 1 && path == 3 && ring_granted()) {

@@ -38,22 +38,6 @@ namespace {
 constexpr uint32_t kParts = 64;
 constexpr uint32_t kThreads = 256;
 
-__device__ __forceinline__ uint64_t argmax_key(float v, uint32_t i) {
-  uint32_t b = __float_as_uint(v);
-  if (b == 0x80000000u) b = 0;  // -0 == +0
-  const uint32_t ord = (b & 0x80000000u) ? ~b : (b | 0x80000000u);
-  return (static_cast<uint64_t>(ord) << 32) | static_cast<uint64_t>(~i);
-}
-
-__device__ __forceinline__ uint64_t max_key_wave(uint64_t k) {
-#pragma unroll
-  for (int off = 32; off > 0; off >>= 1) {
-    const uint64_t o = __shfl_xor(k, off, 64);
-    k = o > k ? o : k;
-  }
-  return k;
-}
-
 __global__ __launch_bounds__(kThreads) void argmax_partial_kernel(const float* __restrict__ x, uint32_t n,
                                                                   size_t stride, uint64_t* __restrict__ part) {
   __shared__ uint64_t red[kThreads / 64];

@@ -327,8 +327,10 @@ Expected<std::unique_ptr<LlamaModel>> LlamaModel::load(const std::string& path, 
   if (axon_hip_malloc(&m->xq_, R * (widest / 32) * sizeof(BlockQ8_0) + 64) != AXON_HIP_OK)
     return m->device_error("activation blocks");
   const std::size_t info_bytes = align_up(12 * R, 8) + 8 * R;
-  if (axon_hip_malloc(reinterpret_cast<void**>(&m->argmax_scratch_), axon_hip_argmax_scratch_words(R) * 8) !=
-          AXON_HIP_OK ||
+  // The greedy keys: argmax_rows' partials for R rows, or one key per workgroup of the planar
+  // Q6_K output (generate_greedy), whichever is more.
+  m->argmax_words_ = std::max(axon_hip_argmax_scratch_words(R), axon_hip_q6k_argmax_parts(c.n_vocab));
+  if (axon_hip_malloc(reinterpret_cast<void**>(&m->argmax_scratch_), m->argmax_words_ * 8) != AXON_HIP_OK ||
       axon_hip_malloc(reinterpret_cast<void**>(&m->ids_), R * 4) != AXON_HIP_OK ||
       axon_hip_malloc(reinterpret_cast<void**>(&m->gen_ids_), (m->max_ctx_ + 1) * 4) != AXON_HIP_OK ||
       axon_hip_malloc(&m->cand_, R * AXON_HIP_MAX_TOPK * 8) != AXON_HIP_OK)
@@ -1197,12 +1199,19 @@ Expected<std::size_t> LlamaModel::generate_greedy(KVCache& cache, std::int32_t t
   const float scale = 1.0f / std::sqrt(static_cast<float>(c.head_dim));
   const bool out_fused = !exact_ && q8_path(output_) &&
                          axon_hip_matvec_fused_supported(static_cast<int>(output_.type), 2, 1, d, false) == 1;
+  // The planar Q6_K output leaves greedy keys behind, and one launch then takes the choice and
+  // the next step's embedding (two launches fewer per token).
+  const bool out_keys = !out_fused && output_.type == DType::Q6_K && output_.planar != nullptr &&
+                        axon_hip_q6k_argmax_parts(c.n_vocab) <= argmax_words_;
+  bool embedded = false;  // x_ already holds the embedding of gen_ids_[i]
   for (std::size_t i = 0; i < n; ++i) {
     // Step i: the embedding of gen_ids_[i] (the previous step's choice), every layer in one
     // launch, the output norm and matrix, the greedy choice into gen_ids_[i + 1].
-    if (axon_hip_embedding_rows(static_cast<int>(token_embd_.type), token_embd_.dev, d, gen_ids_ + i, 1, x_) !=
-        AXON_HIP_OK)
+    if (!embedded &&
+        axon_hip_embedding_rows(static_cast<int>(token_embd_.type), token_embd_.dev, d, gen_ids_ + i, 1, x_) !=
+            AXON_HIP_OK)
       return device_error("generate: embedding");
+    embedded = false;
     axon_hip_decode_layers_args sa{};
     sa.layers = static_cast<const axon_hip_decode_layer*>(step_layers_);
     sa.eps = c.rms_eps;
@@ -1233,6 +1242,20 @@ Expected<std::size_t> LlamaModel::generate_greedy(KVCache& cache, std::int32_t t
       fa.y[0] = logits_;
       fa.y_stride[0] = c.n_vocab;
       if (axon_hip_matvec_fused(&fa) != AXON_HIP_OK) return device_error("generate: output");
+    } else if (out_keys) {
+      if (axon_hip_rmsnorm_rows(x_, static_cast<const float*>(output_norm_.dev), h_, nullptr, d, 1, c.rms_eps) !=
+              AXON_HIP_OK ||
+          axon_hip_matmul_q6_k_planar_argmax(output_.planar, h_, logits_, c.n_vocab, d, argmax_scratch_,
+                                             argmax_words_) != AXON_HIP_OK)
+        return device_error("generate: output");
+      // The choice into gen_ids_[i + 1] and its embedding, the next step's input (after the
+      // last step it goes unused).
+      if (axon_hip_argmax_embed(logits_, argmax_scratch_, axon_hip_q6k_argmax_parts(c.n_vocab), gen_ids_ + i + 1,
+                                static_cast<int>(token_embd_.type), token_embd_.dev, token_embd_.ne1, d,
+                                x_) != AXON_HIP_OK)
+        return device_error("generate: greedy");
+      embedded = true;
+      continue;
     } else {
       const bool out_q8 = q8_path(output_);
       if (axon_hip_rmsnorm_rows(x_, static_cast<const float*>(output_norm_.dev), out_q8 ? nullptr : h_,

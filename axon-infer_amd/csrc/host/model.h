@@ -239,6 +239,7 @@ private:
   void* rowinfo_host_ = nullptr; // pinned staging of the same
   std::size_t scores_floats_ = 0;
   std::uint64_t* argmax_scratch_ = nullptr;
+  std::size_t argmax_words_ = 0;  // its length in 8-byte keys
   std::int32_t* ids_ = nullptr;
   std::int32_t* gen_ids_ = nullptr;  // generate_greedy's ids: [max_ctx + 1]
   void* cand_ = nullptr;  // top-k candidates: [rows][k] logits, then [rows][k] ids

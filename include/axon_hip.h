@@ -170,6 +170,18 @@ int axon_hip_q6k_repack(const void* w, size_t n_out, size_t n_in, void* planar);
  * x 16-byte aligned. */
 int axon_hip_matmul_q6_k_planar(const void* planar, const float* x, float* y, size_t n_rows, size_t n_out,
                                 size_t n_in, size_t y_stride);
+/* One greedy decode step's tail in two launches instead of four (the output matmul of
+ * llama.cpp:628, sampler.cpp:100-102's argmax and the next step's embedding_row,
+ * llama.cpp:482-485). matmul_q6_k_planar_argmax: axon_hip_matmul_q6_k_planar of one row (the
+ * same y, bit for bit) whose workgroups also leave the greedy keys of their outputs in keys
+ * (axon_hip_q6k_argmax_parts(n_out) words; key_words must hold them). argmax_embed: the id
+ * axon_hip_argmax_rows would choose for the logits row x from those n_keys keys, into *out, and
+ * that token's row of the [table_rows][n] embedding table (embedding_rows) into emb. */
+size_t axon_hip_q6k_argmax_parts(size_t n_out);
+int axon_hip_matmul_q6_k_planar_argmax(const void* planar, const float* x, float* y, size_t n_out, size_t n_in,
+                                       uint64_t* keys, size_t key_words);
+int axon_hip_argmax_embed(const float* x, const uint64_t* keys, size_t n_keys, int32_t* out, int type,
+                          const void* table, size_t table_rows, size_t n, float* emb);
 /* Test hook, no counterpart in the reference: which kernel axon_hip_matmul_q6_k_planar runs for
  * one activation row. 0 (the default) chooses by shape; 1 one lane per output row; 2 the
  * products formed by every thread into LDS, then one in-order chain per row (used only where

@@ -129,6 +129,84 @@ def test_one_row_kernels_bit_exact(H, o, path, n_out, n_in):
     assert got[n_out] == np.float32(-7.25)  # nothing written past the last row
 
 
+def greedy_id(y):
+    """std::ranges::max_element with NaN skipped, a NaN first value selecting 0 (sampler.cpp:100-102)."""
+    if np.isnan(y[0]) or np.isnan(y).all():
+        return 0
+    return int(np.nanargmax(y))
+
+
+@pytest.mark.parametrize("n_out, n_in, plant", [(1, 256, None), (7, 256, "tie"), (65, 512, "tie"), (300, 2048, "nan"),
+                                                (16383, 256, "tie"), (65536, 256, None), (70001, 512, "tie")])
+def test_planar_argmax_keys_and_embedding(H, o, n_out, n_in, plant):
+    """axon_hip_matmul_q6_k_planar_argmax (the generate loop's output matmul): y bit for bit as
+    matmul_q6_k_planar, and axon_hip_argmax_embed over its keys picks argmax_rows' id (ties to
+    the first: a copy of the best row's blocks planted before and after it; a NaN first logit
+    selects 0) and writes that row of the embedding table as embedding_rows does, for Q6_K, Q4_0
+    and F32 tables. Workgroups of 64 rows (under 65536 outputs) and of 256 both occur."""
+    import ctypes as C
+    L = H.lib()
+    L.axon_hip_q6k_argmax_parts.restype = C.c_size_t
+    nsb = n_in // 256
+    w = q6k_weights(n_out, n_in, 3 * n_out + n_in)
+    x = random_floats(n_in, n_in + n_out)
+    want_y = o.matmul("q6_k", w, x, n_out, n_in, n_rows=1, y_stride=n_out)
+    if plant == "tie":
+        j = int(np.argmax(want_y))
+        for r in (j - 2, j + 3):
+            if 0 <= r < n_out:
+                w[r * nsb:(r + 1) * nsb] = w[j * nsb:(j + 1) * nsb]
+    elif plant == "nan":
+        w["d"][0:nsb] = 0x7e00  # row 0's scale: a NaN logit first
+    dst, _ = repack(H, w, n_out, n_in)
+    dx = H.DeviceBuffer.of(x)
+    parts = L.axon_hip_q6k_argmax_parts(C.c_size_t(n_out))
+    assert parts == -(-n_out // (256 if -(-n_out // 256) >= 256 else 64))
+    keys = H.DeviceBuffer.of(np.full(parts + 1, 0x5a5a5a5a5a5a5a5a, np.uint64))
+    y = H.DeviceBuffer.of(np.full(n_out + 1, np.float32(-7.25), np.float32))
+    with pytest.raises(H.HipError, match="key words"):
+        H.check(L.axon_hip_matmul_q6_k_planar_argmax(C.c_void_p(dst.ptr), C.c_void_p(dx.ptr), C.c_void_p(y.ptr),
+                                                     C.c_size_t(n_out), C.c_size_t(n_in), C.c_void_p(keys.ptr),
+                                                     C.c_size_t(parts - 1)), "planar_argmax")
+    H.check(L.axon_hip_matmul_q6_k_planar_argmax(C.c_void_p(dst.ptr), C.c_void_p(dx.ptr), C.c_void_p(y.ptr),
+                                                 C.c_size_t(n_out), C.c_size_t(n_in), C.c_void_p(keys.ptr),
+                                                 C.c_size_t(parts)), "planar_argmax")
+    got_y = y.download(np.float32, n_out + 1)
+    assert got_y[n_out] == np.float32(-7.25)
+    ref = H.DeviceBuffer(4 * n_out)
+    H.call("matmul_q6_k_planar", dst, dx, ref, 1, n_out, n_in, n_out)
+    assert np.array_equal(got_y[:n_out].view(np.uint32), ref.download(np.uint32, n_out))
+    assert keys.download(np.uint64, parts + 1)[parts] == 0x5a5a5a5a5a5a5a5a  # no key past the count
+    want_id = greedy_id(got_y[:n_out])
+    if plant == "nan":
+        assert want_id == 0 and np.isnan(got_y[0])
+    if plant == "tie" and n_out > 2:
+        j = int(np.argmax(want_y))
+        assert want_id == (j - 2 if j >= 2 else j)
+    scratch = H.DeviceBuffer(8 * 64)
+    amax = H.DeviceBuffer(4)
+    H.check(L.axon_hip_argmax_rows(C.c_void_p(y.ptr), C.c_size_t(n_out), C.c_size_t(1), C.c_size_t(n_out),
+                                   C.c_void_p(scratch.ptr), C.c_void_p(amax.ptr)), "argmax_rows")
+    assert int(amax.download(np.int32, 1)[0]) == want_id
+    n_emb = 512 if n_out < 20000 else 256
+    for kind, tid in (("q6_k", 14), ("q4_0", 2), ("f32", 0)):
+        rows = max(n_out, 2)
+        table = (random_floats(rows * n_emb, 5) if kind == "f32"
+                 else random_weights(kind, rows, n_emb, 9 + n_out))
+        dtab = H.DeviceBuffer.of(table)
+        emb = H.DeviceBuffer.of(np.full(n_emb, np.float32(3.5), np.float32))
+        out_id = H.DeviceBuffer.of(np.array([-5], np.int32))
+        H.check(L.axon_hip_argmax_embed(C.c_void_p(y.ptr), C.c_void_p(keys.ptr), C.c_size_t(parts),
+                                        C.c_void_p(out_id.ptr), C.c_int(tid), C.c_void_p(dtab.ptr), C.c_size_t(rows),
+                                        C.c_size_t(n_emb), C.c_void_p(emb.ptr)), "argmax_embed")
+        assert int(out_id.download(np.int32, 1)[0]) == want_id, kind
+        ids = H.DeviceBuffer.of(np.array([want_id], np.int32))
+        want_emb = H.DeviceBuffer(4 * n_emb)
+        H.check(L.axon_hip_embedding_rows(C.c_int(tid), C.c_void_p(dtab.ptr), C.c_size_t(n_emb), C.c_void_p(ids.ptr),
+                                          C.c_size_t(1), C.c_void_p(want_emb.ptr)), "embedding_rows")
+        assert np.array_equal(emb.download(np.uint32, n_emb), want_emb.download(np.uint32, n_emb)), kind
+
+
 def test_force_path_bounds(H):
     import ctypes as C
     with pytest.raises(H.HipError, match="0-3"):
