@@ -841,9 +841,11 @@ int matmul_q8_swiglu_launch(int type, MatvecArgs& a) {
   if (a.n_seg != 2 || a.outq == nullptr || a.seg[0].n_out != a.seg[1].n_out || a.seg[0].n_out % kQK != 0 ||
       !matmul_q8_rows_fits(type, probe, true))
     return fail(kUnsupported, "matmul swiglu: shape or alignment");
-  // Decode-sized calls (up to kRowsMaxM rows) take the fused tile only when its one workgroup
-  // per 32 outputs fills the chip; otherwise the caller runs the matmul and silu_mul apart.
-  if (a.m <= kRowsMaxM && a.seg[0].n_out / 32 < kDecodeTileWg)
+  // Decode-sized calls (up to kRowsMaxM rows) take the fused tile when it has at least 128
+  // workgroups (one per 32 outputs: FFNs of 4096 and up); with fewer the caller runs the matmul
+  // and silu_mul apart. C5's 4864-wide FFN (152 workgroups) gained 2-4 % against the rows
+  // kernel and silu_mul.
+  if (a.m <= kRowsMaxM && a.seg[0].n_out / 32 < 128)
     return fail(kUnsupported, "matmul swiglu: %u outputs give too few workgroups for %u rows", a.seg[0].n_out, a.m);
   if (a.m <= 16) return swiglu_launch<16>(type, a);
   if (a.m <= 32) return swiglu_launch<32>(type, a);

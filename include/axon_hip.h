@@ -242,7 +242,7 @@ int axon_hip_sort_rows(const float* x, size_t n, size_t n_rows, size_t stride, v
  * bits as matmul_q8_fused of the two weights, silu_mul_rows and quantize_rows. out: float
  * [n_rows][n_ff] or NULL; outq: [n_rows][n_ff / 32] Q8_0 blocks, which must not alias xq. n_ff a
  * multiple of 32. AXON_HIP_E_UNSUPPORTED (nothing launched) for up to 64 rows with n_ff below
- * 8192 (too few workgroups to fill the chip), or bases the tile kernel cannot load. */
+ * 4096 (too few workgroups), or bases the tile kernel cannot load. */
 int axon_hip_matmul_q8_swiglu(int type, const void* xq, size_t n_rows, size_t n_in, const void* w_gate,
                               const void* w_up, size_t n_ff, float* out, void* outq);
 

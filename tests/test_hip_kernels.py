@@ -231,7 +231,8 @@ def test_q8_fused_segments_many_rows_bit_exact(o, n_rows, n_in, n_out):
 
 @pytest.mark.parametrize("n_rows, n_in, n_ff", [(65, 896, 4864), (130, 2048, 1024), (512, 256, 96),
                                                  (1, 256, 8192), (5, 512, 8192), (16, 256, 8224), (17, 256, 8192),
-                                                 (32, 512, 8192), (48, 256, 8192), (64, 256, 8192)])
+                                                 (32, 512, 8192), (48, 256, 8192), (64, 256, 8192), (16, 896, 4864),
+                                                 (40, 896, 4864), (7, 256, 4096)])
 def test_q8_swiglu_tile_bit_exact(o, n_rows, n_in, n_ff):
     """gate|up with the SwiGLU product and down's Q8_0 input in the tile kernel's epilogue
     (axon_hip_matmul_q8_swiglu): the float product and the Q8_0 blocks equal, bit for bit,
@@ -239,7 +240,7 @@ def test_q8_swiglu_tile_bit_exact(o, n_rows, n_in, n_ff):
     are pinned to the oracle elsewhere; and the product and its blocks equal the oracle's
     matmuls, silu_mul and quantize_row_q8_0. Decode-sized calls (up to 64 rows: tiles of 16, 32
     and 64 activation rows, the first two meeting gate and up in LDS) run when the FFN gives
-    at least 256 workgroups (n_ff 8192 and up)."""
+    at least 128 workgroups (n_ff 4096 and up)."""
     import axon_hip as H
     xs = random_floats(n_rows * n_in, n_rows + n_ff, 3.0)
     xq = np.concatenate([o.quantize_row_q8_0(xs[i * n_in:(i + 1) * n_in]) for i in range(n_rows)])
@@ -271,10 +272,10 @@ def test_q8_swiglu_tile_bit_exact(o, n_rows, n_in, n_ff):
         assert got_q.tobytes() == ref_q.download(np.uint8, want_q.nbytes).tobytes(), kind
         assert np.array_equal(got, prod), kind
         assert got_q.tobytes() == want_q.tobytes(), kind
-    # A decode-sized call whose FFN gives 255 workgroups: refused, nothing launched.
+    # A decode-sized call whose FFN gives 127 workgroups: refused, nothing launched.
     with pytest.raises(H.HipError, match="swiglu"):
         H.check(H.lib().axon_hip_matmul_q8_swiglu(C.c_int(2), C.c_void_p(dx.ptr), C.c_size_t(64), C.c_size_t(n_in),
-                                                  C.c_void_p(dx.ptr), C.c_void_p(dx.ptr), C.c_size_t(8160), None,
+                                                  C.c_void_p(dx.ptr), C.c_void_p(dx.ptr), C.c_size_t(4064), None,
                                                   C.c_void_p(dx.ptr)), "matmul_q8_swiglu")
 
 
