@@ -104,15 +104,16 @@ def test_q8_rows_bit_exact_dot4_and_mfma(h, o, n_rows):
 
 @pytest.mark.parametrize("kind", QUANT_TYPES)
 def test_q8_rows_long_k_and_unaligned_weights(h, o, kind):
-    # K = 8192 spans several LDS chunks of the MFMA path. The weight pointer is then moved 2
-    # bytes off any 4-byte boundary, as a column chunk of an odd block count leaves it
-    # (matmul_columns passes base + begin * row_bytes, llama.cpp:36-37).
+    # K = 8192 spans several LDS chunks of the MFMA path, which also takes 3 and 4 rows at this
+    # length (1 and 2 stay on the dot4 kernel). The weight pointer is then moved 2 bytes off any
+    # 4-byte boundary, as a column chunk of an odd block count leaves it (matmul_columns passes
+    # base + begin * row_bytes, llama.cpp:36-37), which sends every row count to the dot4 kernel.
     import axon_hip as H
     n_in, n_out, n_rows = 8192, 40, 20
     xs = random_floats(n_rows * n_in, 77, 2.0)
     xq = np.concatenate([o.quantize_row_q8_0(xs[i * n_in:(i + 1) * n_in]) for i in range(n_rows)])
     w = random_weights(kind, n_out, n_in, 78)
-    for rows in (1, 3, n_rows):
+    for rows in (1, 2, 3, 4, n_rows):
         want = o.matmul(f"{kind}_q8", w, xq[: rows * n_in // 32], n_out, n_in, n_rows=rows)
         assert np.array_equal(h.matmul(f"{kind}_q8", w, xq[: rows * n_in // 32], n_out, n_in, n_rows=rows), want)
         raw = w.tobytes()
