@@ -91,11 +91,15 @@ int q8_matmul(int type, const void* xq, size_t n_rows, size_t n_in, size_t n_seg
   if (n_rows == 0) return kOk;
   const uint32_t nb = static_cast<uint32_t>(n_in / kQK);
   const size_t xrow = static_cast<size_t>(nb) * kBytesQ8_0;
-  // Fewer rows also take the MFMA rows kernel where the dot4 kernel below holds them poorly:
+  // Fewer rows also take the MFMA kernels where the dot4 kernel below holds them poorly:
   // three or four rows of 8192 inputs and more (C4 down 2048 x 8192: 25 / 34 us at 3 / 4 rows
-  // on the dot4 kernel, 17 us on the rows kernel), and rows beyond what one dot4 launch holds,
-  // each further launch reading the matrix again (4096 x 14336 at 2 rows: 54 us).
-  if (n_rows >= 5 || (n_rows >= 3 && nb >= 256) || n_rows > matvec_q8_max_rows(type, nb)) {
+  // on the dot4 kernel, 17 us on the rows kernel) or of a matrix wide enough for the decode
+  // tile (16384 x 2048 at 4 rows 14.4 -> 11.5 us, 128256 x 2048 at 3 / 4 rows 59 / 65 ->
+  // 53 / 46 us), and rows beyond what one dot4 launch holds, each further launch reading the
+  // matrix again (4096 x 14336 at 2 rows: 54 us).
+  size_t wg64 = 0;
+  for (size_t s = 0; s < n_seg; ++s) wg64 += (n_out[s] + 63) / 64;
+  if (n_rows >= 5 || (n_rows >= 3 && (nb >= 256 || wg64 >= 256)) || n_rows > matvec_q8_max_rows(type, nb)) {
     MatvecArgs a{};
     for (size_t s = 0; s < n_seg; ++s) {
       a.seg[s] = MatvecSeg{static_cast<const uint8_t*>(w[s]), y[s], static_cast<uint32_t>(n_out[s]),

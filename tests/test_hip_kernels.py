@@ -102,6 +102,21 @@ def test_q8_rows_bit_exact_dot4_and_mfma(h, o, n_rows):
         assert np.array_equal(got, want), (kind, n_rows)   # sentinels between rows untouched too
 
 
+@pytest.mark.parametrize("n_rows", [2, 3, 4])
+def test_q8_rows_wide_matrix_few_rows_bit_exact(h, o, n_rows):
+    """Three and four rows of a matrix wide enough for the decode tile (16384 outputs: 256
+    workgroups of 64) take the MFMA tile kernel instead of the dot4 matvec (two rows stay
+    there); strided outputs, against the oracle."""
+    n_in, n_out = 256, 16384
+    xs = random_floats(n_rows * n_in, 60 + n_rows, 3.0)
+    xq = np.concatenate([o.quantize_row_q8_0(xs[i * n_in:(i + 1) * n_in]) for i in range(n_rows)])
+    for kind in QUANT_TYPES:
+        w = random_weights(kind, n_out, n_in, 50 + n_rows)
+        got = h.matmul(f"{kind}_q8", w, xq, n_out, n_in, n_rows=n_rows, y_stride=n_out + 5)
+        want = o.matmul(f"{kind}_q8", w, xq, n_out, n_in, n_rows=n_rows, y_stride=n_out + 5)
+        assert np.array_equal(got, want), (kind, n_rows)
+
+
 @pytest.mark.parametrize("kind", QUANT_TYPES)
 def test_q8_rows_long_k_and_unaligned_weights(h, o, kind):
     # K = 8192 spans several LDS chunks of the MFMA path, which also takes 3 and 4 rows at this
