@@ -72,12 +72,12 @@ int ready() {
 
 bool fits_u32(size_t v) { return v <= 0xffffffffull; }
 
-// The Q8_0-activation path: groups of up to four rows on the dot4 matvec below 5 rows, the
-// few-rows MFMA kernel (every segment in one launch) from 5 to 64 rows, the tile MFMA kernel
-// (every segment in one launch, 64-row tiles) beyond, and from 33 rows on matrices wide enough
-// to fill the chip with its tiles (the output matrix: its weights are read once, not twice); rows whose bases or lengths do not suit their dword
-// loads take the staged 64 x 64 MFMA tiles or the dot4 groups. All of them give the same bits
-// for a row.
+// The Q8_0-activation path: one or two rows on the decode matvec or the dot4 matvec, the
+// few-rows MFMA kernel (every segment in one launch) up to 64 rows (from 3 rows where the dot4
+// kernel holds them poorly), the tile MFMA kernel (every segment in one launch, 64-row tiles)
+// beyond, and from 33 rows on matrices wide enough for 128 of its tiles (their weights read
+// once, not up to four times); rows whose bases or lengths do not suit their dword loads take
+// the staged 64 x 64 MFMA tiles or the dot4 groups. All of them give the same bits for a row.
 int q8_matmul(int type, const void* xq, size_t n_rows, size_t n_in, size_t n_seg, const void* const* w,
               float* const* y, const size_t* n_out, const size_t* y_stride, int accumulate) {
   if (n_in % kQK != 0) return fail(kInvalidArgument, "quantized matmul: n_in %zu is not a multiple of 32", n_in);

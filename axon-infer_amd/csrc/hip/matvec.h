@@ -109,11 +109,11 @@ int matmul_q8_rows_launch(int type, MatvecArgs& a);
 // int8 MFMA for 65 and more activation rows (prefill, mixed passes): TN x 64 tiles, every
 // segment in one grid, the same per-output order.
 int matmul_q8_tile_launch(int type, MatvecArgs& a);
-// 33..64 rows on matrices of at least 512 tiles of 64 weight rows: the tile kernel reads the
-// weights once where the few-rows kernel's 32-row tiles read them twice.
+// 33..64 rows on matrices of at least 128 tiles of 64 weight rows: the tile kernel reads the
+// weights once where the few-rows kernel's 16-row tiles read them up to four times.
 bool matmul_q8_tile_fills(const MatvecArgs& a);
-// gate|up over 65+ rows with the SwiGLU product and its Q8_0 blocks in the epilogue: seg[0]
-// gate (y: the float product, or null), seg[1] up, outq the blocks; n_out a multiple of 32.
+// gate|up with the SwiGLU product and its Q8_0 blocks in the epilogue: seg[0] gate (y: the float
+// product, or null), seg[1] up, outq the blocks; n_out a multiple of 32.
 int matmul_q8_swiglu_launch(int type, MatvecArgs& a);
 
 }  // namespace axon_hip
