@@ -189,7 +189,7 @@ __host__ __device__ constexpr size_t rows_lds() {
 // TN: weight rows per workgroup, 16 or 8. With 8 (a narrow matrix, so twice the workgroups),
 // lanes of weight column col read row col % 8 into the 16-wide MFMA and only columns below 8
 // are folded and stored.
-template <int T, int TM, uint32_t TN = kRowsTN, bool ROPE = false>
+template <int T, int TM, uint32_t TN = kRowsTN, bool ROPE = false, bool CHAINS = false>
 __global__ __launch_bounds__(kThreads) void mfma_rows_kernel(MatvecArgs args, RowsRope rp) {
   static_assert(TN == 16 || TN == 8, "16 or 8 weight rows");
   constexpr int bs = block_bytes<T>();
@@ -321,6 +321,123 @@ __global__ __launch_bounds__(kThreads) void mfma_rows_kernel(MatvecArgs args, Ro
   const uint32_t col = lane & 15;  // weight row (B) within the tile's 16
   const uint32_t wrow = col % TN;  // the LDS row it reads (col itself when TN = 16)
   const uint32_t kq = lane >> 4;   // which 8 of a block's 32 elements this lane feeds
+
+  // The output (activation row r, weight column c of the tile) with value x: stored or added,
+  // or (ROPE) biased, rotated and written to q or the cache. Every lane calls it (the RoPE
+  // partner comes from lane ^ 1, the column next to it).
+  auto finish = [&](uint32_t c, uint32_t r, float x) {
+    if constexpr (ROPE) {
+      // Segments q, k, v: the bias, then the rotation of each pair (2i, 2i + 1) of a head as
+      // rope_rows_kernel forms it (x0 * c - x1 * s, x0 * s + x1 * c); n0 is a multiple of TN,
+      // so output n's partner n ^ 1 is column c ^ 1, held by lane ^ 1.
+      const uint32_t n = n0 + c;
+      if (rp.bias[s] != nullptr && c < nn) x = x + rp.bias[s][n];
+      const float other = __shfl_xor(x, 1, 64);
+      if (c < nn && r < mm) {
+        const int32_t pos = rp.pos[m0 + r];
+        if (s < 2) {
+          const uint32_t i = (n % rp.head_dim) / 2;
+          if (i < rp.rot_half) {
+            const float2 cs = reinterpret_cast<const float2*>(rp.table)[static_cast<size_t>(pos) * rp.rot_half + i];
+            const float x0 = (c & 1) ? other : x;
+            const float x1 = (c & 1) ? x : other;
+            x = (c & 1) ? x0 * cs.y + x1 * cs.x : x0 * cs.x - x1 * cs.y;
+          }
+        }
+        if (s == 0) {
+          seg.y[static_cast<size_t>(m0 + r) * seg.y_stride + n] = x;
+        } else {
+          const size_t at = rp.cache_off[m0 + r] + (s == 1 ? rp.k_layer_off : rp.v_layer_off) +
+                            static_cast<size_t>(pos) * rp.kv_row + n;
+          if (rp.cache_f16) static_cast<uint16_t*>(rp.cache)[at] = static_cast<uint16_t>(float_to_half_bits(x));
+          else static_cast<float*>(rp.cache)[at] = x;
+        }
+      }
+    } else {
+      if (c < nn && r < mm) {
+        float* y = seg.y + static_cast<size_t>(m0 + r) * seg.y_stride + n0 + c;
+        *y = args.accumulate ? *y + x : x;
+      }
+    }
+  };
+
+  if constexpr (CHAINS) {
+    // Terms, then chains. Per chunk, wave w runs the MFMAs of blocks 8w .. 8w + 7 (each once,
+    // all four results of a lane used) and forms their terms float(sumi) * d_w * d_x (+ m_w *
+    // d_x * float(sumx), Q4_1) into LDS ([row][column][block]); after a barrier thread t adds
+    // the chunk's terms of output (row t / 16, column t % 16) in block order. The terms and
+    // the adds are the scalar table's operations, so the bits are the fold's.
+    static_assert(TM == 16, "one tile of 16 activation rows");
+    constexpr uint32_t TP = KC + 4;              // floats per (row, column) of terms
+    constexpr uint32_t BW = KC / 4;              // blocks per wave per chunk
+    float* terms = reinterpret_cast<float*>(xs + TM * KC);  // [16][16][TP]
+    const uint32_t crow = tid >> 4, ccol = tid & 15;        // this thread's chain
+    float acc = 0.0f;
+    auto chunk = [&](uint32_t c, Raw& r) {
+      const uint32_t cb = min(KC, nb - c * KC);
+      expand(c, r);
+      __syncthreads();
+      if (c + 2 < n_chunks) load(c + 2, r);
+      const uint32_t b0 = wave * BW;
+      i32x4 d[BW];
+#pragma unroll
+      for (uint32_t i = 0; i < BW; ++i) {
+        const uint2 wq = *reinterpret_cast<const uint2*>(wa + wrow * P + (b0 + i) * 8 + 2 * kq);
+        const uint2 xq = *reinterpret_cast<const uint2*>(xa + col * P + (b0 + i) * 8 + 2 * kq);
+        const int64_t bw = static_cast<int64_t>((static_cast<uint64_t>(wq.y) << 32) | wq.x);
+        const int64_t ax = static_cast<int64_t>((static_cast<uint64_t>(xq.y) << 32) | xq.x);
+        i32x4 z = {0, 0, 0, 0};
+        d[i] = __builtin_amdgcn_mfma_i32_16x16x32_i8(ax, bw, z, 0, 0, 0);
+      }
+      // Blocks past cb hold stale bytes; their terms are never added.
+#pragma unroll
+      for (uint32_t v = 0; v < 4; ++v) {
+        const uint32_t row = 4 * kq + v;
+        float t[BW];
+#pragma unroll
+        for (uint32_t i = 0; i < BW; ++i) {
+          const uint32_t b = b0 + i;
+          const float dx = xd[row * KC + b];
+          if constexpr (T == Q4_1) {
+            t[i] = static_cast<float>(d[i][v]) * wd[wrow * KC + b] * dx +
+                   wmn[wrow * KC + b] * dx * static_cast<float>(xs[row * KC + b]);
+          } else {
+            // Q4_0: sumi carries the -8 offset already (the weights entered as q - 8).
+            t[i] = static_cast<float>(d[i][v]) * wd[wrow * KC + b] * dx;
+          }
+        }
+        float4* dst = reinterpret_cast<float4*>(terms + (row * 16 + col) * TP + b0);
+#pragma unroll
+        for (uint32_t i = 0; i < BW; i += 4) dst[i / 4] = make_float4(t[i], t[i + 1], t[i + 2], t[i + 3]);
+      }
+      __syncthreads();
+      const float* tp = terms + (crow * 16 + ccol) * TP;
+      if (cb == KC) {
+#pragma unroll
+        for (uint32_t b = 0; b < KC; b += 4) {
+          const float4 q4 = *reinterpret_cast<const float4*>(tp + b);
+          acc += q4.x;
+          acc += q4.y;
+          acc += q4.z;
+          acc += q4.w;
+        }
+      } else {
+        for (uint32_t b = 0; b < cb; ++b) acc += tp[b];
+      }
+      // The next chunk's expand writes only the operand and scale regions, and its barrier
+      // orders these reads before the next terms are written.
+    };
+    Raw ra, rb;
+    load(0, ra);
+    if (n_chunks > 1) load(1, rb);
+    for (uint32_t c = 0; c < n_chunks; c += 2) {
+      chunk(c, ra);
+      if (c + 1 < n_chunks) chunk(c + 1, rb);
+    }
+    finish(ccol, crow, acc);
+    return;
+  }
+
   // Wave w feeds activation row (col + w) % 16 as A row col, which moves D row 4 kq + w (the
   // output this wave folds) into the lane's first result: d[0] = sumi of activation row
   // 4 kq + w and weight row col.
@@ -384,51 +501,8 @@ __global__ __launch_bounds__(kThreads) void mfma_rows_kernel(MatvecArgs args, Ro
     chunk(c, ra);
     if (c + 1 < n_chunks) chunk(c + 1, rb);
   }
-
-  if constexpr (ROPE) {
-    // Segments q, k, v: the bias, then the rotation of each pair (2i, 2i + 1) of a head as
-    // rope_rows_kernel forms it (x0 * c - x1 * s, x0 * s + x1 * c); n0 is a multiple of TN, so
-    // output n sits in lane col and its partner n ^ 1 in lane col ^ 1 of the same 16.
-    const uint32_t n = n0 + col;
 #pragma unroll
-    for (uint32_t t = 0; t < MT; ++t) {
-      const uint32_t r = 16 * t + orow;
-      float x = acc[t];
-      if (rp.bias[s] != nullptr && col < nn) x = x + rp.bias[s][n];
-      const float other = __shfl_xor(x, 1, 64);
-      if (col < nn && r < mm) {
-        const int32_t pos = rp.pos[m0 + r];
-        if (s < 2) {
-          const uint32_t i = (n % rp.head_dim) / 2;
-          if (i < rp.rot_half) {
-            const float2 cs = reinterpret_cast<const float2*>(rp.table)[static_cast<size_t>(pos) * rp.rot_half + i];
-            const float x0 = (col & 1) ? other : x;
-            const float x1 = (col & 1) ? x : other;
-            x = (col & 1) ? x0 * cs.y + x1 * cs.x : x0 * cs.x - x1 * cs.y;
-          }
-        }
-        if (s == 0) {
-          seg.y[static_cast<size_t>(m0 + r) * seg.y_stride + n] = x;
-        } else {
-          const size_t at = rp.cache_off[m0 + r] + (s == 1 ? rp.k_layer_off : rp.v_layer_off) +
-                            static_cast<size_t>(pos) * rp.kv_row + n;
-          if (rp.cache_f16) static_cast<uint16_t*>(rp.cache)[at] = static_cast<uint16_t>(float_to_half_bits(x));
-          else static_cast<float*>(rp.cache)[at] = x;
-        }
-      }
-    }
-    return;
-  }
-  if (col < nn) {
-#pragma unroll
-    for (uint32_t t = 0; t < MT; ++t) {
-      const uint32_t r = 16 * t + orow;
-      if (r < mm) {
-        float* y = seg.y + static_cast<size_t>(m0 + r) * seg.y_stride + n0 + col;
-        *y = args.accumulate ? *y + acc[t] : acc[t];
-      }
-    }
-  }
+  for (uint32_t t = 0; t < MT; ++t) finish(col, 16 * t + orow, acc[t]);
 }
 
 // ---- Many activation rows (prefill, mixed passes): 65 rows and more ------------------------
@@ -758,7 +832,9 @@ int tile_launch(int type, MatvecArgs& a) {
   return check_launch("mfma_tile");
 }
 
-template <int TM, uint32_t TN = kRowsTN, bool ROPE = false>
+constexpr bool kRowsChains = true;  // the few-rows kernel forms terms, then chains them
+
+template <int TM, uint32_t TN = kRowsTN, bool ROPE = false, bool CHAINS = kRowsChains>
 int rows_launch(int type, MatvecArgs& a, const RowsRope& rp = RowsRope{}) {
   uint32_t wg = 0;
   for (int s = 0; s < a.n_seg; ++s) {
@@ -766,12 +842,26 @@ int rows_launch(int type, MatvecArgs& a, const RowsRope& rp = RowsRope{}) {
     wg += static_cast<uint32_t>(ceil_div(a.seg[s].n_out, TN));
   }
   const dim3 grid(wg, static_cast<uint32_t>(ceil_div(a.m, TM)));
-  constexpr size_t lds = rows_lds<TM, TN>();
-  static_assert(lds <= 65536, "within the default LDS grant");
+  // The chains' terms buffer ([16][16][kRowsChunk + 4] floats) after the operands and scales.
+  constexpr size_t lds = rows_lds<TM, TN>() + (CHAINS ? 16 * 16 * (kRowsChunk + 4) * 4 : 0);
+  static_assert(lds <= 163840, "within one CU's LDS");
+  static const bool granted = [] {
+    bool ok = true;
+    auto grant = [&](auto kernel) {
+      if (lds > 65536)
+        ok = ok && hipFuncSetAttribute(reinterpret_cast<const void*>(kernel), hipFuncAttributeMaxDynamicSharedMemorySize,
+                                       static_cast<int>(lds)) == hipSuccess;
+    };
+    grant(mfma_rows_kernel<Q8_0, TM, TN, ROPE, CHAINS>);
+    grant(mfma_rows_kernel<Q4_0, TM, TN, ROPE, CHAINS>);
+    grant(mfma_rows_kernel<Q4_1, TM, TN, ROPE, CHAINS>);
+    return ok;
+  }();
+  if (!granted) return fail(kUnsupported, "matmul rows: the LDS grant was refused");
   switch (type) {
-  case Q8_0: launch(mfma_rows_kernel<Q8_0, TM, TN, ROPE>, grid, dim3(kThreads), lds, a, rp); break;
-  case Q4_0: launch(mfma_rows_kernel<Q4_0, TM, TN, ROPE>, grid, dim3(kThreads), lds, a, rp); break;
-  case Q4_1: launch(mfma_rows_kernel<Q4_1, TM, TN, ROPE>, grid, dim3(kThreads), lds, a, rp); break;
+  case Q8_0: launch(mfma_rows_kernel<Q8_0, TM, TN, ROPE, CHAINS>, grid, dim3(kThreads), lds, a, rp); break;
+  case Q4_0: launch(mfma_rows_kernel<Q4_0, TM, TN, ROPE, CHAINS>, grid, dim3(kThreads), lds, a, rp); break;
+  case Q4_1: launch(mfma_rows_kernel<Q4_1, TM, TN, ROPE, CHAINS>, grid, dim3(kThreads), lds, a, rp); break;
   default: return fail(kUnsupported, "matmul rows: weight type %d", type);
   }
   return check_launch(ROPE ? "mfma_rows (rope)" : "mfma_rows");
