@@ -313,8 +313,10 @@ __global__ __launch_bounds__(kThreads) void mfma_rows_kernel(MatvecArgs args, Ro
       uint4* dst = reinterpret_cast<uint4*>(xa + row * P + b * 8);
       dst[0] = make_uint4(q[0], q[1], q[2], q[3]);
       dst[1] = make_uint4(q[4], q[5], q[6], q[7]);
-      xd[row * KC + b] = half_bits_to_float(v[0] & 0xffffu);
-      if constexpr (T == Q4_1) xs[row * KC + b] = sum;
+      // The chains read a lane's four rows of a block at once: block-major there.
+      const uint32_t xi = CHAINS ? b * TM + row : row * KC + b;
+      xd[xi] = half_bits_to_float(v[0] & 0xffffu);
+      if constexpr (T == Q4_1) xs[xi] = sum;
     }
   };
 
@@ -390,25 +392,31 @@ __global__ __launch_bounds__(kThreads) void mfma_rows_kernel(MatvecArgs args, Ro
         d[i] = __builtin_amdgcn_mfma_i32_16x16x32_i8(ax, bw, z, 0, 0, 0);
       }
       // Blocks past cb hold stale bytes; their terms are never added.
+      float t[4][BW];
+#pragma unroll
+      for (uint32_t i = 0; i < BW; ++i) {
+        const uint32_t b = b0 + i;
+        const float dw = wd[wrow * KC + b];
+        const float4 dx4 = *reinterpret_cast<const float4*>(xd + b * TM + 4 * kq);  // rows 4kq..4kq+3
+        const float dx[4] = {dx4.x, dx4.y, dx4.z, dx4.w};
+        if constexpr (T == Q4_1) {
+          const float mw = wmn[wrow * KC + b];
+          const int4 sx4 = *reinterpret_cast<const int4*>(xs + b * TM + 4 * kq);
+          const int32_t sx[4] = {sx4.x, sx4.y, sx4.z, sx4.w};
+#pragma unroll
+          for (uint32_t v = 0; v < 4; ++v)
+            t[v][i] = static_cast<float>(d[i][v]) * dw * dx[v] + mw * dx[v] * static_cast<float>(sx[v]);
+        } else {
+          // Q4_0: sumi carries the -8 offset already (the weights entered as q - 8).
+#pragma unroll
+          for (uint32_t v = 0; v < 4; ++v) t[v][i] = static_cast<float>(d[i][v]) * dw * dx[v];
+        }
+      }
 #pragma unroll
       for (uint32_t v = 0; v < 4; ++v) {
-        const uint32_t row = 4 * kq + v;
-        float t[BW];
+        float4* dst = reinterpret_cast<float4*>(terms + ((4 * kq + v) * 16 + col) * TP + b0);
 #pragma unroll
-        for (uint32_t i = 0; i < BW; ++i) {
-          const uint32_t b = b0 + i;
-          const float dx = xd[row * KC + b];
-          if constexpr (T == Q4_1) {
-            t[i] = static_cast<float>(d[i][v]) * wd[wrow * KC + b] * dx +
-                   wmn[wrow * KC + b] * dx * static_cast<float>(xs[row * KC + b]);
-          } else {
-            // Q4_0: sumi carries the -8 offset already (the weights entered as q - 8).
-            t[i] = static_cast<float>(d[i][v]) * wd[wrow * KC + b] * dx;
-          }
-        }
-        float4* dst = reinterpret_cast<float4*>(terms + (row * 16 + col) * TP + b0);
-#pragma unroll
-        for (uint32_t i = 0; i < BW; i += 4) dst[i / 4] = make_float4(t[i], t[i + 1], t[i + 2], t[i + 3]);
+        for (uint32_t i = 0; i < BW; i += 4) dst[i / 4] = make_float4(t[v][i], t[v][i + 1], t[v][i + 2], t[v][i + 3]);
       }
       __syncthreads();
       const float* tp = terms + (crow * 16 + ccol) * TP;
