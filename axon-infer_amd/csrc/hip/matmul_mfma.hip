@@ -171,7 +171,6 @@ __global__ __launch_bounds__(kThreads) void mfma_q8_kernel(MatvecArgs args, uint
 // sized to the segment's and the activations' bytes: a load past either returns zero and
 // touches nothing (the last rows, the last blocks, the last partial chunk).
 constexpr uint32_t kRowsChunk = 32;                 // blocks per K chunk
-constexpr uint32_t kRowsPitch = kRowsChunk * 8 + 4;  // dwords per expanded row (padded)
 constexpr uint32_t kRowsTN = 16;                    // weight rows per workgroup
 
 template <int T>
@@ -179,21 +178,21 @@ __host__ __device__ constexpr uint32_t item_dwords() {
   return (block_bytes<T>() + 2 + 3) / 4;  // a 2-byte aligned block from its 4-byte boundary
 }
 
-// LDS: expanded weights [16][kRowsPitch], expanded activations [TM][kRowsPitch] (dwords), then
-// per (row, block) scales: wd, wm [16][KC], xd, xs [TM][KC].
-template <int TM, uint32_t TN = kRowsTN>
+// LDS: expanded weights [16][KC * 8 + 4], expanded activations [TM][KC * 8 + 4] (dwords), then
+// per (row, block) scales: wd, wm [16][KC], xd, xs [TM][KC] (KC blocks per chunk).
+template <int TM, uint32_t TN = kRowsTN, uint32_t KC = kRowsChunk>
 __host__ __device__ constexpr size_t rows_lds() {
-  return (static_cast<size_t>(TN + TM) * kRowsPitch + static_cast<size_t>(TN + TM) * kRowsChunk * 2) * 4;
+  return (static_cast<size_t>(TN + TM) * (KC * 8 + 4) + static_cast<size_t>(TN + TM) * KC * 2) * 4;
 }
 
 // TN: weight rows per workgroup, 16 or 8. With 8 (a narrow matrix, so twice the workgroups),
 // lanes of weight column col read row col % 8 into the 16-wide MFMA and only columns below 8
 // are folded and stored.
-template <int T, int TM, uint32_t TN = kRowsTN, bool ROPE = false, bool CHAINS = false>
+template <int T, int TM, uint32_t TN = kRowsTN, bool ROPE = false, bool CHAINS = false, uint32_t KCH = kRowsChunk>
 __global__ __launch_bounds__(kThreads) void mfma_rows_kernel(MatvecArgs args, RowsRope rp) {
   static_assert(TN == 16 || TN == 8, "16 or 8 weight rows");
   constexpr int bs = block_bytes<T>();
-  constexpr uint32_t KC = kRowsChunk, P = kRowsPitch;
+  constexpr uint32_t KC = KCH, P = KCH * 8 + 4;
   constexpr uint32_t MT = TM / 16;                      // MFMA tiles along the activation rows
   constexpr uint32_t WI = TN * KC / kThreads;           // weight items per thread per chunk
   constexpr uint32_t XI = TM * KC / kThreads;           // activation items per thread per chunk
@@ -842,7 +841,7 @@ int tile_launch(int type, MatvecArgs& a) {
 
 constexpr bool kRowsChains = true;  // the few-rows kernel forms terms, then chains them
 
-template <int TM, uint32_t TN = kRowsTN, bool ROPE = false, bool CHAINS = kRowsChains>
+template <int TM, uint32_t TN = kRowsTN, bool ROPE = false, bool CHAINS = kRowsChains, uint32_t KCH = kRowsChunk>
 int rows_launch(int type, MatvecArgs& a, const RowsRope& rp = RowsRope{}) {
   uint32_t wg = 0;
   for (int s = 0; s < a.n_seg; ++s) {
@@ -850,8 +849,8 @@ int rows_launch(int type, MatvecArgs& a, const RowsRope& rp = RowsRope{}) {
     wg += static_cast<uint32_t>(ceil_div(a.seg[s].n_out, TN));
   }
   const dim3 grid(wg, static_cast<uint32_t>(ceil_div(a.m, TM)));
-  // The chains' terms buffer ([16][16][kRowsChunk + 4] floats) after the operands and scales.
-  constexpr size_t lds = rows_lds<TM, TN>() + (CHAINS ? 16 * 16 * (kRowsChunk + 4) * 4 : 0);
+  // The chains' terms buffer ([16][16][KCH + 4] floats) after the operands and scales.
+  constexpr size_t lds = rows_lds<TM, TN, KCH>() + (CHAINS ? 16 * 16 * (KCH + 4) * 4 : 0);
   static_assert(lds <= 163840, "within one CU's LDS");
   static const bool granted = [] {
     bool ok = true;
@@ -860,16 +859,16 @@ int rows_launch(int type, MatvecArgs& a, const RowsRope& rp = RowsRope{}) {
         ok = ok && hipFuncSetAttribute(reinterpret_cast<const void*>(kernel), hipFuncAttributeMaxDynamicSharedMemorySize,
                                        static_cast<int>(lds)) == hipSuccess;
     };
-    grant(mfma_rows_kernel<Q8_0, TM, TN, ROPE, CHAINS>);
-    grant(mfma_rows_kernel<Q4_0, TM, TN, ROPE, CHAINS>);
-    grant(mfma_rows_kernel<Q4_1, TM, TN, ROPE, CHAINS>);
+    grant(mfma_rows_kernel<Q8_0, TM, TN, ROPE, CHAINS, KCH>);
+    grant(mfma_rows_kernel<Q4_0, TM, TN, ROPE, CHAINS, KCH>);
+    grant(mfma_rows_kernel<Q4_1, TM, TN, ROPE, CHAINS, KCH>);
     return ok;
   }();
   if (!granted) return fail(kUnsupported, "matmul rows: the LDS grant was refused");
   switch (type) {
-  case Q8_0: launch(mfma_rows_kernel<Q8_0, TM, TN, ROPE, CHAINS>, grid, dim3(kThreads), lds, a, rp); break;
-  case Q4_0: launch(mfma_rows_kernel<Q4_0, TM, TN, ROPE, CHAINS>, grid, dim3(kThreads), lds, a, rp); break;
-  case Q4_1: launch(mfma_rows_kernel<Q4_1, TM, TN, ROPE, CHAINS>, grid, dim3(kThreads), lds, a, rp); break;
+  case Q8_0: launch(mfma_rows_kernel<Q8_0, TM, TN, ROPE, CHAINS, KCH>, grid, dim3(kThreads), lds, a, rp); break;
+  case Q4_0: launch(mfma_rows_kernel<Q4_0, TM, TN, ROPE, CHAINS, KCH>, grid, dim3(kThreads), lds, a, rp); break;
+  case Q4_1: launch(mfma_rows_kernel<Q4_1, TM, TN, ROPE, CHAINS, KCH>, grid, dim3(kThreads), lds, a, rp); break;
   default: return fail(kUnsupported, "matmul rows: weight type %d", type);
   }
   return check_launch(ROPE ? "mfma_rows (rope)" : "mfma_rows");
@@ -880,6 +879,18 @@ bool rows_narrow(const MatvecArgs& a) {
   uint32_t wg16 = 0;
   for (int s = 0; s < a.n_seg; ++s) wg16 += static_cast<uint32_t>(ceil_div(a.seg[s].n_out, kRowsTN));
   return static_cast<uint64_t>(wg16) * ceil_div(a.m, 16u) < 256;
+}
+
+// Chunks of 64 blocks where the grid is one round of workgroups (their LDS then holds one per
+// CU) and the row is whole 64-block chunks: C4 down at 16 / 32 rows 15.3 / 18.8 -> 14.8 / 17.1 us,
+// wo 5.5 / 6.3 -> 5.1 / 5.7. Otherwise 32 (q|k|v of C4, C5's matrices, 64 rows: slower at 64).
+template <uint32_t TN, bool ROPE>
+int rows_launch_chunked(int type, MatvecArgs& a, const RowsRope& rp = RowsRope{}) {
+  uint32_t wg = 0;
+  for (int s = 0; s < a.n_seg; ++s) wg += static_cast<uint32_t>(ceil_div(a.seg[s].n_out, TN));
+  if (static_cast<uint64_t>(wg) * ceil_div(a.m, 16u) <= 256 && a.nb % 64 == 0)
+    return rows_launch<16, TN, ROPE, kRowsChains, 64>(type, a, rp);
+  return rows_launch<16, TN, ROPE, kRowsChains, kRowsChunk>(type, a, rp);
 }
 
 }  // namespace
@@ -981,12 +992,12 @@ int matmul_q8_rows_launch(int type, MatvecArgs& a) {
   // Up to 32 rows go in tiles of 16 activation rows (two tiles along the grid's second axis
   // above 16): a workgroup of 32 rows would run twice the folds and read twice the activations
   // for the same weight rows (C4 down at 32 rows 26.9 -> 21.0 us).
-  return rows_narrow(a) ? rows_launch<16, 8>(type, a) : rows_launch<16>(type, a);
+  return rows_narrow(a) ? rows_launch_chunked<8, false>(type, a) : rows_launch_chunked<kRowsTN, false>(type, a);
 }
 
 int matmul_q8_rows_rope_launch(int type, MatvecArgs& a, const RowsRope& rp) {
   if (a.n_seg != 3 || !matmul_q8_rows_fits(type, a)) return fail(kUnsupported, "matmul rows (rope): shape or alignment");
-  return rows_narrow(a) ? rows_launch<16, 8, true>(type, a, rp) : rows_launch<16, kRowsTN, true>(type, a, rp);
+  return rows_narrow(a) ? rows_launch_chunked<8, true>(type, a, rp) : rows_launch_chunked<kRowsTN, true>(type, a, rp);
 }
 
 int matmul_q8_mfma_launch(int type, MatvecArgs& a) {
