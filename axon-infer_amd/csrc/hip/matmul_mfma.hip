@@ -156,14 +156,15 @@ __global__ __launch_bounds__(kThreads) void mfma_q8_kernel(MatvecArgs args, uint
   }
 }
 
-// ---- Few activation rows (batched decode): 5..64 rows -------------------------------------
+// ---- Few activation rows (batched decode): 3..64 rows -------------------------------------
 // The same MFMA sums and the same per-output expression, block after block in order, with the
-// work spread for latency: a workgroup owns 16 weight rows x TM activation rows (TM 16 or 32),
-// every segment of the call (q|k|v, gate|up) is one grid, and each of the four waves runs the
-// tile's MFMAs but folds one of the four outputs a lane's MFMA result holds (wave w: activation
-// rows 4 kq + w), so a wave's float work per block is one output per M tile. MFMAs go in
-// batches of eight blocks ahead of their folds, which stay in block order.
-// K goes in chunks of kRowsChunk blocks. Each thread loads whole (row, block) items of the next
+// work spread for latency: a workgroup owns 16 (or 8) weight rows x 16 activation rows, every
+// segment of the call (q|k|v, gate|up) is one grid, and 17..64 rows take several row tiles
+// along the grid's second axis. Per K chunk the four waves split its blocks, run each block's
+// MFMA once and write its terms float(sumi) * d_w * d_x into LDS; then each thread adds one
+// output's terms in block order (terms, then chains).
+// K goes in chunks of KC blocks (32, or 64 where the grid is one round of workgroups). Each
+// thread loads whole (row, block) items of the next
 // chunk into registers (from the 4-byte boundary at or below the block, enough dwords to cover
 // it) while the current chunk computes, then expands them once into 32 aligned int8 values and
 // the scales in LDS: Q8_0 quants as they are, Q4_0 nibbles as q - 8 ((b + 0x78) ^ 0x80 per
@@ -179,7 +180,8 @@ __host__ __device__ constexpr uint32_t item_dwords() {
 }
 
 // LDS: expanded weights [16][KC * 8 + 4], expanded activations [TM][KC * 8 + 4] (dwords), then
-// per (row, block) scales: wd, wm [16][KC], xd, xs [TM][KC] (KC blocks per chunk).
+// per (row, block) scales: wd, wm [16][KC], xd, xs [KC][TM] (KC blocks per chunk); the launcher
+// adds the terms buffer.
 template <int TM, uint32_t TN = kRowsTN, uint32_t KC = kRowsChunk>
 __host__ __device__ constexpr size_t rows_lds() {
   return (static_cast<size_t>(TN + TM) * (KC * 8 + 4) + static_cast<size_t>(TN + TM) * KC * 2) * 4;
@@ -187,13 +189,13 @@ __host__ __device__ constexpr size_t rows_lds() {
 
 // TN: weight rows per workgroup, 16 or 8. With 8 (a narrow matrix, so twice the workgroups),
 // lanes of weight column col read row col % 8 into the 16-wide MFMA and only columns below 8
-// are folded and stored.
-template <int T, int TM, uint32_t TN = kRowsTN, bool ROPE = false, bool CHAINS = false, uint32_t KCH = kRowsChunk>
+// are stored.
+template <int T, int TM, uint32_t TN = kRowsTN, bool ROPE = false, uint32_t KCH = kRowsChunk>
 __global__ __launch_bounds__(kThreads) void mfma_rows_kernel(MatvecArgs args, RowsRope rp) {
   static_assert(TN == 16 || TN == 8, "16 or 8 weight rows");
   constexpr int bs = block_bytes<T>();
   constexpr uint32_t KC = KCH, P = KCH * 8 + 4;
-  constexpr uint32_t MT = TM / 16;                      // MFMA tiles along the activation rows
+  static_assert(TM == 16, "one tile of 16 activation rows");
   constexpr uint32_t WI = TN * KC / kThreads;           // weight items per thread per chunk
   constexpr uint32_t XI = TM * KC / kThreads;           // activation items per thread per chunk
   constexpr uint32_t WD = item_dwords<T>(), XD = item_dwords<Q8_0>();
@@ -312,8 +314,8 @@ __global__ __launch_bounds__(kThreads) void mfma_rows_kernel(MatvecArgs args, Ro
       uint4* dst = reinterpret_cast<uint4*>(xa + row * P + b * 8);
       dst[0] = make_uint4(q[0], q[1], q[2], q[3]);
       dst[1] = make_uint4(q[4], q[5], q[6], q[7]);
-      // The chains read a lane's four rows of a block at once: block-major there.
-      const uint32_t xi = CHAINS ? b * TM + row : row * KC + b;
+      // The terms read a lane's four rows of a block at once: block-major.
+      const uint32_t xi = b * TM + row;
       xd[xi] = half_bits_to_float(v[0] & 0xffffu);
       if constexpr (T == Q4_1) xs[xi] = sum;
     }
@@ -362,144 +364,75 @@ __global__ __launch_bounds__(kThreads) void mfma_rows_kernel(MatvecArgs args, Ro
     }
   };
 
-  if constexpr (CHAINS) {
-    // Terms, then chains. Per chunk, wave w runs the MFMAs of blocks 8w .. 8w + 7 (each once,
-    // all four results of a lane used) and forms their terms float(sumi) * d_w * d_x (+ m_w *
-    // d_x * float(sumx), Q4_1) into LDS ([row][column][block]); after a barrier thread t adds
-    // the chunk's terms of output (row t / 16, column t % 16) in block order. The terms and
-    // the adds are the scalar table's operations, so the bits are the fold's.
-    static_assert(TM == 16, "one tile of 16 activation rows");
-    constexpr uint32_t TP = KC + 4;              // floats per (row, column) of terms
-    constexpr uint32_t BW = KC / 4;              // blocks per wave per chunk
-    float* terms = reinterpret_cast<float*>(xs + TM * KC);  // [16][16][TP]
-    const uint32_t crow = tid >> 4, ccol = tid & 15;        // this thread's chain
-    float acc = 0.0f;
-    auto chunk = [&](uint32_t c, Raw& r) {
-      const uint32_t cb = min(KC, nb - c * KC);
-      expand(c, r);
-      __syncthreads();
-      if (c + 2 < n_chunks) load(c + 2, r);
-      const uint32_t b0 = wave * BW;
-      i32x4 d[BW];
-#pragma unroll
-      for (uint32_t i = 0; i < BW; ++i) {
-        const uint2 wq = *reinterpret_cast<const uint2*>(wa + wrow * P + (b0 + i) * 8 + 2 * kq);
-        const uint2 xq = *reinterpret_cast<const uint2*>(xa + col * P + (b0 + i) * 8 + 2 * kq);
-        const int64_t bw = static_cast<int64_t>((static_cast<uint64_t>(wq.y) << 32) | wq.x);
-        const int64_t ax = static_cast<int64_t>((static_cast<uint64_t>(xq.y) << 32) | xq.x);
-        i32x4 z = {0, 0, 0, 0};
-        d[i] = __builtin_amdgcn_mfma_i32_16x16x32_i8(ax, bw, z, 0, 0, 0);
-      }
-      // Blocks past cb hold stale bytes; their terms are never added.
-      float t[4][BW];
-#pragma unroll
-      for (uint32_t i = 0; i < BW; ++i) {
-        const uint32_t b = b0 + i;
-        const float dw = wd[wrow * KC + b];
-        const float4 dx4 = *reinterpret_cast<const float4*>(xd + b * TM + 4 * kq);  // rows 4kq..4kq+3
-        const float dx[4] = {dx4.x, dx4.y, dx4.z, dx4.w};
-        if constexpr (T == Q4_1) {
-          const float mw = wmn[wrow * KC + b];
-          const int4 sx4 = *reinterpret_cast<const int4*>(xs + b * TM + 4 * kq);
-          const int32_t sx[4] = {sx4.x, sx4.y, sx4.z, sx4.w};
-#pragma unroll
-          for (uint32_t v = 0; v < 4; ++v)
-            t[v][i] = static_cast<float>(d[i][v]) * dw * dx[v] + mw * dx[v] * static_cast<float>(sx[v]);
-        } else {
-          // Q4_0: sumi carries the -8 offset already (the weights entered as q - 8).
-#pragma unroll
-          for (uint32_t v = 0; v < 4; ++v) t[v][i] = static_cast<float>(d[i][v]) * dw * dx[v];
-        }
-      }
-#pragma unroll
-      for (uint32_t v = 0; v < 4; ++v) {
-        float4* dst = reinterpret_cast<float4*>(terms + ((4 * kq + v) * 16 + col) * TP + b0);
-#pragma unroll
-        for (uint32_t i = 0; i < BW; i += 4) dst[i / 4] = make_float4(t[v][i], t[v][i + 1], t[v][i + 2], t[v][i + 3]);
-      }
-      __syncthreads();
-      const float* tp = terms + (crow * 16 + ccol) * TP;
-      if (cb == KC) {
-#pragma unroll
-        for (uint32_t b = 0; b < KC; b += 4) {
-          const float4 q4 = *reinterpret_cast<const float4*>(tp + b);
-          acc += q4.x;
-          acc += q4.y;
-          acc += q4.z;
-          acc += q4.w;
-        }
-      } else {
-        for (uint32_t b = 0; b < cb; ++b) acc += tp[b];
-      }
-      // The next chunk's expand writes only the operand and scale regions, and its barrier
-      // orders these reads before the next terms are written.
-    };
-    Raw ra, rb;
-    load(0, ra);
-    if (n_chunks > 1) load(1, rb);
-    for (uint32_t c = 0; c < n_chunks; c += 2) {
-      chunk(c, ra);
-      if (c + 1 < n_chunks) chunk(c + 1, rb);
-    }
-    finish(ccol, crow, acc);
-    return;
-  }
-
-  // Wave w feeds activation row (col + w) % 16 as A row col, which moves D row 4 kq + w (the
-  // output this wave folds) into the lane's first result: d[0] = sumi of activation row
-  // 4 kq + w and weight row col.
-  const uint32_t arow = (col + wave) & 15;
-  const uint32_t orow = 4 * kq + wave;
-  float acc[MT];
-#pragma unroll
-  for (uint32_t t = 0; t < MT; ++t) acc[t] = 0.0f;
-  auto sums = [&](uint32_t b, uint32_t t) {
-    const uint2 wq = *reinterpret_cast<const uint2*>(wa + wrow * P + b * 8 + 2 * kq);
-    const uint2 xq = *reinterpret_cast<const uint2*>(xa + (16 * t + arow) * P + b * 8 + 2 * kq);
-    const int64_t bw = static_cast<int64_t>((static_cast<uint64_t>(wq.y) << 32) | wq.x);
-    const int64_t ax = static_cast<int64_t>((static_cast<uint64_t>(xq.y) << 32) | xq.x);
-    i32x4 d = {0, 0, 0, 0};
-    d = __builtin_amdgcn_mfma_i32_16x16x32_i8(ax, bw, d, 0, 0, 0);
-    return d[0];
-  };
-  auto fold = [&](uint32_t b, uint32_t t, int32_t sumi) {
-    const uint32_t r = 16 * t + orow;
-    const float dw = wd[wrow * KC + b];
-    const float dx = xd[r * KC + b];
-    if constexpr (T == Q4_1) {
-      acc[t] += static_cast<float>(sumi) * dw * dx + wmn[wrow * KC + b] * dx * static_cast<float>(xs[r * KC + b]);
-    } else {
-      // Q4_0: sumi carries the -8 offset already (the weights entered as q - 8).
-      acc[t] += static_cast<float>(sumi) * dw * dx;
-    }
-  };
-  constexpr uint32_t kBatch = 8;  // MFMAs issued together before their sums are folded
-  static_assert(KC % kBatch == 0, "whole batches");
-
-  // Two chunks' loads in flight: chunk c + 2 goes into c's registers once they are expanded.
+  // Terms, then chains. Per chunk, wave w runs the MFMAs of its quarter of the blocks (each
+  // once, all four results of a lane used) and forms their terms float(sumi) * d_w * d_x
+  // (+ m_w * d_x * float(sumx), Q4_1) into LDS ([row][column][block]); after a barrier thread t
+  // adds the chunk's terms of output (row t / 16, column t % 16) in block order. The terms and
+  // the adds are the scalar table's operations in its order, so the bits are its bits.
+  constexpr uint32_t TP = KC + 4;              // floats per (row, column) of terms
+  constexpr uint32_t BW = KC / 4;              // blocks per wave per chunk
+  float* terms = reinterpret_cast<float*>(xs + TM * KC);  // [16][16][TP]
+  const uint32_t crow = tid >> 4, ccol = tid & 15;        // this thread's chain
+  float acc = 0.0f;
   auto chunk = [&](uint32_t c, Raw& r) {
     const uint32_t cb = min(KC, nb - c * KC);
     expand(c, r);
     __syncthreads();
     if (c + 2 < n_chunks) load(c + 2, r);
-    if (cb == KC) {
-      for (uint32_t b0 = 0; b0 < KC; b0 += kBatch) {
-        int32_t d[kBatch][MT];
+    const uint32_t b0 = wave * BW;
+    i32x4 d[BW];
 #pragma unroll
-        for (uint32_t k = 0; k < kBatch; ++k)
+    for (uint32_t i = 0; i < BW; ++i) {
+      const uint2 wq = *reinterpret_cast<const uint2*>(wa + wrow * P + (b0 + i) * 8 + 2 * kq);
+      const uint2 xq = *reinterpret_cast<const uint2*>(xa + col * P + (b0 + i) * 8 + 2 * kq);
+      const int64_t bw = static_cast<int64_t>((static_cast<uint64_t>(wq.y) << 32) | wq.x);
+      const int64_t ax = static_cast<int64_t>((static_cast<uint64_t>(xq.y) << 32) | xq.x);
+      i32x4 z = {0, 0, 0, 0};
+      d[i] = __builtin_amdgcn_mfma_i32_16x16x32_i8(ax, bw, z, 0, 0, 0);
+    }
+    // Blocks past cb hold stale bytes; their terms are never added.
+    float t[4][BW];
 #pragma unroll
-          for (uint32_t t = 0; t < MT; ++t) d[k][t] = sums(b0 + k, t);
+    for (uint32_t i = 0; i < BW; ++i) {
+      const uint32_t b = b0 + i;
+      const float dw = wd[wrow * KC + b];
+      const float4 dx4 = *reinterpret_cast<const float4*>(xd + b * TM + 4 * kq);  // rows 4kq..4kq+3
+      const float dx[4] = {dx4.x, dx4.y, dx4.z, dx4.w};
+      if constexpr (T == Q4_1) {
+        const float mw = wmn[wrow * KC + b];
+        const int4 sx4 = *reinterpret_cast<const int4*>(xs + b * TM + 4 * kq);
+        const int32_t sx[4] = {sx4.x, sx4.y, sx4.z, sx4.w};
 #pragma unroll
-        for (uint32_t k = 0; k < kBatch; ++k)
+        for (uint32_t v = 0; v < 4; ++v)
+          t[v][i] = static_cast<float>(d[i][v]) * dw * dx[v] + mw * dx[v] * static_cast<float>(sx[v]);
+      } else {
+        // Q4_0: sumi carries the -8 offset already (the weights entered as q - 8).
 #pragma unroll
-          for (uint32_t t = 0; t < MT; ++t) fold(b0 + k, t, d[k][t]);
+        for (uint32_t v = 0; v < 4; ++v) t[v][i] = static_cast<float>(d[i][v]) * dw * dx[v];
       }
-    } else {
-      for (uint32_t b = 0; b < cb; ++b)
+    }
 #pragma unroll
-        for (uint32_t t = 0; t < MT; ++t) fold(b, t, sums(b, t));
+    for (uint32_t v = 0; v < 4; ++v) {
+      float4* dst = reinterpret_cast<float4*>(terms + ((4 * kq + v) * 16 + col) * TP + b0);
+#pragma unroll
+      for (uint32_t i = 0; i < BW; i += 4) dst[i / 4] = make_float4(t[v][i], t[v][i + 1], t[v][i + 2], t[v][i + 3]);
     }
     __syncthreads();
+    const float* tp = terms + (crow * 16 + ccol) * TP;
+    if (cb == KC) {
+#pragma unroll
+      for (uint32_t b = 0; b < KC; b += 4) {
+        const float4 q4 = *reinterpret_cast<const float4*>(tp + b);
+        acc += q4.x;
+        acc += q4.y;
+        acc += q4.z;
+        acc += q4.w;
+      }
+    } else {
+      for (uint32_t b = 0; b < cb; ++b) acc += tp[b];
+    }
+    // The next chunk's expand writes only the operand and scale regions, and its barrier
+    // orders these reads before the next terms are written.
   };
   Raw ra, rb;
   load(0, ra);
@@ -508,8 +441,8 @@ __global__ __launch_bounds__(kThreads) void mfma_rows_kernel(MatvecArgs args, Ro
     chunk(c, ra);
     if (c + 1 < n_chunks) chunk(c + 1, rb);
   }
-#pragma unroll
-  for (uint32_t t = 0; t < MT; ++t) finish(col, 16 * t + orow, acc[t]);
+  finish(ccol, crow, acc);
+
 }
 
 // ---- Many activation rows (prefill, mixed passes): 65 rows and more ------------------------
@@ -839,9 +772,7 @@ int tile_launch(int type, MatvecArgs& a) {
   return check_launch("mfma_tile");
 }
 
-constexpr bool kRowsChains = true;  // the few-rows kernel forms terms, then chains them
-
-template <int TM, uint32_t TN = kRowsTN, bool ROPE = false, bool CHAINS = kRowsChains, uint32_t KCH = kRowsChunk>
+template <int TM, uint32_t TN = kRowsTN, bool ROPE = false, uint32_t KCH = kRowsChunk>
 int rows_launch(int type, MatvecArgs& a, const RowsRope& rp = RowsRope{}) {
   uint32_t wg = 0;
   for (int s = 0; s < a.n_seg; ++s) {
@@ -849,8 +780,8 @@ int rows_launch(int type, MatvecArgs& a, const RowsRope& rp = RowsRope{}) {
     wg += static_cast<uint32_t>(ceil_div(a.seg[s].n_out, TN));
   }
   const dim3 grid(wg, static_cast<uint32_t>(ceil_div(a.m, TM)));
-  // The chains' terms buffer ([16][16][KCH + 4] floats) after the operands and scales.
-  constexpr size_t lds = rows_lds<TM, TN, KCH>() + (CHAINS ? 16 * 16 * (KCH + 4) * 4 : 0);
+  // The terms buffer ([16][16][KCH + 4] floats) after the operands and scales.
+  constexpr size_t lds = rows_lds<TM, TN, KCH>() + 16 * 16 * (KCH + 4) * 4;
   static_assert(lds <= 163840, "within one CU's LDS");
   static const bool granted = [] {
     bool ok = true;
@@ -859,16 +790,16 @@ int rows_launch(int type, MatvecArgs& a, const RowsRope& rp = RowsRope{}) {
         ok = ok && hipFuncSetAttribute(reinterpret_cast<const void*>(kernel), hipFuncAttributeMaxDynamicSharedMemorySize,
                                        static_cast<int>(lds)) == hipSuccess;
     };
-    grant(mfma_rows_kernel<Q8_0, TM, TN, ROPE, CHAINS, KCH>);
-    grant(mfma_rows_kernel<Q4_0, TM, TN, ROPE, CHAINS, KCH>);
-    grant(mfma_rows_kernel<Q4_1, TM, TN, ROPE, CHAINS, KCH>);
+    grant(mfma_rows_kernel<Q8_0, TM, TN, ROPE, KCH>);
+    grant(mfma_rows_kernel<Q4_0, TM, TN, ROPE, KCH>);
+    grant(mfma_rows_kernel<Q4_1, TM, TN, ROPE, KCH>);
     return ok;
   }();
   if (!granted) return fail(kUnsupported, "matmul rows: the LDS grant was refused");
   switch (type) {
-  case Q8_0: launch(mfma_rows_kernel<Q8_0, TM, TN, ROPE, CHAINS, KCH>, grid, dim3(kThreads), lds, a, rp); break;
-  case Q4_0: launch(mfma_rows_kernel<Q4_0, TM, TN, ROPE, CHAINS, KCH>, grid, dim3(kThreads), lds, a, rp); break;
-  case Q4_1: launch(mfma_rows_kernel<Q4_1, TM, TN, ROPE, CHAINS, KCH>, grid, dim3(kThreads), lds, a, rp); break;
+  case Q8_0: launch(mfma_rows_kernel<Q8_0, TM, TN, ROPE, KCH>, grid, dim3(kThreads), lds, a, rp); break;
+  case Q4_0: launch(mfma_rows_kernel<Q4_0, TM, TN, ROPE, KCH>, grid, dim3(kThreads), lds, a, rp); break;
+  case Q4_1: launch(mfma_rows_kernel<Q4_1, TM, TN, ROPE, KCH>, grid, dim3(kThreads), lds, a, rp); break;
   default: return fail(kUnsupported, "matmul rows: weight type %d", type);
   }
   return check_launch(ROPE ? "mfma_rows (rope)" : "mfma_rows");
@@ -889,8 +820,8 @@ int rows_launch_chunked(int type, MatvecArgs& a, const RowsRope& rp = RowsRope{}
   uint32_t wg = 0;
   for (int s = 0; s < a.n_seg; ++s) wg += static_cast<uint32_t>(ceil_div(a.seg[s].n_out, TN));
   if (static_cast<uint64_t>(wg) * ceil_div(a.m, 16u) <= 256 && a.nb % 64 == 0)
-    return rows_launch<16, TN, ROPE, kRowsChains, 64>(type, a, rp);
-  return rows_launch<16, TN, ROPE, kRowsChains, kRowsChunk>(type, a, rp);
+    return rows_launch<16, TN, ROPE, 64>(type, a, rp);
+  return rows_launch<16, TN, ROPE, kRowsChunk>(type, a, rp);
 }
 
 }  // namespace
