@@ -859,10 +859,12 @@ int matvec_q6k_planar_launch(MatvecArgs& a, uint32_t n_in) {
   // every weight slice is read once per that many rows), but fewer while that leaves under 1024
   // waves of 64 rows: a lane's chains run one element after another, so a short matrix needs
   // the rows spread over more waves more than it needs fewer weight reads. One launch covers
-  // every row.
+  // every row, in chunks of equal size (20 rows: 7, 7 and 6 rather than 8, 8 and 4, whose last
+  // chunk would run eight chains per lane for four rows).
   uint32_t mm = 1;
   while (mm < kQ6MaxRows && mm < a.m) mm *= 2;
   while (mm > 1 && ceil_div(a.m, mm) * ceil_div(n_out, 64) < 1024) mm /= 2;
+  mm = static_cast<uint32_t>(ceil_div(a.m, ceil_div(a.m, mm)));
   const size_t lds = 0;
   const uint32_t chunks = static_cast<uint32_t>(ceil_div(a.m, mm));
   // 256 rows per workgroup when that still gives a workgroup per CU, else 64.
@@ -879,7 +881,11 @@ int matvec_q6k_planar_launch(MatvecArgs& a, uint32_t n_in) {
     break;
   switch (mm) {
     AXON_Q6P(8)
+    AXON_Q6P(7)
+    AXON_Q6P(6)
+    AXON_Q6P(5)
     AXON_Q6P(4)
+    AXON_Q6P(3)
     AXON_Q6P(2)
     default:
       if (wide) launch(q6k_planar_kernel<1, 256>, grid, dim3(256), lds, a, n_in, col_bytes, m_total);

@@ -218,7 +218,7 @@ def test_planar_matmul_equals_the_stream_kernel_on_the_output_shape(H):
     w = q6k_weights(n_out, n_in, 5)
     dst, _ = repack(H, w, n_out, n_in)
     dw = H.DeviceBuffer.of(w)
-    for n_rows in (1, 4, 5, 32):
+    for n_rows in (1, 3, 4, 5, 6, 7, 12, 20, 28, 32):
         x = random_floats(n_rows * n_in, 40 + n_rows)
         dx = H.DeviceBuffer.of(x)
         a = H.DeviceBuffer(4 * n_rows * n_out)
