@@ -959,14 +959,14 @@ __global__ __launch_bounds__(1024) void attn_scores64_kernel(AttnArgs a) {
       const uint4 h = kr[c ^ sw];
       const float4 qa = *reinterpret_cast<const float4*>(qh + 8 * c);
       const float4 qb = *reinterpret_cast<const float4*>(qh + 8 * c + 4);
-      acc += qa.x * half_value(h.x & 0xffffu);
-      acc += qa.y * half_value(h.x >> 16);
-      acc += qa.z * half_value(h.y & 0xffffu);
-      acc += qa.w * half_value(h.y >> 16);
-      acc += qb.x * half_value(h.z & 0xffffu);
-      acc += qb.y * half_value(h.z >> 16);
-      acc += qb.z * half_value(h.w & 0xffffu);
-      acc += qb.w * half_value(h.w >> 16);
+      acc += mul_half_bits(qa.x, h.x);
+      acc += mul_half_bits_hi(qa.y, h.x);
+      acc += mul_half_bits(qa.z, h.y);
+      acc += mul_half_bits_hi(qa.w, h.y);
+      acc += mul_half_bits(qb.x, h.z);
+      acc += mul_half_bits_hi(qb.y, h.z);
+      acc += mul_half_bits(qb.z, h.w);
+      acc += mul_half_bits_hi(qb.w, h.w);
     }
   } else {
 #pragma unroll
@@ -1461,10 +1461,10 @@ __global__ __launch_bounds__(G * 128) void attn_mixd_kernel(AttnArgs a) {
   float va[kDTile], pa[kDTile], vb[kDTile], pb[kDTile];
   auto load_tile = [&](uint32_t t, float (&v)[kDTile], float (&pp)[kDTile]) {
     const float* pt = ph + t * kDTile;
-    if constexpr (F16) {  // each value widened (exactly, but for NaN payloads)
+    if constexpr (F16) {  // each value kept as its fp16 bits (the multiply widens it)
       const uint16_t* vt = reinterpret_cast<const uint16_t*>(ring) + (t % kR) * kDTile * 32 + d;
 #pragma unroll
-      for (uint32_t i = 0; i < kDTile; ++i) v[i] = half_value(vt[i * 32]);
+      for (uint32_t i = 0; i < kDTile; ++i) v[i] = __uint_as_float(vt[i * 32]);
     } else {
       const float* vt = ring + (t % kR) * kDTile * 32 + d;
 #pragma unroll
@@ -1479,9 +1479,13 @@ __global__ __launch_bounds__(G * 128) void attn_mixd_kernel(AttnArgs a) {
       pp[i + 3] = q4.w;
     }
   };
+  auto mul = [](float pv, float v) {
+    if constexpr (F16) return mul_half_bits(pv, __float_as_uint(v));
+    else return pv * v;
+  };
   auto mul_tile = [&](float (&v)[kDTile], const float (&pp)[kDTile]) {
 #pragma unroll
-    for (uint32_t i = 0; i < kDTile; ++i) v[i] = pp[i] * v[i];
+    for (uint32_t i = 0; i < kDTile; ++i) v[i] = mul(pp[i], v[i]);
   };
   auto add_tile = [&](const float (&prod)[kDTile], uint32_t t) {
     const uint32_t cnt = min(kDTile, n_vis - t * kDTile);
@@ -1499,7 +1503,7 @@ __global__ __launch_bounds__(G * 128) void attn_mixd_kernel(AttnArgs a) {
 #pragma unroll
     for (uint32_t i = 0; i < kDTile; ++i) {
       acc += prod[i];
-      v[i] = pp[i] * v[i];
+      v[i] = mul(pp[i], v[i]);
     }
   };
   uint32_t issued = min(n_tiles, kR);

@@ -58,6 +58,23 @@ __device__ __forceinline__ float half_value(uint32_t h) {
   return static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(h)));
 }
 
+// p * half_value(h) for the fp16 bits h in the low half of hb, rounded once as that product of
+// two floats is: v_fma_mix_f32 widens h exactly (fp16 denormals kept) and forms p * h + (-0),
+// and adding -0 leaves every product as it is, -0 included. One instruction in place of the
+// conversion and the multiply.
+__device__ __forceinline__ float mul_half_bits(float p, uint32_t hb) {
+  float r;
+  asm("v_fma_mix_f32 %0, %1, %2, %3 op_sel_hi:[0,1,0]" : "=v"(r) : "v"(p), "v"(hb), "v"(-0.0f));
+  return r;
+}
+
+// The same for the fp16 bits in the high half of hb.
+__device__ __forceinline__ float mul_half_bits_hi(float p, uint32_t hb) {
+  float r;
+  asm("v_fma_mix_f32 %0, %1, %2, %3 op_sel:[0,1,0] op_sel_hi:[0,1,0]" : "=v"(r) : "v"(p), "v"(hb), "v"(-0.0f));
+  return r;
+}
+
 // Round to nearest even, overflow to infinity, gradual underflow, NaN kept non-zero.
 __device__ __forceinline__ uint32_t float_to_half_bits(float f) {
   const uint32_t x = __float_as_uint(f);

@@ -658,8 +658,8 @@ __global__ __launch_bounds__(kStepThreads) void decode_step_kernel(StepK k) {
           for (uint32_t i = 0; i < kHeadDim / 8; ++i) {
 #pragma unroll
             for (uint32_t c = 0; c < 4; ++c) {
-              acc += qh[8 * i + 2 * c] * half_value(hh[i][c] & 0xffffu);
-              acc += qh[8 * i + 2 * c + 1] * half_value(hh[i][c] >> 16);
+              acc += mul_half_bits(qh[8 * i + 2 * c], hh[i][c]);
+              acc += mul_half_bits_hi(qh[8 * i + 2 * c + 1], hh[i][c]);
             }
           }
         } else {
