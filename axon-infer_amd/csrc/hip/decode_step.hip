@@ -732,7 +732,8 @@ __global__ __launch_bounds__(kStepThreads) void decode_step_kernel(StepK k) {
         const uint16_t* vbase16 =
             reinterpret_cast<const uint16_t*>(k.cache) + k.cache_off + L.v_layer_off + g * kHeadDim + dim0;
         // V slices of positions [0, last) in chunks of vchunk positions, kVRegs float4 per thread.
-        float4 vr[kVRegs];
+        float4 vr[kVRegs];  // float cache: the values
+        U2v vh[kVRegs];     // fp16 cache: the values' bits (the products widen them)
         auto vload = [&](uint32_t c) {
 #pragma unroll
           for (uint32_t u = 0; u < kVRegs; ++u) {
@@ -740,11 +741,10 @@ __global__ __launch_bounds__(kStepThreads) void decode_step_kernel(StepK k) {
             const uint32_t j = c * k.vchunk + unit / per;
             if constexpr (f16) {
               if (j < last) {
-                const U2v h = gload_u2(vbase16 + static_cast<size_t>(j) * kv_row + 4 * (unit % per));
-                vr[u] = make_float4(half_value(h[0] & 0xffffu), half_value(h[0] >> 16), half_value(h[1] & 0xffffu),
-                                    half_value(h[1] >> 16));
+                vh[u] = gload_u2(vbase16 + static_cast<size_t>(j) * kv_row + 4 * (unit % per));
               } else {
-                vr[u] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+                vh[u][0] = 0u;
+                vh[u][1] = 0u;
               }
             } else {
               vr[u] = j < last ? gload4(vbase + static_cast<size_t>(j) * kv_row + 4 * (unit % per))
@@ -817,10 +817,17 @@ __global__ __launch_bounds__(kStepThreads) void decode_step_kernel(StepK k) {
               if (jj < cnt) {
                 const float p = sc[j0 + jj] * inv;
                 float* dst = buf + 4 * q * pitch + jj;
-                dst[0] = p * vr[u].x;
-                dst[pitch] = p * vr[u].y;
-                dst[2 * pitch] = p * vr[u].z;
-                dst[3 * pitch] = p * vr[u].w;
+                if constexpr (f16) {
+                  dst[0] = mul_half_bits(p, vh[u][0]);
+                  dst[pitch] = mul_half_bits_hi(p, vh[u][0]);
+                  dst[2 * pitch] = mul_half_bits(p, vh[u][1]);
+                  dst[3 * pitch] = mul_half_bits_hi(p, vh[u][1]);
+                } else {
+                  dst[0] = p * vr[u].x;
+                  dst[pitch] = p * vr[u].y;
+                  dst[2 * pitch] = p * vr[u].z;
+                  dst[3 * pitch] = p * vr[u].w;
+                }
               }
             }
             if (c + 1 < chunks) vload(c + 1);
