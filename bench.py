@@ -929,7 +929,7 @@ def main() -> int:
         return traffic_summary(*args.traffic_summary)
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU; --gpus {args.gpus} is not supported "
-              "(the path would shard by sequence, see DESIGN.md)", file=sys.stderr)
+              "(on several GPUs the path would shard by sequence, one process per GPU)", file=sys.stderr)
         return 2
 
     import axon_hip as H
